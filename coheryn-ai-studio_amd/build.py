@@ -1,0 +1,66 @@
+"""Builds libcohx.so (HIP kernels + C ABI) for gfx950, in-tree.
+
+Flags that carry the engine's float semantics:
+  -ffp-contract=off                    no a*b+c fusion except explicit fmaf
+  -fno-gpu-flush-denormals-to-zero     IEEE subnormals, as on the CPU
+  -fhip-fp32-correctly-rounded-divide-sqrt   IEEE division / sqrt
+Packed fp32 instructions are disabled (-packed-fp32-ops).
+"""
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB = os.path.join(HERE, "libcohx.so")
+SOURCES = ["csrc/kernels.hip", "csrc/cohx.cpp", "csrc/gen.cpp"]
+HEADERS = ["csrc/device.h", "csrc/kernels.h", "csrc/internal.h", "../include/cohx.h"]
+ARCH = os.environ.get("COHX_ARCH", "gfx950")
+
+FLAGS = [
+    "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+    "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function", "-I", os.path.join(ROOT, "include"),
+]
+
+
+def _hipcc():
+    for p in ("/opt/rocm/bin/hipcc", "hipcc"):
+        if os.path.sep not in p or os.path.exists(p):
+            return p
+    return "hipcc"
+
+
+def build(verbose=False):
+    os.makedirs(os.path.join(HERE, "_build"), exist_ok=True)
+    hipcc = _hipcc()
+
+    def compile_one(src):
+        obj = os.path.join(HERE, "_build", os.path.basename(src) + ".o")
+        cmd = [hipcc, *FLAGS, "-x", "hip", "-c", os.path.join(HERE, src), "-o", obj]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        out = (r.stdout + r.stderr).splitlines()
+        out = [l for l in out if "packed-fp32-ops" not in l]
+        if r.returncode != 0 or verbose:
+            sys.stderr.write("\n".join(out) + "\n")
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {src}")
+        return obj
+
+    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+        objs = list(ex.map(compile_one, SOURCES))
+    tmp = LIB + ".tmp"
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("link failed")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,390 @@
+"""Python binding of libcohx.so (the MI355X step's C ABI, include/cohx.h).
+
+Mirrors the engine's API for this path so parity tests read like the
+reference's own (crates/coheryn-engine/tests/batching.rs):
+
+    model = Model.from_gguf(path, max_lanes=16, max_context=512)
+    state = model.begin_generation(prompt_ids, GenerationOptions(max_tokens=8))
+    while not state.is_finished():
+        if state.needs_forward():
+            model.step_batch([state])
+        state.sample()
+
+The product path is the HIP library: importing this module on a machine
+without the built library raises, and nothing here falls back to the CPU.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+import gguf
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libcohx.so")
+
+OK, INVALID_REQUEST, INVALID_GGUF, RESOURCE, CANCELLED, UNSUPPORTED, DEAD_END, DEVICE = range(8)
+STATUS_NAMES = {0: "ok", 1: "invalid_request", 2: "invalid_gguf", 3: "resource",
+                4: "cancelled", 5: "unsupported", 6: "dead_end", 7: "device"}
+FINISH = {0: None, 1: "stop", 2: "length", 3: "cancelled"}
+PAGE = 16
+
+
+class CohxError(RuntimeError):
+    def __init__(self, code, msg=""):
+        super().__init__(f"{STATUS_NAMES.get(code, code)}: {msg}")
+        self.code = code
+
+
+class ModelDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "layers", "hidden", "intermediate", "heads", "kv_heads", "head_dim", "vocabulary",
+        "context")] + [("rope_base", ctypes.c_float), ("norm_epsilon", ctypes.c_float)] + [
+        (n, ctypes.c_uint32) for n in (
+            "weight_dtype", "tied", "kv_dtype", "max_lanes", "max_rows", "max_seqs",
+            "max_context", "kv_pages", "n_eog")] + [("eog", ctypes.c_uint32 * 4)]
+
+
+class Lane(ctypes.Structure):
+    _fields_ = [("seq", ctypes.c_uint32), ("n_tokens", ctypes.c_uint32),
+                ("tokens", ctypes.POINTER(ctypes.c_uint32)), ("start_position", ctypes.c_uint32),
+                ("want_logits", ctypes.c_uint32)]
+
+
+class Batch(ctypes.Structure):
+    _fields_ = [("n_lanes", ctypes.c_uint32), ("lanes", ctypes.POINTER(Lane))]
+
+
+class LaneOut(ctypes.Structure):
+    _fields_ = [("status", ctypes.c_int32), ("argmax", ctypes.c_uint32),
+                ("logits", ctypes.POINTER(ctypes.c_float))]
+
+
+class StepOut(ctypes.Structure):
+    _fields_ = [("lanes", ctypes.POINTER(LaneOut)), ("width", ctypes.c_uint32),
+                ("rows", ctypes.c_uint32), ("matrix_bytes", ctypes.c_uint64),
+                ("kv_bytes", ctypes.c_uint64), ("elapsed_ns", ctypes.c_uint64)]
+
+
+class GenOptions(ctypes.Structure):
+    _fields_ = [("max_tokens", ctypes.c_uint32), ("temperature", ctypes.c_float),
+                ("top_k", ctypes.c_uint32), ("top_p", ctypes.c_float), ("seed", ctypes.c_uint64),
+                ("repetition_penalty", ctypes.c_float), ("frequency_penalty", ctypes.c_float),
+                ("presence_penalty", ctypes.c_float), ("n_stop_tokens", ctypes.c_uint32),
+                ("stop_tokens", ctypes.POINTER(ctypes.c_uint32)), ("context", ctypes.c_uint32)]
+
+
+class BatchStepC(ctypes.Structure):
+    _fields_ = [("width", ctypes.c_uint32), ("completed_tokens", ctypes.c_uint32),
+                ("matrix_tiles", ctypes.c_uint64), ("matrix_bytes", ctypes.c_uint64)]
+
+
+EXPORTS = {
+    "cohx_create": (ctypes.c_int, [ctypes.POINTER(ModelDesc), ctypes.c_int,
+                                   ctypes.POINTER(ctypes.c_void_p)]),
+    "cohx_destroy": (None, [ctypes.c_void_p]),
+    "cohx_last_error": (ctypes.c_char_p, [ctypes.c_void_p]),
+    "cohx_upload_tensor": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_uint32,
+                                          ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p,
+                                          ctypes.c_size_t]),
+    "cohx_finalize": (ctypes.c_int, [ctypes.c_void_p]),
+    "cohx_seq_alloc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32,
+                                      ctypes.POINTER(ctypes.c_uint32)]),
+    "cohx_seq_fork": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                     ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32)]),
+    "cohx_seq_free": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32]),
+    "cohx_seq_truncate": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32]),
+    "cohx_seq_length": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32,
+                                       ctypes.POINTER(ctypes.c_uint32)]),
+    "cohx_seq_pages": (ctypes.c_uint32, [ctypes.c_void_p, ctypes.c_uint32,
+                                         ctypes.POINTER(ctypes.c_int32), ctypes.c_uint32]),
+    "cohx_seq_read_kv": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                        ctypes.c_int, ctypes.POINTER(ctypes.c_float)]),
+    "cohx_seq_fill_synthetic": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                               ctypes.c_uint64, ctypes.c_uint32]),
+    "cohx_step": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Batch), ctypes.POINTER(StepOut)]),
+    "cohx_pack": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Batch),
+                                 ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32),
+                                 ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_uint32)]),
+    "cohx_gen_begin": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32),
+                                      ctypes.c_uint32, ctypes.POINTER(GenOptions), ctypes.c_void_p,
+                                      ctypes.POINTER(ctypes.c_void_p)]),
+    "cohx_step_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p),
+                                       ctypes.c_uint32, ctypes.POINTER(BatchStepC)]),
+    "cohx_step_generation": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+    "cohx_gen_sample": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64)]),
+    "cohx_gen_needs_forward": (ctypes.c_int, [ctypes.c_void_p]),
+    "cohx_gen_is_finished": (ctypes.c_int, [ctypes.c_void_p]),
+    "cohx_gen_is_prefilling": (ctypes.c_int, [ctypes.c_void_p]),
+    "cohx_gen_finish_reason": (ctypes.c_uint32, [ctypes.c_void_p]),
+    "cohx_gen_tokens": (ctypes.c_uint32, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32),
+                                          ctypes.c_uint32]),
+    "cohx_gen_cancel": (None, [ctypes.c_void_p]),
+    "cohx_gen_free": (None, [ctypes.c_void_p]),
+}
+
+
+def load_library(path=LIB_PATH):
+    if not os.path.exists(path):
+        raise OSError(f"{path} is not built (run __graft_entry__.build()); there is no CPU fallback")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in EXPORTS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        _lib = load_library()
+    return _lib
+
+
+def _u32p(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
+
+
+DTYPE = {"f16": 1, "q8_0": 8, "q4_0": 2}
+
+
+class Model:
+    """An MI355X context holding one Qwen2 model (Model::load, inference.rs:238-297)."""
+
+    def __init__(self, config, tensors, max_lanes=16, max_rows=None, max_seqs=None,
+                 max_context=None, kv_pages=0, device=0, eog=None):
+        self.config = dict(config)
+        L = lib()
+        mats = [t for n, t in tensors.items() if len(t.shape) == 2]
+        wdt = mats[0].dtype
+        d = ModelDesc()
+        for k in ("layers", "hidden", "intermediate", "heads", "kv_heads", "head_dim",
+                  "vocabulary", "context"):
+            setattr(d, k, int(config[k]))
+        d.rope_base = float(config["rope_base"])
+        d.norm_epsilon = float(config["norm_epsilon"])
+        d.weight_dtype = wdt
+        d.tied = 0 if "output.weight" in tensors else 1
+        d.kv_dtype = 0
+        d.max_lanes = max_lanes
+        d.max_rows = max_rows or max_lanes
+        d.max_seqs = max_seqs or max_lanes
+        d.max_context = max_context or min(int(config["context"]), 4096)
+        d.kv_pages = kv_pages
+        eog = list(eog if eog is not None else ([config["eos_token_id"]]
+                                                 if config.get("eos_token_id") is not None else []))
+        d.n_eog = len(eog)
+        for i, e in enumerate(eog):
+            d.eog[i] = e
+        self.desc = d
+        h = ctypes.c_void_p()
+        rc = L.cohx_create(ctypes.byref(d), device, ctypes.byref(h))
+        if rc:
+            raise CohxError(rc, "cohx_create")
+        self.h = h
+        self.max_lanes = max_lanes
+        self.max_context = d.max_context
+        for name, t in tensors.items():
+            data = np.ascontiguousarray(t.data)
+            ne1 = t.shape[1] if len(t.shape) > 1 else 1
+            rc = L.cohx_upload_tensor(h, name.encode(), t.dtype, t.shape[0], ne1,
+                                      data.ctypes.data, data.nbytes)
+            self._check(rc)
+        self._check(L.cohx_finalize(h))
+
+    @classmethod
+    def from_gguf(cls, path, **kw):
+        meta, tensors = gguf.read(path)
+        return cls(gguf.qwen2_config(meta), tensors, **kw)
+
+    def _check(self, rc):
+        if rc:
+            raise CohxError(rc, lib().cohx_last_error(self.h).decode())
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().cohx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    # ---- sequences ---------------------------------------------------------
+    def seq_alloc(self, capacity=None):
+        s = ctypes.c_uint32()
+        self._check(lib().cohx_seq_alloc(self.h, capacity or self.max_context, ctypes.byref(s)))
+        return s.value
+
+    def seq_fork(self, src, rows, capacity=None):
+        s = ctypes.c_uint32()
+        self._check(lib().cohx_seq_fork(self.h, src, rows, capacity or self.max_context,
+                                        ctypes.byref(s)))
+        return s.value
+
+    def seq_free(self, seq):
+        self._check(lib().cohx_seq_free(self.h, seq))
+
+    def seq_truncate(self, seq, rows):
+        self._check(lib().cohx_seq_truncate(self.h, seq, rows))
+
+    def seq_length(self, seq):
+        n = ctypes.c_uint32()
+        self._check(lib().cohx_seq_length(self.h, seq, ctypes.byref(n)))
+        return n.value
+
+    def seq_pages(self, seq):
+        n = lib().cohx_seq_pages(self.h, seq, None, 0)
+        out = np.zeros(n, np.int32)
+        lib().cohx_seq_pages(self.h, seq, out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), n)
+        return out
+
+    def seq_read_kv(self, seq, layer, values=False):
+        c = self.config
+        out = np.zeros((self.seq_length(seq), c["kv_heads"] * c["head_dim"]), np.float32)
+        self._check(lib().cohx_seq_read_kv(self.h, seq, layer, 1 if values else 0,
+                                           out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+        return out
+
+    def seq_fill_synthetic(self, seq, rows, seed, stream):
+        self._check(lib().cohx_seq_fill_synthetic(self.h, seq, rows, seed, stream))
+
+    # ---- the device step -----------------------------------------------------
+    def _batch(self, lanes):
+        arr = (Lane * len(lanes))()
+        keep = []
+        for i, ln in enumerate(lanes):
+            toks = np.ascontiguousarray(ln["tokens"], np.uint32)
+            keep.append(toks)
+            arr[i].seq = ln["seq"]
+            arr[i].n_tokens = toks.size
+            arr[i].tokens = _u32p(toks)
+            arr[i].start_position = ln.get("start", self.seq_length(ln["seq"]))
+            arr[i].want_logits = 1 if ln.get("logits") else 0
+        return Batch(len(lanes), arr), keep
+
+    def step(self, lanes):
+        """lanes: [{"seq", "tokens", "start"?, "logits"?: bool}] -> list of dicts."""
+        batch, keep = self._batch(lanes)
+        outs = (LaneOut * len(lanes))()
+        bufs = []
+        V = self.config["vocabulary"]
+        for i, ln in enumerate(lanes):
+            if ln.get("logits"):
+                b = np.zeros(V, np.float32)
+                bufs.append(b)
+                outs[i].logits = b.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+            else:
+                bufs.append(None)
+        so = StepOut()
+        so.lanes = outs
+        self._check(lib().cohx_step(self.h, ctypes.byref(batch), ctypes.byref(so)))
+        res = [dict(status=outs[i].status, argmax=outs[i].argmax, logits=bufs[i])
+               for i in range(len(lanes))]
+        self.last_step = dict(width=so.width, rows=so.rows, matrix_bytes=so.matrix_bytes,
+                              kv_bytes=so.kv_bytes, elapsed_ns=so.elapsed_ns)
+        return res
+
+    def pack(self, lanes):
+        batch, keep = self._batch(lanes)
+        n = len(lanes)
+        R = sum(len(l["tokens"]) for l in lanes)
+        cu = np.zeros(n + 1, np.uint32)
+        pos = np.zeros(R, np.uint32)
+        slot = np.zeros(R, np.int64)
+        lane = np.zeros(R, np.uint32)
+        self._check(lib().cohx_pack(self.h, ctypes.byref(batch), _u32p(cu), _u32p(pos),
+                                    slot.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                                    _u32p(lane)))
+        return cu, pos, slot, lane
+
+    # ---- generation API (generation.rs / batch.rs mirror) --------------------
+    def begin_generation(self, prompt, options=None, prior=None):
+        o = options or GenerationOptions()
+        p = np.ascontiguousarray(prompt, np.uint32)
+        stops = np.ascontiguousarray(o.stop_tokens, np.uint32)
+        c = GenOptions(o.max_tokens, o.temperature, o.top_k, o.top_p, o.seed,
+                       o.repetition_penalty, o.frequency_penalty, o.presence_penalty,
+                       stops.size, _u32p(stops), o.context)
+        h = ctypes.c_void_p()
+        rc = lib().cohx_gen_begin(self.h, _u32p(p), p.size, ctypes.byref(c),
+                                  prior.h if prior is not None else None, ctypes.byref(h))
+        self._check(rc)
+        return GenerationState(self, h)
+
+    def step_batch(self, states):
+        arr = (ctypes.c_void_p * len(states))(*[s.h for s in states])
+        st = BatchStepC()
+        self._check(lib().cohx_step_batch(self.h, arr, len(states), ctypes.byref(st)))
+        return dict(width=st.width, completed_tokens=st.completed_tokens,
+                    matrix_tiles=st.matrix_tiles, matrix_bytes=st.matrix_bytes)
+
+    def step_generation(self, state):
+        rc = lib().cohx_step_generation(self.h, state.h)
+        if rc:
+            raise CohxError(rc, lib().cohx_last_error(self.h).decode())
+
+
+class GenerationOptions:
+    def __init__(self, max_tokens=128, temperature=0.0, top_k=0, top_p=1.0, seed=0,
+                 repetition_penalty=1.0, frequency_penalty=0.0, presence_penalty=0.0,
+                 stop_tokens=(), context=0):
+        self.max_tokens, self.temperature, self.top_k, self.top_p = (max_tokens, temperature,
+                                                                     top_k, top_p)
+        self.seed, self.repetition_penalty = seed, repetition_penalty
+        self.frequency_penalty, self.presence_penalty = frequency_penalty, presence_penalty
+        self.stop_tokens, self.context = list(stop_tokens), context
+
+
+class GenerationState:
+    def __init__(self, model, h):
+        self.model, self.h = model, h
+
+    def __del__(self):
+        self.free()
+
+    def free(self):
+        if getattr(self, "h", None):
+            lib().cohx_gen_free(self.h)
+            self.h = None
+
+    def needs_forward(self):
+        return bool(lib().cohx_gen_needs_forward(self.h))
+
+    def is_finished(self):
+        return bool(lib().cohx_gen_is_finished(self.h))
+
+    def is_prefilling(self):
+        return bool(lib().cohx_gen_is_prefilling(self.h))
+
+    def finish_reason(self):
+        return FINISH[lib().cohx_gen_finish_reason(self.h)]
+
+    def sample(self):
+        t = ctypes.c_int64()
+        rc = lib().cohx_gen_sample(self.h, ctypes.byref(t))
+        if rc:
+            raise CohxError(rc, "sample")
+        return None if t.value < 0 else t.value
+
+    def token_ids(self):
+        n = lib().cohx_gen_tokens(self.h, None, 0)
+        out = np.zeros(n, np.uint32)
+        lib().cohx_gen_tokens(self.h, _u32p(out), n)
+        return [int(v) for v in out]
+
+    def cancel(self):
+        lib().cohx_gen_cancel(self.h)
+
+
+def generate(model, prompt, options):
+    """Model::generate's token loop (inference.rs:641-684) on one lane."""
+    st = model.begin_generation(prompt, options)
+    while not st.is_finished():
+        if st.needs_forward():
+            model.step_generation(st)
+        st.sample()
+    return st

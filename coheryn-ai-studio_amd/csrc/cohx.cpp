@@ -1,0 +1,765 @@
+// cohx context: HBM-resident weights, paged KV pool and the ragged step driver.
+//
+// Host-side counterpart of Model::load / Model::forward_batch
+// (crates/coheryn-engine/src/inference.rs:238-297, inference/batch.rs:117-273):
+// weights are repacked once into the matrix-core tile layout and stay in HBM
+// (the engine re-reads them from the file every step, README.md:77); each
+// sequence owns a page table into one KV pool (the engine's per-session
+// Vec<f32>, inference.rs:1019-1043).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "device.h"
+#include "internal.h"
+
+using namespace cohx;
+
+namespace cohx {
+int fail(cohx_ctx *ctx, int code, const std::string &msg) {
+  if (ctx) ctx->err = msg;
+  return code;
+}
+}  // namespace cohx
+
+#define HIP_TRY(expr)                                                                  \
+  do {                                                                                 \
+    hipError_t e_ = (expr);                                                            \
+    if (e_ != hipSuccess)                                                              \
+      return fail(ctx, COHX_DEVICE, std::string(#expr ": ") + hipGetErrorString(e_)); \
+  } while (0)
+
+namespace {
+
+int even(int n) { return (n + 1) & ~1; }
+
+template <typename T>
+int dalloc(cohx_ctx *ctx, T **p, size_t count) {
+  *p = nullptr;
+  if (count == 0) count = 1;
+  hipError_t e = hipMalloc(reinterpret_cast<void **>(p), count * sizeof(T));
+  if (e != hipSuccess) {
+    return fail(ctx, COHX_RESOURCE,
+                "device allocation of " + std::to_string(count * sizeof(T)) + " bytes failed");
+  }
+  ctx->allocations.push_back(*p);
+  e = hipMemset(*p, 0, count * sizeof(T));
+  if (e != hipSuccess) return fail(ctx, COHX_DEVICE, hipGetErrorString(e));
+  return COHX_OK;
+}
+
+template <typename T>
+int halloc(cohx_ctx *ctx, T **p, size_t count) {
+  hipError_t e = hipHostMalloc(reinterpret_cast<void **>(p), std::max<size_t>(count, 1) * sizeof(T),
+                               hipHostMallocDefault);
+  if (e != hipSuccess) return fail(ctx, COHX_RESOURCE, "pinned host allocation failed");
+  return COHX_OK;
+}
+
+// Matrix-core tile view of a Q8_0 matrix with `rows` rows of width K.
+int make_q8(cohx_ctx *ctx, DeviceMatrix &m, int rows, int K, int mtiles) {
+  m.view.dtype = 8;
+  m.view.rows = rows;
+  m.view.K = K;
+  m.view.nb = K / 32;
+  m.view.nbp = even(m.view.nb);
+  m.view.mtiles = mtiles;
+  const size_t tile_bytes = (size_t)m.view.nbp * 512;
+  int rc = dalloc(ctx, &m.qs, (size_t)mtiles * tile_bytes);
+  if (!rc) rc = dalloc(ctx, &m.ds, (size_t)mtiles * m.view.nbp * 16);
+  m.view.qs = m.qs;
+  m.view.ds = m.ds;
+  return rc;
+}
+
+int make_f16(cohx_ctx *ctx, DeviceMatrix &m, int rows, int K) {
+  m.view.dtype = 1;
+  m.view.rows = rows;
+  m.view.K = K;
+  m.view.nb = K / 32;
+  m.view.nbp = even(m.view.nb);
+  m.view.mtiles = (rows + 15) / 16;
+  int rc = dalloc(ctx, &m.f16, (size_t)rows * K);
+  m.view.f16 = m.f16;
+  return rc;
+}
+
+// GGUF Q8_0 rows -> tiles [tile_first, ...) of the device layout, tile i of the
+// source landing on tile tile_first + i*tile_step.
+int upload_q8(cohx_ctx *ctx, DeviceMatrix &m, const uint8_t *src, int rows, int tile_first,
+              int tile_step) {
+  const int nb = m.view.nb, nbp = m.view.nbp;
+  const int tiles = (rows + 15) / 16;
+  const size_t tile_bytes = (size_t)nbp * 512, tile_scales = (size_t)nbp * 16;
+  std::vector<int8_t> qs(tiles * tile_bytes, 0);
+  std::vector<uint16_t> ds(tiles * tile_scales, 0);
+  for (int r = 0; r < rows; r++) {
+    const int t = r / 16, c = r % 16;
+    for (int b = 0; b < nb; b++) {
+      const uint8_t *blk = src + ((size_t)r * nb + b) * 34;
+      ds[q8_scale(t, nbp, b, c)] = (uint16_t)(blk[0] | (blk[1] << 8));
+      for (int g = 0; g < 4; g++)
+        for (int j = 0; j < 8; j++)
+          qs[q8_byte(t, nbp, b, g * 16 + c, j)] = (int8_t)blk[2 + g * 8 + j];
+    }
+  }
+  HIP_TRY(hipMemcpy2D(m.qs + (size_t)tile_first * tile_bytes, tile_bytes * tile_step, qs.data(),
+                      tile_bytes, tile_bytes, tiles, hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy2D(m.ds + (size_t)tile_first * tile_scales, tile_scales * 2 * tile_step,
+                      ds.data(), tile_scales * 2, tile_scales * 2, tiles, hipMemcpyHostToDevice));
+  return COHX_OK;
+}
+
+int upload_f16(cohx_ctx *ctx, DeviceMatrix &m, const void *src, int rows, int row_first) {
+  HIP_TRY(hipMemcpy(m.f16 + (size_t)row_first * m.view.K, src, (size_t)rows * m.view.K * 2,
+                    hipMemcpyHostToDevice));
+  return COHX_OK;
+}
+
+int upload_matrix(cohx_ctx *ctx, DeviceMatrix &m, uint32_t dtype, const void *data, int rows,
+                  int first, int step) {
+  if (dtype != (uint32_t)m.view.dtype)
+    return fail(ctx, COHX_UNSUPPORTED, "matrix dtype differs from the context's weight dtype");
+  if (dtype == 8) return upload_q8(ctx, m, (const uint8_t *)data, rows, first, step);
+  return upload_f16(ctx, m, data, rows, first);
+}
+
+size_t row_bytes(uint32_t dtype, uint64_t width) {
+  switch (dtype) {
+    case 0: return width * 4;
+    case 1: return width * 2;
+    case 2: return width / 32 * 18;
+    case 8: return width / 32 * 34;
+    default: return 0;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *cohx_last_error(const cohx_ctx *ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
+  if (!d || !out) return COHX_INVALID_REQUEST;
+  *out = nullptr;
+  if (!d->layers || !d->hidden || !d->heads || !d->kv_heads || d->hidden % d->heads ||
+      d->heads % d->kv_heads || d->head_dim != d->hidden / d->heads || d->head_dim % 32 ||
+      d->head_dim > 128 || d->heads / d->kv_heads > (uint32_t)kMaxGroup || d->hidden % 32 ||
+      d->intermediate % 32 || !d->vocabulary)
+    return COHX_INVALID_GGUF;
+  if (d->weight_dtype != COHX_Q8_0 && d->weight_dtype != COHX_F16) return COHX_UNSUPPORTED;
+  if (d->kv_dtype != 0) return COHX_UNSUPPORTED;
+  if (!d->max_lanes || d->max_lanes > 1024 || !d->max_rows || d->max_rows < d->max_lanes ||
+      !d->max_seqs || !d->max_context || d->max_context > d->context || d->n_eog > 4)
+    return COHX_INVALID_REQUEST;
+  cohx_ctx *ctx = new cohx_ctx();
+  ctx->desc = *d;
+  ctx->device = device;
+  auto bail = [&](int rc) {
+    cohx_destroy(ctx);
+    return rc;
+  };
+  if (hipSetDevice(device) != hipSuccess) return bail(COHX_DEVICE);
+  if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess)
+    return bail(COHX_DEVICE);
+  const int H = d->hidden, F = d->intermediate, V = d->vocabulary, NH = d->heads,
+            NKV = d->kv_heads, D = d->head_dim, KVD = NKV * D, L = d->layers;
+  const int R = d->max_rows;
+  ctx->nbp_h = even(H / 32);
+  ctx->nbp_f = even(F / 32);
+  ctx->nbp_max = std::max(ctx->nbp_h, ctx->nbp_f);
+  ctx->max_pages = (int)((d->max_context + kPage - 1) / kPage);
+  ctx->max_chunks = (int)((d->max_context + kChunk - 1) / kChunk);
+  const uint32_t pages = d->kv_pages ? d->kv_pages : d->max_seqs * (uint32_t)ctx->max_pages;
+  ctx->layer_stride = (size_t)pages * NKV * kPage * D;
+  int rc = COHX_OK;
+  // weights
+  ctx->layers.resize(L);
+  const bool q8 = d->weight_dtype == COHX_Q8_0;
+  for (int l = 0; l < L && !rc; l++) {
+    Layer &ly = ctx->layers[l];
+    rc = dalloc(ctx, &ly.attn_norm, H);
+    if (!rc) rc = dalloc(ctx, &ly.ffn_norm, H);
+    if (!rc) rc = dalloc(ctx, &ly.bqkv, H + 2 * KVD);
+    if (q8) {
+      if (!rc) rc = make_q8(ctx, ly.qkv, H + 2 * KVD, H, H / 16 + 2 * ((KVD + 15) / 16));
+      if (!rc) rc = make_q8(ctx, ly.o, H, H, (H + 15) / 16);
+      if (!rc) rc = make_q8(ctx, ly.gu, 2 * F, H, 2 * ((F + 15) / 16));
+      if (!rc) rc = make_q8(ctx, ly.down, H, F, (H + 15) / 16);
+    } else {
+      if (!rc) rc = make_f16(ctx, ly.qkv, H + 2 * KVD, H);
+      if (!rc) rc = make_f16(ctx, ly.o, H, H);
+      if (!rc) rc = make_f16(ctx, ly.gu, 2 * F, H);
+      if (!rc) rc = make_f16(ctx, ly.down, H, F);
+    }
+  }
+  if (H % 16 || KVD % 16) rc = rc ? rc : COHX_INVALID_GGUF;
+  if (!rc) rc = dalloc(ctx, &ctx->output_norm, H);
+  if (!rc) rc = q8 ? make_q8(ctx, ctx->embd, V, H, (V + 15) / 16) : make_f16(ctx, ctx->embd, V, H);
+  if (!rc && !d->tied)
+    rc = q8 ? make_q8(ctx, ctx->output, V, H, (V + 15) / 16) : make_f16(ctx, ctx->output, V, H);
+  // RoPE table: (cos, sin) of the engine's iterative angle (cpu.rs:59-73).
+  if (!rc) {
+    std::vector<float2> tab((size_t)d->max_context * (D / 2));
+    const float step = powf(d->rope_base, -2.0f / (float)D);
+    for (uint32_t p = 0; p < d->max_context; p++) {
+      float angle = (float)p;
+      for (int i = 0; i < D / 2; i++) {
+        tab[(size_t)p * (D / 2) + i] = make_float2(cosf(angle), sinf(angle));
+        angle *= step;
+      }
+    }
+    rc = dalloc(ctx, &ctx->rope, tab.size());
+    if (!rc && hipMemcpy(ctx->rope, tab.data(), tab.size() * sizeof(float2),
+                         hipMemcpyHostToDevice) != hipSuccess)
+      rc = COHX_DEVICE;
+  }
+  // KV pool and page tables
+  if (!rc) rc = dalloc(ctx, &ctx->kpool, ctx->layer_stride * L);
+  if (!rc) rc = dalloc(ctx, &ctx->vpool, ctx->layer_stride * L);
+  if (!rc) rc = dalloc(ctx, &ctx->page_table, (size_t)d->max_seqs * ctx->max_pages);
+  ctx->h_page_table.assign((size_t)d->max_seqs * ctx->max_pages, -1);
+  ctx->pt_dirty.assign(d->max_seqs, 1);
+  ctx->page_refs.assign(pages, 0);
+  for (int32_t p = (int32_t)pages - 1; p >= 0; p--) ctx->free_pages.push_back(p);
+  ctx->seqs.resize(d->max_seqs);
+  for (int32_t s = (int32_t)d->max_seqs - 1; s >= 0; s--) ctx->free_seqs.push_back((uint32_t)s);
+  // step workspaces
+  Workspace &w = ctx->ws;
+  const size_t rtiles = (size_t)(R + 15) / 16;
+  const uint32_t NL = d->max_lanes;
+  if (!rc) rc = dalloc(ctx, &w.lane_info, (size_t)NL * 4);
+  if (!rc) rc = dalloc(ctx, &w.tokens, R);
+  if (!rc) rc = dalloc(ctx, &w.cu, NL + 1);
+  if (!rc) rc = dalloc(ctx, &w.row_pos, R);
+  if (!rc) rc = dalloc(ctx, &w.row_slot, R);
+  if (!rc) rc = dalloc(ctx, &w.row_lane, R);
+  if (!rc) rc = dalloc(ctx, &w.row_token, R);
+  if (!rc) rc = dalloc(ctx, &w.row_seq, R);
+  if (!rc) rc = dalloc(ctx, &w.lane_last, NL);
+  if (!rc) rc = dalloc(ctx, &w.row_err, R);
+  if (!rc) rc = dalloc(ctx, &w.x, (size_t)R * H);
+  if (!rc) rc = dalloc(ctx, &w.qkv, (size_t)R * (H + 2 * KVD));
+  if (!rc) rc = dalloc(ctx, &w.q_rot, (size_t)R * H);
+  if (!rc) rc = dalloc(ctx, &w.h, (size_t)R * F);
+  if (!rc) rc = dalloc(ctx, &w.act_qs, rtiles * ctx->nbp_max * 512);
+  if (!rc) rc = dalloc(ctx, &w.act_ds, rtiles * ctx->nbp_max * 16);
+  if (!rc) rc = dalloc(ctx, &w.act_f16, (size_t)R * std::max(H, F));
+  if (!rc) rc = dalloc(ctx, &w.scores, (size_t)R * NH * d->max_context);
+  if (!rc) rc = dalloc(ctx, &w.chunk_max, (size_t)R * NH * ctx->max_chunks);
+  if (!rc) rc = dalloc(ctx, &w.partial, (size_t)R * NH * ctx->max_chunks * D);
+  if (!rc) rc = dalloc(ctx, &w.logits, (size_t)NL * V);
+  if (!rc) rc = dalloc(ctx, &w.argmax, NL);
+  if (!rc) rc = halloc(ctx, &w.h_upload, (size_t)NL * 4 + R);
+  if (!rc) rc = halloc(ctx, &w.h_row_err, R);
+  if (!rc) rc = halloc(ctx, &w.h_argmax, NL);
+  if (rc) return bail(rc);
+  *out = ctx;
+  return COHX_OK;
+}
+
+void cohx_destroy(cohx_ctx *ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  for (void *p : ctx->allocations) (void)hipFree(p);
+  if (ctx->ws.h_upload) (void)hipHostFree(ctx->ws.h_upload);
+  if (ctx->ws.h_row_err) (void)hipHostFree(ctx->ws.h_row_err);
+  if (ctx->ws.h_argmax) (void)hipHostFree(ctx->ws.h_argmax);
+  if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+// compat.rs:161-221: names and shapes of the Qwen2 graph.
+int cohx_upload_tensor(cohx_ctx *ctx, const char *name, uint32_t dtype, uint64_t ne0,
+                       uint64_t ne1, const void *data, size_t bytes) {
+  if (!ctx || !name || !data) return COHX_INVALID_REQUEST;
+  if (hipSetDevice(ctx->device) != hipSuccess) return fail(ctx, COHX_DEVICE, "hipSetDevice");
+  const cohx_model_desc &d = ctx->desc;
+  const uint64_t H = d.hidden, F = d.intermediate, V = d.vocabulary,
+                 KVD = (uint64_t)d.kv_heads * d.head_dim;
+  const size_t rb = row_bytes(dtype, ne0);
+  if (!rb) return fail(ctx, COHX_UNSUPPORTED, std::string("unsupported dtype for ") + name);
+  if (rb * ne1 != bytes) return fail(ctx, COHX_INVALID_GGUF, std::string("size mismatch: ") + name);
+  const std::string n(name);
+  auto expect = [&](uint64_t e0, uint64_t e1) { return ne0 == e0 && ne1 == e1; };
+  auto vec_f32 = [&](float *dst, uint64_t len, uint64_t offset) -> int {
+    if (dtype != 0 || !expect(len, 1))
+      return fail(ctx, COHX_INVALID_GGUF, "incorrect shape or dtype for " + n);
+    HIP_TRY(hipMemcpy(dst + offset, data, len * 4, hipMemcpyHostToDevice));
+    return COHX_OK;
+  };
+  int rc = COHX_OK;
+  if (n == "token_embd.weight") {
+    if (!expect(H, V)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
+    rc = upload_matrix(ctx, ctx->embd, dtype, data, (int)V, 0, 1);
+    ctx->embd.gguf_bytes = bytes;
+  } else if (n == "output.weight") {
+    if (d.tied) return fail(ctx, COHX_INVALID_REQUEST, "context was created with a tied head");
+    if (!expect(H, V)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
+    rc = upload_matrix(ctx, ctx->output, dtype, data, (int)V, 0, 1);
+    ctx->output.gguf_bytes = bytes;
+  } else if (n == "output_norm.weight") {
+    rc = vec_f32(ctx->output_norm, H, 0);
+  } else {
+    unsigned layer = 0;
+    char suffix[64] = {0};
+    if (std::sscanf(name, "blk.%u.%63s", &layer, suffix) != 2 || layer >= d.layers)
+      return fail(ctx, COHX_INVALID_GGUF, "unexpected tensor " + n);
+    Layer &ly = ctx->layers[layer];
+    const std::string s(suffix);
+    if (s == "attn_norm.weight") rc = vec_f32(ly.attn_norm, H, 0);
+    else if (s == "ffn_norm.weight") rc = vec_f32(ly.ffn_norm, H, 0);
+    else if (s == "attn_q.bias") rc = vec_f32(ly.bqkv, H, 0);
+    else if (s == "attn_k.bias") rc = vec_f32(ly.bqkv, KVD, H);
+    else if (s == "attn_v.bias") rc = vec_f32(ly.bqkv, KVD, H + KVD);
+    else if (s == "attn_q.weight" || s == "attn_k.weight" || s == "attn_v.weight") {
+      const uint64_t rows = s == "attn_q.weight" ? H : KVD;
+      const uint64_t first = s == "attn_q.weight" ? 0 : s == "attn_k.weight" ? H : H + KVD;
+      if (!expect(H, rows)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
+      rc = upload_matrix(ctx, ly.qkv, dtype, data, (int)rows,
+                         (int)(dtype == 8 ? first / 16 : first), 1);
+      ly.qkv.gguf_bytes += bytes;
+    } else if (s == "attn_output.weight") {
+      if (!expect(H, H)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
+      rc = upload_matrix(ctx, ly.o, dtype, data, (int)H, 0, 1);
+      ly.o.gguf_bytes = bytes;
+    } else if (s == "ffn_gate.weight" || s == "ffn_up.weight") {
+      if (!expect(H, F)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
+      const bool up = s == "ffn_up.weight";
+      // Q8_0: gate tile i -> tile 2i, up tile i -> tile 2i+1; F16: gate rows then up rows.
+      rc = dtype == 8 ? upload_matrix(ctx, ly.gu, dtype, data, (int)F, up ? 1 : 0, 2)
+                      : upload_matrix(ctx, ly.gu, dtype, data, (int)F, up ? (int)F : 0, 1);
+      ly.gu.gguf_bytes += bytes;
+    } else if (s == "ffn_down.weight") {
+      if (!expect(F, H)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
+      rc = upload_matrix(ctx, ly.down, dtype, data, (int)H, 0, 1);
+      ly.down.gguf_bytes = bytes;
+    } else {
+      return fail(ctx, COHX_UNSUPPORTED, "unexpected tensor in Qwen2 graph: " + n);
+    }
+  }
+  if (!rc && std::find(ctx->uploaded.begin(), ctx->uploaded.end(), n) == ctx->uploaded.end())
+    ctx->uploaded.push_back(n);
+  return rc;
+}
+
+int cohx_finalize(cohx_ctx *ctx) {
+  if (!ctx) return COHX_INVALID_REQUEST;
+  const cohx_model_desc &d = ctx->desc;
+  std::vector<std::string> need = {"token_embd.weight", "output_norm.weight"};
+  if (!d.tied) need.push_back("output.weight");
+  const char *per[] = {"attn_norm.weight", "ffn_norm.weight", "attn_q.weight", "attn_k.weight",
+                       "attn_v.weight", "attn_q.bias", "attn_k.bias", "attn_v.bias",
+                       "attn_output.weight", "ffn_gate.weight", "ffn_up.weight",
+                       "ffn_down.weight"};
+  for (uint32_t l = 0; l < d.layers; l++)
+    for (const char *s : per) need.push_back("blk." + std::to_string(l) + "." + s);
+  for (const auto &n : need)
+    if (std::find(ctx->uploaded.begin(), ctx->uploaded.end(), n) == ctx->uploaded.end())
+      return fail(ctx, COHX_INVALID_GGUF, "missing required tensor " + n);
+  if (ctx->uploaded.size() != need.size())
+    return fail(ctx, COHX_UNSUPPORTED, "unexpected tensors in Qwen2 graph");
+  uint64_t total = ctx->embd.gguf_bytes + (d.tied ? 0 : ctx->output.gguf_bytes);
+  for (auto &ly : ctx->layers)
+    total += ly.qkv.gguf_bytes + ly.o.gguf_bytes + ly.gu.gguf_bytes + ly.down.gguf_bytes;
+  // the embedding is read as a matrix only as the tied head
+  ctx->matrix_bytes = d.tied ? total : total - ctx->embd.gguf_bytes;
+  ctx->finalized = true;
+  return COHX_OK;
+}
+
+// ---- sequences -------------------------------------------------------------
+
+static int take_page(cohx_ctx *ctx, int32_t *page) {
+  if (ctx->free_pages.empty()) return fail(ctx, COHX_RESOURCE, "KV pool exhausted");
+  *page = ctx->free_pages.back();
+  ctx->free_pages.pop_back();
+  ctx->page_refs[*page] = 1;
+  return COHX_OK;
+}
+
+static void drop_page(cohx_ctx *ctx, int32_t page) {
+  if (page < 0) return;
+  if (--ctx->page_refs[page] == 0) ctx->free_pages.push_back(page);
+}
+
+static void set_table(cohx_ctx *ctx, uint32_t seq, size_t idx, int32_t page) {
+  ctx->h_page_table[(size_t)seq * ctx->max_pages + idx] = page;
+  ctx->pt_dirty[seq] = 1;
+}
+
+static bool valid_seq(const cohx_ctx *ctx, uint32_t seq) {
+  return seq < ctx->seqs.size() && ctx->seqs[seq].live;
+}
+
+// Pages for positions [0, rows) present and writable from `from` on.
+static int ensure_pages(cohx_ctx *ctx, uint32_t seq, uint32_t from, uint32_t rows) {
+  Sequence &s = ctx->seqs[seq];
+  const size_t need = (rows + kPage - 1) / kPage;
+  for (size_t i = from / kPage; i < need; i++) {
+    if (i >= s.pages.size()) s.pages.resize(i + 1, -1);
+    int32_t p = s.pages[i];
+    if (p < 0) {
+      int rc = take_page(ctx, &p);
+      if (rc) return rc;
+      s.pages[i] = p;
+      set_table(ctx, seq, i, p);
+    } else if (ctx->page_refs[p] > 1) {  // copy on write of a shared page
+      int32_t q;
+      int rc = take_page(ctx, &q);
+      if (rc) return rc;
+      launch_copy_page(ctx->stream, ctx->kpool, ctx->vpool, ctx->layer_stride,
+                       (int)ctx->desc.layers, (int)(ctx->desc.kv_heads * kPage * ctx->desc.head_dim),
+                       p, q);
+      drop_page(ctx, p);
+      s.pages[i] = q;
+      set_table(ctx, seq, i, q);
+    }
+  }
+  return COHX_OK;
+}
+
+static int sync_page_table(cohx_ctx *ctx) {
+  for (uint32_t s = 0; s < ctx->pt_dirty.size(); s++) {
+    if (!ctx->pt_dirty[s]) continue;
+    HIP_TRY(hipMemcpyAsync(ctx->page_table + (size_t)s * ctx->max_pages,
+                           ctx->h_page_table.data() + (size_t)s * ctx->max_pages,
+                           (size_t)ctx->max_pages * sizeof(int32_t), hipMemcpyHostToDevice,
+                           ctx->stream));
+    ctx->pt_dirty[s] = 0;
+  }
+  // pageable source: make the copies complete before the host mirror changes
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return COHX_OK;
+}
+
+int cohx_seq_alloc(cohx_ctx *ctx, uint32_t capacity, uint32_t *seq) {
+  if (!ctx || !seq) return COHX_INVALID_REQUEST;
+  if (capacity == 0 || capacity > ctx->desc.max_context)
+    return fail(ctx, COHX_INVALID_REQUEST, "sequence capacity outside 1..=max_context");
+  if (ctx->free_seqs.empty()) return fail(ctx, COHX_RESOURCE, "no free sequence slots");
+  const uint32_t s = ctx->free_seqs.back();
+  ctx->free_seqs.pop_back();
+  Sequence &q = ctx->seqs[s];
+  q.live = true;
+  q.length = 0;
+  q.capacity = capacity;
+  q.pages.clear();
+  *seq = s;
+  return COHX_OK;
+}
+
+int cohx_seq_free(cohx_ctx *ctx, uint32_t seq) {
+  if (!ctx || !valid_seq(ctx, seq)) return COHX_INVALID_REQUEST;
+  Sequence &q = ctx->seqs[seq];
+  for (size_t i = 0; i < q.pages.size(); i++) {
+    drop_page(ctx, q.pages[i]);
+    set_table(ctx, seq, i, -1);
+  }
+  q = Sequence();
+  ctx->free_seqs.push_back(seq);
+  return COHX_OK;
+}
+
+int cohx_seq_fork(cohx_ctx *ctx, uint32_t src, uint32_t rows, uint32_t capacity, uint32_t *seq) {
+  if (!ctx || !valid_seq(ctx, src) || !seq) return COHX_INVALID_REQUEST;
+  if (rows > ctx->seqs[src].length || rows > capacity)
+    return fail(ctx, COHX_INVALID_REQUEST, "fork longer than the source or the capacity");
+  int rc = cohx_seq_alloc(ctx, capacity, seq);
+  if (rc) return rc;
+  Sequence &d = ctx->seqs[*seq];
+  const Sequence &s = ctx->seqs[src];
+  const size_t pages = (rows + kPage - 1) / kPage;
+  d.pages.assign(pages, -1);
+  for (size_t i = 0; i < pages; i++) {
+    d.pages[i] = s.pages[i];
+    ctx->page_refs[s.pages[i]]++;
+    set_table(ctx, *seq, i, s.pages[i]);
+  }
+  d.length = rows;
+  return COHX_OK;
+}
+
+int cohx_seq_truncate(cohx_ctx *ctx, uint32_t seq, uint32_t rows) {
+  if (!ctx || !valid_seq(ctx, seq)) return COHX_INVALID_REQUEST;
+  Sequence &q = ctx->seqs[seq];
+  if (rows > q.length) return fail(ctx, COHX_INVALID_REQUEST, "truncate beyond length");
+  const size_t keep = (rows + kPage - 1) / kPage;
+  for (size_t i = keep; i < q.pages.size(); i++) {
+    drop_page(ctx, q.pages[i]);
+    set_table(ctx, seq, i, -1);
+  }
+  if (q.pages.size() > keep) q.pages.resize(keep);
+  q.length = rows;
+  return COHX_OK;
+}
+
+int cohx_seq_length(const cohx_ctx *ctx, uint32_t seq, uint32_t *rows) {
+  if (!ctx || !valid_seq(ctx, seq) || !rows) return COHX_INVALID_REQUEST;
+  *rows = ctx->seqs[seq].length;
+  return COHX_OK;
+}
+
+uint32_t cohx_seq_pages(const cohx_ctx *ctx, uint32_t seq, int32_t *out, uint32_t cap) {
+  if (!ctx || !valid_seq(ctx, seq)) return 0;
+  const Sequence &q = ctx->seqs[seq];
+  const uint32_t n = (uint32_t)q.pages.size();
+  if (out) std::memcpy(out, q.pages.data(), std::min(n, cap) * sizeof(int32_t));
+  return n;
+}
+
+int cohx_seq_read_kv(cohx_ctx *ctx, uint32_t seq, uint32_t layer, int values, float *out) {
+  if (!ctx || !valid_seq(ctx, seq) || layer >= ctx->desc.layers || !out)
+    return COHX_INVALID_REQUEST;
+  HIP_TRY(hipSetDevice(ctx->device));
+  const Sequence &q = ctx->seqs[seq];
+  const int NKV = ctx->desc.kv_heads, D = ctx->desc.head_dim;
+  const float *pool = (values ? ctx->vpool : ctx->kpool) + (size_t)layer * ctx->layer_stride;
+  std::vector<float> page((size_t)NKV * kPage * D);
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  for (size_t i = 0; i * kPage < q.length; i++) {
+    HIP_TRY(hipMemcpy(page.data(), pool + (size_t)q.pages[i] * page.size(),
+                      page.size() * sizeof(float), hipMemcpyDeviceToHost));
+    for (int o = 0; o < kPage && i * kPage + o < q.length; o++)
+      for (int g = 0; g < NKV; g++)
+        std::memcpy(out + ((i * kPage + o) * NKV + g) * D, page.data() + ((size_t)g * kPage + o) * D,
+                    D * sizeof(float));
+  }
+  return COHX_OK;
+}
+
+int cohx_seq_fill_synthetic(cohx_ctx *ctx, uint32_t seq, uint32_t rows, uint64_t seed,
+                            uint32_t stream) {
+  if (!ctx || !valid_seq(ctx, seq)) return COHX_INVALID_REQUEST;
+  Sequence &q = ctx->seqs[seq];
+  if (rows > q.capacity) return fail(ctx, COHX_RESOURCE, "rows exceed the sequence capacity");
+  HIP_TRY(hipSetDevice(ctx->device));
+  int rc = ensure_pages(ctx, seq, 0, rows);
+  if (rc) return rc;
+  if (rows) {
+    int32_t *pages = nullptr;
+    HIP_TRY(hipMalloc(&pages, q.pages.size() * sizeof(int32_t)));
+    hipError_t e = hipMemcpy(pages, q.pages.data(), q.pages.size() * sizeof(int32_t),
+                             hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+      launch_fill_synthetic(ctx->stream, ctx->kpool, ctx->vpool, ctx->layer_stride,
+                            (int)ctx->desc.layers, pages, (int)rows, (int)ctx->desc.kv_heads,
+                            (int)ctx->desc.head_dim, seed, stream);
+      e = hipStreamSynchronize(ctx->stream);
+    }
+    (void)hipFree(pages);
+    if (e != hipSuccess) return fail(ctx, COHX_DEVICE, hipGetErrorString(e));
+  }
+  q.length = rows;
+  return COHX_OK;
+}
+
+}  // extern "C"
+
+// ---- the step ----------------------------------------------------------------
+
+namespace {
+
+struct Prepared {
+  std::vector<int> included;  // batch lane index of each device lane
+  uint32_t rows = 0;
+  uint32_t max_kv = 0;
+  uint64_t kv_rows_read = 0;
+};
+
+// Host validation (batch.rs:119-131) and upload of the device batch.
+int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, Prepared &p) {
+  const cohx_model_desc &d = ctx->desc;
+  if (!batch || batch->n_lanes == 0 || batch->n_lanes > d.max_lanes || !batch->lanes)
+    return fail(ctx, COHX_INVALID_REQUEST,
+                "batch width must be in 1..=" + std::to_string(d.max_lanes));
+  if (!ctx->finalized) return fail(ctx, COHX_INVALID_REQUEST, "model tensors not finalized");
+  uint32_t *info = ctx->ws.h_upload;
+  uint32_t *toks = info + (size_t)d.max_lanes * 4;
+  // duplicate sequences within one step are a shared failure
+  for (uint32_t i = 0; i < batch->n_lanes; i++)
+    for (uint32_t j = i + 1; j < batch->n_lanes; j++)
+      if (batch->lanes[i].seq == batch->lanes[j].seq)
+        return fail(ctx, COHX_INVALID_REQUEST, "a sequence appears twice in one batch");
+  for (uint32_t i = 0; i < batch->n_lanes; i++) {
+    const cohx_lane &ln = batch->lanes[i];
+    int32_t status = COHX_OK;
+    if (!valid_seq(ctx, ln.seq) || ln.n_tokens == 0 || !ln.tokens ||
+        ln.start_position != ctx->seqs[ln.seq].length) {
+      status = COHX_INVALID_REQUEST;
+    } else {
+      for (uint32_t j = 0; j < ln.n_tokens; j++)
+        if (ln.tokens[j] >= d.vocabulary) status = COHX_INVALID_REQUEST;  // token outside vocabulary
+      if (!status && (uint64_t)ln.start_position + ln.n_tokens > ctx->seqs[ln.seq].capacity)
+        status = COHX_RESOURCE;  // context capacity exhausted
+      if (!status && p.rows + ln.n_tokens > d.max_rows) status = COHX_RESOURCE;
+      if (!status) status = ensure_pages(ctx, ln.seq, ln.start_position,
+                                         ln.start_position + ln.n_tokens);
+    }
+    if (outs) {
+      outs[i].status = status;
+      outs[i].argmax = 0;
+    }
+    if (status) continue;
+    const uint32_t k = (uint32_t)p.included.size();
+    info[k * 4 + 0] = ln.n_tokens;
+    info[k * 4 + 1] = ln.start_position;
+    info[k * 4 + 2] = ln.seq;
+    info[k * 4 + 3] = p.rows;
+    std::memcpy(toks + p.rows, ln.tokens, ln.n_tokens * sizeof(uint32_t));
+    for (uint32_t j = 0; j < ln.n_tokens; j++)
+      p.kv_rows_read += (uint64_t)ln.start_position + j + 1;
+    p.rows += ln.n_tokens;
+    p.max_kv = std::max(p.max_kv, ln.start_position + ln.n_tokens);
+    p.included.push_back((int)i);
+  }
+  if (p.included.empty()) return COHX_OK;
+  int rc = sync_page_table(ctx);
+  if (rc) return rc;
+  const size_t n = p.included.size();
+  HIP_TRY(hipMemcpyAsync(ctx->ws.lane_info, info, n * 4 * sizeof(uint32_t), hipMemcpyHostToDevice,
+                         ctx->stream));
+  HIP_TRY(hipMemcpyAsync(ctx->ws.tokens, toks, p.rows * sizeof(uint32_t), hipMemcpyHostToDevice,
+                         ctx->stream));
+  Workspace &w = ctx->ws;
+  launch_pack(ctx->stream, (int)n, w.lane_info, w.tokens, ctx->page_table, ctx->max_pages, w.cu,
+              w.row_pos, w.row_slot, w.row_lane, w.row_token, w.row_seq, w.lane_last, w.row_err);
+  HIP_TRY(hipGetLastError());
+  return COHX_OK;
+}
+
+ActView act_view(cohx_ctx *ctx) {
+  return ActView{ctx->ws.act_qs, ctx->ws.act_ds, ctx->ws.act_f16};
+}
+
+}  // namespace
+
+extern "C" int cohx_pack(cohx_ctx *ctx, const cohx_batch *batch, uint32_t *cu, uint32_t *positions,
+                         int64_t *slots, uint32_t *lanes) {
+  if (!ctx) return COHX_INVALID_REQUEST;
+  HIP_TRY(hipSetDevice(ctx->device));
+  Prepared p;
+  std::vector<cohx_lane_out> outs(batch ? batch->n_lanes : 0);
+  int rc = prepare_batch(ctx, batch, outs.data(), p);
+  if (rc) return rc;
+  if (p.included.size() != batch->n_lanes)
+    return fail(ctx, COHX_INVALID_REQUEST, "a lane failed validation");
+  std::vector<int32_t> slot32(p.rows);
+  Workspace &w = ctx->ws;
+  HIP_TRY(hipMemcpyAsync(cu, w.cu, (batch->n_lanes + 1) * 4, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(hipMemcpyAsync(positions, w.row_pos, p.rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(hipMemcpyAsync(slot32.data(), w.row_slot, p.rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(hipMemcpyAsync(lanes, w.row_lane, p.rows * 4, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  for (uint32_t r = 0; r < p.rows; r++) slots[r] = slot32[r];
+  return COHX_OK;
+}
+
+extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
+  if (!ctx || !out || !out->lanes) return COHX_INVALID_REQUEST;
+  const auto t_start = std::chrono::steady_clock::now();
+  HIP_TRY(hipSetDevice(ctx->device));
+  const cohx_model_desc &d = ctx->desc;
+  Prepared p;
+  int rc = prepare_batch(ctx, batch, out->lanes, p);
+  if (rc) return rc;
+  out->width = (uint32_t)p.included.size();
+  out->rows = p.rows;
+  out->matrix_bytes = 0;
+  out->kv_bytes = 0;
+  if (p.included.empty()) {
+    out->elapsed_ns = 0;
+    return COHX_OK;
+  }
+  const int R = (int)p.rows, NL = (int)p.included.size();
+  const int H = d.hidden, F = d.intermediate, NH = d.heads, NKV = d.kv_heads, D = d.head_dim,
+            KVD = NKV * D;
+  const int act_dtype = d.weight_dtype == COHX_Q8_0 ? 8 : 1;
+  Workspace &w = ctx->ws;
+  hipStream_t s = ctx->stream;
+  StepDims sd{H, F, (int)d.vocabulary, NH, NKV, D, KVD, NH / NKV, d.norm_epsilon,
+              1.0f / sqrtf((float)D), ctx->max_pages, (int)d.max_context, ctx->max_chunks};
+  const ActView act = act_view(ctx);
+  launch_embed(s, R, ctx->embd.view, w.row_token, w.x, H, w.row_err);
+  for (uint32_t l = 0; l < d.layers; l++) {
+    Layer &ly = ctx->layers[l];
+    float *kp = ctx->kpool + (size_t)l * ctx->layer_stride;
+    float *vp = ctx->vpool + (size_t)l * ctx->layer_stride;
+    launch_norm_act(s, R, w.x, nullptr, ly.attn_norm, H, d.norm_epsilon, act_dtype, ctx->nbp_h, act,
+                    w.row_err);
+    launch_matvec(s, kEpiStore, ly.qkv.view, act, R,
+                  MatvecOut{w.qkv, H + 2 * KVD, nullptr, nullptr, w.row_err, nullptr});
+    launch_qkv_post(s, R, sd, w.qkv, ly.bqkv, ctx->rope, w.row_pos, w.row_slot, w.q_rot, kp, vp,
+                    w.row_err);
+    launch_attention(s, R, (int)p.max_kv, sd, w.q_rot, kp, vp, w.row_pos, w.row_seq,
+                     ctx->page_table, w.scores, w.chunk_max, w.partial, act_dtype, ctx->nbp_h, act,
+                     w.row_err);
+    launch_matvec(s, kEpiResidual, ly.o.view, act, R,
+                  MatvecOut{w.x, H, nullptr, nullptr, w.row_err, nullptr});
+    launch_norm_act(s, R, w.x, nullptr, ly.ffn_norm, H, d.norm_epsilon, act_dtype, ctx->nbp_h, act,
+                    w.row_err);
+    launch_matvec(s, kEpiSwiglu, ly.gu.view, act, R,
+                  MatvecOut{w.h, F, nullptr, nullptr, w.row_err, nullptr});
+    launch_quant_act(s, R, w.h, F, act_dtype, ctx->nbp_f, act, w.row_err);
+    launch_matvec(s, kEpiResidual, ly.down.view, act, R,
+                  MatvecOut{w.x, H, nullptr, nullptr, w.row_err, nullptr});
+  }
+  // final norm and head over the last row of every lane (batch.rs:250-266)
+  launch_norm_act(s, NL, w.x, w.lane_last, ctx->output_norm, H, d.norm_epsilon, act_dtype,
+                  ctx->nbp_h, act, w.row_err);
+  bool any_logits = false;
+  for (int k = 0; k < NL; k++)
+    if (batch->lanes[p.included[k]].want_logits && out->lanes[p.included[k]].logits)
+      any_logits = true;
+  launch_fill_u64(s, w.argmax, NL, 0ull);
+  const DeviceMatrix &head = d.tied ? ctx->embd : ctx->output;
+  launch_matvec(s, kEpiArgmax, head.view, act, NL,
+                MatvecOut{nullptr, 0, w.argmax, any_logits ? w.logits : nullptr, w.row_err,
+                          w.lane_last});
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(hipMemcpyAsync(w.h_argmax, w.argmax, NL * sizeof(unsigned long long),
+                         hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(w.h_row_err, w.row_err, R * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  for (int k = 0; k < NL; k++) {
+    const cohx_lane &ln = batch->lanes[p.included[k]];
+    float *dst = out->lanes[p.included[k]].logits;
+    if (ln.want_logits && dst)
+      HIP_TRY(hipMemcpyAsync(dst, w.logits + (size_t)k * d.vocabulary, d.vocabulary * sizeof(float),
+                             hipMemcpyDeviceToHost, s));
+  }
+  HIP_TRY(hipStreamSynchronize(s));
+  // lane statuses from row error bits; advance healthy sequences
+  uint32_t row = 0;
+  for (int k = 0; k < NL; k++) {
+    const int i = p.included[k];
+    const cohx_lane &ln = batch->lanes[i];
+    uint32_t bits = 0;
+    for (uint32_t j = 0; j < ln.n_tokens; j++) bits |= w.h_row_err[row + j];
+    row += ln.n_tokens;
+    cohx_lane_out &o = out->lanes[i];
+    o.argmax = 0xffffffffu - (uint32_t)(w.h_argmax[k] & 0xffffffffull);
+    if (bits & kErrPage)
+      o.status = COHX_RESOURCE;
+    else if (bits)
+      o.status = COHX_INVALID_GGUF;
+    else
+      ctx->seqs[ln.seq].length += ln.n_tokens;
+  }
+  uint32_t width = 0;
+  for (uint32_t i = 0; i < batch->n_lanes; i++) width += out->lanes[i].status == COHX_OK;
+  out->width = width;
+  out->matrix_bytes = ctx->matrix_bytes;
+  out->kv_bytes = p.kv_rows_read * (uint64_t)KVD * 4 * 2 * d.layers +
+                  (uint64_t)R * KVD * 4 * 2 * d.layers;
+  out->elapsed_ns = (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+                        std::chrono::steady_clock::now() - t_start)
+                        .count();
+  return COHX_OK;
+}

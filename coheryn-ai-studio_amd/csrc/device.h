@@ -1,0 +1,151 @@
+// Device helpers shared by the step kernels (gfx950, wave64).
+//
+// Everything here is compiled with -ffp-contract=off: the engine's float
+// semantics (crates/coheryn-engine/src/cpu.rs, quant.rs) never fuse a*b+c
+// except where the Rust source calls mul_add, which these kernels spell fmaf.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cohx {
+
+constexpr int kWave = 64;
+constexpr int kPage = 16;         // tokens per KV page
+constexpr int kChunk = 128;       // tokens per attention work item
+constexpr int kMaxGroup = 8;      // q heads per kv head handled by one work item
+
+// Row error bits (per packed row); folded into per-lane statuses on the host.
+constexpr uint32_t kErrNonFinite = 1u;  // Error::invalid (non-finite value)
+constexpr uint32_t kErrScale = 2u;      // Error::invalid (activation scale overflow)
+constexpr uint32_t kErrPage = 4u;       // Error::resource (slot outside the page table)
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// exp for binary32 with the same results as glibc's expf on x86-64, which is
+// what the engine's f32::exp calls on Linux.  Method: Szabolcs Nagy's exp2
+// table reduction (ARM optimized-routines, glibc >= 2.28 e_expf.c):
+// x*32/ln2 = k + r, 2^(k/32) from a 32-entry table, a cubic in r, all in
+// binary64, one final rounding.  Table entries are asuint64(2^(i/32)) - (i<<47)
+// with 2^(i/32) correctly rounded (derived independently in high precision);
+// the reduction uses fused multiply-adds, matching the FMA build that glibc
+// selects on CPUs with FMA.  Agreement with the host libm was checked on all
+// 2^32 inputs.
+// ---------------------------------------------------------------------------
+__constant__ static const uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
+
+__device__ __forceinline__ float exp_f32(float x) {
+  uint32_t ux = __float_as_uint(x);
+  uint32_t abstop = (ux >> 20) & 0x7ffu;
+  if (abstop >= 0x42bu) {  // |x| >= 88 or nan
+    if (ux == 0xff800000u) return 0.0f;
+    if (abstop >= 0x7f8u) return x + x;
+    if (x > 0x1.62e42ep6f) return __builtin_inff();
+    if (x < -0x1.9fe368p6f) return 0.0f;
+  }
+  const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+  const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+               c2 = 0x1.62e42ff0c52d6p-1 / 32;
+  double xd = (double)x;
+  double kd = __fma_rn(inv_ln2_n, xd, shift);
+  uint64_t ki = (uint64_t)__double_as_longlong(kd);
+  kd -= shift;
+  double r = __fma_rn(inv_ln2_n, xd, -kd);
+  uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+  double s = __longlong_as_double((long long)t);
+  double z = __fma_rn(c0, r, c1), r2 = r * r, y = __fma_rn(c2, r, 1.0);
+  y = __fma_rn(z, r2, y);
+  y = y * s;
+  return (float)y;
+}
+
+// binary16 <-> binary32 (round to nearest even; the `half` crate contract).
+__device__ __forceinline__ float h2f(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+__device__ __forceinline__ bool finitef(float v) { return __builtin_isfinite(v); }
+
+// Rust `f as i8` (saturating; NaN -> 0).
+__device__ __forceinline__ int8_t sat_i8(float v) {
+  if (v != v) return 0;
+  if (v >= 127.0f) return 127;
+  if (v <= -128.0f) return -128;
+  return (int8_t)v;
+}
+
+// Wave-level reductions (butterfly: every lane ends with the result; the
+// combination order is fixed, so results are deterministic).
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+// Max over aligned groups of 32 lanes.
+__device__ __forceinline__ float half_max_f32(float v) {
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+
+// Block reduction of one f64 per thread, fixed order; all threads get the sum.
+template <int kThreads>
+__device__ __forceinline__ double block_sum_f64(double v, double *scratch) {
+  constexpr int kWaves = kThreads / kWave;
+  v = wave_sum_f64(v);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if ((threadIdx.x % kWave) == 0) scratch[w] = v;
+  __syncthreads();
+  double total = scratch[0];
+#pragma unroll
+  for (int i = 1; i < kWaves; i++) total += scratch[i];
+  return total;
+}
+template <int kThreads>
+__device__ __forceinline__ float block_max_f32(float v, float *scratch) {
+  constexpr int kWaves = kThreads / kWave;
+  v = wave_max_f32(v);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();
+  if ((threadIdx.x % kWave) == 0) scratch[w] = v;
+  __syncthreads();
+  float m = scratch[0];
+#pragma unroll
+  for (int i = 1; i < kWaves; i++) m = fmaxf(m, scratch[i]);
+  return m;
+}
+
+// ---------------------------------------------------------------------------
+// Q8 tile layout shared by weights (A operand, 16 matrix rows per tile) and
+// activations (B operand, 16 batch rows per tile).  For tile t, 32-element
+// block b (nbp = blocks rounded up to even) and lane l of a wave:
+//   bytes  ((t*(nbp/2) + b/2)*64 + l)*16 + (b%2)*8 + j,  j < 8
+// hold row t*16 + l%16, elements b*32 + (l/16)*8 + j — the per-lane operand
+// of v_mfma_i32_16x16x32_i8, two blocks per 16-byte lane load.
+// Block scales (binary16) sit at (t*nbp + b)*16 + row%16.
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ size_t q8_byte(size_t tile, int nbp, int b, int lane, int j) {
+  return ((tile * (size_t)(nbp / 2) + (size_t)(b / 2)) * 64 + (size_t)lane) * 16 +
+         (size_t)(b % 2) * 8 + (size_t)j;
+}
+__host__ __device__ __forceinline__ size_t q8_scale(size_t tile, int nbp, int b, int row16) {
+  return (tile * (size_t)nbp + (size_t)b) * 16 + (size_t)row16;
+}
+
+}  // namespace cohx

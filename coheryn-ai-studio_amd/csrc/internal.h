@@ -1,0 +1,82 @@
+// Host-side state of a cohx context (not part of the C ABI).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../include/cohx.h"
+#include "kernels.h"
+
+namespace cohx {
+
+struct DeviceMatrix {
+  MatrixView view{};
+  int8_t *qs = nullptr;
+  uint16_t *ds = nullptr;
+  uint16_t *f16 = nullptr;
+  uint64_t gguf_bytes = 0;  // bytes of the GGUF payload(s) it holds
+};
+
+struct Layer {
+  float *attn_norm = nullptr, *ffn_norm = nullptr, *bqkv = nullptr;
+  DeviceMatrix qkv, o, gu, down;
+};
+
+struct Sequence {
+  bool live = false;
+  uint32_t length = 0, capacity = 0;
+  std::vector<int32_t> pages;  // logical page -> physical page
+};
+
+struct Workspace {
+  uint32_t *lane_info = nullptr, *tokens = nullptr;
+  uint32_t *cu = nullptr, *row_pos = nullptr, *row_lane = nullptr, *row_token = nullptr,
+           *row_seq = nullptr, *lane_last = nullptr, *row_err = nullptr;
+  int32_t *row_slot = nullptr;
+  float *x = nullptr, *qkv = nullptr, *q_rot = nullptr, *h = nullptr;
+  int8_t *act_qs = nullptr;
+  uint16_t *act_ds = nullptr, *act_f16 = nullptr;
+  float *scores = nullptr, *chunk_max = nullptr, *logits = nullptr;
+  double *partial = nullptr;
+  unsigned long long *argmax = nullptr;
+  // pinned host staging
+  uint32_t *h_upload = nullptr;  // lane_info then tokens
+  uint32_t *h_row_err = nullptr;
+  unsigned long long *h_argmax = nullptr;
+};
+
+}  // namespace cohx
+
+struct cohx_ctx {
+  cohx_model_desc desc{};
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string err;
+  int nbp_h = 0, nbp_f = 0, nbp_max = 0;
+  int max_pages = 0;  // pages per sequence
+  int max_chunks = 0;
+  size_t layer_stride = 0;  // floats per layer in each KV pool
+  std::vector<cohx::Layer> layers;
+  cohx::DeviceMatrix embd, output;
+  float *output_norm = nullptr;
+  float2 *rope = nullptr;
+  float *kpool = nullptr, *vpool = nullptr;
+  int32_t *page_table = nullptr;
+  std::vector<int32_t> h_page_table;
+  std::vector<uint8_t> pt_dirty;
+  std::vector<int32_t> free_pages;
+  std::vector<int32_t> page_refs;
+  std::vector<cohx::Sequence> seqs;
+  std::vector<uint32_t> free_seqs;
+  std::vector<std::string> uploaded;
+  bool finalized = false;
+  uint64_t matrix_bytes = 0;
+  cohx::Workspace ws;
+  std::vector<void *> allocations;
+};
+
+namespace cohx {
+int fail(cohx_ctx *ctx, int code, const std::string &msg);
+}

@@ -1,0 +1,78 @@
+// Launch interface between the host step driver (cohx.cpp) and the kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cohx {
+
+// Device view of one matrix.  Q8_0: tiled int8 + f16 block scales (device.h
+// layout).  F16: row-major binary16 exactly as in the GGUF file.
+struct MatrixView {
+  int dtype;     // 1 = F16, 8 = Q8_0
+  int rows;      // logical output rows
+  int K;         // input width
+  int nb, nbp;   // 32-element blocks, rounded up to even
+  int mtiles;    // ceil(rows/16)
+  const int8_t *qs;
+  const uint16_t *ds;
+  const uint16_t *f16;
+};
+
+// Activation operand buffers for the next matrix.
+struct ActView {
+  int8_t *qs;     // Q8 tiled (B operand)
+  uint16_t *ds;   // Q8 block scales
+  uint16_t *f16;  // binary16-rounded activations, row-major [rows][K]
+};
+
+struct StepDims {
+  int H, F, V, NH, NKV, D, KVD, G;  // G = NH/NKV
+  float eps, scale;                  // scale = 1/sqrt(D)
+  int max_pages;                     // page-table row stride
+  int kv_cap;                        // score row stride (>= max kv length this step)
+  int max_chunks;                    // partial-sum stride
+};
+
+enum Epilogue { kEpiStore = 0, kEpiResidual = 1, kEpiSwiglu = 2, kEpiArgmax = 3 };
+
+struct MatvecOut {
+  float *out;          // kEpiStore: [rows_b][ld]; kEpiResidual: x [rows_b][ld]; kEpiSwiglu: h
+  int ld;
+  unsigned long long *argmax;  // kEpiArgmax: per batch row key
+  float *logits;               // kEpiArgmax: optional [rows_b][V] (nullptr: none)
+  uint32_t *row_err;           // per batch row error bits
+  const uint32_t *err_rows;    // batch row -> packed row index for error bits (nullptr: same)
+};
+
+void launch_pack(hipStream_t s, int n_lanes, const uint32_t *lane_info, const uint32_t *tokens,
+                 const int32_t *page_table, int max_pages, uint32_t *cu, uint32_t *row_pos,
+                 int32_t *row_slot, uint32_t *row_lane, uint32_t *row_token, uint32_t *row_seq,
+                 uint32_t *lane_last, uint32_t *row_err);
+void launch_embed(hipStream_t s, int rows, const MatrixView &emb, const uint32_t *row_token,
+                  float *x, int H, uint32_t *row_err);
+// in_rows: optional map from output batch row to input row of x (final norm over logit rows).
+void launch_norm_act(hipStream_t s, int rows, const float *x, const uint32_t *in_rows,
+                     const float *weight, int H, float eps, int act_dtype, int nbp, ActView act,
+                     uint32_t *row_err);
+void launch_quant_act(hipStream_t s, int rows, const float *src, int K, int act_dtype, int nbp,
+                      ActView act, uint32_t *row_err);
+void launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActView &act,
+                   int rows_b, const MatvecOut &o);
+void launch_qkv_post(hipStream_t s, int rows, const StepDims &d, const float *qkv,
+                     const float *bias, const float2 *rope, const uint32_t *row_pos,
+                     const int32_t *row_slot, float *q_rot, float *kpool, float *vpool,
+                     uint32_t *row_err);
+void launch_attention(hipStream_t s, int rows, int max_kv, const StepDims &d, const float *q_rot,
+                      const float *kpool, const float *vpool, const uint32_t *row_pos,
+                      const uint32_t *row_seq, const int32_t *page_table, float *scores,
+                      float *chunk_max, double *partial, int act_dtype, int nbp, ActView act,
+                      uint32_t *row_err);
+void launch_fill_synthetic(hipStream_t s, float *kpool, float *vpool, size_t layer_stride,
+                           int layers, const int32_t *pages, int rows, int NKV, int D,
+                           uint64_t seed, uint32_t stream);
+void launch_copy_page(hipStream_t s, float *kpool, float *vpool, size_t layer_stride, int layers,
+                      int page_floats, int src_page, int dst_page);
+void launch_fill_u64(hipStream_t s, unsigned long long *p, size_t n, unsigned long long v);
+void launch_fill_u32(hipStream_t s, uint32_t *p, size_t n, uint32_t v);
+
+}  // namespace cohx

@@ -1,0 +1,196 @@
+/*
+ * cohx — MI355X (gfx950) continuous-batching forward step for the Coheryn
+ * engine's Qwen2 graph, as a C ABI.
+ *
+ * Two layers:
+ *  1. The device step (cohx_create .. cohx_step): HBM-resident weights, a paged
+ *     KV pool, and one call that advances a ragged batch of lanes.  This is what
+ *     an `extern "C"` FFI crate binds in place of the engine's CPU kernels
+ *     (crates/coheryn-engine/src/inference/batch.rs:117-273 forward_batch,
+ *     tensor.rs:302-436 matmul_batch_cooperative, cpu.rs:49-210, quant.rs:175-349).
+ *  2. The host mirror of the engine's generation API (cohx_gen_*, cohx_step_batch):
+ *     the same state machine as inference/generation.rs:18-394 and the
+ *     `BatchModel::step` contract of crates/coheryn-api/src/scheduler/batching.rs:11-21,
+ *     so a scheduler written against the reference drives the GPU step unchanged.
+ *
+ * Every entry point returns a status code (no exceptions cross the ABI) and is
+ * single-threaded per context: the caller serializes calls on one context, as
+ * the reference scheduler does with its single compute permit
+ * (crates/coheryn-api/src/scheduler.rs:201).  Pointers are borrowed for the
+ * duration of the call only.
+ */
+#ifndef COHX_H
+#define COHX_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes; classes of crates/coheryn-engine/src/error.rs:6-41. */
+enum {
+  COHX_OK = 0,
+  COHX_INVALID_REQUEST = 1, /* Error::request (bad token, bad batch, bad handle) */
+  COHX_INVALID_GGUF = 2,    /* Error::invalid (shapes, non-finite values) */
+  COHX_RESOURCE = 3,        /* Error::resource (context / KV pool exhausted) */
+  COHX_CANCELLED = 4,       /* ErrorCode::Cancelled */
+  COHX_UNSUPPORTED = 5,     /* unsupported dtype / feature */
+  COHX_DEAD_END = 6,        /* ErrorCode::ConstraintDeadEnd (empty sampling mask) */
+  COHX_DEVICE = 7           /* HIP runtime failure */
+};
+
+/* GGML dtypes accepted for matrices (gguf.rs:104-128). */
+enum { COHX_F32 = 0, COHX_F16 = 1, COHX_Q4_0 = 2, COHX_Q8_0 = 8 };
+
+typedef struct cohx_ctx cohx_ctx;
+
+/* Model and capacity description; the first ten fields are compat.rs:12-23
+ * ModelConfig. */
+typedef struct {
+  uint32_t layers, hidden, intermediate, heads, kv_heads, head_dim, vocabulary, context;
+  float rope_base, norm_epsilon;
+  uint32_t weight_dtype; /* dtype of every 2-D matrix: COHX_F16, COHX_Q8_0 or COHX_Q4_0 */
+  uint32_t tied;         /* 1: logits use token_embd.weight (batch.rs:261-265) */
+  uint32_t kv_dtype;     /* 0: f32 KV cache (the engine's, README.md:78) */
+  uint32_t max_lanes;    /* lanes per step */
+  uint32_t max_rows;     /* packed token rows per step (sum of lane n_tokens) */
+  uint32_t max_seqs;     /* live sequences */
+  uint32_t max_context;  /* tokens per sequence (<= context) */
+  uint32_t kv_pages;     /* KV pool size in pages of COHX_PAGE tokens (0: max_seqs*max_context) */
+  uint32_t n_eog;        /* end-of-generation ids (tokenizer.rs:224-236,304-306) */
+  uint32_t eog[4];
+} cohx_model_desc;
+
+#define COHX_PAGE 16
+
+/* Model::load counterpart (inference.rs:238-297): allocates HBM for weights,
+ * the KV pool and per-step workspaces on `device`. */
+int cohx_create(const cohx_model_desc *desc, int device, cohx_ctx **out);
+void cohx_destroy(cohx_ctx *ctx);
+/* Human-readable text of the last failure on this context. */
+const char *cohx_last_error(const cohx_ctx *ctx);
+
+/* Upload one GGUF tensor by name, payload in the file's block layout
+ * (gguf.rs:96-103 Tensor; the library repacks into its HBM layout).
+ * Names are the engine's (compat.rs:161-221). */
+int cohx_upload_tensor(cohx_ctx *ctx, const char *name, uint32_t dtype, uint64_t ne0,
+                       uint64_t ne1, const void *data, size_t bytes);
+/* Checks that the exact Qwen2 tensor set is present (compat.rs:161-221 graph). */
+int cohx_finalize(cohx_ctx *ctx);
+
+/* Sequences: a KV slot map (page table) per session (inference.rs:1019-1055 Kv/Session). */
+int cohx_seq_alloc(cohx_ctx *ctx, uint32_t capacity, uint32_t *seq);
+/* New sequence sharing `src`'s first `rows` tokens of KV (full pages are shared,
+ * a partial last page is copied): the GPU form of prefix reuse
+ * (generation.rs:189-202, PrefixCache inference.rs:687-710). */
+int cohx_seq_fork(cohx_ctx *ctx, uint32_t src, uint32_t rows, uint32_t capacity, uint32_t *seq);
+int cohx_seq_free(cohx_ctx *ctx, uint32_t seq);
+int cohx_seq_truncate(cohx_ctx *ctx, uint32_t seq, uint32_t rows);
+int cohx_seq_length(const cohx_ctx *ctx, uint32_t seq, uint32_t *rows);
+/* The sequence's slot map: physical page of each logical page (-1: none).
+ * Returns the number of logical pages (copies at most cap). */
+uint32_t cohx_seq_pages(const cohx_ctx *ctx, uint32_t seq, int32_t *out, uint32_t cap);
+/* Copy one layer's K (values=0) or V (values=1) rows [0, length) to host,
+ * kv_heads*head_dim floats per row. */
+int cohx_seq_read_kv(cohx_ctx *ctx, uint32_t seq, uint32_t layer, int values, float *out);
+/* Benchmark/test utility with no engine counterpart: fill rows [0, rows) of
+ * every layer with seeded values hash(seed, stream, layer, K/V, pos, elem) on
+ * the device and set the length to `rows`. */
+int cohx_seq_fill_synthetic(cohx_ctx *ctx, uint32_t seq, uint32_t rows, uint64_t seed,
+                            uint32_t stream);
+
+/* One lane of a ragged step: n_tokens >= 1 consecutive tokens of one sequence
+ * starting at its current length (a decode row or a prefill chunk). */
+typedef struct {
+  uint32_t seq;
+  uint32_t n_tokens;
+  const uint32_t *tokens;
+  uint32_t start_position;
+  uint32_t want_logits; /* copy the last row's logits to cohx_lane_out.logits */
+} cohx_lane;
+
+typedef struct {
+  uint32_t n_lanes;
+  const cohx_lane *lanes;
+} cohx_batch;
+
+typedef struct {
+  int32_t status;  /* COHX_OK or the lane's own failure (batch.rs:16-29) */
+  uint32_t argmax; /* greedy token of the last row, lowest id on ties (sampling.rs:160-173) */
+  float *logits;   /* optional caller buffer of `vocabulary` floats, or NULL */
+} cohx_lane_out;
+
+typedef struct {
+  cohx_lane_out *lanes; /* n_lanes entries */
+  uint32_t width;       /* lanes without error (batch.rs:94-97) */
+  uint32_t rows;        /* packed token rows */
+  uint64_t matrix_bytes;/* weight bytes streamed (BatchStep::matrix_bytes, batch.rs:3-9) */
+  uint64_t kv_bytes;    /* KV bytes read + written */
+  uint64_t elapsed_ns;
+} cohx_step_out;
+
+/* Model::forward_batch counterpart (batch.rs:117-273) over a ragged batch.
+ * Shared failures return non-zero; lane failures are reported per lane and
+ * never perturb other lanes.  A lane's sequence advances by n_tokens on
+ * success. */
+int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out);
+
+/* Packing only (test hook for the bit-exact packer): runs the device packer for
+ * `batch` and copies cu_seqlens[n+1], positions[R], slots[R] (page*16 + offset)
+ * and lanes[R] back.  Sequences are not advanced. */
+int cohx_pack(cohx_ctx *ctx, const cohx_batch *batch, uint32_t *cu_seqlens, uint32_t *positions,
+              int64_t *slots, uint32_t *lanes);
+
+/* ---- host mirror of the engine's generation API ------------------------- */
+
+typedef struct cohx_gen cohx_gen;
+
+/* GenerationOptions (inference.rs:68-108) restricted to the token path. */
+typedef struct {
+  uint32_t max_tokens;
+  float temperature;
+  uint32_t top_k;
+  float top_p;
+  uint64_t seed;
+  float repetition_penalty, frequency_penalty, presence_penalty;
+  uint32_t n_stop_tokens;
+  const uint32_t *stop_tokens;
+  uint32_t context; /* session context (0: max_context) */
+} cohx_gen_options;
+
+/* BatchStep (batch.rs:3-9). */
+typedef struct {
+  uint32_t width;
+  uint32_t completed_tokens;
+  uint64_t matrix_tiles;
+  uint64_t matrix_bytes;
+} cohx_batch_step;
+
+enum { COHX_FINISH_NONE = 0, COHX_FINISH_STOP = 1, COHX_FINISH_LENGTH = 2,
+       COHX_FINISH_CANCELLED = 3 };
+
+/* Model::begin_generation (generation.rs:53-242) from prompt token ids.
+ * `prior` (may be NULL) is a finished generation whose KV is reused by
+ * longest common token prefix, capped at prompt_len-1 (generation.rs:189-202). */
+int cohx_gen_begin(cohx_ctx *ctx, const uint32_t *prompt, uint32_t n_prompt,
+                   const cohx_gen_options *options, cohx_gen *prior, cohx_gen **out);
+/* Model::step_batch (batch.rs:64-116): one token per lane, 1..=max_lanes lanes. */
+int cohx_step_batch(cohx_ctx *ctx, cohx_gen *const *states, uint32_t n, cohx_batch_step *out);
+/* Model::step_generation (generation.rs:244-257): the single-lane path. */
+int cohx_step_generation(cohx_ctx *ctx, cohx_gen *state);
+/* GenerationState::sample (generation.rs:319-394): *token = id or -1 for none. */
+int cohx_gen_sample(cohx_gen *state, int64_t *token);
+int cohx_gen_needs_forward(const cohx_gen *state);
+int cohx_gen_is_finished(const cohx_gen *state);
+int cohx_gen_is_prefilling(const cohx_gen *state);
+uint32_t cohx_gen_finish_reason(const cohx_gen *state);
+/* Generated ids so far; returns the count (copies at most cap). */
+uint32_t cohx_gen_tokens(const cohx_gen *state, uint32_t *out, uint32_t cap);
+void cohx_gen_cancel(cohx_gen *state);
+void cohx_gen_free(cohx_gen *state);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,221 @@
+"""GPU parity: the HIP step (through the C ABI) against the CPU oracle.
+
+Bit-exact targets: packing (cu_seqlens, positions, slots, lanes), KV rows,
+greedy token ids.  Logits are compared bitwise too: the kernels keep the
+reference's reduction orders (exact int8 block sums + the fmaf block chain for
+Q8_0; q.k in element order), and the remaining f64 tree sums agree with the
+sequential ones unless a partial sum rounds — the test reports any such
+difference with its size rather than hiding it (tolerance: max-abs <= 1e-2 for
+F16, <= 3e-2 for quantized, the bound stated for this path).
+"""
+import numpy as np
+import pytest
+
+import cohx
+import orc
+import synth
+
+pytestmark = pytest.mark.gpu
+
+TINY = synth.config(layers=2, hidden=128, intermediate=256, heads=4, kv_heads=2,
+                    vocabulary=300, context=512)
+TOL = {"f16": 1e-2, "q8_0": 3e-2}
+
+
+def build(dtype, seed, cfg=TINY, **kw):
+    c, t = synth.in_memory(cfg, dtype, seed=seed)
+    kw.setdefault("max_lanes", 8)
+    kw.setdefault("max_rows", 64)
+    kw.setdefault("max_seqs", 8)
+    kw.setdefault("max_context", 256)
+    return c, t, cohx.Model(c, t, **kw), orc.Model(c, t, threads=8)
+
+
+def compare_logits(got, want, dtype, what):
+    bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+    diff = float(np.abs(got.astype(np.float64) - want).max())
+    print(f"{what}: {bad.size} of {got.size} logits differ in bits, max-abs {diff:.3g}",
+          flush=True)
+    assert diff <= TOL[dtype], what
+    return bad.size
+
+
+def test_pack_matches_oracle():
+    print("case: pack", flush=True)
+    c, t, m, o = build("q8_0", 1)
+    seqs = [m.seq_alloc() for _ in range(4)]
+    for s, n in zip(seqs, (0, 17, 40, 5)):
+        if n:
+            m.seq_fill_synthetic(s, n, 7, s)
+    lanes = [dict(seq=s, tokens=list(range(k))) for s, k in zip(seqs, (3, 1, 5, 16))]
+    cu, pos, slot, lane = m.pack(lanes)
+    pages = [m.seq_pages(s) for s in seqs]
+    width = max(len(p) for p in pages)
+    table = np.full((len(seqs), width), -1, np.int32)
+    for i, p in enumerate(pages):
+        table[i, :len(p)] = p
+    rc, cu2, pos2, slot2, lane2 = orc.pack([3, 1, 5, 16], [0, 17, 40, 5], table, cohx.PAGE)
+    assert rc == 0
+    assert np.array_equal(cu, cu2) and np.array_equal(pos, pos2)
+    assert np.array_equal(slot, slot2) and np.array_equal(lane, lane2)
+
+
+@pytest.mark.parametrize("dtype", ["q8_0", "f16"])
+def test_ragged_steps_match_oracle(dtype):
+    print(f"case: ragged steps {dtype}", flush=True)
+    c, t, m, o = build(dtype, 2)
+    rng = np.random.default_rng(3)
+    V = c["vocabulary"]
+    seqs = [m.seq_alloc() for _ in range(3)]
+    sess = [o.session(256) for _ in range(3)]
+    # (lane -> n_tokens) per step: mixed prefill chunks and single decode rows
+    plan = [{0: 5, 1: 3}, {0: 1, 1: 1, 2: 4}, {0: 1, 2: 1}, {1: 2, 2: 1, 0: 1}]
+    mismatched = 0
+    for step, spec in enumerate(plan):
+        lanes, toks = [], {}
+        for i, n in spec.items():
+            toks[i] = [int(v) for v in rng.integers(0, V, n)]
+            lanes.append(dict(seq=seqs[i], tokens=toks[i], logits=True))
+        res = m.step(lanes)
+        for (i, n), r in zip(spec.items(), res):
+            assert r["status"] == 0
+            for tok in toks[i]:
+                assert o.forward_batch([sess[i]], [tok])[0] == 0
+            want = sess[i].logits()
+            mismatched += compare_logits(r["logits"], want, dtype, f"step {step} lane {i}")
+            assert r["argmax"] == orc.Sampler().sample(want)[1]
+    for i in range(3):
+        assert m.seq_length(seqs[i]) == sess[i].position
+        for layer in range(c["layers"]):
+            for values in (False, True):
+                got, want = m.seq_read_kv(seqs[i], layer, values), sess[i].kv(layer, values)
+                assert np.array_equal(got, want), (i, layer, values)
+    assert mismatched == 0
+
+
+def run_generation(m, prompts, options, arrive=None):
+    """tests/batching.rs:40-125 protocol: step every lane that needs a forward,
+    sample each, admit a late arrival, retire finished lanes."""
+    arrive = arrive or {}
+    states = {i: m.begin_generation(p, options[i]) for i, p in enumerate(prompts)
+              if i not in arrive}
+    done = {}
+    for rnd in range(400):
+        for i, r in arrive.items():
+            if r == rnd:
+                states[i] = m.begin_generation(prompts[i], options[i])
+        lanes = [s for s in states.values() if s.needs_forward()]
+        if lanes:
+            m.step_batch(lanes)
+        for i in list(states):
+            s = states[i]
+            s.sample()
+            if s.is_finished():
+                done[i] = (s.token_ids(), s.finish_reason())
+                s.free()
+                del states[i]
+        if len(done) == len(prompts):
+            break
+    return done
+
+
+def oracle_generate(o, prompt, opt, eos):
+    s = o.session(256)
+    sampler = orc.Sampler(opt.temperature, opt.top_k, opt.top_p, opt.seed,
+                          opt.repetition_penalty, opt.frequency_penalty, opt.presence_penalty)
+    sampler.history(o.config["vocabulary"], prompt)  # generation.rs:151
+    for tok in prompt:
+        assert o.forward_batch([s], [tok])[0] == 0
+    ids = []
+    while len(ids) < opt.max_tokens:
+        rc, tok = sampler.sample(s.logits())
+        assert rc == 0
+        sampler.observe(tok)
+        ids.append(tok)
+        if tok == eos:
+            return ids, "stop"
+        if len(ids) == opt.max_tokens:
+            break
+        assert o.forward_batch([s], [tok])[0] == 0
+    return ids, "length"
+
+
+@pytest.mark.parametrize("dtype", ["q8_0", "f16"])
+def test_batched_generation_equals_individual_and_oracle(dtype):
+    print(f"case: generation {dtype}", flush=True)
+    c, t, m, o = build(dtype, 4)
+    rng = np.random.default_rng(5)
+    prompts = [[int(v) for v in rng.integers(0, c["vocabulary"], n)] for n in (2, 9, 5)]
+    opts = [cohx.GenerationOptions(max_tokens=6),
+            cohx.GenerationOptions(max_tokens=7, temperature=0.7, top_k=16, top_p=0.9, seed=48,
+                                   repetition_penalty=1.1, frequency_penalty=0.2,
+                                   presence_penalty=0.3),
+            cohx.GenerationOptions(max_tokens=5, temperature=0.9, seed=49)]
+    batched = run_generation(m, prompts, opts, arrive={2: 4})
+    for i, p in enumerate(prompts):
+        single = cohx.generate(m, p, opts[i])
+        assert single.token_ids() == batched[i][0]
+        want, reason = oracle_generate(o, p, opts[i], c["eos_token_id"])
+        assert batched[i] == (want, reason), i
+        single.free()
+
+
+def test_lane_errors_are_isolated():
+    print("case: lane errors", flush=True)
+    c, t, m, o = build("q8_0", 6)
+    a, b, d = m.seq_alloc(), m.seq_alloc(capacity=2), m.seq_alloc()
+    m.step([dict(seq=a, tokens=[1, 2]), dict(seq=b, tokens=[3, 4])])
+    res = m.step([dict(seq=a, tokens=[c["vocabulary"] + 1]), dict(seq=b, tokens=[5]),
+                  dict(seq=d, tokens=[7], logits=True)])
+    assert res[0]["status"] == cohx.INVALID_REQUEST
+    assert res[1]["status"] == cohx.RESOURCE
+    assert res[2]["status"] == 0
+    s = o.session(256)
+    o.forward_batch([s], [7])
+    assert np.array_equal(res[2]["logits"], s.logits())
+    assert m.seq_length(a) == 2 and m.seq_length(b) == 2
+
+
+def test_zero_weights_give_token_zero_and_eos_stops():
+    print("case: closed forms", flush=True)
+    c, t = synth.in_memory(TINY, "q8_0", seed=0)
+    for name, tensor in t.items():
+        if len(tensor.shape) == 2:
+            tensor.data[:] = 0
+    m = cohx.Model(c, t, max_lanes=2, max_rows=8, max_seqs=4, max_context=64)
+    st = cohx.generate(m, [5, 6], cohx.GenerationOptions(max_tokens=4))
+    assert st.token_ids() == [0, 0, 0, 0] and st.finish_reason() == "length"
+    # EOS (tests/engine.rs:187-217): embeddings of ones, zero matrices and an
+    # output row of ones for the end-of-generation id make it the argmax.
+    c2, t2 = synth.in_memory(TINY, "q8_0", seed=0, eos_token_id=258, tied=False)
+    ones = np.tile(np.r_[np.frombuffer(np.float16(1.0).tobytes(), np.uint8),
+                         np.ones(32, np.uint8)], c2["hidden"] // 32)
+    for name, tensor in t2.items():
+        if len(tensor.shape) == 2:
+            tensor.data[:] = 0
+    t2["token_embd.weight"].data.reshape(c2["vocabulary"], -1)[:] = ones
+    t2["output.weight"].data.reshape(c2["vocabulary"], -1)[258] = ones
+    m2 = cohx.Model(c2, t2, max_lanes=2, max_rows=8, max_seqs=4, max_context=64)
+    st = cohx.generate(m2, [5, 6], cohx.GenerationOptions(max_tokens=4))
+    assert st.token_ids() == [258] and st.finish_reason() == "stop"
+
+
+def test_shared_prefix_fork_equals_recompute():
+    print("case: fork", flush=True)
+    c, t, m, o = build("q8_0", 7)
+    base = m.seq_alloc()
+    prefix = list(range(1, 40))
+    m.step([dict(seq=base, tokens=prefix)])
+    fa, fb = m.seq_fork(base, 32), m.seq_fork(base, 37)
+    fresh = m.seq_alloc()
+    m.step([dict(seq=fresh, tokens=prefix[:37])])
+    ra = m.step([dict(seq=fa, tokens=[9], logits=True), dict(seq=fb, tokens=[11], logits=True),
+                 dict(seq=fresh, tokens=[11], logits=True)])
+    s = o.session(256)
+    for tok in prefix[:32] + [9]:
+        o.forward_batch([s], [tok])
+    assert np.array_equal(ra[0]["logits"], s.logits())
+    assert np.array_equal(ra[1]["logits"], ra[2]["logits"])
+    # the shared source is untouched by the forks' writes (copy on write)
+    for layer in range(c["layers"]):
+        assert np.array_equal(m.seq_read_kv(fb, layer)[:37], m.seq_read_kv(base, layer)[:37])
