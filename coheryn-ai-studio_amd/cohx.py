@@ -74,6 +74,12 @@ class GenOptions(ctypes.Structure):
                 ("stop_tokens", ctypes.POINTER(ctypes.c_uint32)), ("context", ctypes.c_uint32)]
 
 
+class KernelStat(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("launches", ctypes.c_uint64),
+                ("total_ms", ctypes.c_double), ("bytes", ctypes.c_double),
+                ("flops", ctypes.c_double)]
+
+
 class BatchStepC(ctypes.Structure):
     _fields_ = [("width", ctypes.c_uint32), ("completed_tokens", ctypes.c_uint32),
                 ("matrix_tiles", ctypes.c_uint64), ("matrix_bytes", ctypes.c_uint64)]
@@ -106,6 +112,9 @@ EXPORTS = {
     "cohx_pack": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Batch),
                                  ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32),
                                  ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_uint32)]),
+    "cohx_profile": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    "cohx_profile_read": (ctypes.c_uint32, [ctypes.c_void_p, ctypes.POINTER(KernelStat),
+                                            ctypes.c_uint32]),
     "cohx_gen_begin": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32),
                                       ctypes.c_uint32, ctypes.POINTER(GenOptions), ctypes.c_void_p,
                                       ctypes.POINTER(ctypes.c_void_p)]),
@@ -287,6 +296,20 @@ class Model:
         self.last_step = dict(width=so.width, rows=so.rows, matrix_bytes=so.matrix_bytes,
                               kv_bytes=so.kv_bytes, elapsed_ns=so.elapsed_ns)
         return res
+
+    @property
+    def matrix_bytes(self):
+        return self.last_step["matrix_bytes"]
+
+    def profile(self, enable):
+        self._check(lib().cohx_profile(self.h, 1 if enable else 0))
+
+    def profile_read(self):
+        n = lib().cohx_profile_read(self.h, None, 0)
+        arr = (KernelStat * n)()
+        lib().cohx_profile_read(self.h, arr, n)
+        return [dict(name=a.name.decode(), launches=a.launches, total_ms=a.total_ms,
+                     bytes=a.bytes, flops=a.flops) for a in arr]
 
     def pack(self, lanes):
         batch, keep = self._batch(lanes)

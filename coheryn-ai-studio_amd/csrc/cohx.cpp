@@ -662,19 +662,101 @@ extern "C" int cohx_pack(cohx_ctx *ctx, const cohx_batch *batch, uint32_t *cu, u
   return COHX_OK;
 }
 
+// ---- profiling -----------------------------------------------------------------
+
+namespace {
+
+const char *kCatNames[kCatCount] = {
+    "pack", "embed", "rmsnorm_act", "matvec_qkv", "qkv_rope_append", "attn_scores",
+    "attn_softmax", "attn_pv", "attn_combine_act", "matvec_o_residual", "matvec_gate_up_swiglu",
+    "swiglu_act", "matvec_down_residual", "matvec_head_argmax"};
+
+int prof_begin(cohx_ctx *ctx, int cat, double bytes, double flops) {
+  Profiler &p = ctx->prof;
+  if (!p.on) return -1;
+  while (p.pool.size() < p.next + 2) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return -1;
+    p.pool.push_back(e);
+  }
+  Profiler::Launch l{cat, bytes, flops, p.pool[p.next], p.pool[p.next + 1]};
+  p.next += 2;
+  if (hipEventRecord(l.a, ctx->stream) != hipSuccess) return -1;
+  p.pending.push_back(l);
+  return (int)p.pending.size() - 1;
+}
+
+void prof_end(cohx_ctx *ctx, int idx) {
+  if (idx >= 0) (void)hipEventRecord(ctx->prof.pending[idx].b, ctx->stream);
+}
+
+// After the stream has synchronized.
+void prof_collect(cohx_ctx *ctx) {
+  Profiler &p = ctx->prof;
+  for (const auto &l : p.pending) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, l.a, l.b) == hipSuccess) {
+      p.launches[l.cat]++;
+      p.ms[l.cat] += ms;
+      p.bytes[l.cat] += l.bytes;
+      p.flops[l.cat] += l.flops;
+    }
+  }
+  p.pending.clear();
+  p.next = 0;
+}
+
+// Algorithmic bytes of one Q8_0/F16 matrix pass over rows_b activation rows.
+double matrix_pass_bytes(const MatrixView &w, int rows_b, int out_rows, bool residual) {
+  const double wbytes = w.dtype == 8 ? (double)w.rows * w.K / 32 * 34 : (double)w.rows * w.K * 2;
+  const double abytes = w.dtype == 8 ? (double)rows_b * w.K / 32 * 34 : (double)rows_b * w.K * 2;
+  return wbytes + abytes + (double)rows_b * out_rows * 4 * (residual ? 2 : 1);
+}
+
+}  // namespace
+
+extern "C" int cohx_profile(cohx_ctx *ctx, int enable) {
+  if (!ctx) return COHX_INVALID_REQUEST;
+  Profiler &p = ctx->prof;
+  if (enable) {
+    std::fill(std::begin(p.launches), std::end(p.launches), 0);
+    std::fill(std::begin(p.ms), std::end(p.ms), 0.0);
+    std::fill(std::begin(p.bytes), std::end(p.bytes), 0.0);
+    std::fill(std::begin(p.flops), std::end(p.flops), 0.0);
+  }
+  p.on = enable != 0;
+  return COHX_OK;
+}
+
+extern "C" uint32_t cohx_profile_read(const cohx_ctx *ctx, cohx_kernel_stat *out, uint32_t cap) {
+  if (!ctx) return 0;
+  const Profiler &p = ctx->prof;
+  for (uint32_t i = 0; i < (uint32_t)kCatCount && out && i < cap; i++)
+    out[i] = cohx_kernel_stat{kCatNames[i], p.launches[i], p.ms[i], p.bytes[i], p.flops[i]};
+  return kCatCount;
+}
+
 extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
   if (!ctx || !out || !out->lanes) return COHX_INVALID_REQUEST;
   const auto t_start = std::chrono::steady_clock::now();
   HIP_TRY(hipSetDevice(ctx->device));
   const cohx_model_desc &d = ctx->desc;
   Prepared p;
+  const int pk = prof_begin(ctx, kCatPack, 0.0, 0.0);
   int rc = prepare_batch(ctx, batch, out->lanes, p);
-  if (rc) return rc;
+  prof_end(ctx, pk);
+  if (rc) {
+    ctx->prof.pending.clear();
+    ctx->prof.next = 0;
+    return rc;
+  }
   out->width = (uint32_t)p.included.size();
   out->rows = p.rows;
   out->matrix_bytes = 0;
   out->kv_bytes = 0;
   if (p.included.empty()) {
+    ctx->prof.pending.clear();
+    ctx->prof.next = 0;
     out->elapsed_ns = 0;
     return COHX_OK;
   }
@@ -682,47 +764,97 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
   const int H = d.hidden, F = d.intermediate, NH = d.heads, NKV = d.kv_heads, D = d.head_dim,
             KVD = NKV * D;
   const int act_dtype = d.weight_dtype == COHX_Q8_0 ? 8 : 1;
+  const double act_row = act_dtype == 8 ? (double)H / 32 * 34 : (double)H * 2;
   Workspace &w = ctx->ws;
   hipStream_t s = ctx->stream;
   StepDims sd{H, F, (int)d.vocabulary, NH, NKV, D, KVD, NH / NKV, d.norm_epsilon,
               1.0f / sqrtf((float)D), ctx->max_pages, (int)d.max_context, ctx->max_chunks};
   const ActView act = act_view(ctx);
+  const int chunks = (int)((p.max_kv + kChunk - 1) / kChunk);
+  const double kv_rows = (double)p.kv_rows_read;  // sum over rows of attended positions
+  int e;
+  // per-launch algorithmic bytes
+  const double b_norm = (double)R * H * 4 + H * 4 + R * act_row;
+  const double b_scores = kv_rows * KVD * 4 + (double)R * H * 4 + kv_rows * NH * 4;
+  const double b_softmax = kv_rows * NH * 4 * 2;
+  const double b_pv = kv_rows * KVD * 4 + kv_rows * NH * 4 + (double)R * H * 4;
+  const double f_attn = kv_rows * NH * D * 2;
+  const double b_combine = (double)R * H * 4 + R * act_row;
+  const double b_post = (double)R * (H + 2 * KVD) * 4 * 2 + (H + 2 * KVD) * 4;
+  e = prof_begin(ctx, kCatEmbed, (double)R * act_row + (double)R * H * 4, 0);
   launch_embed(s, R, ctx->embd.view, w.row_token, w.x, H, w.row_err);
+  prof_end(ctx, e);
   for (uint32_t l = 0; l < d.layers; l++) {
     Layer &ly = ctx->layers[l];
     float *kp = ctx->kpool + (size_t)l * ctx->layer_stride;
     float *vp = ctx->vpool + (size_t)l * ctx->layer_stride;
+    e = prof_begin(ctx, kCatNorm, b_norm, 0);
     launch_norm_act(s, R, w.x, nullptr, ly.attn_norm, H, d.norm_epsilon, act_dtype, ctx->nbp_h, act,
                     w.row_err);
+    prof_end(ctx, e);
+    e = prof_begin(ctx, kCatMvQkv, matrix_pass_bytes(ly.qkv.view, R, H + 2 * KVD, false),
+                   2.0 * R * (H + 2 * KVD) * H);
     launch_matvec(s, kEpiStore, ly.qkv.view, act, R,
                   MatvecOut{w.qkv, H + 2 * KVD, nullptr, nullptr, w.row_err, nullptr});
+    prof_end(ctx, e);
+    e = prof_begin(ctx, kCatQkvPost, b_post, 0);
     launch_qkv_post(s, R, sd, w.qkv, ly.bqkv, ctx->rope, w.row_pos, w.row_slot, w.q_rot, kp, vp,
                     w.row_err);
-    launch_attention(s, R, (int)p.max_kv, sd, w.q_rot, kp, vp, w.row_pos, w.row_seq,
-                     ctx->page_table, w.scores, w.chunk_max, w.partial, act_dtype, ctx->nbp_h, act,
-                     w.row_err);
+    prof_end(ctx, e);
+    e = prof_begin(ctx, kCatAttnScores, b_scores, f_attn);
+    launch_attn_scores(s, R, chunks, sd, w.q_rot, kp, w.row_pos, w.row_seq, ctx->page_table,
+                       w.scores, w.chunk_max, w.row_err);
+    prof_end(ctx, e);
+    e = prof_begin(ctx, kCatAttnSoftmax, b_softmax, 0);
+    launch_attn_softmax(s, R, sd, w.row_pos, w.scores, w.chunk_max);
+    prof_end(ctx, e);
+    e = prof_begin(ctx, kCatAttnPv, b_pv, f_attn);
+    launch_attn_pv(s, R, chunks, sd, vp, w.row_pos, w.row_seq, ctx->page_table, w.scores,
+                   w.partial);
+    prof_end(ctx, e);
+    e = prof_begin(ctx, kCatAttnCombine, b_combine, 0);
+    launch_attn_combine(s, R, sd, w.row_pos, w.partial, act_dtype, ctx->nbp_h, act, w.row_err);
+    prof_end(ctx, e);
+    e = prof_begin(ctx, kCatMvO, matrix_pass_bytes(ly.o.view, R, H, true), 2.0 * R * H * H);
     launch_matvec(s, kEpiResidual, ly.o.view, act, R,
                   MatvecOut{w.x, H, nullptr, nullptr, w.row_err, nullptr});
+    prof_end(ctx, e);
+    e = prof_begin(ctx, kCatNorm, b_norm, 0);
     launch_norm_act(s, R, w.x, nullptr, ly.ffn_norm, H, d.norm_epsilon, act_dtype, ctx->nbp_h, act,
                     w.row_err);
+    prof_end(ctx, e);
+    e = prof_begin(ctx, kCatMvGateUp, matrix_pass_bytes(ly.gu.view, R, F, false),
+                   2.0 * R * 2 * F * H);
     launch_matvec(s, kEpiSwiglu, ly.gu.view, act, R,
                   MatvecOut{w.h, F, nullptr, nullptr, w.row_err, nullptr});
+    prof_end(ctx, e);
+    e = prof_begin(ctx, kCatQuant, (double)R * F * 4 + (act_dtype == 8 ? (double)R * F / 32 * 34
+                                                                         : (double)R * F * 2), 0);
     launch_quant_act(s, R, w.h, F, act_dtype, ctx->nbp_f, act, w.row_err);
+    prof_end(ctx, e);
+    e = prof_begin(ctx, kCatMvDown, matrix_pass_bytes(ly.down.view, R, H, true), 2.0 * R * H * F);
     launch_matvec(s, kEpiResidual, ly.down.view, act, R,
                   MatvecOut{w.x, H, nullptr, nullptr, w.row_err, nullptr});
+    prof_end(ctx, e);
   }
   // final norm and head over the last row of every lane (batch.rs:250-266)
+  e = prof_begin(ctx, kCatNorm, (double)NL * H * 4 + H * 4 + NL * act_row, 0);
   launch_norm_act(s, NL, w.x, w.lane_last, ctx->output_norm, H, d.norm_epsilon, act_dtype,
                   ctx->nbp_h, act, w.row_err);
+  prof_end(ctx, e);
   bool any_logits = false;
   for (int k = 0; k < NL; k++)
     if (batch->lanes[p.included[k]].want_logits && out->lanes[p.included[k]].logits)
       any_logits = true;
-  launch_fill_u64(s, w.argmax, NL, 0ull);
   const DeviceMatrix &head = d.tied ? ctx->embd : ctx->output;
+  e = prof_begin(ctx, kCatMvHead,
+                 matrix_pass_bytes(head.view, NL, 0, false) + (any_logits ? (double)NL * d.vocabulary * 4 : 0.0) + NL * 8.0,
+                 2.0 * NL * d.vocabulary * H);
+  launch_fill_u64(s, w.argmax, NL, 0ull);
   launch_matvec(s, kEpiArgmax, head.view, act, NL,
                 MatvecOut{nullptr, 0, w.argmax, any_logits ? w.logits : nullptr, w.row_err,
                           w.lane_last});
+  prof_end(ctx, e);
   HIP_TRY(hipGetLastError());
   HIP_TRY(hipMemcpyAsync(w.h_argmax, w.argmax, NL * sizeof(unsigned long long),
                          hipMemcpyDeviceToHost, s));
@@ -735,6 +867,7 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
                              hipMemcpyDeviceToHost, s));
   }
   HIP_TRY(hipStreamSynchronize(s));
+  prof_collect(ctx);
   // lane statuses from row error bits; advance healthy sequences
   uint32_t row = 0;
   for (int k = 0; k < NL; k++) {

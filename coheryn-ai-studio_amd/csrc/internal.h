@@ -47,6 +47,25 @@ struct Workspace {
   unsigned long long *h_argmax = nullptr;
 };
 
+enum ProfCat {
+  kCatPack, kCatEmbed, kCatNorm, kCatMvQkv, kCatQkvPost, kCatAttnScores, kCatAttnSoftmax,
+  kCatAttnPv, kCatAttnCombine, kCatMvO, kCatMvGateUp, kCatQuant, kCatMvDown, kCatMvHead, kCatCount
+};
+
+struct Profiler {
+  struct Launch {
+    int cat;
+    double bytes, flops;
+    hipEvent_t a, b;
+  };
+  bool on = false;
+  std::vector<hipEvent_t> pool;
+  size_t next = 0;
+  std::vector<Launch> pending;
+  uint64_t launches[kCatCount] = {};
+  double ms[kCatCount] = {}, bytes[kCatCount] = {}, flops[kCatCount] = {};
+};
+
 }  // namespace cohx
 
 struct cohx_ctx {
@@ -74,6 +93,7 @@ struct cohx_ctx {
   bool finalized = false;
   uint64_t matrix_bytes = 0;
   cohx::Workspace ws;
+  cohx::Profiler prof;
   std::vector<void *> allocations;
 };
 

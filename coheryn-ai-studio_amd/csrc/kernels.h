@@ -62,11 +62,18 @@ void launch_qkv_post(hipStream_t s, int rows, const StepDims &d, const float *qk
                      const float *bias, const float2 *rope, const uint32_t *row_pos,
                      const int32_t *row_slot, float *q_rot, float *kpool, float *vpool,
                      uint32_t *row_err);
-void launch_attention(hipStream_t s, int rows, int max_kv, const StepDims &d, const float *q_rot,
-                      const float *kpool, const float *vpool, const uint32_t *row_pos,
-                      const uint32_t *row_seq, const int32_t *page_table, float *scores,
-                      float *chunk_max, double *partial, int act_dtype, int nbp, ActView act,
-                      uint32_t *row_err);
+void launch_attn_scores(hipStream_t s, int rows, int chunks, const StepDims &d, const float *q_rot,
+                        const float *kpool, const uint32_t *row_pos, const uint32_t *row_seq,
+                        const int32_t *page_table, float *scores, float *chunk_max,
+                        uint32_t *row_err);
+void launch_attn_softmax(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
+                         float *scores, const float *chunk_max);
+void launch_attn_pv(hipStream_t s, int rows, int chunks, const StepDims &d, const float *vpool,
+                    const uint32_t *row_pos, const uint32_t *row_seq, const int32_t *page_table,
+                    const float *scores, double *partial);
+void launch_attn_combine(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
+                         const double *partial, int act_dtype, int nbp, ActView act,
+                         uint32_t *row_err);
 void launch_fill_synthetic(hipStream_t s, float *kpool, float *vpool, size_t layer_stride,
                            int layers, const int32_t *pages, int rows, int NKV, int D,
                            uint64_t seed, uint32_t stream);

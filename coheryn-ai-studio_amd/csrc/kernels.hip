@@ -687,25 +687,37 @@ void launch_qkv_post(hipStream_t s, int rows, const StepDims &d, const float *qk
                      row_slot, q_rot, kpool, vpool);
 }
 
-void launch_attention(hipStream_t s, int rows, int max_kv, const StepDims &d, const float *q_rot,
-                      const float *kpool, const float *vpool, const uint32_t *row_pos,
-                      const uint32_t *row_seq, const int32_t *page_table, float *scores,
-                      float *chunk_max, double *partial, int act_dtype, int nbp, ActView act,
-                      uint32_t *row_err) {
-  const int chunks = (max_kv + kChunk - 1) / kChunk;
+void launch_attn_scores(hipStream_t s, int rows, int chunks, const StepDims &d, const float *q_rot,
+                        const float *kpool, const uint32_t *row_pos, const uint32_t *row_seq,
+                        const int32_t *page_table, float *scores, float *chunk_max,
+                        uint32_t *row_err) {
   hipLaunchKernelGGL(k_attn_scores, dim3(rows, d.NKV, chunks), dim3(128), 0, s, d, q_rot, kpool,
                      row_pos, row_seq, page_table, scores, chunk_max, row_err);
+}
+
+void launch_attn_softmax(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
+                         float *scores, const float *chunk_max) {
   hipLaunchKernelGGL(k_attn_softmax, dim3(rows, d.NH), dim3(256), 0, s, d, row_pos, scores,
                      chunk_max);
-  const int pv_threads = ((d.G * d.D + kWave - 1) / kWave) * kWave;
-  hipLaunchKernelGGL(k_attn_pv, dim3(rows, d.NKV, chunks), dim3(pv_threads), 0, s, d, vpool,
-                     row_pos, row_seq, page_table, scores, partial);
-  const int cthreads = ((d.D + kWave - 1) / kWave) * kWave;
+}
+
+void launch_attn_pv(hipStream_t s, int rows, int chunks, const StepDims &d, const float *vpool,
+                    const uint32_t *row_pos, const uint32_t *row_seq, const int32_t *page_table,
+                    const float *scores, double *partial) {
+  const int threads = ((d.G * d.D + kWave - 1) / kWave) * kWave;
+  hipLaunchKernelGGL(k_attn_pv, dim3(rows, d.NKV, chunks), dim3(threads), 0, s, d, vpool, row_pos,
+                     row_seq, page_table, scores, partial);
+}
+
+void launch_attn_combine(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
+                         const double *partial, int act_dtype, int nbp, ActView act,
+                         uint32_t *row_err) {
+  const int threads = ((d.D + kWave - 1) / kWave) * kWave;
   if (act_dtype == 8)
-    hipLaunchKernelGGL(k_attn_combine<8>, dim3(rows, d.NH), dim3(cthreads), 0, s, d, row_pos,
+    hipLaunchKernelGGL(k_attn_combine<8>, dim3(rows, d.NH), dim3(threads), 0, s, d, row_pos,
                        partial, nbp, act, row_err);
   else
-    hipLaunchKernelGGL(k_attn_combine<1>, dim3(rows, d.NH), dim3(cthreads), 0, s, d, row_pos,
+    hipLaunchKernelGGL(k_attn_combine<1>, dim3(rows, d.NH), dim3(threads), 0, s, d, row_pos,
                        partial, nbp, act, row_err);
 }
 

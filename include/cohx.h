@@ -142,6 +142,22 @@ int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out);
 int cohx_pack(cohx_ctx *ctx, const cohx_batch *batch, uint32_t *cu_seqlens, uint32_t *positions,
               int64_t *slots, uint32_t *lanes);
 
+/* Opt-in per-kernel timing of cohx_step (no engine counterpart; the engine
+ * reports only BatchStep byte counts, batch.rs:3-9).  enable=1 clears the
+ * counters and starts timing every launch with HIP events on the context's
+ * stream; enable=0 stops.  Each record names a kernel and gives its launches,
+ * summed device time and summed algorithmic bytes / flops (the minimum traffic
+ * and arithmetic of the operation, independent of how the kernel achieves it). */
+typedef struct {
+  const char *name;
+  uint64_t launches;
+  double total_ms;
+  double bytes;
+  double flops;
+} cohx_kernel_stat;
+int cohx_profile(cohx_ctx *ctx, int enable);
+uint32_t cohx_profile_read(const cohx_ctx *ctx, cohx_kernel_stat *out, uint32_t cap);
+
 /* ---- host mirror of the engine's generation API ------------------------- */
 
 typedef struct cohx_gen cohx_gen;
