@@ -154,6 +154,8 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
       d->intermediate % 32 || !d->vocabulary)
     return COHX_INVALID_GGUF;
   if (d->weight_dtype != COHX_Q8_0 && d->weight_dtype != COHX_F16) return COHX_UNSUPPORTED;
+  if (!attention_shape_supported((int)d->head_dim, (int)(d->heads / d->kv_heads)))
+    return COHX_UNSUPPORTED;
   if (d->kv_dtype != 0) return COHX_UNSUPPORTED;
   if (!d->max_lanes || d->max_lanes > 1024 || !d->max_rows || d->max_rows < d->max_lanes ||
       !d->max_seqs || !d->max_context || d->max_context > d->context || d->n_eog > 4)
@@ -252,10 +254,11 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   if (!rc) rc = dalloc(ctx, &w.act_ds, rtiles * ctx->nbp_max * 16);
   if (!rc) rc = dalloc(ctx, &w.act_f16, (size_t)R * std::max(H, F));
   if (!rc) rc = dalloc(ctx, &w.scores, (size_t)R * NH * d->max_context);
-  if (!rc) rc = dalloc(ctx, &w.chunk_max, (size_t)R * NH * ctx->max_chunks);
+  if (!rc) rc = dalloc(ctx, &w.chunk_max, (size_t)R * NH * ((d->max_context + 255) / 256));
   if (!rc) rc = dalloc(ctx, &w.partial, (size_t)R * NH * ctx->max_chunks * D);
   if (!rc) rc = dalloc(ctx, &w.logits, (size_t)NL * V);
   if (!rc) rc = dalloc(ctx, &w.argmax, NL);
+  if (!rc) rc = dalloc(ctx, &w.argmax_part, (size_t)NL * ((V + 15) / 16));
   if (!rc) rc = halloc(ctx, &w.h_upload, (size_t)NL * 4 + R);
   if (!rc) rc = halloc(ctx, &w.h_row_err, R);
   if (!rc) rc = halloc(ctx, &w.h_argmax, NL);
@@ -668,7 +671,7 @@ namespace {
 
 const char *kCatNames[kCatCount] = {
     "pack", "embed", "rmsnorm_act", "matvec_qkv", "qkv_rope_append", "attn_scores",
-    "attn_softmax", "attn_pv", "attn_combine_act", "matvec_o_residual", "matvec_gate_up_swiglu",
+    "attn_softmax_stats", "attn_pv", "attn_combine_act", "matvec_o_residual", "matvec_gate_up_swiglu",
     "swiglu_act", "matvec_down_residual", "matvec_head_argmax"};
 
 int prof_begin(cohx_ctx *ctx, int cat, double bytes, double flops) {
@@ -770,7 +773,6 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
   StepDims sd{H, F, (int)d.vocabulary, NH, NKV, D, KVD, NH / NKV, d.norm_epsilon,
               1.0f / sqrtf((float)D), ctx->max_pages, (int)d.max_context, ctx->max_chunks};
   const ActView act = act_view(ctx);
-  const int chunks = (int)((p.max_kv + kChunk - 1) / kChunk);
   const double kv_rows = (double)p.kv_rows_read;  // sum over rows of attended positions
   int e;
   // per-launch algorithmic bytes
@@ -802,14 +804,14 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
                     w.row_err);
     prof_end(ctx, e);
     e = prof_begin(ctx, kCatAttnScores, b_scores, f_attn);
-    launch_attn_scores(s, R, chunks, sd, w.q_rot, kp, w.row_pos, w.row_seq, ctx->page_table,
-                       w.scores, w.chunk_max, w.row_err);
+    launch_attn_scores(s, R, (int)p.max_kv, sd, w.q_rot, kp, w.row_pos, w.row_seq,
+                       ctx->page_table, w.scores, w.chunk_max, w.row_err);
     prof_end(ctx, e);
     e = prof_begin(ctx, kCatAttnSoftmax, b_softmax, 0);
-    launch_attn_softmax(s, R, sd, w.row_pos, w.scores, w.chunk_max);
+    launch_attn_stats(s, R, sd, w.row_pos, w.scores, w.chunk_max);
     prof_end(ctx, e);
     e = prof_begin(ctx, kCatAttnPv, b_pv, f_attn);
-    launch_attn_pv(s, R, chunks, sd, vp, w.row_pos, w.row_seq, ctx->page_table, w.scores,
+    launch_attn_pv(s, R, (int)p.max_kv, sd, vp, w.row_pos, w.row_seq, ctx->page_table, w.scores,
                    w.partial);
     prof_end(ctx, e);
     e = prof_begin(ctx, kCatAttnCombine, b_combine, 0);
@@ -850,10 +852,17 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
   e = prof_begin(ctx, kCatMvHead,
                  matrix_pass_bytes(head.view, NL, 0, false) + (any_logits ? (double)NL * d.vocabulary * 4 : 0.0) + NL * 8.0,
                  2.0 * NL * d.vocabulary * H);
-  launch_fill_u64(s, w.argmax, NL, 0ull);
-  launch_matvec(s, kEpiArgmax, head.view, act, NL,
-                MatvecOut{nullptr, 0, w.argmax, any_logits ? w.logits : nullptr, w.row_err,
-                          w.lane_last});
+  if (head.view.dtype == 8) {
+    launch_matvec(s, kEpiArgmax, head.view, act, NL,
+                  MatvecOut{nullptr, 0, w.argmax_part, any_logits ? w.logits : nullptr, w.row_err,
+                            w.lane_last});
+    launch_argmax_reduce(s, NL, w.argmax_part, head.view.mtiles, w.argmax);
+  } else {
+    launch_fill_u64(s, w.argmax, NL, 0ull);
+    launch_matvec(s, kEpiArgmax, head.view, act, NL,
+                  MatvecOut{nullptr, 0, w.argmax, any_logits ? w.logits : nullptr, w.row_err,
+                            w.lane_last});
+  }
   prof_end(ctx, e);
   HIP_TRY(hipGetLastError());
   HIP_TRY(hipMemcpyAsync(w.h_argmax, w.argmax, NL * sizeof(unsigned long long),

@@ -41,6 +41,7 @@ struct Workspace {
   float *scores = nullptr, *chunk_max = nullptr, *logits = nullptr;
   double *partial = nullptr;
   unsigned long long *argmax = nullptr;
+  unsigned long long *argmax_part = nullptr;  // [max_lanes][head m-tiles]
   // pinned host staging
   uint32_t *h_upload = nullptr;  // lane_info then tokens
   uint32_t *h_row_err = nullptr;

@@ -38,7 +38,8 @@ enum Epilogue { kEpiStore = 0, kEpiResidual = 1, kEpiSwiglu = 2, kEpiArgmax = 3 
 struct MatvecOut {
   float *out;          // kEpiStore: [rows_b][ld]; kEpiResidual: x [rows_b][ld]; kEpiSwiglu: h
   int ld;
-  unsigned long long *argmax;  // kEpiArgmax: per batch row key
+  unsigned long long *argmax;  // kEpiArgmax: Q8_0 -> per (batch row, tile) partial keys
+                               // [rows_b][mtiles]; F16 -> per batch row key (atomic max)
   float *logits;               // kEpiArgmax: optional [rows_b][V] (nullptr: none)
   uint32_t *row_err;           // per batch row error bits
   const uint32_t *err_rows;    // batch row -> packed row index for error bits (nullptr: same)
@@ -58,19 +59,24 @@ void launch_quant_act(hipStream_t s, int rows, const float *src, int K, int act_
                       ActView act, uint32_t *row_err);
 void launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActView &act,
                    int rows_b, const MatvecOut &o);
+void launch_argmax_reduce(hipStream_t s, int rows, const unsigned long long *part, int units,
+                          unsigned long long *out);
 void launch_qkv_post(hipStream_t s, int rows, const StepDims &d, const float *qkv,
                      const float *bias, const float2 *rope, const uint32_t *row_pos,
                      const int32_t *row_slot, float *q_rot, float *kpool, float *vpool,
                      uint32_t *row_err);
-void launch_attn_scores(hipStream_t s, int rows, int chunks, const StepDims &d, const float *q_rot,
+// (head_dim, q heads per KV head) pairs the attention kernels are built for
+bool attention_shape_supported(int D, int G);
+void launch_attn_scores(hipStream_t s, int rows, int max_kv, const StepDims &d, const float *q_rot,
                         const float *kpool, const uint32_t *row_pos, const uint32_t *row_seq,
                         const int32_t *page_table, float *scores, float *chunk_max,
                         uint32_t *row_err);
-void launch_attn_softmax(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
-                         float *scores, const float *chunk_max);
-void launch_attn_pv(hipStream_t s, int rows, int chunks, const StepDims &d, const float *vpool,
+// Rewrites scores in place as normalized weights.
+void launch_attn_stats(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
+                       float *scores, const float *chunk_max);
+void launch_attn_pv(hipStream_t s, int rows, int max_kv, const StepDims &d, const float *vpool,
                     const uint32_t *row_pos, const uint32_t *row_seq, const int32_t *page_table,
-                    const float *scores, double *partial);
+                    const float *probs, double *partial);
 void launch_attn_combine(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
                          const double *partial, int act_dtype, int nbp, ActView act,
                          uint32_t *row_err);

@@ -199,110 +199,153 @@ __device__ __forceinline__ void argmax_commit(float best, int best_row, bool val
 }
 
 // ---------------------------------------------------------------------------
-// Q8_0 matvec on the matrix cores.  One wave owns kNM m-tiles (16 matrix rows
-// each; kNM = 2 pairs a gate tile with its up tile) and kNT n-tiles (16 batch
-// rows each).  Per 32-element block: int32 isum of the 16x16 tile from one
-// MFMA, then acc = fmaf(float(isum), dw*da, acc) — the reference chain, block
-// by block, for each of the lane's 4 (row, batch-row) outputs.
+// Split-K Q8_0 matvec.  A workgroup of 8 waves owns one output tile: kNM
+// m-tiles (16 matrix rows each; 2 = a gate tile and its up tile) x one n-tile
+// (16 batch rows).  K is walked in chunks of 16 blocks; in each chunk every
+// wave takes one block pair, computes the exact int32 block sums on the matrix
+// cores and parks them (as f32, exact below 2^24) in LDS with the block scales;
+// then 256 threads, one per (row, batch row), run the reference chain
+// acc = fmaf(isum, dw*da, acc) over the chunk's blocks in order.  The next
+// chunk's operands are loaded before the current chunk is consumed.
+// Block -> (tile, n-tile) mapping keeps all n-tiles of a weight tile on one
+// XCD (blockIdx % 8), so the tile is fetched into that XCD's L2 once.
 // ---------------------------------------------------------------------------
-template <int kEpi, int kNT, int kNM>
-__global__ __launch_bounds__(256) void k_mv_q8(MatrixView w, ActView act, int rows_b,
-                                               MatvecOut o) {
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const int unit = blockIdx.x * 4 + wave;
-  if (unit * kNM >= w.mtiles) return;
-  const int nt0 = blockIdx.y * kNT;
-  const int n_tiles = (rows_b + 15) / 16;
+template <int kNM>
+struct Q8Regs {
+  uint4 a[kNM];
+  uint4 b;
+  uint32_t dw[kNM];
+  uint32_t da;
+};
+
+template <int kNM>
+__device__ __forceinline__ void q8_load(Q8Regs<kNM> &r, const MatrixView &w, const ActView &act,
+                                        int unit, int nt, int pair, int lane) {
   const int nbp = w.nbp;
-  float acc[kNM][kNT][4];
 #pragma unroll
   for (int m = 0; m < kNM; m++)
-#pragma unroll
-    for (int n = 0; n < kNT; n++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) acc[m][n][i] = 0.0f;
-  const v4i zero = {0, 0, 0, 0};
-  const int rsub = 4 * (lane / 16);
-  for (int bp = 0; bp < nbp / 2; bp++) {
-    uint4 a[kNM], bq[kNT];
+    r.a[m] = *reinterpret_cast<const uint4 *>(w.qs + q8_byte(unit * kNM + m, nbp, pair * 2, lane, 0));
+  r.b = *reinterpret_cast<const uint4 *>(act.qs + q8_byte(nt, nbp, pair * 2, lane, 0));
+  if (lane < 16) {
 #pragma unroll
     for (int m = 0; m < kNM; m++)
-      a[m] = *reinterpret_cast<const uint4 *>(w.qs + q8_byte(unit * kNM + m, nbp, bp * 2, lane, 0));
+      r.dw[m] = (uint32_t)w.ds[q8_scale(unit * kNM + m, nbp, pair * 2, lane)] |
+                ((uint32_t)w.ds[q8_scale(unit * kNM + m, nbp, pair * 2 + 1, lane)] << 16);
+    r.da = (uint32_t)act.ds[q8_scale(nt, nbp, pair * 2, lane)] |
+           ((uint32_t)act.ds[q8_scale(nt, nbp, pair * 2 + 1, lane)] << 16);
+  }
+}
+
+__device__ __forceinline__ long lo64(uint4 v) {
+  return (long)(((unsigned long)v.y << 32) | v.x);
+}
+__device__ __forceinline__ long hi64(uint4 v) {
+  return (long)(((unsigned long)v.w << 32) | v.z);
+}
+
+template <int kEpi, int kNM>
+__global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int rows_b,
+                                                int n_tiles, MatvecOut o) {
+  constexpr int kW = 8, kCB = 2 * kW;
+  __shared__ float s_isum[kCB][kNM * 256];
+  __shared__ float s_dw[kCB][kNM * 16];
+  __shared__ float s_da[kCB][16];
+  __shared__ unsigned long long s_key[4][16];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int units = w.mtiles / kNM;
+  const int group = blockIdx.x / (8 * n_tiles), rem = blockIdx.x % (8 * n_tiles);
+  const int nt = rem / 8, unit = group * 8 + rem % 8;
+  if (unit >= units) return;
+  const int nbp = w.nbp, npairs = nbp / 2, nchunks = (nbp + kCB - 1) / kCB;
+  const int rsub = 4 * (lane / 16);
+  const v4i zero = {0, 0, 0, 0};
+  // phase-2 ownership: thread t < 256 owns (row t/16, batch column t%16) of every m-tile
+  const int t = threadIdx.x, prow = t / 16, pcol = t % 16;
+  float acc[kNM];
 #pragma unroll
-    for (int n = 0; n < kNT; n++)
-      if (nt0 + n < n_tiles)
-        bq[n] = *reinterpret_cast<const uint4 *>(act.qs + q8_byte(nt0 + n, nbp, bp * 2, lane, 0));
+  for (int m = 0; m < kNM; m++) acc[m] = 0.0f;
+  Q8Regs<kNM> cur, nxt;
+  if (wave < npairs) q8_load(cur, w, act, unit, nt, wave, lane);
+  for (int c = 0; c < nchunks; c++) {
+    const int pair = c * kW + wave;
+    if (c + 1 < nchunks && pair + kW < npairs) q8_load(nxt, w, act, unit, nt, pair + kW, lane);
+    if (pair < npairs) {
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const int b = bp * 2 + h;
-      float dw[kNM][4];
-#pragma unroll
-      for (int m = 0; m < kNM; m++) {
-        const uint2 s2 =
-            *reinterpret_cast<const uint2 *>(w.ds + q8_scale(unit * kNM + m, nbp, b, rsub));
-        dw[m][0] = h2f((uint16_t)(s2.x & 0xffffu));
-        dw[m][1] = h2f((uint16_t)(s2.x >> 16));
-        dw[m][2] = h2f((uint16_t)(s2.y & 0xffffu));
-        dw[m][3] = h2f((uint16_t)(s2.y >> 16));
-      }
-#pragma unroll
-      for (int n = 0; n < kNT; n++) {
-        if (nt0 + n >= n_tiles) continue;
-        const float da = h2f(act.ds[q8_scale(nt0 + n, nbp, b, lane % 16)]);
-        const long bop = h ? (long)(((unsigned long)bq[n].w << 32) | bq[n].z)
-                           : (long)(((unsigned long)bq[n].y << 32) | bq[n].x);
+      for (int h = 0; h < 2; h++) {
+        const int blk = 2 * wave + h;
+        const long bop = h ? hi64(cur.b) : lo64(cur.b);
 #pragma unroll
         for (int m = 0; m < kNM; m++) {
-          const long aop = h ? (long)(((unsigned long)a[m].w << 32) | a[m].z)
-                             : (long)(((unsigned long)a[m].y << 32) | a[m].x);
-          const v4i s = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, zero, 0, 0, 0);
+          const v4i s = __builtin_amdgcn_mfma_i32_16x16x32_i8(h ? hi64(cur.a[m]) : lo64(cur.a[m]),
+                                                              bop, zero, 0, 0, 0);
 #pragma unroll
-          for (int i = 0; i < 4; i++) acc[m][n][i] = fmaf((float)s[i], dw[m][i] * da, acc[m][n][i]);
+          for (int i = 0; i < 4; i++)
+            s_isum[blk][m * 256 + (rsub + i) * 16 + lane % 16] = (float)s[i];
         }
+      }
+      if (lane < 16) {
+#pragma unroll
+        for (int m = 0; m < kNM; m++) {
+          s_dw[2 * wave][m * 16 + lane] = h2f((uint16_t)(cur.dw[m] & 0xffffu));
+          s_dw[2 * wave + 1][m * 16 + lane] = h2f((uint16_t)(cur.dw[m] >> 16));
+        }
+        s_da[2 * wave][lane] = h2f((uint16_t)(cur.da & 0xffffu));
+        s_da[2 * wave + 1][lane] = h2f((uint16_t)(cur.da >> 16));
       }
     }
+    __syncthreads();
+    if (t < 256) {
+      const int nblk = min(kCB, nbp - c * kCB);
+      for (int blk = 0; blk < nblk; blk++) {
+        const float da = s_da[blk][pcol];
+#pragma unroll
+        for (int m = 0; m < kNM; m++)
+          acc[m] = fmaf(s_isum[blk][m * 256 + t], s_dw[blk][m * 16 + prow] * da, acc[m]);
+      }
+    }
+    __syncthreads();
+    cur = nxt;
   }
   // ---- epilogue
+  const int r = nt * 16 + pcol;
+  const bool rvalid = t < 256 && r < rows_b;
+  const int er = (rvalid && o.err_rows) ? (int)o.err_rows[r] : r;
+  bool bad = false;
+  if (kEpi == kEpiArgmax) {
+    const int row = unit * 16 + prow;
+    const bool valid = rvalid && row < w.rows;
+    const float v = acc[0];
+    if (valid) {
+      bad = !finitef(v);
+      if (o.logits) o.logits[(size_t)r * w.rows + row] = v;
+    }
+    unsigned long long key = valid ? argmax_key(v, row) : 0ull;
+    unsigned long long x = __shfl_xor(key, 16, kWave);
+    key = x > key ? x : key;
+    x = __shfl_xor(key, 32, kWave);
+    key = x > key ? x : key;
+    if (t < 256 && lane < 16) s_key[wave][lane] = key;
+    __syncthreads();
+    if (t < 16) {
+      unsigned long long best = s_key[0][t];
 #pragma unroll
-  for (int n = 0; n < kNT; n++) {
-    const int r = (nt0 + n) * 16 + lane % 16;
-    const bool rvalid = (nt0 + n < n_tiles) && r < rows_b;
-    const int er = (rvalid && o.err_rows) ? (int)o.err_rows[r] : r;
-    bool bad = false;
-    if (kEpi == kEpiArgmax) {
-      float best = 0.0f;
-      int best_row = 0;
-      bool have = false;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int row = unit * 16 + rsub + i;
-        if (!rvalid || row >= w.rows) continue;
-        const float v = acc[0][n][i];
-        bad |= !finitef(v);
-        if (o.logits) o.logits[(size_t)r * w.rows + row] = v;
-        if (!have || v > best) {
-          best = v;
-          best_row = row;
-          have = true;
-        }
-      }
-      argmax_commit(best, best_row, rvalid && have, r, o.argmax);
-    } else if (kEpi == kEpiSwiglu) {
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int row = unit * 16 + rsub + i;
-        if (!rvalid || row >= w.rows / 2) continue;
-        const float g = acc[0][n][i], u = acc[1][n][i];
-        bad |= !finitef(g) || !finitef(u);
+      for (int i = 1; i < 4; i++) best = s_key[i][t] > best ? s_key[i][t] : best;
+      // per-(batch row, tile) partial; reduced by k_argmax_reduce
+      if (nt * 16 + t < rows_b) o.argmax[(size_t)(nt * 16 + t) * units + unit] = best;
+    }
+  } else if (rvalid) {
+    if (kEpi == kEpiSwiglu) {
+      const int row = unit * 16 + prow;
+      if (row < w.rows / 2) {
+        const float g = acc[0], u = acc[kNM - 1];
+        bad = !finitef(g) || !finitef(u);
         o.out[(size_t)r * o.ld + row] = (g / (1.0f + exp_f32(-g))) * u;
       }
     } else {
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int row = unit * 16 + rsub + i;
-        if (!rvalid || row >= w.rows) continue;
-        const float v = acc[0][n][i];
-        bad |= !finitef(v);
+      const int row = unit * 16 + prow;
+      if (row < w.rows) {
+        const float v = acc[0];
+        bad = !finitef(v);
         float *p = o.out + (size_t)r * o.ld + row;
         if (kEpi == kEpiResidual)
           *p = *p + v;
@@ -310,7 +353,30 @@ __global__ __launch_bounds__(256) void k_mv_q8(MatrixView w, ActView act, int ro
           *p = v;
       }
     }
-    if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
+  }
+  if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
+}
+
+// Final argmax over the per-tile partial keys of each batch row.
+__global__ __launch_bounds__(256) void k_argmax_reduce(const unsigned long long *__restrict__ part,
+                                                       int units, unsigned long long *out) {
+  __shared__ unsigned long long red[4];
+  const int r = blockIdx.x;
+  unsigned long long best = 0;
+  for (int u = threadIdx.x; u < units; u += 256) {
+    const unsigned long long k = part[(size_t)r * units + u];
+    best = k > best ? k : best;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const unsigned long long x = __shfl_xor(best, m, kWave);
+    best = x > best ? x : best;
+  }
+  if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < 4; i++) best = red[i] > best ? red[i] : best;
+    out[r] = red[0] > best ? red[0] : best;
   }
 }
 
@@ -408,11 +474,22 @@ __global__ __launch_bounds__(256) void k_qkv_post(StepDims d, const float *__res
 }
 
 // ---------------------------------------------------------------------------
-// Attention (cpu.rs:133-210 attention_rows), split over 128-token chunks.
-// Pass 1: scores s = f32(sum_j f64(q_j*k_j)) * scale for the G query heads
-// sharing a KV head, plus per-chunk maxima.
+// Attention (cpu.rs:133-210 attention_rows), exact form.
+// Operands that are uniform across a wave (the query of a head in pass 1, the
+// normalized score of a token in pass 3) are read with scalar loads and used
+// as SGPR operands, so each (token, head, element) costs the reference's own
+// three operations: f32 product, widening, f64 add.
+//
+// Pass 1 (scores): one thread per cached token; its K row sits in VGPRs; for
+// each query head the dot is summed in f64 in element order (cpu.rs:31-35),
+// two heads interleaved.  s = f32(dot) * scale; per-256-token chunk maxima.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(128) void k_attn_scores(StepDims d, const float *__restrict__ q_rot,
+__device__ __forceinline__ float f4get(const float4 &v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+template <int kD, int kG>
+__global__ __launch_bounds__(256) void k_attn_scores(StepDims d, const float *__restrict__ q_rot,
                                                      const float *__restrict__ kpool,
                                                      const uint32_t *__restrict__ row_pos,
                                                      const uint32_t *__restrict__ row_seq,
@@ -420,106 +497,154 @@ __global__ __launch_bounds__(128) void k_attn_scores(StepDims d, const float *__
                                                      float *__restrict__ scores,
                                                      float *__restrict__ chunk_max,
                                                      uint32_t *row_err) {
+  constexpr int kT = 256;
   const int r = blockIdx.x, g = blockIdx.y, c = blockIdx.z;
   const int kv = (int)row_pos[r] + 1;
-  const int t0 = c * kChunk;
+  const int t0 = c * kT;
   if (t0 >= kv) return;
-  __shared__ float qs[kMaxGroup * 128];
-  __shared__ float red[2];
-  for (int e = threadIdx.x; e < d.G * d.D; e += 128)
-    qs[e] = q_rot[(size_t)r * d.H + (size_t)g * d.G * d.D + e];
-  __syncthreads();
+  __shared__ float wmax[4][kG];
   const int t = t0 + threadIdx.x;
   const bool valid = t < kv;
-  double acc[kMaxGroup];
-#pragma unroll
-  for (int hh = 0; hh < kMaxGroup; hh++) acc[hh] = -0.0;
+  float4 k4[kD / 4];
   if (valid) {
     const int32_t phys = pt[(size_t)row_seq[r] * d.max_pages + t / kPage];
-    const float *krow = kpool + ((size_t)(phys * d.NKV + g) * kPage + t % kPage) * d.D;
-    for (int j = 0; j < d.D; j += 4) {
-      const float4 k4 = *reinterpret_cast<const float4 *>(krow + j);
+    const float4 *krow = reinterpret_cast<const float4 *>(
+        kpool + ((size_t)(phys * d.NKV + g) * kPage + t % kPage) * kD);
 #pragma unroll
-      for (int hh = 0; hh < kMaxGroup; hh++) {
-        if (hh < d.G) {
-          const float *q = qs + hh * d.D + j;
-          acc[hh] += (double)(q[0] * k4.x);
-          acc[hh] += (double)(q[1] * k4.y);
-          acc[hh] += (double)(q[2] * k4.z);
-          acc[hh] += (double)(q[3] * k4.w);
-        }
-      }
+    for (int j = 0; j < kD / 4; j++) k4[j] = krow[j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < kD / 4; j++) k4[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const float *qbase = q_rot + (size_t)r * d.H + (size_t)g * kG * kD;
+  float sc[kG];
+#pragma unroll
+  for (int h0 = 0; h0 < kG; h0 += 2) {
+    const float *q0 = qbase + h0 * kD;
+    const float *q1 = qbase + (h0 + 1 < kG ? h0 + 1 : h0) * kD;
+    double a0 = -0.0, a1 = -0.0;
+#pragma unroll
+    for (int j = 0; j < kD; j++) {
+      const float kj = f4get(k4[j / 4], j % 4);
+      a0 += (double)(q0[j] * kj);
+      if (h0 + 1 < kG) a1 += (double)(q1[j] * kj);
     }
+    sc[h0] = (float)a0 * d.scale;
+    if (h0 + 1 < kG) sc[h0 + 1] = (float)a1 * d.scale;
   }
   bool bad = false;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
 #pragma unroll
-  for (int hh = 0; hh < kMaxGroup; hh++) {
-    if (hh >= d.G) break;
-    const int head = g * d.G + hh;
-    const float s = valid ? (float)acc[hh] * d.scale : -__builtin_inff();
+  for (int hh = 0; hh < kG; hh++) {
+    const int head = g * kG + hh;
     if (valid) {
-      bad |= !finitef(s);
-      scores[((size_t)r * d.NH + head) * d.kv_cap + t] = s;
+      bad |= !finitef(sc[hh]);
+      scores[((size_t)r * d.NH + head) * d.kv_cap + t] = sc[hh];
     }
-    const float m = block_max_f32<128>(s, red);
-    if (threadIdx.x == 0) chunk_max[((size_t)r * d.NH + head) * d.max_chunks + c] = m;
+    const float m = wave_max_f32(valid ? sc[hh] : -__builtin_inff());
+    if (lane == 0) wmax[wave][hh] = m;
+  }
+  __syncthreads();
+  const int nsc = (d.kv_cap + kT - 1) / kT;
+  if (threadIdx.x < kG) {
+    float m = wmax[0][threadIdx.x];
+#pragma unroll
+    for (int w = 1; w < 4; w++) m = fmaxf(m, wmax[w][threadIdx.x]);
+    chunk_max[((size_t)r * d.NH + g * kG + threadIdx.x) * nsc + c] = m;
   }
   if (bad) atomicOr(&row_err[r], kErrNonFinite);
 }
 
-// Pass 2: p = exp(s - max) (f32), denominator in f64, p *= f32(1/den).
-__global__ __launch_bounds__(256) void k_attn_softmax(StepDims d,
-                                                      const uint32_t *__restrict__ row_pos,
-                                                      float *__restrict__ scores,
-                                                      const float *__restrict__ chunk_max) {
+// Pass 2 (softmax): max over the chunk maxima; denominator sum f64(exp(s-max))
+// in a fixed tree; inv = f32(1/den); scores rewritten in place as the
+// reference's normalized weights p = f32(exp(s - max)) * inv.
+__global__ __launch_bounds__(256) void k_attn_stats(StepDims d, const uint32_t *__restrict__ row_pos,
+                                                    float *__restrict__ scores,
+                                                    const float *__restrict__ chunk_max) {
   __shared__ float redf[4];
   __shared__ double redd[4];
   const int r = blockIdx.x, h = blockIdx.y;
-  const int kv = (int)row_pos[r] + 1, nch = (kv + kChunk - 1) / kChunk;
+  const int kv = (int)row_pos[r] + 1, nch = (kv + 255) / 256, nsc = (d.kv_cap + 255) / 256;
   float *s = scores + ((size_t)r * d.NH + h) * d.kv_cap;
   float m = -__builtin_inff();
-  for (int c = threadIdx.x; c < nch; c += 256)
-    m = fmaxf(m, chunk_max[((size_t)r * d.NH + h) * d.max_chunks + c]);
+  for (int c = threadIdx.x; c < nch; c += 256) m = fmaxf(m, chunk_max[((size_t)r * d.NH + h) * nsc + c]);
   m = block_max_f32<256>(m, redf);
   double den = 0.0;
   for (int t = threadIdx.x; t < kv; t += 256) {
-    const float p = exp_f32(s[t] - m);
-    s[t] = p;
-    den += (double)p;
+    const float e = exp_f32(s[t] - m);
+    s[t] = e;
+    den += (double)e;
   }
   den = block_sum_f64<256>(den, redd);
   const float inv = (float)(1.0 / den);
   for (int t = threadIdx.x; t < kv; t += 256) s[t] = s[t] * inv;
 }
 
-// Pass 3: per-chunk f64 partials of sum_t f64(p_t * v_t[j]) in token order.
-__global__ __launch_bounds__(1024) void k_attn_pv(StepDims d, const float *__restrict__ vpool,
-                                                  const uint32_t *__restrict__ row_pos,
-                                                  const uint32_t *__restrict__ row_seq,
-                                                  const int32_t *__restrict__ pt,
-                                                  const float *__restrict__ scores,
-                                                  double *__restrict__ partial) {
+// Pass 3 (values): a block takes 128 tokens of one (row, KV head); wave w
+// takes 32 consecutive tokens, lane = element j.  For each token the V row is
+// one coalesced vector load and the G normalized weights are scalar loads:
+// acc[h] += f64(p_t[h] * v_t[j]) in token order; the 4 waves' sums are
+// combined in a fixed order into the chunk's f64 partial.
+template <int kD, int kG>
+__global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__restrict__ vpool,
+                                                 const uint32_t *__restrict__ row_pos,
+                                                 const uint32_t *__restrict__ row_seq,
+                                                 const int32_t *__restrict__ pt,
+                                                 const float *__restrict__ p,
+                                                 double *__restrict__ partial) {
+  constexpr int kE = (kD + kWave - 1) / kWave;  // elements per lane (lanes >= kD idle when kD < 64)
+  constexpr int kTW = kChunk / 4;  // tokens per wave
   const int r = blockIdx.x, g = blockIdx.y, c = blockIdx.z;
   const int kv = (int)row_pos[r] + 1, t0 = c * kChunk;
   if (t0 >= kv) return;
-  const int t1 = min(t0 + kChunk, kv);
-  __shared__ int32_t slots[kChunk];
-  for (int i = threadIdx.x; i < t1 - t0; i += blockDim.x) {
-    const int t = t0 + i;
-    slots[i] = pt[(size_t)row_seq[r] * d.max_pages + t / kPage] * kPage + t % kPage;
+  __shared__ double red[3][kG][kD];
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int tw0 = t0 + wave * kTW;
+  const int nw = max(0, min(kTW, kv - tw0));
+  const int32_t *ptr = pt + (size_t)row_seq[r] * d.max_pages;
+  const float *prow = p + ((size_t)r * d.NH + (size_t)g * kG) * d.kv_cap;
+  double acc[kG][kE];
+#pragma unroll
+  for (int hh = 0; hh < kG; hh++)
+#pragma unroll
+    for (int e = 0; e < kE; e++) acc[hh][e] = 0.0;
+#pragma unroll 4
+  for (int i = 0; i < nw; i++) {
+    const int t = tw0 + i;
+    const int32_t phys = ptr[t / kPage];
+    const float *vrow = vpool + ((size_t)(phys * d.NKV + g) * kPage + t % kPage) * kD;
+    float v[kE];
+#pragma unroll
+    for (int e = 0; e < kE; e++) v[e] = (lane + e * kWave < kD) ? vrow[lane + e * kWave] : 0.0f;
+#pragma unroll
+    for (int hh = 0; hh < kG; hh++) {
+      const float ph = prow[(size_t)hh * d.kv_cap + t];
+#pragma unroll
+      for (int e = 0; e < kE; e++) acc[hh][e] += (double)(ph * v[e]);
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int hh = 0; hh < kG; hh++)
+#pragma unroll
+      for (int e = 0; e < kE; e++)
+        if (lane + e * kWave < kD) red[wave - 1][hh][lane + e * kWave] = acc[hh][e];
   }
   __syncthreads();
-  const int hh = threadIdx.x / d.D, j = threadIdx.x % d.D;
-  if (hh >= d.G) return;
-  const int head = g * d.G + hh;
-  const float *p = scores + ((size_t)r * d.NH + head) * d.kv_cap;
-  double acc = 0.0;
-  for (int t = t0; t < t1; t++) {
-    const int32_t sl = slots[t - t0];
-    const float v = vpool[((size_t)((sl / kPage) * d.NKV + g) * kPage + sl % kPage) * d.D + j];
-    acc += (double)(p[t] * v);
+  if (wave == 0) {
+#pragma unroll
+    for (int hh = 0; hh < kG; hh++)
+#pragma unroll
+      for (int e = 0; e < kE; e++) {
+        const int j = lane + e * kWave;
+        if (j >= kD) continue;
+        double sum = acc[hh][e];
+#pragma unroll
+        for (int w = 0; w < 3; w++) sum += red[w][hh][j];
+        partial[(((size_t)r * d.NH + g * kG + hh) * d.max_chunks + c) * kD + j] = sum;
+      }
   }
-  partial[(((size_t)r * d.NH + head) * d.max_chunks + c) * d.D + j] = acc;
 }
 
 // Pass 4: chunks combined in order, rounded to f32, and prepared as the
@@ -645,11 +770,11 @@ void launch_quant_act(hipStream_t s, int rows, const float *src, int K, int act_
 template <int kEpi, int kNM>
 static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
                   const MatvecOut &o) {
-  constexpr int kNT = 2;
   const int units = w.mtiles / kNM;
   const int n_tiles = (rows_b + 15) / 16;
-  dim3 grid((units + 3) / 4, (n_tiles + kNT - 1) / kNT);
-  hipLaunchKernelGGL((k_mv_q8<kEpi, kNT, kNM>), grid, dim3(256), 0, s, w, act, rows_b, o);
+  const int groups = (units + 7) / 8;
+  hipLaunchKernelGGL((k_mv_q8s<kEpi, kNM>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
+                     rows_b, n_tiles, o);
 }
 
 template <int kEpi>
@@ -678,6 +803,11 @@ void launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActVi
   }
 }
 
+void launch_argmax_reduce(hipStream_t s, int rows, const unsigned long long *part, int units,
+                          unsigned long long *out) {
+  hipLaunchKernelGGL(k_argmax_reduce, dim3(rows), dim3(256), 0, s, part, units, out);
+}
+
 void launch_qkv_post(hipStream_t s, int rows, const StepDims &d, const float *qkv,
                      const float *bias, const float2 *rope, const uint32_t *row_pos,
                      const int32_t *row_slot, float *q_rot, float *kpool, float *vpool,
@@ -687,26 +817,66 @@ void launch_qkv_post(hipStream_t s, int rows, const StepDims &d, const float *qk
                      row_slot, q_rot, kpool, vpool);
 }
 
-void launch_attn_scores(hipStream_t s, int rows, int chunks, const StepDims &d, const float *q_rot,
+#define COHX_DG_DISPATCH(D, G, LAUNCH)                                                    \
+  do {                                                                                     \
+    switch ((D) * 16 + (G)) {                                                              \
+      case 64 * 16 + 7: LAUNCH(64, 7); break;                                              \
+      case 64 * 16 + 8: LAUNCH(64, 8); break;                                              \
+      case 64 * 16 + 4: LAUNCH(64, 4); break;                                              \
+      case 64 * 16 + 2: LAUNCH(64, 2); break;                                              \
+      case 64 * 16 + 1: LAUNCH(64, 1); break;                                              \
+      case 128 * 16 + 6: LAUNCH(128, 6); break;                                            \
+      case 128 * 16 + 7: LAUNCH(128, 7); break;                                            \
+      case 128 * 16 + 8: LAUNCH(128, 8); break;                                            \
+      case 128 * 16 + 4: LAUNCH(128, 4); break;                                            \
+      case 128 * 16 + 2: LAUNCH(128, 2); break;                                            \
+      case 128 * 16 + 1: LAUNCH(128, 1); break;                                            \
+      case 32 * 16 + 2: LAUNCH(32, 2); break;                                              \
+      case 32 * 16 + 4: LAUNCH(32, 4); break;                                              \
+      case 32 * 16 + 1: LAUNCH(32, 1); break;                                              \
+      default: ok = false;                                                                 \
+    }                                                                                      \
+  } while (0)
+
+bool attention_shape_supported(int D, int G) {
+  bool ok = true;
+#define NOOP(a, b) (void)0
+  COHX_DG_DISPATCH(D, G, NOOP);
+#undef NOOP
+  return ok;
+}
+
+void launch_attn_scores(hipStream_t s, int rows, int max_kv, const StepDims &d, const float *q_rot,
                         const float *kpool, const uint32_t *row_pos, const uint32_t *row_seq,
                         const int32_t *page_table, float *scores, float *chunk_max,
                         uint32_t *row_err) {
-  hipLaunchKernelGGL(k_attn_scores, dim3(rows, d.NKV, chunks), dim3(128), 0, s, d, q_rot, kpool,
-                     row_pos, row_seq, page_table, scores, chunk_max, row_err);
+  const dim3 grid(rows, d.NKV, (max_kv + 255) / 256);
+  bool ok = true;
+#define L(DD, GG)                                                                           \
+  hipLaunchKernelGGL((k_attn_scores<DD, GG>), grid, dim3(256), 0, s, d, q_rot, kpool, row_pos, \
+                     row_seq, page_table, scores, chunk_max, row_err)
+  COHX_DG_DISPATCH(d.D, d.G, L);
+#undef L
+  (void)ok;
 }
 
-void launch_attn_softmax(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
-                         float *scores, const float *chunk_max) {
-  hipLaunchKernelGGL(k_attn_softmax, dim3(rows, d.NH), dim3(256), 0, s, d, row_pos, scores,
+void launch_attn_stats(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
+                       float *scores, const float *chunk_max) {
+  hipLaunchKernelGGL(k_attn_stats, dim3(rows, d.NH), dim3(256), 0, s, d, row_pos, scores,
                      chunk_max);
 }
 
-void launch_attn_pv(hipStream_t s, int rows, int chunks, const StepDims &d, const float *vpool,
+void launch_attn_pv(hipStream_t s, int rows, int max_kv, const StepDims &d, const float *vpool,
                     const uint32_t *row_pos, const uint32_t *row_seq, const int32_t *page_table,
-                    const float *scores, double *partial) {
-  const int threads = ((d.G * d.D + kWave - 1) / kWave) * kWave;
-  hipLaunchKernelGGL(k_attn_pv, dim3(rows, d.NKV, chunks), dim3(threads), 0, s, d, vpool, row_pos,
-                     row_seq, page_table, scores, partial);
+                    const float *probs, double *partial) {
+  const dim3 grid(rows, d.NKV, (max_kv + kChunk - 1) / kChunk);
+  bool ok = true;
+#define L(DD, GG)                                                                          \
+  hipLaunchKernelGGL((k_attn_pv<DD, GG>), grid, dim3(256), 0, s, d, vpool, row_pos, row_seq, \
+                     page_table, probs, partial)
+  COHX_DG_DISPATCH(d.D, d.G, L);
+#undef L
+  (void)ok;
 }
 
 void launch_attn_combine(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
