@@ -87,22 +87,38 @@ __global__ __launch_bounds__(256) void k_embed(MatrixView e, const uint32_t *__r
 }
 
 // ---------------------------------------------------------------------------
-// Q8_0 activation blocks (QuantizedInput::prepare, quant.rs:193-213) for one
-// 32-element block held by 32 consecutive lanes: d = max|x|/127, inv = 1/d
-// (0 when d == 0), stored scale f16(d), q = round-half-away(x*inv) as i8.
-// Writes the B-operand tile layout. Returns true if the block is invalid.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ bool quant_block_q8(float v, bool active, int row, int b, int t, int nbp,
-                                               ActView act) {
-  bool bad = active && !finitef(v);
-  const float amax = half_max_f32(active ? fabsf(v) : 0.0f);
-  const float d = amax / 127.0f;
+// Q8_0 activation blocks (QuantizedInput::prepare, quant.rs:193-213):
+// d = max|x|/127 over the 32-element block, inv = 1/d (0 when d == 0), stored
+// scale f16(d), q = round-half-away(x*inv) as i8, in the B-operand tile layout.
+// One thread quantizes an 8-element group (a quarter of a block); the four groups of a block sit in four consecutive lanes (aligned),
+// combine their maxima with two shuffles, and each writes its 8 quantized
+// values as one 8-byte store into the B-operand tile layout.
+__device__ __forceinline__ bool quant_group_q8(const float (&v)[8], bool active, int row, int kg,
+                                               int nbp, ActView act) {
+  float m = 0.0f;
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    bad |= active && !finitef(v[i]);
+    m = fmaxf(m, active ? fabsf(v[i]) : 0.0f);
+  }
+  m = fmaxf(m, __shfl_xor(m, 1, kWave));
+  m = fmaxf(m, __shfl_xor(m, 2, kWave));
+  const float d = m / 127.0f;
   const float inv = d == 0.0f ? 0.0f : 1.0f / d;
   const uint16_t hd = f2h(d);
   if (active) {
     bad |= !finitef(h2f(hd)) || !finitef(inv);
-    act.qs[q8_byte(row / 16, nbp, b, (t / 8) * 16 + row % 16, t % 8)] = sat_i8(roundf(v * inv));
-    if (t == 0) act.ds[q8_scale(row / 16, nbp, b, row % 16)] = hd;
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      lo |= (uint32_t)(uint8_t)sat_i8(roundf(v[i] * inv)) << (8 * i);
+      hi |= (uint32_t)(uint8_t)sat_i8(roundf(v[i + 4] * inv)) << (8 * i);
+    }
+    const int b = kg / 4, g = kg % 4;
+    *reinterpret_cast<uint2 *>(act.qs + q8_byte(row / 16, nbp, b, g * 16 + row % 16, 0)) =
+        make_uint2(lo, hi);
+    if (g == 0) act.ds[q8_scale(row / 16, nbp, b, row % 16)] = hd;
   }
   return bad;
 }
@@ -134,12 +150,13 @@ __global__ __launch_bounds__(256) void k_norm_act(const float *__restrict__ x,
   __syncthreads();
   bool bad = false;
   if (kAct == 8) {
-    const int hw = threadIdx.x / 32, t = threadIdx.x % 32;
-    for (int base = 0; base < nbp; base += 8) {
-      const int b = base + hw, k = b * 32 + t;
-      const bool active = b < nbp;
-      const float v = (active && k < H) ? y[k] : 0.0f;
-      bad |= quant_block_q8(v, active, ob, b, t, nbp, act);
+    for (int base = 0; base < nbp * 4; base += 256) {
+      const int kg = base + threadIdx.x;
+      const bool active = kg < nbp * 4;
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = (active && kg * 8 + i < H) ? y[kg * 8 + i] : 0.0f;
+      bad |= quant_group_q8(v, active, ob, kg, nbp, act);
     }
   } else {
     for (int k = threadIdx.x; k < H; k += 256) {
@@ -159,12 +176,20 @@ __global__ __launch_bounds__(256) void k_quant_act(const float *__restrict__ src
   const float *s = src + (size_t)r * K;
   bool bad = false;
   if (kAct == 8) {
-    const int hw = threadIdx.x / 32, t = threadIdx.x % 32;
-    for (int base = 0; base < nbp; base += 8) {
-      const int b = base + hw, k = b * 32 + t;
-      const bool active = b < nbp;
-      const float v = (active && k < K) ? s[k] : 0.0f;
-      bad |= quant_block_q8(v, active, r, b, t, nbp, act);
+    for (int base = 0; base < nbp * 4; base += 256) {
+      const int kg = base + threadIdx.x;
+      const bool active = kg < nbp * 4;
+      float v[8];
+      if (active && kg * 8 + 8 <= K) {
+        const float4 a = reinterpret_cast<const float4 *>(s)[kg * 2];
+        const float4 c = reinterpret_cast<const float4 *>(s)[kg * 2 + 1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = (active && kg * 8 + i < K) ? s[kg * 8 + i] : 0.0f;
+      }
+      bad |= quant_group_q8(v, active, r, kg, nbp, act);
     }
   } else {
     for (int k = threadIdx.x; k < K; k += 256) {
@@ -352,6 +377,139 @@ __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int r
         else
           *p = v;
       }
+    }
+  }
+  if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
+}
+
+// ---------------------------------------------------------------------------
+// Wave-chain Q8_0 matvec for short K: one wave owns kNM m-tiles x one n-tile
+// and runs the reference block chain in registers (no LDS, no barriers); the
+// operands of the next kDepth block pairs are in flight in a register ring.
+// A workgroup is the n_tiles waves of one weight tile (A loads shared in L1).
+// ---------------------------------------------------------------------------
+template <int kNM>
+struct Q8Pair {
+  uint4 a[kNM];
+  uint4 b;
+  uint2 dw[kNM][2];  // the lane's 4 output rows, blocks 2p and 2p+1
+  uint32_t da;       // the lane's batch column, blocks 2p (low) and 2p+1 (high)
+};
+
+template <int kNM>
+__device__ __forceinline__ void q8_pair_load(Q8Pair<kNM> &r, const MatrixView &w,
+                                             const ActView &act, int unit, int nt, int pair,
+                                             int lane, int rsub) {
+  const int nbp = w.nbp;
+#pragma unroll
+  for (int m = 0; m < kNM; m++) {
+    r.a[m] = *reinterpret_cast<const uint4 *>(w.qs + q8_byte(unit * kNM + m, nbp, pair * 2, lane, 0));
+    r.dw[m][0] = *reinterpret_cast<const uint2 *>(w.ds + q8_scale(unit * kNM + m, nbp, pair * 2, rsub));
+    r.dw[m][1] = *reinterpret_cast<const uint2 *>(w.ds + q8_scale(unit * kNM + m, nbp, pair * 2 + 1, rsub));
+  }
+  r.b = *reinterpret_cast<const uint4 *>(act.qs + q8_byte(nt, nbp, pair * 2, lane, 0));
+  r.da = (uint32_t)act.ds[q8_scale(nt, nbp, pair * 2, lane % 16)] |
+         ((uint32_t)act.ds[q8_scale(nt, nbp, pair * 2 + 1, lane % 16)] << 16);
+}
+
+template <int kNM>
+__device__ __forceinline__ void q8_pair_chain(const Q8Pair<kNM> &r, float (&acc)[kNM][4]) {
+  const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const long bop = h ? hi64(r.b) : lo64(r.b);
+    const float da = h2f((uint16_t)(h ? (r.da >> 16) : (r.da & 0xffffu)));
+#pragma unroll
+    for (int m = 0; m < kNM; m++) {
+      const v4i sum = __builtin_amdgcn_mfma_i32_16x16x32_i8(h ? hi64(r.a[m]) : lo64(r.a[m]), bop,
+                                                            zero, 0, 0, 0);
+      const uint2 s2 = r.dw[m][h];
+      const float dw[4] = {h2f((uint16_t)(s2.x & 0xffffu)), h2f((uint16_t)(s2.x >> 16)),
+                           h2f((uint16_t)(s2.y & 0xffffu)), h2f((uint16_t)(s2.y >> 16))};
+#pragma unroll
+      for (int i = 0; i < 4; i++) acc[m][i] = fmaf((float)sum[i], dw[i] * da, acc[m][i]);
+    }
+  }
+}
+
+template <int kEpi, int kNM>
+__global__ __launch_bounds__(512) void k_mv_q8w(MatrixView w, ActView act, int rows_b,
+                                                int n_tiles, MatvecOut o) {
+  constexpr int kDepth = 4;
+  const int lane = threadIdx.x % kWave;
+  const int nt = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int unit = blockIdx.x;
+  const int units = w.mtiles / kNM;
+  if (unit >= units || nt >= n_tiles) return;
+  const int npairs = w.nbp / 2, rsub = 4 * (lane / 16);
+  float acc[kNM][4];
+#pragma unroll
+  for (int m = 0; m < kNM; m++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[m][i] = 0.0f;
+  Q8Pair<kNM> ring[kDepth];
+#pragma unroll
+  for (int i = 0; i < kDepth; i++)
+    if (i < npairs) q8_pair_load(ring[i], w, act, unit, nt, i, lane, rsub);
+  for (int p0 = 0; p0 < npairs; p0 += kDepth) {
+#pragma unroll
+    for (int u = 0; u < kDepth; u++) {
+      const int pr = p0 + u;
+      if (pr < npairs) {
+        q8_pair_chain(ring[u], acc);
+        if (pr + kDepth < npairs) q8_pair_load(ring[u], w, act, unit, nt, pr + kDepth, lane, rsub);
+      }
+    }
+  }
+  // ---- epilogue: lane holds rows unit*16 + rsub + i (per m-tile), batch row nt*16 + lane%16
+  const int r = nt * 16 + lane % 16;
+  const bool rvalid = r < rows_b;
+  const int er = (rvalid && o.err_rows) ? (int)o.err_rows[r] : r;
+  bool bad = false;
+  if (kEpi == kEpiArgmax) {
+    float best = 0.0f;
+    int best_row = 0;
+    bool have = false;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = unit * 16 + rsub + i;
+      if (!rvalid || row >= w.rows) continue;
+      const float v = acc[0][i];
+      bad |= !finitef(v);
+      if (o.logits) o.logits[(size_t)r * w.rows + row] = v;
+      if (!have || v > best) {
+        best = v;
+        best_row = row;
+        have = true;
+      }
+    }
+    unsigned long long key = have ? argmax_key(best, best_row) : 0ull;
+    unsigned long long x = __shfl_xor(key, 16, kWave);
+    key = x > key ? x : key;
+    x = __shfl_xor(key, 32, kWave);
+    key = x > key ? x : key;
+    if (lane < 16 && rvalid) o.argmax[(size_t)r * units + unit] = key;
+  } else if (kEpi == kEpiSwiglu) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = unit * 16 + rsub + i;
+      if (!rvalid || row >= w.rows / 2) continue;
+      const float g = acc[0][i], u = acc[kNM - 1][i];
+      bad |= !finitef(g) || !finitef(u);
+      o.out[(size_t)r * o.ld + row] = (g / (1.0f + exp_f32(-g))) * u;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = unit * 16 + rsub + i;
+      if (!rvalid || row >= w.rows) continue;
+      const float v = acc[0][i];
+      bad |= !finitef(v);
+      float *q = o.out + (size_t)r * o.ld + row;
+      if (kEpi == kEpiResidual)
+        *q = *q + v;
+      else
+        *q = v;
     }
   }
   if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
@@ -654,6 +812,7 @@ __global__ __launch_bounds__(128) void k_attn_combine(StepDims d,
                                                       const uint32_t *__restrict__ row_pos,
                                                       const double *__restrict__ partial, int nbp,
                                                       ActView act, uint32_t *row_err) {
+  __shared__ float o_s[128];
   const int r = blockIdx.x, h = blockIdx.y, j = threadIdx.x;
   const int kv = (int)row_pos[r] + 1, nch = (kv + kChunk - 1) / kChunk;
   const double *pp = partial + ((size_t)r * d.NH + h) * d.max_chunks * d.D;
@@ -664,14 +823,20 @@ __global__ __launch_bounds__(128) void k_attn_combine(StepDims d,
     for (int c = 1; c < nch; c++) acc += pp[(size_t)c * d.D + j];
   }
   const float o = (float)acc;
-  const int e = h * d.D + j;
   bool bad = active && !finitef(o);
   if (kAct == 8) {
-    bad |= quant_block_q8(o, active, r, e / 32, e % 32, nbp, act);
+    if (active) o_s[j] = o;
+    __syncthreads();
+    // D/8 groups of this head: group kg of the row is h*D/8 + j
+    const int ng = d.D / 8;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = j < ng ? o_s[j * 8 + i] : 0.0f;
+    if (j < ((ng + 3) & ~3)) bad |= quant_group_q8(v, j < ng, r, h * ng + j, nbp, act);
   } else if (active) {
     const uint16_t hv = f2h(o);
     bad |= !finitef(h2f(hv));
-    act.f16[(size_t)r * d.H + e] = hv;
+    act.f16[(size_t)r * d.H + h * d.D + j] = hv;
   }
   if (bad) atomicOr(&row_err[r], kErrNonFinite);
 }
@@ -772,9 +937,16 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
                   const MatvecOut &o) {
   const int units = w.mtiles / kNM;
   const int n_tiles = (rows_b + 15) / 16;
-  const int groups = (units + 7) / 8;
-  hipLaunchKernelGGL((k_mv_q8s<kEpi, kNM>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
-                     rows_b, n_tiles, o);
+  if (kEpi == kEpiArgmax && w.nbp <= 64 && n_tiles <= 8) {
+    // the head: many weight tiles, short K — one wave per output tile, the
+    // n-tiles of a weight tile in one workgroup
+    hipLaunchKernelGGL((k_mv_q8w<kEpi, kNM>), dim3(units), dim3(64 * n_tiles), 0, s, w, act,
+                       rows_b, n_tiles, o);
+  } else {
+    const int groups = (units + 7) / 8;
+    hipLaunchKernelGGL((k_mv_q8s<kEpi, kNM>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w,
+                       act, rows_b, n_tiles, o);
+  }
 }
 
 template <int kEpi>
