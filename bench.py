@@ -32,6 +32,21 @@ import synth  # noqa: E402
 METRIC = "batched decode tok/s, Qwen2.5-0.5B Q8_0 @32 & 128 ragged seqs; % of HBM peak"
 HBM_PEAK = 8.0e12
 KV_LO, KV_HI = 64, 2048
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on
+# this workload, scaled by the same counters on a copy of known size
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_decode128.json")
+# profiler category -> the kernel instance it times at the Qwen2.5-0.5B shape
+# (o and down share one instance and grid, so counters cannot tell them apart)
+CATEGORY_KERNEL = {"attn_scores": "k_attn_scores<64, 7>", "attn_softmax_stats": "k_attn_exp<7>",
+                   "attn_pv": "k_attn_pv<64, 7>", "attn_combine_act": "k_attn_combine<8>",
+                   "matvec_gate_up_swiglu": "k_mv_q8s<2, 2>", "matvec_head_argmax": "k_mv_q8w<3, 1>"}
+PMC_CMD = ("rocprofv3 --pmc {counter} --kernel-include-regex \"k_attn|k_mv\" --output-format csv "
+           "-d <dir> -o <name> -- python3 bench.py --steps 2 --warmup 1 --secondary-lanes 0 "
+           "--no-cpu-baseline")
+COPY_CMD = ("rocprofv3 --pmc {counter} --output-format csv -d <dir> -o <name> -- "
+            "python3 bench.py --copy-probe")
+TRACE_CMD = ("rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o <name> -- "
+             "python3 bench.py")
 
 
 def log(*a):
@@ -62,7 +77,11 @@ def step_bytes(cfg, kv_lens, matrix_bytes):
             + n * H // 32 * 34 + vectors)
 
 
-def run_workload(model, cfg, lanes, steps, warmup, seed, profile_steps):
+def run_workload(model, cfg, lanes, steps, warmup, seed):
+    """Warm up, time `steps` plain steps (the throughput figure), then rewind
+    every sequence to where the timed region began and replay the same steps
+    with per-kernel timing events (identical work: greedy decode is
+    deterministic, which the replay checks)."""
     rng = np.random.default_rng(seed + lanes)
     kv = [int(v) for v in rng.integers(KV_LO, KV_HI + 1, lanes)]
     tokens = [int(v) for v in rng.integers(0, cfg["vocabulary"], lanes)]
@@ -73,44 +92,73 @@ def run_workload(model, cfg, lanes, steps, warmup, seed, profile_steps):
         seqs.append(s)
     first = None
 
-    def one_step():
-        nonlocal tokens, first
-        res = model.step([dict(seq=s, tokens=[t]) for s, t in zip(seqs, tokens)])
+    def one_step(toks):
+        res = model.step([dict(seq=s, tokens=[t]) for s, t in zip(seqs, toks)])
         if any(r["status"] for r in res):
             raise RuntimeError(f"lane failure {[r['status'] for r in res]}")
-        if first is None:
-            first = [r["argmax"] for r in res]
-        tokens = [r["argmax"] for r in res]
+        return [r["argmax"] for r in res]
 
     start_tokens = list(tokens)
     for _ in range(warmup):
-        one_step()
+        tokens = one_step(tokens)
+        if first is None:
+            first = list(tokens)
+    if first is None:
+        first = one_step(tokens)
+        tokens = first
     kv_at_timing = [model.seq_length(s) for s in seqs]
+    timed_tokens = list(tokens)
+    trace = []
     t0 = time.perf_counter()
     for _ in range(steps):
-        one_step()
+        tokens = one_step(tokens)
+        trace.append(tokens)
     elapsed = time.perf_counter() - t0
-    # per-kernel profile over a few more steps (events add overhead, so not timed above)
+    # replay of the timed region with dispatch-packet timing events
+    for s, n in zip(seqs, kv_at_timing):
+        model.seq_truncate(s, n)
+    tokens = timed_tokens
     model.profile(True)
-    for _ in range(profile_steps):
-        one_step()
+    replay_equal = True
+    tp = time.perf_counter()
+    for i in range(steps):
+        tokens = one_step(tokens)
+        replay_equal &= tokens == trace[i]
+    prof_elapsed = time.perf_counter() - tp
     stats = model.profile_read()
     model.profile(False)
+    log(f"[bench] {lanes} lanes: replay with timing events {prof_elapsed * 1e3 / steps:.3f} ms/step, "
+        f"same tokens: {replay_equal}")
     mean_kv = [k + (steps - 1) / 2.0 for k in kv_at_timing]
     sb = step_bytes(cfg, mean_kv, model.matrix_bytes)
     for s in seqs:
         model.seq_free(s)
     return dict(kv=kv, start_tokens=start_tokens, first_argmax=first, elapsed=elapsed,
                 stats=stats, step_bytes=sb, tok_s=lanes * steps / elapsed,
-                ms_per_step=elapsed * 1e3 / steps)
+                ms_per_step=elapsed * 1e3 / steps, replay_equal=replay_equal,
+                replay_ms_per_step=prof_elapsed * 1e3 / steps)
 
 
-def roofline(stats):
+def measured_traffic(category, lanes):
+    """HBM bytes per launch of `category`'s kernel from the committed counter
+    summary, or None when it does not cover this kernel and workload."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k = t.get("kernels", {}).get(CATEGORY_KERNEL.get(category, ""))
+    if not k or t.get("lanes") != lanes:
+        return None
+    return k["hbm_bytes_per_launch"]
+
+
+def roofline(stats, lanes):
     top = max(stats, key=lambda s: s["total_ms"])
     avg_s = top["total_ms"] / 1e3 / top["launches"]
     achieved = top["bytes"] / top["launches"] / avg_s
     return {"kernel": top["name"], "bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
-            "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": None,
+            "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": measured_traffic(top["name"], lanes),
             "avg_launch_us": avg_s * 1e6, "bytes_per_launch": top["bytes"] / top["launches"],
             "share_of_step": top["total_ms"] / sum(s["total_ms"] for s in stats)}
 
@@ -137,6 +185,99 @@ def cpu_baseline(cfg, tensors, kv, start_tokens, seed, lanes, steps, threads):
     return first, lanes * steps / elapsed, elapsed
 
 
+def kernel_instance(name):
+    import re
+    m = re.search(r"cohx::(k_\w+)(<[^>]*>)?", name)
+    return m.group(1) + (m.group(2) or "") if m else name
+
+
+def counter_means(path):
+    """{kernel instance: mean counter value (KiB) per dispatch} of a
+    rocprofv3 --pmc counter_collection.csv."""
+    import csv
+    acc = {}
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            k = kernel_instance(row["Kernel_Name"])
+            v = acc.setdefault(k, [0.0, 0])
+            v[0] += float(row["Counter_Value"])
+            v[1] += 1
+    return {k: (v[0] / v[1], v[1]) for k, v in acc.items()}
+
+
+def summarize_counters(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, lanes):
+    """Scale FETCH_SIZE / WRITE_SIZE (KiB per dispatch) to bytes with the same
+    counters read over a device copy of 1 GiB; write the traffic summary."""
+    copy_bytes = float(1 << 30)
+    cf = counter_means(copy_fetch_csv)["__amd_rocclr_copyBuffer"][0] * 1024
+    cw = counter_means(copy_write_csv)["__amd_rocclr_copyBuffer"][0] * 1024
+    ff, fw = copy_bytes / cf, copy_bytes / cw
+    fetch, write = counter_means(fetch_csv), counter_means(write_csv)
+    kernels = {}
+    for k, (fk, n) in sorted(fetch.items()):
+        wk = write.get(k, (0.0, 0))[0]
+        kernels[k] = {"dispatches": n, "fetch_kib": fk, "write_kib": wk,
+                      "hbm_bytes_per_launch": fk * 1024 * ff + wk * 1024 * fw}
+    out = {"workload": "Qwen2.5-0.5B-shape Q8_0 decode, 128 ragged lanes, KV U[64,2048] f32",
+           "lanes": lanes,
+           "calibration": {"copy_bytes": copy_bytes, "fetch_counter_bytes": cf,
+                           "write_counter_bytes": cw, "fetch_factor": ff, "write_factor": fw},
+           "commands": {"fetch": PMC_CMD.format(counter="FETCH_SIZE"),
+                        "write": PMC_CMD.format(counter="WRITE_SIZE"),
+                        "copy_fetch": COPY_CMD.format(counter="FETCH_SIZE"),
+                        "copy_write": COPY_CMD.format(counter="WRITE_SIZE")},
+           "kernels": kernels}
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out, indent=1))
+
+
+def summarize_trace(trace_csv, bench_json):
+    """Markdown summary of a rocprofv3 --kernel-trace run of the default bench
+    command: per kernel instance and grid width (which tells the 32- and
+    128-lane workloads apart) the dispatch count and mean duration, next to
+    the dispatch-event means of a plain run of the same command on the same
+    machine (under the tracer those events also time the tracer's work)."""
+    import csv
+    groups = {}
+    with open(trace_csv) as f:
+        for row in csv.DictReader(f):
+            k = (kernel_instance(row["Kernel_Name"]), int(row["Grid_Size_X"]))
+            g = groups.setdefault(k, [])
+            g.append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+    with open(bench_json) as f:
+        line = json.loads(f.read().strip().splitlines()[-1])
+    print(f"Command: `{TRACE_CMD}`\n")
+    print(f"Plain run of the same command: {line['value']:.0f} tok/s, {line['ms_per_step']:.3f} ms/step; "
+          f"dominant kernel {line['roofline']['kernel']} {line['roofline']['avg_launch_us']:.2f} us "
+          f"per launch (dispatch events over the replayed timed region).\n")
+    print("Plain-run dispatch-event means, 128 lanes (us per launch):\n")
+    for name, v in line["kernels"].items():
+        print(f"- {name}: {v['ms_per_step'] * 1e3 / v['launches_per_step']:.2f}")
+    print("\n| kernel | grid x | dispatches | mean us | min us | max us | total ms |")
+    print("|---|---:|---:|---:|---:|---:|---:|")
+    for (name, gx), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        if sum(d) < 1000:
+            continue
+        print(f"| {name} | {gx} | {len(d)} | {sum(d) / len(d):.2f} | {min(d):.2f} | {max(d):.2f} | "
+              f"{sum(d) / 1e3:.2f} |")
+
+
+def copy_probe():
+    """A plain device copy of known size, for scaling the FETCH_SIZE and
+    WRITE_SIZE counters to bytes (the tensors are plumbing, not the product)."""
+    import torch
+    n = 1 << 28  # 2^28 floats = 1 GiB
+    src = torch.empty(n, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": n * 4, "copy_probe_bytes_written": n * 4, "copies": 4}),
+          flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -145,10 +286,24 @@ def main():
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--lanes", type=int, default=128)
     ap.add_argument("--secondary-lanes", type=int, default=32)
-    ap.add_argument("--profile-steps", type=int, default=8)
-    ap.add_argument("--cpu-steps", type=int, default=2)
+    ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only copy 1 GiB device-to-device 4 times (counter calibration)")
+    ap.add_argument("--summarize-counters", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
+                    help="write the traffic summary from rocprofv3 --pmc csv files (no GPU)")
+    ap.add_argument("--summarize-trace", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_JSON"),
+                    help="print a markdown summary of a rocprofv3 --kernel-trace run (no GPU)")
     args = ap.parse_args()
+    if args.copy_probe:
+        copy_probe()
+        return
+    if args.summarize_counters:
+        summarize_counters(*args.summarize_counters, lanes=args.lanes)
+        return
+    if args.summarize_trace:
+        summarize_trace(*args.summarize_trace)
+        return
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
               "(the step shards by sequence with no collectives; see DESIGN.md)", file=sys.stderr)
@@ -156,15 +311,14 @@ def main():
     path = model_file(args.seed)
     meta, tensors = gguf.read(path)
     cfg = gguf.qwen2_config(meta)
-    ctx_len = KV_HI + args.warmup + args.steps + args.profile_steps + 16
+    ctx_len = KV_HI + args.warmup + args.steps + 16
     log(f"[bench] uploading model (max_lanes={args.lanes}, max_context={ctx_len})")
     model = cohx.Model(cfg, tensors, max_lanes=args.lanes, max_rows=args.lanes,
                        max_seqs=args.lanes, max_context=ctx_len)
     results = {}
-    for lanes in (args.secondary_lanes, args.lanes):
+    for lanes in ([args.secondary_lanes] if args.secondary_lanes else []) + [args.lanes]:
         log(f"[bench] {lanes} lanes: warmup {args.warmup}, timed {args.steps}")
-        results[lanes] = run_workload(model, cfg, lanes, args.steps, args.warmup, args.seed,
-                                      args.profile_steps)
+        results[lanes] = run_workload(model, cfg, lanes, args.steps, args.warmup, args.seed)
         log(f"[bench] {lanes} lanes: {results[lanes]['tok_s']:.0f} tok/s, "
             f"{results[lanes]['ms_per_step']:.3f} ms/step")
     main_r = results[args.lanes]
@@ -178,22 +332,25 @@ def main():
                                f"KV U[{KV_LO},{KV_HI}] f32, 1 token/lane/step",
                    "lanes": args.lanes, "kv_range": [KV_LO, KV_HI], "kv_dtype": "f32",
                    "seed": args.seed},
-        "roofline": roofline(main_r["stats"]),
+        "roofline": roofline(main_r["stats"], args.lanes),
         "step_roofline": {"bound": "hbm", "bytes_per_step": main_r["step_bytes"],
                           "achieved": main_r["step_bytes"] / (main_r["ms_per_step"] / 1e3) / 1e9,
                           "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                           "frac": main_r["step_bytes"] / (main_r["ms_per_step"] / 1e3) / HBM_PEAK},
-        "kernels": {s["name"]: {"ms_per_step": s["total_ms"] / args.profile_steps,
-                                "launches_per_step": s["launches"] / args.profile_steps,
+        "timing_replay": {"ms_per_step": main_r["replay_ms_per_step"], "same_tokens": main_r["replay_equal"],
+                          "note": "timed steps replayed from the same KV lengths with per-kernel "
+                                  "dispatch-packet events; roofline and kernels come from it"},
+        "kernels": {s["name"]: {"ms_per_step": s["total_ms"] / args.steps,
+                                "launches_per_step": s["launches"] / args.steps,
                                 "GB_s": (s["bytes"] / (s["total_ms"] / 1e3) / 1e9) if s["total_ms"] else 0}
                     for s in main_r["stats"] if s["launches"]},
     }
-    sec = results[args.secondary_lanes]
-    line["secondary"] = {
+    sec = results.get(args.secondary_lanes)
+    line["secondary"] = None if sec is None else {
         "lanes": args.secondary_lanes, "value": sec["tok_s"], "unit": "tok/s",
         "ms_per_step": sec["ms_per_step"],
         "step_frac": sec["step_bytes"] / (sec["ms_per_step"] / 1e3) / HBM_PEAK,
-        "roofline": roofline(sec["stats"])}
+        "roofline": roofline(sec["stats"], args.secondary_lanes)}
     if not args.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)
         n_cpu = min(16, args.lanes)

@@ -253,8 +253,9 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   if (!rc) rc = dalloc(ctx, &w.act_qs, rtiles * ctx->nbp_max * 512);
   if (!rc) rc = dalloc(ctx, &w.act_ds, rtiles * ctx->nbp_max * 16);
   if (!rc) rc = dalloc(ctx, &w.act_f16, (size_t)R * std::max(H, F));
-  if (!rc) rc = dalloc(ctx, &w.scores, (size_t)R * NH * d->max_context);
+  if (!rc) rc = dalloc(ctx, &w.scores, (size_t)R * NKV * d->max_context * 8);
   if (!rc) rc = dalloc(ctx, &w.chunk_max, (size_t)R * NH * ((d->max_context + 255) / 256));
+  if (!rc) rc = dalloc(ctx, &w.den_part, (size_t)R * NH * ((d->max_context + 255) / 256));
   if (!rc) rc = dalloc(ctx, &w.partial, (size_t)R * NH * ctx->max_chunks * D);
   if (!rc) rc = dalloc(ctx, &w.logits, (size_t)NL * V);
   if (!rc) rc = dalloc(ctx, &w.argmax, NL);
@@ -684,13 +685,15 @@ int prof_begin(cohx_ctx *ctx, int cat, double bytes, double flops) {
   }
   Profiler::Launch l{cat, bytes, flops, p.pool[p.next], p.pool[p.next + 1]};
   p.next += 2;
-  if (hipEventRecord(l.a, ctx->stream) != hipSuccess) return -1;
+  // the category's first kernel records a at its start, every kernel records b at its end
+  set_launch_events(l.a, l.b);
   p.pending.push_back(l);
   return (int)p.pending.size() - 1;
 }
 
 void prof_end(cohx_ctx *ctx, int idx) {
-  if (idx >= 0) (void)hipEventRecord(ctx->prof.pending[idx].b, ctx->stream);
+  (void)ctx;
+  if (idx >= 0) set_launch_events(nullptr, nullptr);
 }
 
 // After the stream has synchronized.
@@ -808,11 +811,11 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
                        ctx->page_table, w.scores, w.chunk_max, w.row_err);
     prof_end(ctx, e);
     e = prof_begin(ctx, kCatAttnSoftmax, b_softmax, 0);
-    launch_attn_stats(s, R, sd, w.row_pos, w.scores, w.chunk_max);
+    launch_attn_exp(s, R, (int)p.max_kv, sd, w.row_pos, w.scores, w.chunk_max, w.den_part);
     prof_end(ctx, e);
     e = prof_begin(ctx, kCatAttnPv, b_pv, f_attn);
     launch_attn_pv(s, R, (int)p.max_kv, sd, vp, w.row_pos, w.row_seq, ctx->page_table, w.scores,
-                   w.partial);
+                   w.den_part, w.partial);
     prof_end(ctx, e);
     e = prof_begin(ctx, kCatAttnCombine, b_combine, 0);
     launch_attn_combine(s, R, sd, w.row_pos, w.partial, act_dtype, ctx->nbp_h, act, w.row_err);

@@ -38,8 +38,10 @@ struct Workspace {
   float *x = nullptr, *qkv = nullptr, *q_rot = nullptr, *h = nullptr;
   int8_t *act_qs = nullptr;
   uint16_t *act_ds = nullptr, *act_f16 = nullptr;
-  float *scores = nullptr, *chunk_max = nullptr, *logits = nullptr;
+  float *scores = nullptr;  // [rows][kv_heads][max_context][8]: scores, then weights
+  float *chunk_max = nullptr, *logits = nullptr;
   double *partial = nullptr;
+  double *den_part = nullptr;  // [rows][heads][256-token chunks] softmax denominator partials
   unsigned long long *argmax = nullptr;
   unsigned long long *argmax_part = nullptr;  // [max_lanes][head m-tiles]
   // pinned host staging

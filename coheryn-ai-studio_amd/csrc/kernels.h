@@ -57,6 +57,9 @@ void launch_norm_act(hipStream_t s, int rows, const float *x, const uint32_t *in
                      uint32_t *row_err);
 void launch_quant_act(hipStream_t s, int rows, const float *src, int K, int act_dtype, int nbp,
                       ActView act, uint32_t *row_err);
+// Timing events for the next launches (see the launch helper); both null ends it.
+void set_launch_events(hipEvent_t start, hipEvent_t stop);
+
 void launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActView &act,
                    int rows_b, const MatvecOut &o);
 void launch_argmax_reduce(hipStream_t s, int rows, const unsigned long long *part, int units,
@@ -71,12 +74,14 @@ void launch_attn_scores(hipStream_t s, int rows, int max_kv, const StepDims &d, 
                         const float *kpool, const uint32_t *row_pos, const uint32_t *row_seq,
                         const int32_t *page_table, float *scores, float *chunk_max,
                         uint32_t *row_err);
-// Rewrites scores in place as normalized weights.
-void launch_attn_stats(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
-                       float *scores, const float *chunk_max);
+// Scores [row][kv_head][t][8] replaced in place by e = exp(s - max); the f64
+// sums of e per 256-token chunk into den_part[row][head][chunk].
+void launch_attn_exp(hipStream_t s, int rows, int max_kv, const StepDims &d,
+                     const uint32_t *row_pos, float *scores, const float *chunk_max,
+                     double *den_part);
 void launch_attn_pv(hipStream_t s, int rows, int max_kv, const StepDims &d, const float *vpool,
                     const uint32_t *row_pos, const uint32_t *row_seq, const int32_t *page_table,
-                    const float *probs, double *partial);
+                    const float *escores, const double *den_part, double *partial);
 void launch_attn_combine(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
                          const double *partial, int act_dtype, int nbp, ActView act,
                          uint32_t *row_err);

@@ -11,12 +11,38 @@
 //    fixed tree / chunk order; they equal the sequential sum whenever no
 //    partial sum rounds, and otherwise differ below 2^-52 relative before the
 //    final rounding to f32.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include "device.h"
 #include "kernels.h"
 
 namespace cohx {
+
+// ---------------------------------------------------------------------------
+// Launch helper.  While timing events are set, the next launch carries the
+// start event in its own dispatch packet and every launch carries the stop
+// event, so the interval is the kernels' execution (the same quantity
+// rocprofv3's kernel trace reports) rather than marker-to-marker time.
+// ---------------------------------------------------------------------------
+namespace {
+thread_local hipEvent_t t_ev_start = nullptr, t_ev_stop = nullptr;
+
+template <typename F, typename... Args>
+void launch_k(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args... args) {
+  if (t_ev_start || t_ev_stop) {
+    hipExtLaunchKernelGGL(kernel, grid, block, shm, s, t_ev_start, t_ev_stop, 0u, args...);
+    t_ev_start = nullptr;
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, shm, s, args...);
+  }
+}
+}  // namespace
+
+void set_launch_events(hipEvent_t start, hipEvent_t stop) {
+  t_ev_start = start;
+  t_ev_stop = stop;
+}
 
 // ---------------------------------------------------------------------------
 // Packer: cu_seqlens (exclusive scan of lane token counts), per-row position,
@@ -640,7 +666,9 @@ __global__ __launch_bounds__(256) void k_qkv_post(StepDims d, const float *__res
 //
 // Pass 1 (scores): one thread per cached token; its K row sits in VGPRs; for
 // each query head the dot is summed in f64 in element order (cpu.rs:31-35),
-// two heads interleaved.  s = f32(dot) * scale; per-256-token chunk maxima.
+// two heads interleaved.  s = f32(dot) * scale, stored per token as 8 floats
+// (scores[row][kv_head][t][8], slot = q head within the group, unused slots 0);
+// per-256-token chunk maxima per head.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float f4get(const float4 &v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
@@ -692,13 +720,19 @@ __global__ __launch_bounds__(256) void k_attn_scores(StepDims d, const float *__
   }
   bool bad = false;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  if (valid) {
+    float o8[8];
+#pragma unroll
+    for (int hh = 0; hh < 8; hh++) {
+      o8[hh] = hh < kG ? sc[hh] : 0.0f;
+      if (hh < kG) bad |= !finitef(sc[hh]);
+    }
+    float4 *dst = reinterpret_cast<float4 *>(scores + (((size_t)r * d.NKV + g) * d.kv_cap + t) * 8);
+    dst[0] = make_float4(o8[0], o8[1], o8[2], o8[3]);
+    dst[1] = make_float4(o8[4], o8[5], o8[6], o8[7]);
+  }
 #pragma unroll
   for (int hh = 0; hh < kG; hh++) {
-    const int head = g * kG + hh;
-    if (valid) {
-      bad |= !finitef(sc[hh]);
-      scores[((size_t)r * d.NH + head) * d.kv_cap + t] = sc[hh];
-    }
     const float m = wave_max_f32(valid ? sc[hh] : -__builtin_inff());
     if (lane == 0) wmax[wave][hh] = m;
   }
@@ -713,34 +747,72 @@ __global__ __launch_bounds__(256) void k_attn_scores(StepDims d, const float *__
   if (bad) atomicOr(&row_err[r], kErrNonFinite);
 }
 
-// Pass 2 (softmax): max over the chunk maxima; denominator sum f64(exp(s-max))
-// in a fixed tree; inv = f32(1/den); scores rewritten in place as the
-// reference's normalized weights p = f32(exp(s - max)) * inv.
-__global__ __launch_bounds__(256) void k_attn_stats(StepDims d, const uint32_t *__restrict__ row_pos,
-                                                    float *__restrict__ scores,
-                                                    const float *__restrict__ chunk_max) {
-  __shared__ float redf[4];
-  __shared__ double redd[4];
-  const int r = blockIdx.x, h = blockIdx.y;
-  const int kv = (int)row_pos[r] + 1, nch = (kv + 255) / 256, nsc = (d.kv_cap + 255) / 256;
-  float *s = scores + ((size_t)r * d.NH + h) * d.kv_cap;
-  float m = -__builtin_inff();
-  for (int c = threadIdx.x; c < nch; c += 256) m = fmaxf(m, chunk_max[((size_t)r * d.NH + h) * nsc + c]);
-  m = block_max_f32<256>(m, redf);
-  double den = 0.0;
-  for (int t = threadIdx.x; t < kv; t += 256) {
-    const float e = exp_f32(s[t] - m);
-    s[t] = e;
-    den += (double)e;
+// Pass 2 (exponentials), one block per (row, KV head, 256-token chunk); a
+// thread owns one head slot (tid % 8) of tokens tid/8 + 32k, k < 8, so the
+// scores are read and written as consecutive floats.  M = max over the
+// row's chunk maxima; e = f32(exp(s - M)) replaces s in place; the chunk's
+// f64 sum of e per head (token order within a thread, then a fixed tree)
+// goes to den_part[row][head][chunk].
+template <int kG>
+__global__ __launch_bounds__(256) void k_attn_exp(StepDims d, const uint32_t *__restrict__ row_pos,
+                                                  float *__restrict__ scores,
+                                                  const float *__restrict__ chunk_max,
+                                                  double *__restrict__ den_part) {
+  constexpr int kT = 256, kW = kT / kWave, kK = kT / 32;
+  __shared__ float redf[kW][8];
+  __shared__ double redd[kW][8];
+  const int r = blockIdx.x, g = blockIdx.y, c = blockIdx.z;
+  const int kv = (int)row_pos[r] + 1, t0 = c * kT;
+  if (t0 >= kv) return;
+  const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+  const int slot = threadIdx.x % 8, tok = threadIdx.x / 8;
+  const int nch = (kv + kT - 1) / kT, nsc = (d.kv_cap + kT - 1) / kT;
+  const bool live = slot < kG;
+  float *base = scores + (((size_t)r * d.NKV + g) * d.kv_cap + t0) * 8 + threadIdx.x;
+  float sv[kK];
+#pragma unroll
+  for (int k = 0; k < kK; k++) {
+    const int t = t0 + tok + 32 * k;
+    sv[k] = (t < kv && live) ? base[k * kT] : 0.0f;
   }
-  den = block_sum_f64<256>(den, redd);
-  const float inv = (float)(1.0 / den);
-  for (int t = threadIdx.x; t < kv; t += 256) s[t] = s[t] * inv;
+  float m = -__builtin_inff();
+  if (live) {
+    const float *cm = chunk_max + ((size_t)r * d.NH + g * kG + slot) * nsc;
+    for (int i = tok; i < nch; i += 32) m = fmaxf(m, cm[i]);
+  }
+  m = fmaxf(m, __shfl_xor(m, 8, kWave));
+  m = fmaxf(m, __shfl_xor(m, 16, kWave));
+  m = fmaxf(m, __shfl_xor(m, 32, kWave));
+  if (lane < 8) redf[w][lane] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(redf[0][slot], redf[1][slot]), fmaxf(redf[2][slot], redf[3][slot]));
+  double den = 0.0;
+#pragma unroll
+  for (int k = 0; k < kK; k++) {
+    const int t = t0 + tok + 32 * k;
+    if (t < kv && live) {
+      const float e = exp_f32(sv[k] - m);
+      base[k * kT] = e;
+      den += (double)e;
+    }
+  }
+  den += __shfl_xor(den, 8, kWave);
+  den += __shfl_xor(den, 16, kWave);
+  den += __shfl_xor(den, 32, kWave);
+  if (lane < 8) redd[w][lane] = den;
+  __syncthreads();
+  if (threadIdx.x < kG) {
+    const double total = ((redd[0][threadIdx.x] + redd[1][threadIdx.x]) + redd[2][threadIdx.x]) +
+                         redd[3][threadIdx.x];
+    den_part[((size_t)r * d.NH + g * kG + threadIdx.x) * nsc + c] = total;
+  }
 }
 
-// Pass 3 (values): a block takes 128 tokens of one (row, KV head); wave w
-// takes 32 consecutive tokens, lane = element j.  For each token the V row is
-// one coalesced vector load and the G normalized weights are scalar loads:
+// Pass 3 (values).  Prologue: den = the row's chunk partials summed in a
+// fixed order (lane-strided, then butterfly), inv = f32(1/den), and the
+// block's 128 tokens of weights p = e * inv (cpu.rs:196-201) staged in LDS.
+// Then wave w takes pages 2w and 2w+1 of the block's 128 tokens (16 tokens
+// each), lane = element j: one base address per page, one V load per token,
 // acc[h] += f64(p_t[h] * v_t[j]) in token order; the 4 waves' sums are
 // combined in a fixed order into the chunk's f64 partial.
 template <int kD, int kG>
@@ -748,38 +820,83 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
                                                  const uint32_t *__restrict__ row_pos,
                                                  const uint32_t *__restrict__ row_seq,
                                                  const int32_t *__restrict__ pt,
-                                                 const float *__restrict__ p,
+                                                 const float *__restrict__ escores,
+                                                 const double *__restrict__ den_part,
                                                  double *__restrict__ partial) {
   constexpr int kE = (kD + kWave - 1) / kWave;  // elements per lane (lanes >= kD idle when kD < 64)
-  constexpr int kTW = kChunk / 4;  // tokens per wave
+  static_assert(kChunk * 2 == 256, "one float4 of weights per thread");
   const int r = blockIdx.x, g = blockIdx.y, c = blockIdx.z;
   const int kv = (int)row_pos[r] + 1, t0 = c * kChunk;
   if (t0 >= kv) return;
   __shared__ double red[3][kG][kD];
+  __shared__ float s_inv[8];
+  __shared__ float4 s_p[kChunk * 2];
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int tw0 = t0 + wave * kTW;
-  const int nw = max(0, min(kTW, kv - tw0));
+  const int nch = (kv + 255) / 256, nsc = (d.kv_cap + 255) / 256;
+  for (int hh = wave; hh < kG; hh += 4) {
+    const double *dp = den_part + ((size_t)r * d.NH + g * kG + hh) * nsc;
+    double v = 0.0;
+    for (int i = lane; i < nch; i += kWave) v += dp[i];
+    v = wave_sum_f64(v);
+    if (lane == 0) s_inv[hh] = (float)(1.0 / v);
+  }
+  __syncthreads();
+  {
+    const int t = t0 + threadIdx.x / 2, half = threadIdx.x % 2;
+    float4 e = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (t < kv) {
+      e = reinterpret_cast<const float4 *>(escores + (((size_t)r * d.NKV + g) * d.kv_cap + t) * 8)[half];
+      const int b = half * 4;
+      e.x = b + 0 < kG ? e.x * s_inv[b + 0] : 0.0f;
+      e.y = b + 1 < kG ? e.y * s_inv[b + 1] : 0.0f;
+      e.z = b + 2 < kG ? e.z * s_inv[b + 2] : 0.0f;
+      e.w = b + 3 < kG ? e.w * s_inv[b + 3] : 0.0f;
+    }
+    s_p[threadIdx.x] = e;
+  }
+  __syncthreads();
   const int32_t *ptr = pt + (size_t)row_seq[r] * d.max_pages;
-  const float *prow = p + ((size_t)r * d.NH + (size_t)g * kG) * d.kv_cap;
+  const float *pl = reinterpret_cast<const float *>(s_p);
   double acc[kG][kE];
 #pragma unroll
   for (int hh = 0; hh < kG; hh++)
 #pragma unroll
     for (int e = 0; e < kE; e++) acc[hh][e] = 0.0;
-#pragma unroll 4
-  for (int i = 0; i < nw; i++) {
-    const int t = tw0 + i;
-    const int32_t phys = ptr[t / kPage];
-    const float *vrow = vpool + ((size_t)(phys * d.NKV + g) * kPage + t % kPage) * kD;
-    float v[kE];
 #pragma unroll
-    for (int e = 0; e < kE; e++) v[e] = (lane + e * kWave < kD) ? vrow[lane + e * kWave] : 0.0f;
+  for (int pg = 0; pg < 2; pg++) {
+    const int tp = t0 + (wave * 2 + pg) * kPage;  // first token of the page
+    if (tp >= kv) break;
+    const int n = min(kPage, kv - tp);
+    const float *vbase = vpool + (size_t)(ptr[tp / kPage] * d.NKV + g) * kPage * kD;
+    const float *pbase = pl + (tp - t0) * 8;
+    if (n == kPage) {
 #pragma unroll
-    for (int hh = 0; hh < kG; hh++) {
-      const float ph = prow[(size_t)hh * d.kv_cap + t];
+      for (int i = 0; i < kPage; i++) {
+        float v[kE];
 #pragma unroll
-      for (int e = 0; e < kE; e++) acc[hh][e] += (double)(ph * v[e]);
+        for (int e = 0; e < kE; e++)
+          v[e] = (lane + e * kWave < kD) ? vbase[i * kD + lane + e * kWave] : 0.0f;
+#pragma unroll
+        for (int hh = 0; hh < kG; hh++) {
+          const float ph = pbase[i * 8 + hh];
+#pragma unroll
+          for (int e = 0; e < kE; e++) acc[hh][e] += (double)(ph * v[e]);
+        }
+      }
+    } else {
+      for (int i = 0; i < n; i++) {
+        float v[kE];
+#pragma unroll
+        for (int e = 0; e < kE; e++)
+          v[e] = (lane + e * kWave < kD) ? vbase[i * kD + lane + e * kWave] : 0.0f;
+#pragma unroll
+        for (int hh = 0; hh < kG; hh++) {
+          const float ph = pbase[i * 8 + hh];
+#pragma unroll
+          for (int e = 0; e < kE; e++) acc[hh][e] += (double)(ph * v[e]);
+        }
+      }
     }
   }
   if (wave > 0) {
@@ -902,14 +1019,14 @@ void launch_pack(hipStream_t s, int n_lanes, const uint32_t *lane_info, const ui
                  const int32_t *page_table, int max_pages, uint32_t *cu, uint32_t *row_pos,
                  int32_t *row_slot, uint32_t *row_lane, uint32_t *row_token, uint32_t *row_seq,
                  uint32_t *lane_last, uint32_t *row_err) {
-  hipLaunchKernelGGL(k_pack, dim3(1), dim3(1024), 0, s, n_lanes, lane_info, tokens, page_table,
+  launch_k(k_pack, dim3(1), dim3(1024), 0, s, n_lanes, lane_info, tokens, page_table,
                      max_pages, cu, row_pos, row_slot, row_lane, row_token, row_seq, lane_last,
                      row_err);
 }
 
 void launch_embed(hipStream_t s, int rows, const MatrixView &emb, const uint32_t *row_token,
                   float *x, int H, uint32_t *row_err) {
-  hipLaunchKernelGGL(k_embed, dim3(rows), dim3(256), 0, s, emb, row_token, x, H, row_err);
+  launch_k(k_embed, dim3(rows), dim3(256), 0, s, emb, row_token, x, H, row_err);
 }
 
 void launch_norm_act(hipStream_t s, int rows, const float *x, const uint32_t *in_rows,
@@ -917,19 +1034,19 @@ void launch_norm_act(hipStream_t s, int rows, const float *x, const uint32_t *in
                      uint32_t *row_err) {
   const size_t lds = (size_t)H * sizeof(float);
   if (act_dtype == 8)
-    hipLaunchKernelGGL(k_norm_act<8>, dim3(rows), dim3(256), lds, s, x, in_rows, weight, H, eps,
+    launch_k(k_norm_act<8>, dim3(rows), dim3(256), lds, s, x, in_rows, weight, H, eps,
                        nbp, act, row_err);
   else
-    hipLaunchKernelGGL(k_norm_act<1>, dim3(rows), dim3(256), lds, s, x, in_rows, weight, H, eps,
+    launch_k(k_norm_act<1>, dim3(rows), dim3(256), lds, s, x, in_rows, weight, H, eps,
                        nbp, act, row_err);
 }
 
 void launch_quant_act(hipStream_t s, int rows, const float *src, int K, int act_dtype, int nbp,
                       ActView act, uint32_t *row_err) {
   if (act_dtype == 8)
-    hipLaunchKernelGGL(k_quant_act<8>, dim3(rows), dim3(256), 0, s, src, K, nbp, act, row_err);
+    launch_k(k_quant_act<8>, dim3(rows), dim3(256), 0, s, src, K, nbp, act, row_err);
   else
-    hipLaunchKernelGGL(k_quant_act<1>, dim3(rows), dim3(256), 0, s, src, K, nbp, act, row_err);
+    launch_k(k_quant_act<1>, dim3(rows), dim3(256), 0, s, src, K, nbp, act, row_err);
 }
 
 template <int kEpi, int kNM>
@@ -940,11 +1057,11 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
   if (kEpi == kEpiArgmax && w.nbp <= 64 && n_tiles <= 8) {
     // the head: many weight tiles, short K — one wave per output tile, the
     // n-tiles of a weight tile in one workgroup
-    hipLaunchKernelGGL((k_mv_q8w<kEpi, kNM>), dim3(units), dim3(64 * n_tiles), 0, s, w, act,
+    launch_k((k_mv_q8w<kEpi, kNM>), dim3(units), dim3(64 * n_tiles), 0, s, w, act,
                        rows_b, n_tiles, o);
   } else {
     const int groups = (units + 7) / 8;
-    hipLaunchKernelGGL((k_mv_q8s<kEpi, kNM>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w,
+    launch_k((k_mv_q8s<kEpi, kNM>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w,
                        act, rows_b, n_tiles, o);
   }
 }
@@ -953,7 +1070,7 @@ template <int kEpi>
 static void mv_f16(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
                    const MatvecOut &o) {
   const int out_rows = kEpi == kEpiSwiglu ? w.rows / 2 : w.rows;
-  hipLaunchKernelGGL(k_mv_f16<kEpi>, dim3((out_rows + 3) / 4), dim3(256), 0, s, w, act, rows_b, o);
+  launch_k(k_mv_f16<kEpi>, dim3((out_rows + 3) / 4), dim3(256), 0, s, w, act, rows_b, o);
 }
 
 void launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActView &act,
@@ -977,7 +1094,7 @@ void launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActVi
 
 void launch_argmax_reduce(hipStream_t s, int rows, const unsigned long long *part, int units,
                           unsigned long long *out) {
-  hipLaunchKernelGGL(k_argmax_reduce, dim3(rows), dim3(256), 0, s, part, units, out);
+  launch_k(k_argmax_reduce, dim3(rows), dim3(256), 0, s, part, units, out);
 }
 
 void launch_qkv_post(hipStream_t s, int rows, const StepDims &d, const float *qkv,
@@ -985,7 +1102,7 @@ void launch_qkv_post(hipStream_t s, int rows, const StepDims &d, const float *qk
                      const int32_t *row_slot, float *q_rot, float *kpool, float *vpool,
                      uint32_t *row_err) {
   (void)row_err;
-  hipLaunchKernelGGL(k_qkv_post, dim3(rows), dim3(256), 0, s, d, qkv, bias, rope, row_pos,
+  launch_k(k_qkv_post, dim3(rows), dim3(256), 0, s, d, qkv, bias, rope, row_pos,
                      row_slot, q_rot, kpool, vpool);
 }
 
@@ -1025,27 +1142,37 @@ void launch_attn_scores(hipStream_t s, int rows, int max_kv, const StepDims &d, 
   const dim3 grid(rows, d.NKV, (max_kv + 255) / 256);
   bool ok = true;
 #define L(DD, GG)                                                                           \
-  hipLaunchKernelGGL((k_attn_scores<DD, GG>), grid, dim3(256), 0, s, d, q_rot, kpool, row_pos, \
+  launch_k((k_attn_scores<DD, GG>), grid, dim3(256), 0, s, d, q_rot, kpool, row_pos, \
                      row_seq, page_table, scores, chunk_max, row_err)
   COHX_DG_DISPATCH(d.D, d.G, L);
 #undef L
   (void)ok;
 }
 
-void launch_attn_stats(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
-                       float *scores, const float *chunk_max) {
-  hipLaunchKernelGGL(k_attn_stats, dim3(rows, d.NH), dim3(256), 0, s, d, row_pos, scores,
-                     chunk_max);
+void launch_attn_exp(hipStream_t s, int rows, int max_kv, const StepDims &d,
+                     const uint32_t *row_pos, float *scores, const float *chunk_max,
+                     double *den_part) {
+  const dim3 grid(rows, d.NKV, (max_kv + 255) / 256);
+  switch (d.G) {
+#define L(GG)                                                                               \
+  case GG:                                                                                  \
+    launch_k(k_attn_exp<GG>, grid, dim3(256), 0, s, d, row_pos, scores, chunk_max, \
+                       den_part);                                                           \
+    break;
+    L(1) L(2) L(4) L(6) L(7) L(8)
+#undef L
+    default: break;
+  }
 }
 
 void launch_attn_pv(hipStream_t s, int rows, int max_kv, const StepDims &d, const float *vpool,
                     const uint32_t *row_pos, const uint32_t *row_seq, const int32_t *page_table,
-                    const float *probs, double *partial) {
+                    const float *escores, const double *den_part, double *partial) {
   const dim3 grid(rows, d.NKV, (max_kv + kChunk - 1) / kChunk);
   bool ok = true;
 #define L(DD, GG)                                                                          \
-  hipLaunchKernelGGL((k_attn_pv<DD, GG>), grid, dim3(256), 0, s, d, vpool, row_pos, row_seq, \
-                     page_table, probs, partial)
+  launch_k((k_attn_pv<DD, GG>), grid, dim3(256), 0, s, d, vpool, row_pos, row_seq, \
+                     page_table, escores, den_part, partial)
   COHX_DG_DISPATCH(d.D, d.G, L);
 #undef L
   (void)ok;
@@ -1056,10 +1183,10 @@ void launch_attn_combine(hipStream_t s, int rows, const StepDims &d, const uint3
                          uint32_t *row_err) {
   const int threads = ((d.D + kWave - 1) / kWave) * kWave;
   if (act_dtype == 8)
-    hipLaunchKernelGGL(k_attn_combine<8>, dim3(rows, d.NH), dim3(threads), 0, s, d, row_pos,
+    launch_k(k_attn_combine<8>, dim3(rows, d.NH), dim3(threads), 0, s, d, row_pos,
                        partial, nbp, act, row_err);
   else
-    hipLaunchKernelGGL(k_attn_combine<1>, dim3(rows, d.NH), dim3(threads), 0, s, d, row_pos,
+    launch_k(k_attn_combine<1>, dim3(rows, d.NH), dim3(threads), 0, s, d, row_pos,
                        partial, nbp, act, row_err);
 }
 
@@ -1070,13 +1197,13 @@ void launch_fill_synthetic(hipStream_t s, float *kpool, float *vpool, size_t lay
   int blocks = (int)((total + 255) / 256);
   if (blocks > 1024) blocks = 1024;
   if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(k_fill_synthetic, dim3(blocks, layers), dim3(256), 0, s, kpool, vpool,
+  launch_k(k_fill_synthetic, dim3(blocks, layers), dim3(256), 0, s, kpool, vpool,
                      layer_stride, pages, rows, NKV, D, seed, stream);
 }
 
 void launch_copy_page(hipStream_t s, float *kpool, float *vpool, size_t layer_stride, int layers,
                       int page_floats, int src_page, int dst_page) {
-  hipLaunchKernelGGL(k_copy_page, dim3((page_floats + 255) / 256, layers), dim3(256), 0, s, kpool,
+  launch_k(k_copy_page, dim3((page_floats + 255) / 256, layers), dim3(256), 0, s, kpool,
                      vpool, layer_stride, page_floats, src_page, dst_page);
 }
 
@@ -1084,14 +1211,14 @@ void launch_fill_u64(hipStream_t s, unsigned long long *p, size_t n, unsigned lo
   int blocks = (int)((n + 255) / 256);
   if (blocks > 1024) blocks = 1024;
   if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(k_fill_u64, dim3(blocks), dim3(256), 0, s, p, n, v);
+  launch_k(k_fill_u64, dim3(blocks), dim3(256), 0, s, p, n, v);
 }
 
 void launch_fill_u32(hipStream_t s, uint32_t *p, size_t n, uint32_t v) {
   int blocks = (int)((n + 255) / 256);
   if (blocks > 1024) blocks = 1024;
   if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(k_fill_u32, dim3(blocks), dim3(256), 0, s, p, n, v);
+  launch_k(k_fill_u32, dim3(blocks), dim3(256), 0, s, p, n, v);
 }
 
 }  // namespace cohx

@@ -144,8 +144,10 @@ int cohx_pack(cohx_ctx *ctx, const cohx_batch *batch, uint32_t *cu_seqlens, uint
 
 /* Opt-in per-kernel timing of cohx_step (no engine counterpart; the engine
  * reports only BatchStep byte counts, batch.rs:3-9).  enable=1 clears the
- * counters and starts timing every launch with HIP events on the context's
- * stream; enable=0 stops.  Each record names a kernel and gives its launches,
+ * counters and starts timing every launch on the context's stream with start
+ * and stop events carried in the launches' own dispatch packets (kernel
+ * execution time; each timed launch costs a few microseconds more to issue);
+ * enable=0 stops.  Each record names a kernel and gives its launches,
  * summed device time and summed algorithmic bytes / flops (the minimum traffic
  * and arithmetic of the operation, independent of how the kernel achieves it). */
 typedef struct {
