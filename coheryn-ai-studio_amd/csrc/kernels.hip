@@ -541,6 +541,181 @@ __global__ __launch_bounds__(512) void k_mv_q8w(MatrixView w, ActView act, int r
   if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
 }
 
+// ---------------------------------------------------------------------------
+// Register-chain Q8_0 matvec for short K.  A wave owns kNM weight tiles x kNN
+// batch tiles and walks the blocks in order, as the reference chain does
+// (quant.rs:265-272): per block one int8 MFMA gives the exact isum of every
+// (row, batch row) pair, then acc = fmaf((float)isum, dw*da, acc).  dw*da is
+// one v_fma_mix_f32 of the two binary16 scales with a +0 addend: the product
+// of two binary16 values is exact in f32, and the accumulator, starting at
+// +0, is never -0, so the sign of a zero product cannot reach the result.
+// Operands come through buffer resources (scalar base, per-lane offset); a
+// batch tile past the last one gets an empty resource and reads zeros.
+// ---------------------------------------------------------------------------
+template <int WH, int AH>
+__device__ __forceinline__ float scale_mul(uint32_t w, uint32_t a) {
+  float r;
+  if constexpr (WH == 0 && AH == 0)
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,1,0]" : "=v"(r) : "v"(w), "v"(a));
+  else if constexpr (WH == 1 && AH == 0)
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,1,0]" : "=v"(r) : "v"(w), "v"(a));
+  else if constexpr (WH == 0 && AH == 1)
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[1,1,0]" : "=v"(r) : "v"(w), "v"(a));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,1,0] op_sel_hi:[1,1,0]" : "=v"(r) : "v"(w), "v"(a));
+  return r;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int kNM, int kNN>
+struct ChainPair {
+  uint4 a[kNM];        // weight tiles, blocks 2p and 2p+1
+  uint4 b[kNN];        // batch tiles, blocks 2p and 2p+1
+  uint2 dw[kNM][2];    // the lane's 4 rows' scales, block 2p / 2p+1
+  uint32_t da[kNN][2]; // the lane's batch row scale, block 2p / 2p+1
+};
+
+constexpr int kChainWaves = 4;  // batch groups per workgroup
+
+template <int kEpi, int kNM, int kNN, int kDepth>
+__global__ __launch_bounds__(64 * kChainWaves) void k_mv_q8c(MatrixView w, ActView act, int rows_b,
+                                                            int n_tiles, MatvecOut o) {
+  const int lane = threadIdx.x % kWave;
+  const int ng = blockIdx.y * kChainWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int unit = blockIdx.x;
+  if (ng * kNN >= n_tiles) return;
+  const int npairs = w.nbp / 2, nbp = w.nbp, rsub = 4 * (lane / 16), col = lane % 16;
+  __amdgpu_buffer_rsrc_t ra[kNM], rw[kNM], rb[kNN], rd[kNN];
+#pragma unroll
+  for (int m = 0; m < kNM; m++) {
+    const int tile = unit * kNM + m;
+    ra[m] = buffer_rsrc(w.qs + (size_t)tile * npairs * 1024, (uint32_t)npairs * 1024);
+    rw[m] = buffer_rsrc(w.ds + (size_t)tile * nbp * 16, (uint32_t)nbp * 32);
+  }
+#pragma unroll
+  for (int n = 0; n < kNN; n++) {
+    const int nt = ng * kNN + n;
+    const bool live = nt < n_tiles;
+    rb[n] = buffer_rsrc(act.qs + (size_t)(live ? nt : 0) * npairs * 1024, live ? (uint32_t)npairs * 1024 : 0u);
+    rd[n] = buffer_rsrc(act.ds + (size_t)(live ? nt : 0) * nbp * 16, live ? (uint32_t)nbp * 32 : 0u);
+  }
+  const int voff = lane * 16, woff = rsub * 2, doff = col * 2;
+  auto load = [&](ChainPair<kNM, kNN> &r, int p) {
+#pragma unroll
+    for (int m = 0; m < kNM; m++) {
+      r.a[m] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra[m], voff, p * 1024, 0));
+      r.dw[m][0] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw[m], woff, p * 64, 0));
+      r.dw[m][1] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw[m], woff + 32, p * 64, 0));
+    }
+#pragma unroll
+    for (int n = 0; n < kNN; n++) {
+      r.b[n] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rb[n], voff, p * 1024, 0));
+      r.da[n][0] = __builtin_amdgcn_raw_buffer_load_b16(rd[n], doff, p * 64, 0);
+      r.da[n][1] = __builtin_amdgcn_raw_buffer_load_b16(rd[n], doff + 32, p * 64, 0);
+    }
+  };
+  float acc[kNM][kNN][4];
+#pragma unroll
+  for (int m = 0; m < kNM; m++)
+#pragma unroll
+    for (int n = 0; n < kNN; n++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) acc[m][n][i] = 0.0f;
+  const v4i zero = {0, 0, 0, 0};
+  ChainPair<kNM, kNN> ring[kDepth];
+#pragma unroll
+  for (int i = 0; i < kDepth; i++)
+    if (i < npairs) load(ring[i], i);
+  for (int p0 = 0; p0 < npairs; p0 += kDepth) {
+#pragma unroll
+    for (int u = 0; u < kDepth; u++) {
+      const int pr = p0 + u;
+      if (pr < npairs) {
+        const ChainPair<kNM, kNN> &r = ring[u];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+#pragma unroll
+          for (int m = 0; m < kNM; m++) {
+            const long aop = h ? hi64(r.a[m]) : lo64(r.a[m]);
+#pragma unroll
+            for (int n = 0; n < kNN; n++) {
+              const v4i sum = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, h ? hi64(r.b[n]) : lo64(r.b[n]),
+                                                                    zero, 0, 0, 0);
+              const uint2 s2 = r.dw[m][h];
+              const float sc[4] = {scale_mul<0, 0>(s2.x, r.da[n][h]), scale_mul<1, 0>(s2.x, r.da[n][h]),
+                                   scale_mul<0, 0>(s2.y, r.da[n][h]), scale_mul<1, 0>(s2.y, r.da[n][h])};
+#pragma unroll
+              for (int i = 0; i < 4; i++) acc[m][n][i] = fmaf((float)sum[i], sc[i], acc[m][n][i]);
+            }
+          }
+        }
+        if (pr + kDepth < npairs) load(ring[u], pr + kDepth);
+      }
+    }
+  }
+  // ---- epilogue: lane holds rows (unit*kNM + m)*16 + rsub + i of batch row (ng*kNN + n)*16 + col
+  const int units = w.mtiles / kNM;
+#pragma unroll
+  for (int n = 0; n < kNN; n++) {
+    const int r = (ng * kNN + n) * 16 + col;
+    const bool rvalid = r < rows_b;
+    const int er = (rvalid && o.err_rows) ? (int)o.err_rows[r] : r;
+    bool bad = false;
+    if (kEpi == kEpiArgmax) {
+      float best = 0.0f;
+      int best_row = 0;
+      bool have = false;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int row = unit * 16 + rsub + i;
+        if (!rvalid || row >= w.rows) continue;
+        const float v = acc[0][n][i];
+        bad |= !finitef(v);
+        if (o.logits) o.logits[(size_t)r * w.rows + row] = v;
+        if (!have || v > best) {
+          best = v;
+          best_row = row;
+          have = true;
+        }
+      }
+      unsigned long long key = have ? argmax_key(best, best_row) : 0ull;
+      unsigned long long x = __shfl_xor(key, 16, kWave);
+      key = x > key ? x : key;
+      x = __shfl_xor(key, 32, kWave);
+      key = x > key ? x : key;
+      if (lane < 16 && rvalid) o.argmax[(size_t)r * units + unit] = key;
+    } else if (kEpi == kEpiSwiglu) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int row = unit * 16 + rsub + i;
+        if (!rvalid || row >= w.rows / 2) continue;
+        const float g = acc[0][n][i], u = acc[kNM - 1][n][i];
+        bad |= !finitef(g) || !finitef(u);
+        o.out[(size_t)r * o.ld + row] = (g / (1.0f + exp_f32(-g))) * u;
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < kNM; m++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int row = (unit * kNM + m) * 16 + rsub + i;
+          if (!rvalid || row >= w.rows) continue;
+          const float v = acc[m][n][i];
+          bad |= !finitef(v);
+          float *q = o.out + (size_t)r * o.ld + row;
+          if (kEpi == kEpiResidual)
+            *q = *q + v;
+          else
+            *q = v;
+        }
+    }
+    if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
+  }
+}
+
 // Final argmax over the per-tile partial keys of each batch row.
 __global__ __launch_bounds__(256) void k_argmax_reduce(const unsigned long long *__restrict__ part,
                                                        int units, unsigned long long *out) {
@@ -1054,15 +1229,18 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
                   const MatvecOut &o) {
   const int units = w.mtiles / kNM;
   const int n_tiles = (rows_b + 15) / 16;
-  if (kEpi == kEpiArgmax && w.nbp <= 64 && n_tiles <= 8) {
-    // the head: many weight tiles, short K — one wave per output tile, the
-    // n-tiles of a weight tile in one workgroup
-    launch_k((k_mv_q8w<kEpi, kNM>), dim3(units), dim3(64 * n_tiles), 0, s, w, act,
-                       rows_b, n_tiles, o);
+  if ((kEpi == kEpiArgmax || kEpi == kEpiSwiglu) && w.nbp <= 64) {
+    // short K, many weight tiles (the LM head, gate+up): register chains,
+    // 2 batch tiles per wave, 4 waves per workgroup
+    constexpr int kNN = 2;
+    const int groups = (n_tiles + kNN - 1) / kNN;
+    const int waves = groups < kChainWaves ? groups : kChainWaves;
+    launch_k((k_mv_q8c<kEpi, kNM, kNN, 4>), dim3(units, (groups + kChainWaves - 1) / kChainWaves),
+             dim3(64 * waves), 0, s, w, act, rows_b, n_tiles, o);
   } else {
     const int groups = (units + 7) / 8;
-    launch_k((k_mv_q8s<kEpi, kNM>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w,
-                       act, rows_b, n_tiles, o);
+    launch_k((k_mv_q8s<kEpi, kNM>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act, rows_b,
+             n_tiles, o);
   }
 }
 
