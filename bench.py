@@ -91,23 +91,25 @@ def run_workload(model, cfg, lanes, steps, warmup, seed):
         model.seq_fill_synthetic(s, kv[i], seed, i)
         seqs.append(s)
     first = None
+    seq_arr = np.asarray(seqs, np.uint32)
 
     def one_step(toks):
-        res = model.step([dict(seq=s, tokens=[t]) for s, t in zip(seqs, toks)])
-        if any(r["status"] for r in res):
-            raise RuntimeError(f"lane failure {[r['status'] for r in res]}")
-        return [r["argmax"] for r in res]
+        status, argmax = model.step_decode(seq_arr, toks)
+        if status.any():
+            raise RuntimeError(f"lane failure {status.tolist()}")
+        return argmax
 
     start_tokens = list(tokens)
+    tokens = np.asarray(tokens, np.uint32)
     for _ in range(warmup):
         tokens = one_step(tokens)
         if first is None:
-            first = list(tokens)
+            first = tokens.tolist()
     if first is None:
-        first = one_step(tokens)
-        tokens = first
+        tokens = one_step(tokens)
+        first = tokens.tolist()
     kv_at_timing = [model.seq_length(s) for s in seqs]
-    timed_tokens = list(tokens)
+    timed_tokens = tokens.copy()
     trace = []
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -123,7 +125,7 @@ def run_workload(model, cfg, lanes, steps, warmup, seed):
     tp = time.perf_counter()
     for i in range(steps):
         tokens = one_step(tokens)
-        replay_equal &= tokens == trace[i]
+        replay_equal &= bool(np.array_equal(tokens, trace[i]))
     prof_elapsed = time.perf_counter() - tp
     stats = model.profile_read()
     model.profile(False)

@@ -60,6 +60,17 @@ class LaneOut(ctypes.Structure):
                 ("logits", ctypes.POINTER(ctypes.c_float))]
 
 
+AT_END = 0xFFFFFFFF  # COHX_AT_END: the sequence's current length
+
+# numpy views of the same layouts, for building a whole step without per-lane Python work
+LANE_DTYPE = np.dtype({"names": ["seq", "n_tokens", "tokens", "start_position", "want_logits"],
+                       "formats": [np.uint32, np.uint32, np.uint64, np.uint32, np.uint32],
+                       "offsets": [0, 4, 8, 16, 20], "itemsize": ctypes.sizeof(Lane)})
+LANE_OUT_DTYPE = np.dtype({"names": ["status", "argmax", "logits"],
+                           "formats": [np.int32, np.uint32, np.uint64],
+                           "offsets": [0, 4, 8], "itemsize": ctypes.sizeof(LaneOut)})
+
+
 class StepOut(ctypes.Structure):
     _fields_ = [("lanes", ctypes.POINTER(LaneOut)), ("width", ctypes.c_uint32),
                 ("rows", ctypes.c_uint32), ("matrix_bytes", ctypes.c_uint64),
@@ -271,7 +282,7 @@ class Model:
             arr[i].seq = ln["seq"]
             arr[i].n_tokens = toks.size
             arr[i].tokens = _u32p(toks)
-            arr[i].start_position = ln.get("start", self.seq_length(ln["seq"]))
+            arr[i].start_position = ln.get("start", AT_END)
             arr[i].want_logits = 1 if ln.get("logits") else 0
         return Batch(len(lanes), arr), keep
 
@@ -296,6 +307,28 @@ class Model:
         self.last_step = dict(width=so.width, rows=so.rows, matrix_bytes=so.matrix_bytes,
                               kv_bytes=so.kv_bytes, elapsed_ns=so.elapsed_ns)
         return res
+
+    def step_decode(self, seqs, tokens):
+        """One decode token per lane, vectorized: seqs and tokens are equal-length
+        uint32 arrays.  Returns (status, argmax) int32/uint32 arrays."""
+        seqs = np.ascontiguousarray(seqs, np.uint32)
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        n = seqs.size
+        if tokens.size != n:
+            raise ValueError("one token per sequence")
+        lanes = np.zeros(n, LANE_DTYPE)
+        lanes["seq"] = seqs
+        lanes["n_tokens"] = 1
+        lanes["tokens"] = tokens.ctypes.data + 4 * np.arange(n, dtype=np.uint64)
+        lanes["start_position"] = AT_END
+        outs = np.zeros(n, LANE_OUT_DTYPE)
+        batch = Batch(n, lanes.ctypes.data_as(ctypes.POINTER(Lane)))
+        so = StepOut()
+        so.lanes = outs.ctypes.data_as(ctypes.POINTER(LaneOut))
+        self._check(lib().cohx_step(self.h, ctypes.byref(batch), ctypes.byref(so)))
+        self.last_step = dict(width=so.width, rows=so.rows, matrix_bytes=so.matrix_bytes,
+                              kv_bytes=so.kv_bytes, elapsed_ns=so.elapsed_ns)
+        return outs["status"].copy(), outs["argmax"].copy()
 
     @property
     def matrix_bytes(self):

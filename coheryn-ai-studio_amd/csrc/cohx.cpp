@@ -595,17 +595,18 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
   for (uint32_t i = 0; i < batch->n_lanes; i++) {
     const cohx_lane &ln = batch->lanes[i];
     int32_t status = COHX_OK;
-    if (!valid_seq(ctx, ln.seq) || ln.n_tokens == 0 || !ln.tokens ||
-        ln.start_position != ctx->seqs[ln.seq].length) {
+    const bool live = valid_seq(ctx, ln.seq);
+    const uint32_t start =
+        (live && ln.start_position == COHX_AT_END) ? ctx->seqs[ln.seq].length : ln.start_position;
+    if (!live || ln.n_tokens == 0 || !ln.tokens || start != ctx->seqs[ln.seq].length) {
       status = COHX_INVALID_REQUEST;
     } else {
       for (uint32_t j = 0; j < ln.n_tokens; j++)
         if (ln.tokens[j] >= d.vocabulary) status = COHX_INVALID_REQUEST;  // token outside vocabulary
-      if (!status && (uint64_t)ln.start_position + ln.n_tokens > ctx->seqs[ln.seq].capacity)
+      if (!status && (uint64_t)start + ln.n_tokens > ctx->seqs[ln.seq].capacity)
         status = COHX_RESOURCE;  // context capacity exhausted
       if (!status && p.rows + ln.n_tokens > d.max_rows) status = COHX_RESOURCE;
-      if (!status) status = ensure_pages(ctx, ln.seq, ln.start_position,
-                                         ln.start_position + ln.n_tokens);
+      if (!status) status = ensure_pages(ctx, ln.seq, start, start + ln.n_tokens);
     }
     if (outs) {
       outs[i].status = status;
@@ -614,14 +615,14 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
     if (status) continue;
     const uint32_t k = (uint32_t)p.included.size();
     info[k * 4 + 0] = ln.n_tokens;
-    info[k * 4 + 1] = ln.start_position;
+    info[k * 4 + 1] = start;
     info[k * 4 + 2] = ln.seq;
     info[k * 4 + 3] = p.rows;
     std::memcpy(toks + p.rows, ln.tokens, ln.n_tokens * sizeof(uint32_t));
     for (uint32_t j = 0; j < ln.n_tokens; j++)
-      p.kv_rows_read += (uint64_t)ln.start_position + j + 1;
+      p.kv_rows_read += (uint64_t)start + j + 1;
     p.rows += ln.n_tokens;
-    p.max_kv = std::max(p.max_kv, ln.start_position + ln.n_tokens);
+    p.max_kv = std::max(p.max_kv, start + ln.n_tokens);
     p.included.push_back((int)i);
   }
   if (p.included.empty()) return COHX_OK;

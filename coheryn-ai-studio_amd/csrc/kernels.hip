@@ -252,8 +252,8 @@ __device__ __forceinline__ void argmax_commit(float best, int best_row, bool val
 // ---------------------------------------------------------------------------
 // Split-K Q8_0 matvec.  A workgroup of 8 waves owns one output tile: kNM
 // m-tiles (16 matrix rows each; 2 = a gate tile and its up tile) x one n-tile
-// (16 batch rows).  K is walked in chunks of 16 blocks; in each chunk every
-// wave takes one block pair, computes the exact int32 block sums on the matrix
+// (16 batch rows).  K is walked in chunks of 16*kP blocks; in each chunk every
+// wave takes kP block pairs, computes the exact int32 block sums on the matrix
 // cores and parks them (as f32, exact below 2^24) in LDS with the block scales;
 // then 256 threads, one per (row, batch row), run the reference chain
 // acc = fmaf(isum, dw*da, acc) over the chunk's blocks in order.  The next
@@ -294,10 +294,10 @@ __device__ __forceinline__ long hi64(uint4 v) {
   return (long)(((unsigned long)v.w << 32) | v.z);
 }
 
-template <int kEpi, int kNM>
+template <int kEpi, int kNM, int kP>
 __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int rows_b,
                                                 int n_tiles, MatvecOut o) {
-  constexpr int kW = 8, kCB = 2 * kW;
+  constexpr int kW = 8, kCB = 2 * kW * kP;  // blocks per chunk: kP pairs per wave
   __shared__ float s_isum[kCB][kNM * 256];
   __shared__ float s_dw[kCB][kNM * 16];
   __shared__ float s_da[kCB][16];
@@ -310,43 +310,58 @@ __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int r
   const int nbp = w.nbp, npairs = nbp / 2, nchunks = (nbp + kCB - 1) / kCB;
   const int rsub = 4 * (lane / 16);
   const v4i zero = {0, 0, 0, 0};
-  // phase-2 ownership: thread t < 256 owns (row t/16, batch column t%16) of every m-tile
-  const int t = threadIdx.x, prow = t / 16, pcol = t % 16;
+  // phase-2 ownership: thread t < 256 owns the output the matrix-core layout
+  // puts in lane t%64, slot t/64: row 4*((t%64)/16) + t/64, batch column t%16.
+  // The block sums are parked as [slot][lane], so the MFMA lanes' writes and
+  // the owners' reads are both consecutive (no bank conflicts).
+  const int t = threadIdx.x, prow = 4 * ((t % 64) / 16) + t / 64, pcol = t % 16;
   float acc[kNM];
 #pragma unroll
   for (int m = 0; m < kNM; m++) acc[m] = 0.0f;
-  Q8Regs<kNM> cur, nxt;
-  if (wave < npairs) q8_load(cur, w, act, unit, nt, wave, lane);
+  Q8Regs<kNM> cur[kP], nxt[kP];
+#pragma unroll
+  for (int pp = 0; pp < kP; pp++)
+    if (pp * kW + wave < npairs) q8_load(cur[pp], w, act, unit, nt, pp * kW + wave, lane);
   for (int c = 0; c < nchunks; c++) {
-    const int pair = c * kW + wave;
-    if (c + 1 < nchunks && pair + kW < npairs) q8_load(nxt, w, act, unit, nt, pair + kW, lane);
-    if (pair < npairs) {
+    if (c + 1 < nchunks) {
 #pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const int blk = 2 * wave + h;
-        const long bop = h ? hi64(cur.b) : lo64(cur.b);
-#pragma unroll
-        for (int m = 0; m < kNM; m++) {
-          const v4i s = __builtin_amdgcn_mfma_i32_16x16x32_i8(h ? hi64(cur.a[m]) : lo64(cur.a[m]),
-                                                              bop, zero, 0, 0, 0);
-#pragma unroll
-          for (int i = 0; i < 4; i++)
-            s_isum[blk][m * 256 + (rsub + i) * 16 + lane % 16] = (float)s[i];
-        }
+      for (int pp = 0; pp < kP; pp++) {
+        const int pair = (c + 1) * kW * kP + pp * kW + wave;
+        if (pair < npairs) q8_load(nxt[pp], w, act, unit, nt, pair, lane);
       }
-      if (lane < 16) {
+    }
 #pragma unroll
-        for (int m = 0; m < kNM; m++) {
-          s_dw[2 * wave][m * 16 + lane] = h2f((uint16_t)(cur.dw[m] & 0xffffu));
-          s_dw[2 * wave + 1][m * 16 + lane] = h2f((uint16_t)(cur.dw[m] >> 16));
+    for (int pp = 0; pp < kP; pp++) {
+      const int cp = pp * kW + wave;  // pair index within the chunk
+      if (c * kW * kP + cp < npairs) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const int blk = 2 * cp + h;
+          const long bop = h ? hi64(cur[pp].b) : lo64(cur[pp].b);
+#pragma unroll
+          for (int m = 0; m < kNM; m++) {
+            const v4i s4 = __builtin_amdgcn_mfma_i32_16x16x32_i8(h ? hi64(cur[pp].a[m]) : lo64(cur[pp].a[m]),
+                                                                 bop, zero, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+              s_isum[blk][m * 256 + i * 64 + lane] = (float)s4[i];
+          }
         }
-        s_da[2 * wave][lane] = h2f((uint16_t)(cur.da & 0xffffu));
-        s_da[2 * wave + 1][lane] = h2f((uint16_t)(cur.da >> 16));
+        if (lane < 16) {
+#pragma unroll
+          for (int m = 0; m < kNM; m++) {
+            s_dw[2 * cp][m * 16 + lane] = h2f((uint16_t)(cur[pp].dw[m] & 0xffffu));
+            s_dw[2 * cp + 1][m * 16 + lane] = h2f((uint16_t)(cur[pp].dw[m] >> 16));
+          }
+          s_da[2 * cp][lane] = h2f((uint16_t)(cur[pp].da & 0xffffu));
+          s_da[2 * cp + 1][lane] = h2f((uint16_t)(cur[pp].da >> 16));
+        }
       }
     }
     __syncthreads();
     if (t < 256) {
       const int nblk = min(kCB, nbp - c * kCB);
+#pragma unroll 8
       for (int blk = 0; blk < nblk; blk++) {
         const float da = s_da[blk][pcol];
 #pragma unroll
@@ -355,7 +370,8 @@ __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int r
       }
     }
     __syncthreads();
-    cur = nxt;
+#pragma unroll
+    for (int pp = 0; pp < kP; pp++) cur[pp] = nxt[pp];
   }
   // ---- epilogue
   const int r = nt * 16 + pcol;
@@ -1238,9 +1254,17 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
     launch_k((k_mv_q8c<kEpi, kNM, kNN, 4>), dim3(units, (groups + kChainWaves - 1) / kChainWaves),
              dim3(64 * waves), 0, s, w, act, rows_b, n_tiles, o);
   } else {
+    // blocks per LDS chunk: 32 covers K <= 1024 in one chunk, 64 keeps long K to few chunks
     const int groups = (units + 7) / 8;
-    launch_k((k_mv_q8s<kEpi, kNM>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act, rows_b,
-             n_tiles, o);
+    if (kNM == 1 && w.nbp > 32)
+      launch_k((k_mv_q8s<kEpi, kNM, 4>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
+               rows_b, n_tiles, o);
+    else if (kNM == 1)
+      launch_k((k_mv_q8s<kEpi, kNM, 2>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
+               rows_b, n_tiles, o);
+    else
+      launch_k((k_mv_q8s<kEpi, kNM, 1>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
+               rows_b, n_tiles, o);
   }
 }
 

@@ -101,7 +101,10 @@ int cohx_seq_fill_synthetic(cohx_ctx *ctx, uint32_t seq, uint32_t rows, uint64_t
                             uint32_t stream);
 
 /* One lane of a ragged step: n_tokens >= 1 consecutive tokens of one sequence
- * starting at its current length (a decode row or a prefill chunk). */
+ * starting at its current length (a decode row or a prefill chunk).
+ * start_position must equal that length (the engine's session position,
+ * generation.rs:279-317) or be COHX_AT_END, which stands for it. */
+#define COHX_AT_END 0xFFFFFFFFu
 typedef struct {
   uint32_t seq;
   uint32_t n_tokens;

@@ -219,3 +219,33 @@ def test_shared_prefix_fork_equals_recompute():
     # the shared source is untouched by the forks' writes (copy on write)
     for layer in range(c["layers"]):
         assert np.array_equal(m.seq_read_kv(fb, layer)[:37], m.seq_read_kv(base, layer)[:37])
+
+
+def test_step_decode_matches_lane_step():
+    """The vectorized decode path (start position COHX_AT_END) and the per-lane
+    step advance identical contexts identically, and an explicit wrong start
+    position fails only its own lane."""
+    print("case: step_decode vs step", flush=True)
+    c, t, m1, o = build("q8_0", 5)
+    m2 = cohx.Model(c, t, max_lanes=8, max_rows=64, max_seqs=8, max_context=256)
+    kv = [37, 5, 90, 16, 64]
+    s1, s2 = [], []
+    for i, n in enumerate(kv):
+        a, b = m1.seq_alloc(), m2.seq_alloc()
+        m1.seq_fill_synthetic(a, n, 3, i)
+        m2.seq_fill_synthetic(b, n, 3, i)
+        s1.append(a)
+        s2.append(b)
+    toks = np.array([11, 250, 3, 299, 0], np.uint32)
+    for step in range(3):
+        res = m1.step([dict(seq=a, tokens=[int(x)], start=m1.seq_length(a)) for a, x in zip(s1, toks)])
+        status, argmax = m2.step_decode(s2, toks)
+        assert not status.any()
+        assert [r["argmax"] for r in res] == argmax.tolist(), step
+        toks = argmax
+    for a, b in zip(s1, s2):
+        assert m1.seq_length(a) == m2.seq_length(b)
+        assert np.array_equal(m1.seq_read_kv(a, 1, True), m2.seq_read_kv(b, 1, True))
+    res = m1.step([dict(seq=s1[0], tokens=[1], start=m1.seq_length(s1[0]) + 1),
+                   dict(seq=s1[1], tokens=[1])])
+    assert res[0]["status"] == 1 and res[1]["status"] == 0
