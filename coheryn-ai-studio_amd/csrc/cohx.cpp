@@ -12,6 +12,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -24,6 +25,10 @@ namespace cohx {
 int fail(cohx_ctx *ctx, int code, const std::string &msg) {
   if (ctx) ctx->err = msg;
   return code;
+}
+void drop_graphs(cohx_ctx *ctx) {
+  for (auto &g : ctx->graphs) (void)hipGraphExecDestroy(g.second);
+  ctx->graphs.clear();
 }
 }  // namespace cohx
 
@@ -77,6 +82,22 @@ int make_q8(cohx_ctx *ctx, DeviceMatrix &m, int rows, int K, int mtiles) {
   return rc;
 }
 
+// Q4_0 tiles: 4 bits per value (q4_byte), scales as for Q8_0.
+int make_q4(cohx_ctx *ctx, DeviceMatrix &m, int rows, int K, int mtiles) {
+  m.view.dtype = 2;
+  m.view.rows = rows;
+  m.view.K = K;
+  m.view.nb = K / 32;
+  m.view.nbp = even(m.view.nb);
+  m.view.mtiles = mtiles;
+  const size_t tile_bytes = (size_t)m.view.nbp * 256;
+  int rc = dalloc(ctx, &m.qs, (size_t)mtiles * tile_bytes);
+  if (!rc) rc = dalloc(ctx, &m.ds, (size_t)mtiles * m.view.nbp * 16);
+  m.view.qs = m.qs;
+  m.view.ds = m.ds;
+  return rc;
+}
+
 int make_f16(cohx_ctx *ctx, DeviceMatrix &m, int rows, int K) {
   m.view.dtype = 1;
   m.view.rows = rows;
@@ -115,6 +136,35 @@ int upload_q8(cohx_ctx *ctx, DeviceMatrix &m, const uint8_t *src, int rows, int 
   return COHX_OK;
 }
 
+// GGUF Q4_0 rows (quant.rs:97-101: value j = low nibble of byte j, value
+// j+16 = high nibble) -> Q4 tiles, tile i of the source at tile_first + i*tile_step.
+int upload_q4(cohx_ctx *ctx, DeviceMatrix &m, const uint8_t *src, int rows, int tile_first,
+              int tile_step) {
+  const int nb = m.view.nb, nbp = m.view.nbp;
+  const int tiles = (rows + 15) / 16;
+  const size_t tile_bytes = (size_t)nbp * 256, tile_scales = (size_t)nbp * 16;
+  std::vector<uint8_t> qs(tiles * tile_bytes, 0);
+  std::vector<uint16_t> ds(tiles * tile_scales, 0);
+  for (int r = 0; r < rows; r++) {
+    const int t = r / 16, c = r % 16;
+    for (int b = 0; b < nb; b++) {
+      const uint8_t *blk = src + ((size_t)r * nb + b) * 18;
+      ds[q8_scale(t, nbp, b, c)] = (uint16_t)(blk[0] | (blk[1] << 8));
+      for (int e = 0; e < 32; e++) {
+        const uint8_t nib = e < 16 ? (blk[2 + e] & 15) : (blk[2 + e - 16] >> 4);
+        const int g = e / 8, k = e % 8;
+        uint8_t &byte = qs[q4_byte(t, nbp, b, g * 16 + c, k)];
+        byte |= k < 4 ? nib : (uint8_t)(nib << 4);
+      }
+    }
+  }
+  HIP_TRY(hipMemcpy2D(m.qs + (size_t)tile_first * tile_bytes, tile_bytes * tile_step, qs.data(),
+                      tile_bytes, tile_bytes, tiles, hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy2D(m.ds + (size_t)tile_first * tile_scales, tile_scales * 2 * tile_step,
+                      ds.data(), tile_scales * 2, tile_scales * 2, tiles, hipMemcpyHostToDevice));
+  return COHX_OK;
+}
+
 int upload_f16(cohx_ctx *ctx, DeviceMatrix &m, const void *src, int rows, int row_first) {
   HIP_TRY(hipMemcpy(m.f16 + (size_t)row_first * m.view.K, src, (size_t)rows * m.view.K * 2,
                     hipMemcpyHostToDevice));
@@ -126,6 +176,7 @@ int upload_matrix(cohx_ctx *ctx, DeviceMatrix &m, uint32_t dtype, const void *da
   if (dtype != (uint32_t)m.view.dtype)
     return fail(ctx, COHX_UNSUPPORTED, "matrix dtype differs from the context's weight dtype");
   if (dtype == 8) return upload_q8(ctx, m, (const uint8_t *)data, rows, first, step);
+  if (dtype == 2) return upload_q4(ctx, m, (const uint8_t *)data, rows, first, step);
   return upload_f16(ctx, m, data, rows, first);
 }
 
@@ -153,7 +204,8 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
       d->head_dim > 128 || d->heads / d->kv_heads > (uint32_t)kMaxGroup || d->hidden % 32 ||
       d->intermediate % 32 || !d->vocabulary)
     return COHX_INVALID_GGUF;
-  if (d->weight_dtype != COHX_Q8_0 && d->weight_dtype != COHX_F16) return COHX_UNSUPPORTED;
+  if (d->weight_dtype != COHX_Q8_0 && d->weight_dtype != COHX_Q4_0 && d->weight_dtype != COHX_F16)
+    return COHX_UNSUPPORTED;
   if (!attention_shape_supported((int)d->head_dim, (int)(d->heads / d->kv_heads)))
     return COHX_UNSUPPORTED;
   if (d->kv_dtype != 0) return COHX_UNSUPPORTED;
@@ -163,6 +215,8 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   cohx_ctx *ctx = new cohx_ctx();
   ctx->desc = *d;
   ctx->device = device;
+  // COHX_GRAPHS=0 issues every launch directly (graphs are on by default)
+  if (const char *g = std::getenv("COHX_GRAPHS")) ctx->use_graphs = std::strcmp(g, "0") != 0;
   auto bail = [&](int rc) {
     cohx_destroy(ctx);
     return rc;
@@ -183,17 +237,21 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   int rc = COHX_OK;
   // weights
   ctx->layers.resize(L);
-  const bool q8 = d->weight_dtype == COHX_Q8_0;
+  const bool packed = d->weight_dtype == COHX_Q8_0 || d->weight_dtype == COHX_Q4_0;
+  auto make_packed = [&](DeviceMatrix &m, int rows, int K, int mtiles) {
+    return d->weight_dtype == COHX_Q8_0 ? make_q8(ctx, m, rows, K, mtiles)
+                                        : make_q4(ctx, m, rows, K, mtiles);
+  };
   for (int l = 0; l < L && !rc; l++) {
     Layer &ly = ctx->layers[l];
     rc = dalloc(ctx, &ly.attn_norm, H);
     if (!rc) rc = dalloc(ctx, &ly.ffn_norm, H);
     if (!rc) rc = dalloc(ctx, &ly.bqkv, H + 2 * KVD);
-    if (q8) {
-      if (!rc) rc = make_q8(ctx, ly.qkv, H + 2 * KVD, H, H / 16 + 2 * ((KVD + 15) / 16));
-      if (!rc) rc = make_q8(ctx, ly.o, H, H, (H + 15) / 16);
-      if (!rc) rc = make_q8(ctx, ly.gu, 2 * F, H, 2 * ((F + 15) / 16));
-      if (!rc) rc = make_q8(ctx, ly.down, H, F, (H + 15) / 16);
+    if (packed) {
+      if (!rc) rc = make_packed(ly.qkv, H + 2 * KVD, H, H / 16 + 2 * ((KVD + 15) / 16));
+      if (!rc) rc = make_packed(ly.o, H, H, (H + 15) / 16);
+      if (!rc) rc = make_packed(ly.gu, 2 * F, H, 2 * ((F + 15) / 16));
+      if (!rc) rc = make_packed(ly.down, H, F, (H + 15) / 16);
     } else {
       if (!rc) rc = make_f16(ctx, ly.qkv, H + 2 * KVD, H);
       if (!rc) rc = make_f16(ctx, ly.o, H, H);
@@ -203,9 +261,9 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   }
   if (H % 16 || KVD % 16) rc = rc ? rc : COHX_INVALID_GGUF;
   if (!rc) rc = dalloc(ctx, &ctx->output_norm, H);
-  if (!rc) rc = q8 ? make_q8(ctx, ctx->embd, V, H, (V + 15) / 16) : make_f16(ctx, ctx->embd, V, H);
+  if (!rc) rc = packed ? make_packed(ctx->embd, V, H, (V + 15) / 16) : make_f16(ctx, ctx->embd, V, H);
   if (!rc && !d->tied)
-    rc = q8 ? make_q8(ctx, ctx->output, V, H, (V + 15) / 16) : make_f16(ctx, ctx->output, V, H);
+    rc = packed ? make_packed(ctx->output, V, H, (V + 15) / 16) : make_f16(ctx, ctx->output, V, H);
   // RoPE table: (cos, sin) of the engine's iterative angle (cpu.rs:59-73).
   if (!rc) {
     std::vector<float2> tab((size_t)d->max_context * (D / 2));
@@ -272,6 +330,7 @@ void cohx_destroy(cohx_ctx *ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  drop_graphs(ctx);
   for (void *p : ctx->allocations) (void)hipFree(p);
   if (ctx->ws.h_upload) (void)hipHostFree(ctx->ws.h_upload);
   if (ctx->ws.h_row_err) (void)hipHostFree(ctx->ws.h_row_err);
@@ -328,7 +387,7 @@ int cohx_upload_tensor(cohx_ctx *ctx, const char *name, uint32_t dtype, uint64_t
       const uint64_t first = s == "attn_q.weight" ? 0 : s == "attn_k.weight" ? H : H + KVD;
       if (!expect(H, rows)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
       rc = upload_matrix(ctx, ly.qkv, dtype, data, (int)rows,
-                         (int)(dtype == 8 ? first / 16 : first), 1);
+                         (int)(dtype == 8 || dtype == 2 ? first / 16 : first), 1);
       ly.qkv.gguf_bytes += bytes;
     } else if (s == "attn_output.weight") {
       if (!expect(H, H)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
@@ -337,8 +396,8 @@ int cohx_upload_tensor(cohx_ctx *ctx, const char *name, uint32_t dtype, uint64_t
     } else if (s == "ffn_gate.weight" || s == "ffn_up.weight") {
       if (!expect(H, F)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
       const bool up = s == "ffn_up.weight";
-      // Q8_0: gate tile i -> tile 2i, up tile i -> tile 2i+1; F16: gate rows then up rows.
-      rc = dtype == 8 ? upload_matrix(ctx, ly.gu, dtype, data, (int)F, up ? 1 : 0, 2)
+      // Q8_0/Q4_0: gate tile i -> tile 2i, up tile i -> tile 2i+1; F16: gate rows then up rows.
+      rc = dtype == 8 || dtype == 2 ? upload_matrix(ctx, ly.gu, dtype, data, (int)F, up ? 1 : 0, 2)
                       : upload_matrix(ctx, ly.gu, dtype, data, (int)F, up ? (int)F : 0, 1);
       ly.gu.gguf_bytes += bytes;
     } else if (s == "ffn_down.weight") {
@@ -633,11 +692,14 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
                          ctx->stream));
   HIP_TRY(hipMemcpyAsync(ctx->ws.tokens, toks, p.rows * sizeof(uint32_t), hipMemcpyHostToDevice,
                          ctx->stream));
-  Workspace &w = ctx->ws;
-  launch_pack(ctx->stream, (int)n, w.lane_info, w.tokens, ctx->page_table, ctx->max_pages, w.cu,
-              w.row_pos, w.row_slot, w.row_lane, w.row_token, w.row_seq, w.lane_last, w.row_err);
-  HIP_TRY(hipGetLastError());
   return COHX_OK;
+}
+
+// The device packer over the uploaded lanes (ragged rows, positions, slots).
+void enqueue_pack(cohx_ctx *ctx, int n_lanes) {
+  Workspace &w = ctx->ws;
+  launch_pack(ctx->stream, n_lanes, w.lane_info, w.tokens, ctx->page_table, ctx->max_pages, w.cu,
+              w.row_pos, w.row_slot, w.row_lane, w.row_token, w.row_seq, w.lane_last, w.row_err);
 }
 
 ActView act_view(cohx_ctx *ctx) {
@@ -656,6 +718,8 @@ extern "C" int cohx_pack(cohx_ctx *ctx, const cohx_batch *batch, uint32_t *cu, u
   if (rc) return rc;
   if (p.included.size() != batch->n_lanes)
     return fail(ctx, COHX_INVALID_REQUEST, "a lane failed validation");
+  enqueue_pack(ctx, (int)p.included.size());
+  HIP_TRY(hipGetLastError());
   std::vector<int32_t> slot32(p.rows);
   Workspace &w = ctx->ws;
   HIP_TRY(hipMemcpyAsync(cu, w.cu, (batch->n_lanes + 1) * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -715,8 +779,10 @@ void prof_collect(cohx_ctx *ctx) {
 
 // Algorithmic bytes of one Q8_0/F16 matrix pass over rows_b activation rows.
 double matrix_pass_bytes(const MatrixView &w, int rows_b, int out_rows, bool residual) {
-  const double wbytes = w.dtype == 8 ? (double)w.rows * w.K / 32 * 34 : (double)w.rows * w.K * 2;
-  const double abytes = w.dtype == 8 ? (double)rows_b * w.K / 32 * 34 : (double)rows_b * w.K * 2;
+  const double wbytes = w.dtype == 8   ? (double)w.rows * w.K / 32 * 34
+                        : w.dtype == 2 ? (double)w.rows * w.K / 32 * 18
+                                       : (double)w.rows * w.K * 2;
+  const double abytes = w.dtype != 1 ? (double)rows_b * w.K / 32 * 34 : (double)rows_b * w.K * 2;
   return wbytes + abytes + (double)rows_b * out_rows * 4 * (residual ? 2 : 1);
 }
 
@@ -743,34 +809,20 @@ extern "C" uint32_t cohx_profile_read(const cohx_ctx *ctx, cohx_kernel_stat *out
   return kCatCount;
 }
 
-extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
-  if (!ctx || !out || !out->lanes) return COHX_INVALID_REQUEST;
-  const auto t_start = std::chrono::steady_clock::now();
-  HIP_TRY(hipSetDevice(ctx->device));
+// Everything one step runs on the device, in stream order: packer, embedding,
+// the layers, final norm, LM head and argmax.  Launch-only (no host waits), so
+// it can be captured into a graph.  kv_grid (>= the longest attended length)
+// sizes the attention grids; blocks past a row's length exit at once.
+int enqueue_device_step(cohx_ctx *ctx, const Prepared &p, int kv_grid, bool any_logits) {
   const cohx_model_desc &d = ctx->desc;
-  Prepared p;
   const int pk = prof_begin(ctx, kCatPack, 0.0, 0.0);
-  int rc = prepare_batch(ctx, batch, out->lanes, p);
+  enqueue_pack(ctx, (int)p.included.size());
   prof_end(ctx, pk);
-  if (rc) {
-    ctx->prof.pending.clear();
-    ctx->prof.next = 0;
-    return rc;
-  }
-  out->width = (uint32_t)p.included.size();
-  out->rows = p.rows;
-  out->matrix_bytes = 0;
-  out->kv_bytes = 0;
-  if (p.included.empty()) {
-    ctx->prof.pending.clear();
-    ctx->prof.next = 0;
-    out->elapsed_ns = 0;
-    return COHX_OK;
-  }
   const int R = (int)p.rows, NL = (int)p.included.size();
   const int H = d.hidden, F = d.intermediate, NH = d.heads, NKV = d.kv_heads, D = d.head_dim,
             KVD = NKV * D;
-  const int act_dtype = d.weight_dtype == COHX_Q8_0 ? 8 : 1;
+  // packed weights (Q8_0, Q4_0) take Q8_0 activation blocks (quant.rs:181-183)
+  const int act_dtype = d.weight_dtype == COHX_F16 ? 1 : 8;
   const double act_row = act_dtype == 8 ? (double)H / 32 * 34 : (double)H * 2;
   Workspace &w = ctx->ws;
   hipStream_t s = ctx->stream;
@@ -808,14 +860,14 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
                     w.row_err);
     prof_end(ctx, e);
     e = prof_begin(ctx, kCatAttnScores, b_scores, f_attn);
-    launch_attn_scores(s, R, (int)p.max_kv, sd, w.q_rot, kp, w.row_pos, w.row_seq,
+    launch_attn_scores(s, R, kv_grid, sd, w.q_rot, kp, w.row_pos, w.row_seq,
                        ctx->page_table, w.scores, w.chunk_max, w.row_err);
     prof_end(ctx, e);
     e = prof_begin(ctx, kCatAttnSoftmax, b_softmax, 0);
-    launch_attn_exp(s, R, (int)p.max_kv, sd, w.row_pos, w.scores, w.chunk_max, w.den_part);
+    launch_attn_exp(s, R, kv_grid, sd, w.row_pos, w.scores, w.chunk_max, w.den_part);
     prof_end(ctx, e);
     e = prof_begin(ctx, kCatAttnPv, b_pv, f_attn);
-    launch_attn_pv(s, R, (int)p.max_kv, sd, vp, w.row_pos, w.row_seq, ctx->page_table, w.scores,
+    launch_attn_pv(s, R, kv_grid, sd, vp, w.row_pos, w.row_seq, ctx->page_table, w.scores,
                    w.den_part, w.partial);
     prof_end(ctx, e);
     e = prof_begin(ctx, kCatAttnCombine, b_combine, 0);
@@ -848,15 +900,11 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
   launch_norm_act(s, NL, w.x, w.lane_last, ctx->output_norm, H, d.norm_epsilon, act_dtype,
                   ctx->nbp_h, act, w.row_err);
   prof_end(ctx, e);
-  bool any_logits = false;
-  for (int k = 0; k < NL; k++)
-    if (batch->lanes[p.included[k]].want_logits && out->lanes[p.included[k]].logits)
-      any_logits = true;
   const DeviceMatrix &head = d.tied ? ctx->embd : ctx->output;
   e = prof_begin(ctx, kCatMvHead,
                  matrix_pass_bytes(head.view, NL, 0, false) + (any_logits ? (double)NL * d.vocabulary * 4 : 0.0) + NL * 8.0,
                  2.0 * NL * d.vocabulary * H);
-  if (head.view.dtype == 8) {
+  if (head.view.dtype != 1) {
     launch_matvec(s, kEpiArgmax, head.view, act, NL,
                   MatvecOut{nullptr, 0, w.argmax_part, any_logits ? w.logits : nullptr, w.row_err,
                             w.lane_last});
@@ -869,6 +917,64 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
   }
   prof_end(ctx, e);
   HIP_TRY(hipGetLastError());
+  return COHX_OK;
+}
+
+extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
+  if (!ctx || !out || !out->lanes) return COHX_INVALID_REQUEST;
+  const auto t_start = std::chrono::steady_clock::now();
+  HIP_TRY(hipSetDevice(ctx->device));
+  const cohx_model_desc &d = ctx->desc;
+  Prepared p;
+  int rc = prepare_batch(ctx, batch, out->lanes, p);
+  if (rc) {
+    ctx->prof.pending.clear();
+    ctx->prof.next = 0;
+    return rc;
+  }
+  out->width = (uint32_t)p.included.size();
+  out->rows = p.rows;
+  out->matrix_bytes = 0;
+  out->kv_bytes = 0;
+  if (p.included.empty()) {
+    ctx->prof.pending.clear();
+    ctx->prof.next = 0;
+    out->elapsed_ns = 0;
+    return COHX_OK;
+  }
+  const int R = (int)p.rows, NL = (int)p.included.size();
+  const int KVD = d.kv_heads * d.head_dim;
+  Workspace &w = ctx->ws;
+  hipStream_t s = ctx->stream;
+  bool any_logits = false;
+  for (int k = 0; k < NL; k++)
+    if (batch->lanes[p.included[k]].want_logits && out->lanes[p.included[k]].logits)
+      any_logits = true;
+  const int kv_grid = (int)((p.max_kv + 255) / 256 * 256);
+  if (ctx->prof.on || !ctx->use_graphs) {
+    rc = enqueue_device_step(ctx, p, kv_grid, any_logits);
+    if (rc) return rc;
+  } else {
+    const StepKey key{(uint32_t)R, (uint32_t)NL, (uint32_t)kv_grid, any_logits};
+    auto it = ctx->graphs.find(key);
+    if (it == ctx->graphs.end()) {
+      if (ctx->graphs.size() >= kMaxGraphs) drop_graphs(ctx);
+      hipGraph_t g = nullptr;
+      HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+      rc = enqueue_device_step(ctx, p, kv_grid, any_logits);
+      const hipError_t ec = hipStreamEndCapture(s, &g);
+      if (rc || ec != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc ? rc : fail(ctx, COHX_DEVICE, std::string("step capture: ") + hipGetErrorString(ec));
+      }
+      hipGraphExec_t ex = nullptr;
+      const hipError_t ei = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      if (ei != hipSuccess) return fail(ctx, COHX_DEVICE, std::string("step graph: ") + hipGetErrorString(ei));
+      it = ctx->graphs.emplace(key, ex).first;
+    }
+    HIP_TRY(hipGraphLaunch(it->second, s));
+  }
   HIP_TRY(hipMemcpyAsync(w.h_argmax, w.argmax, NL * sizeof(unsigned long long),
                          hipMemcpyDeviceToHost, s));
   HIP_TRY(hipMemcpyAsync(w.h_row_err, w.row_err, R * sizeof(uint32_t), hipMemcpyDeviceToHost, s));

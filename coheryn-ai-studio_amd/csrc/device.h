@@ -148,4 +148,24 @@ __host__ __device__ __forceinline__ size_t q8_scale(size_t tile, int nbp, int b,
   return (tile * (size_t)nbp + (size_t)b) * 16 + (size_t)row16;
 }
 
+// Q4_0 weights keep 4 bits per value in the same tile order: lane l holds the
+// 8 values of k-group l/16 of row l%16 for blocks 2p and 2p+1 in 8 bytes
+// (4 per block).  Byte k (0..3) of a block's word holds value k in its low
+// nibble and value k+4 in its high nibble, so one AND and one shift yield the
+// 8 operand bytes in order.  Scales use the Q8_0 scale layout.
+__host__ __device__ __forceinline__ size_t q4_byte(size_t tile, int nbp, int b, int lane, int k) {
+  return ((tile * (size_t)(nbp / 2) + (size_t)(b / 2)) * 64 + (size_t)lane) * 8 +
+         (size_t)(b % 2) * 4 + (size_t)(k % 4);
+}
+
+// One block's 4-byte word -> the 8 signed operand bytes (nibble - 8), as the
+// low 64 bits of an MFMA A/B operand.  Bytewise (n | 0x80) - 8 never borrows
+// across bytes; the final XOR removes the 0x80 bias.
+__device__ __forceinline__ long q4_operand(uint32_t x) {
+  const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
+  const uint32_t a = ((lo | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+  const uint32_t b = ((hi | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+  return (long)(((unsigned long)b << 32) | a);
+}
+
 }  // namespace cohx

@@ -3,7 +3,9 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <map>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "../../include/cohx.h"
@@ -69,6 +71,17 @@ struct Profiler {
   double ms[kCatCount] = {}, bytes[kCatCount] = {}, flops[kCatCount] = {};
 };
 
+// A step's device work depends on these alone (pointers and model dimensions
+// are fixed per context), so one captured graph serves every step with them.
+struct StepKey {
+  uint32_t rows, lanes, kv_grid;
+  bool logits;
+  bool operator<(const StepKey &o) const {
+    return std::tie(rows, lanes, kv_grid, logits) < std::tie(o.rows, o.lanes, o.kv_grid, o.logits);
+  }
+};
+constexpr size_t kMaxGraphs = 64;
+
 }  // namespace cohx
 
 struct cohx_ctx {
@@ -98,8 +111,11 @@ struct cohx_ctx {
   cohx::Workspace ws;
   cohx::Profiler prof;
   std::vector<void *> allocations;
+  bool use_graphs = true;  // replay each step's launches as one captured graph
+  std::map<cohx::StepKey, hipGraphExec_t> graphs;
 };
 
 namespace cohx {
 int fail(cohx_ctx *ctx, int code, const std::string &msg);
+void drop_graphs(cohx_ctx *ctx);
 }

@@ -103,6 +103,13 @@ __global__ __launch_bounds__(256) void k_embed(MatrixView e, const uint32_t *__r
       const float d = h2f(e.ds[q8_scale(mt, e.nbp, b, c)]);
       bad |= !finitef(d);
       v = d * (float)q;
+    } else if (e.dtype == 2) {  // Q4_0: d * (nibble - 8) (quant.rs:97-101)
+      const int mt = tok / 16, c = tok % 16, b = k / 32, g = (k % 32) / 8, j = k % 8;
+      const uint8_t byte = (uint8_t)e.qs[q4_byte(mt, e.nbp, b, g * 16 + c, j)];
+      const int q = (j < 4 ? (byte & 15) : (byte >> 4)) - 8;
+      const float d = h2f(e.ds[q8_scale(mt, e.nbp, b, c)]);
+      bad |= !finitef(d);
+      v = d * (float)q;
     } else {
       v = h2f(e.f16[(size_t)tok * H + k]);
       bad |= !finitef(v);
@@ -269,13 +276,19 @@ struct Q8Regs {
   uint32_t da;
 };
 
-template <int kNM>
+template <int kNM, int kFmt>
 __device__ __forceinline__ void q8_load(Q8Regs<kNM> &r, const MatrixView &w, const ActView &act,
                                         int unit, int nt, int pair, int lane) {
   const int nbp = w.nbp;
 #pragma unroll
-  for (int m = 0; m < kNM; m++)
-    r.a[m] = *reinterpret_cast<const uint4 *>(w.qs + q8_byte(unit * kNM + m, nbp, pair * 2, lane, 0));
+  for (int m = 0; m < kNM; m++) {
+    if constexpr (kFmt == 8) {
+      r.a[m] = *reinterpret_cast<const uint4 *>(w.qs + q8_byte(unit * kNM + m, nbp, pair * 2, lane, 0));
+    } else {
+      const uint2 v = *reinterpret_cast<const uint2 *>(w.qs + q4_byte(unit * kNM + m, nbp, pair * 2, lane, 0));
+      r.a[m] = make_uint4(v.x, v.y, 0u, 0u);
+    }
+  }
   r.b = *reinterpret_cast<const uint4 *>(act.qs + q8_byte(nt, nbp, pair * 2, lane, 0));
   if (lane < 16) {
 #pragma unroll
@@ -294,7 +307,7 @@ __device__ __forceinline__ long hi64(uint4 v) {
   return (long)(((unsigned long)v.w << 32) | v.z);
 }
 
-template <int kEpi, int kNM, int kP>
+template <int kEpi, int kNM, int kP, int kFmt>
 __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int rows_b,
                                                 int n_tiles, MatvecOut o) {
   constexpr int kW = 8, kCB = 2 * kW * kP;  // blocks per chunk: kP pairs per wave
@@ -321,13 +334,13 @@ __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int r
   Q8Regs<kNM> cur[kP], nxt[kP];
 #pragma unroll
   for (int pp = 0; pp < kP; pp++)
-    if (pp * kW + wave < npairs) q8_load(cur[pp], w, act, unit, nt, pp * kW + wave, lane);
+    if (pp * kW + wave < npairs) q8_load<kNM, kFmt>(cur[pp], w, act, unit, nt, pp * kW + wave, lane);
   for (int c = 0; c < nchunks; c++) {
     if (c + 1 < nchunks) {
 #pragma unroll
       for (int pp = 0; pp < kP; pp++) {
         const int pair = (c + 1) * kW * kP + pp * kW + wave;
-        if (pair < npairs) q8_load(nxt[pp], w, act, unit, nt, pair, lane);
+        if (pair < npairs) q8_load<kNM, kFmt>(nxt[pp], w, act, unit, nt, pair, lane);
       }
     }
 #pragma unroll
@@ -340,8 +353,12 @@ __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int r
           const long bop = h ? hi64(cur[pp].b) : lo64(cur[pp].b);
 #pragma unroll
           for (int m = 0; m < kNM; m++) {
-            const v4i s4 = __builtin_amdgcn_mfma_i32_16x16x32_i8(h ? hi64(cur[pp].a[m]) : lo64(cur[pp].a[m]),
-                                                                 bop, zero, 0, 0, 0);
+            long aop;
+            if constexpr (kFmt == 8)
+              aop = h ? hi64(cur[pp].a[m]) : lo64(cur[pp].a[m]);
+            else
+              aop = q4_operand(h ? cur[pp].a[m].y : cur[pp].a[m].x);
+            const v4i s4 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, zero, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; i++)
               s_isum[blk][m * 256 + i * 64 + lane] = (float)s4[i];
@@ -365,8 +382,12 @@ __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int r
       for (int blk = 0; blk < nblk; blk++) {
         const float da = s_da[blk][pcol];
 #pragma unroll
-        for (int m = 0; m < kNM; m++)
-          acc[m] = fmaf(s_isum[blk][m * 256 + t], s_dw[blk][m * 16 + prow] * da, acc[m]);
+        for (int m = 0; m < kNM; m++) {
+          if constexpr (kFmt == 8)
+            acc[m] = fmaf(s_isum[blk][m * 256 + t], s_dw[blk][m * 16 + prow] * da, acc[m]);
+          else
+            acc[m] = fmaf(s_isum[blk][m * 256 + t] * s_dw[blk][m * 16 + prow], da, acc[m]);
+        }
       }
     }
     __syncthreads();
@@ -582,6 +603,24 @@ __device__ __forceinline__ float scale_mul(uint32_t w, uint32_t a) {
   return r;
 }
 
+// Q4_0 chain (quant.rs:286-292): t = f32(isum) * dw rounded once, then
+// acc = fmaf(t, da, acc); the binary16 scale is read from the low (H=0) or
+// high (H=1) half of a packed register by the mixed-precision FMA.
+template <int WH>
+__device__ __forceinline__ float mul_half(float a, uint32_t w) {
+  float r;
+  if constexpr (WH == 0)
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(w));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(w));
+  return r;
+}
+__device__ __forceinline__ float fma_half(float t, uint32_t a, float acc) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(t), "v"(a), "v"(acc));
+  return r;
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
@@ -596,9 +635,10 @@ struct ChainPair {
 
 constexpr int kChainWaves = 4;  // batch groups per workgroup
 
-template <int kEpi, int kNM, int kNN, int kDepth>
+template <int kEpi, int kNM, int kNN, int kDepth, int kFmt>
 __global__ __launch_bounds__(64 * kChainWaves) void k_mv_q8c(MatrixView w, ActView act, int rows_b,
                                                             int n_tiles, MatvecOut o) {
+  constexpr uint32_t kPairBytes = kFmt == 8 ? 1024 : 512;  // weight bytes per tile per block pair
   const int lane = threadIdx.x % kWave;
   const int ng = blockIdx.y * kChainWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int unit = blockIdx.x;
@@ -608,7 +648,7 @@ __global__ __launch_bounds__(64 * kChainWaves) void k_mv_q8c(MatrixView w, ActVi
 #pragma unroll
   for (int m = 0; m < kNM; m++) {
     const int tile = unit * kNM + m;
-    ra[m] = buffer_rsrc(w.qs + (size_t)tile * npairs * 1024, (uint32_t)npairs * 1024);
+    ra[m] = buffer_rsrc(w.qs + (size_t)tile * npairs * kPairBytes, (uint32_t)npairs * kPairBytes);
     rw[m] = buffer_rsrc(w.ds + (size_t)tile * nbp * 16, (uint32_t)nbp * 32);
   }
 #pragma unroll
@@ -622,7 +662,12 @@ __global__ __launch_bounds__(64 * kChainWaves) void k_mv_q8c(MatrixView w, ActVi
   auto load = [&](ChainPair<kNM, kNN> &r, int p) {
 #pragma unroll
     for (int m = 0; m < kNM; m++) {
-      r.a[m] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra[m], voff, p * 1024, 0));
+      if constexpr (kFmt == 8) {
+        r.a[m] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra[m], voff, p * 1024, 0));
+      } else {
+        const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ra[m], lane * 8, p * 512, 0));
+        r.a[m] = make_uint4(v.x, v.y, 0u, 0u);
+      }
       r.dw[m][0] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw[m], woff, p * 64, 0));
       r.dw[m][1] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw[m], woff + 32, p * 64, 0));
     }
@@ -655,16 +700,27 @@ __global__ __launch_bounds__(64 * kChainWaves) void k_mv_q8c(MatrixView w, ActVi
         for (int h = 0; h < 2; h++) {
 #pragma unroll
           for (int m = 0; m < kNM; m++) {
-            const long aop = h ? hi64(r.a[m]) : lo64(r.a[m]);
+            long aop;
+            if constexpr (kFmt == 8)
+              aop = h ? hi64(r.a[m]) : lo64(r.a[m]);
+            else
+              aop = q4_operand(h ? r.a[m].y : r.a[m].x);
 #pragma unroll
             for (int n = 0; n < kNN; n++) {
               const v4i sum = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, h ? hi64(r.b[n]) : lo64(r.b[n]),
                                                                     zero, 0, 0, 0);
               const uint2 s2 = r.dw[m][h];
-              const float sc[4] = {scale_mul<0, 0>(s2.x, r.da[n][h]), scale_mul<1, 0>(s2.x, r.da[n][h]),
-                                   scale_mul<0, 0>(s2.y, r.da[n][h]), scale_mul<1, 0>(s2.y, r.da[n][h])};
+              if constexpr (kFmt == 8) {
+                const float sc[4] = {scale_mul<0, 0>(s2.x, r.da[n][h]), scale_mul<1, 0>(s2.x, r.da[n][h]),
+                                     scale_mul<0, 0>(s2.y, r.da[n][h]), scale_mul<1, 0>(s2.y, r.da[n][h])};
 #pragma unroll
-              for (int i = 0; i < 4; i++) acc[m][n][i] = fmaf((float)sum[i], sc[i], acc[m][n][i]);
+                for (int i = 0; i < 4; i++) acc[m][n][i] = fmaf((float)sum[i], sc[i], acc[m][n][i]);
+              } else {
+                const float t[4] = {mul_half<0>((float)sum[0], s2.x), mul_half<1>((float)sum[1], s2.x),
+                                    mul_half<0>((float)sum[2], s2.y), mul_half<1>((float)sum[3], s2.y)};
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[m][n][i] = fma_half(t[i], r.da[n][h], acc[m][n][i]);
+              }
             }
           }
         }
@@ -1240,7 +1296,7 @@ void launch_quant_act(hipStream_t s, int rows, const float *src, int K, int act_
     launch_k(k_quant_act<1>, dim3(rows), dim3(256), 0, s, src, K, nbp, act, row_err);
 }
 
-template <int kEpi, int kNM>
+template <int kEpi, int kNM, int kFmt>
 static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
                   const MatvecOut &o) {
   const int units = w.mtiles / kNM;
@@ -1251,19 +1307,19 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
     constexpr int kNN = 2;
     const int groups = (n_tiles + kNN - 1) / kNN;
     const int waves = groups < kChainWaves ? groups : kChainWaves;
-    launch_k((k_mv_q8c<kEpi, kNM, kNN, 4>), dim3(units, (groups + kChainWaves - 1) / kChainWaves),
+    launch_k((k_mv_q8c<kEpi, kNM, kNN, 4, kFmt>), dim3(units, (groups + kChainWaves - 1) / kChainWaves),
              dim3(64 * waves), 0, s, w, act, rows_b, n_tiles, o);
   } else {
     // blocks per LDS chunk: 32 covers K <= 1024 in one chunk, 64 keeps long K to few chunks
     const int groups = (units + 7) / 8;
     if (kNM == 1 && w.nbp > 32)
-      launch_k((k_mv_q8s<kEpi, kNM, 4>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
+      launch_k((k_mv_q8s<kEpi, kNM, 4, kFmt>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
                rows_b, n_tiles, o);
     else if (kNM == 1)
-      launch_k((k_mv_q8s<kEpi, kNM, 2>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
+      launch_k((k_mv_q8s<kEpi, kNM, 2, kFmt>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
                rows_b, n_tiles, o);
     else
-      launch_k((k_mv_q8s<kEpi, kNM, 1>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
+      launch_k((k_mv_q8s<kEpi, kNM, 1, kFmt>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
                rows_b, n_tiles, o);
   }
 }
@@ -1279,10 +1335,17 @@ void launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActVi
                    int rows_b, const MatvecOut &o) {
   if (w.dtype == 8) {
     switch (epi) {
-      case kEpiStore: mv_q8<kEpiStore, 1>(s, w, act, rows_b, o); break;
-      case kEpiResidual: mv_q8<kEpiResidual, 1>(s, w, act, rows_b, o); break;
-      case kEpiSwiglu: mv_q8<kEpiSwiglu, 2>(s, w, act, rows_b, o); break;
-      case kEpiArgmax: mv_q8<kEpiArgmax, 1>(s, w, act, rows_b, o); break;
+      case kEpiStore: mv_q8<kEpiStore, 1, 8>(s, w, act, rows_b, o); break;
+      case kEpiResidual: mv_q8<kEpiResidual, 1, 8>(s, w, act, rows_b, o); break;
+      case kEpiSwiglu: mv_q8<kEpiSwiglu, 2, 8>(s, w, act, rows_b, o); break;
+      case kEpiArgmax: mv_q8<kEpiArgmax, 1, 8>(s, w, act, rows_b, o); break;
+    }
+  } else if (w.dtype == 2) {
+    switch (epi) {
+      case kEpiStore: mv_q8<kEpiStore, 1, 2>(s, w, act, rows_b, o); break;
+      case kEpiResidual: mv_q8<kEpiResidual, 1, 2>(s, w, act, rows_b, o); break;
+      case kEpiSwiglu: mv_q8<kEpiSwiglu, 2, 2>(s, w, act, rows_b, o); break;
+      case kEpiArgmax: mv_q8<kEpiArgmax, 1, 2>(s, w, act, rows_b, o); break;
     }
   } else {
     switch (epi) {

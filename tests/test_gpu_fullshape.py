@@ -122,3 +122,42 @@ def test_f16_continuous_batch_greedy_tokens():
                 o.forward_batch([sess], [tok])
         print(f"prompt {len(p)}: gpu {st.token_ids()} oracle {ids}", flush=True)
         assert st.token_ids() == ids
+
+
+def test_q4_0_shared_prefix_groups_decode():
+    """Config 4's form at the full shape, shortened so the oracle finishes in
+    seconds: Q4_0 weights; two groups of lanes, each forked from one 48-token
+    prefix (three full pages shared, copy on write), decoding together.  Every
+    lane's logits equal the oracle's unshared recomputation bit for bit, and
+    greedy tokens match."""
+    print("case: full-shape Q4_0 shared-prefix groups", flush=True)
+    c, t = synth.in_memory(FULL, "q4_0", seed=23)
+    m = cohx.Model(c, t, max_lanes=8, max_rows=128, max_seqs=8, max_context=128)
+    o = orc.Model(c, t, threads=16)
+    rng = np.random.default_rng(4)
+    P, per_group = 48, 2
+    prefixes = [[int(v) for v in rng.integers(0, c["vocabulary"], P)] for _ in range(2)]
+    bases = [m.seq_alloc() for _ in prefixes]
+    res = m.step([dict(seq=b, tokens=p) for b, p in zip(bases, prefixes)])
+    assert all(r["status"] == 0 for r in res)
+    lanes = [m.seq_fork(b, P) for b in bases for _ in range(per_group)]
+    for b in bases:
+        m.seq_free(b)
+    sessions = [o.session(128) for _ in lanes]
+    for j in range(P):
+        o.forward_batch(sessions, [prefixes[i // per_group][j] for i in range(len(lanes))])
+    toks = [int(v) for v in rng.integers(0, c["vocabulary"], len(lanes))]
+    bits = 0
+    for step in range(2):
+        res = m.step([dict(seq=a, tokens=[tk], logits=True) for a, tk in zip(lanes, toks)])
+        o.forward_batch(sessions, toks)
+        nxt = []
+        for i, r in enumerate(res):
+            assert r["status"] == 0
+            bits += check(r["logits"], sessions[i].logits(), 3e-2, f"step {step} lane {i}")
+            assert r["argmax"] == orc.Sampler().sample(sessions[i].logits())[1]
+            nxt.append(r["argmax"])
+        toks = nxt
+    for a in lanes[1:per_group]:
+        assert np.array_equal(m.seq_read_kv(a, 7)[:P], m.seq_read_kv(lanes[0], 7)[:P])
+    assert bits == 0
