@@ -603,17 +603,20 @@ int cohx_seq_fill_synthetic(cohx_ctx *ctx, uint32_t seq, uint32_t rows, uint64_t
   if (!ctx || !valid_seq(ctx, seq)) return COHX_INVALID_REQUEST;
   Sequence &q = ctx->seqs[seq];
   if (rows > q.capacity) return fail(ctx, COHX_RESOURCE, "rows exceed the sequence capacity");
+  if (rows < q.length) return fail(ctx, COHX_INVALID_REQUEST, "rows below the sequence length");
   HIP_TRY(hipSetDevice(ctx->device));
-  int rc = ensure_pages(ctx, seq, 0, rows);
+  const uint32_t from = q.length;
+  int rc = ensure_pages(ctx, seq, from, rows);
   if (rc) return rc;
-  if (rows) {
+  if (rows > from) {
     int32_t *pages = nullptr;
     HIP_TRY(hipMalloc(&pages, q.pages.size() * sizeof(int32_t)));
     hipError_t e = hipMemcpy(pages, q.pages.data(), q.pages.size() * sizeof(int32_t),
                              hipMemcpyHostToDevice);
     if (e == hipSuccess) {
       launch_fill_synthetic(ctx->stream, ctx->kpool, ctx->vpool, ctx->layer_stride,
-                            (int)ctx->desc.layers, pages, (int)rows, (int)ctx->desc.kv_heads,
+                            (int)ctx->desc.layers, pages, (int)from, (int)rows,
+                            (int)ctx->desc.kv_heads,
                             (int)ctx->desc.head_dim, seed, stream);
       e = hipStreamSynchronize(ctx->stream);
     }

@@ -86,7 +86,7 @@ void launch_attn_combine(hipStream_t s, int rows, const StepDims &d, const uint3
                          const double *partial, int act_dtype, int nbp, ActView act,
                          uint32_t *row_err);
 void launch_fill_synthetic(hipStream_t s, float *kpool, float *vpool, size_t layer_stride,
-                           int layers, const int32_t *pages, int rows, int NKV, int D,
+                           int layers, const int32_t *pages, int from, int rows, int NKV, int D,
                            uint64_t seed, uint32_t stream);
 void launch_copy_page(hipStream_t s, float *kpool, float *vpool, size_t layer_stride, int layers,
                       int page_floats, int src_page, int dst_page);

@@ -1223,13 +1223,13 @@ __device__ __forceinline__ float synthetic_kv(uint64_t seed, uint32_t stream, ui
 }
 
 __global__ void k_fill_synthetic(float *kpool, float *vpool, size_t layer_stride,
-                                 const int32_t *__restrict__ pages, int rows, int NKV, int D,
-                                 uint64_t seed, uint32_t stream) {
+                                 const int32_t *__restrict__ pages, int from, int rows, int NKV,
+                                 int D, uint64_t seed, uint32_t stream) {
   const int layer = blockIdx.y;
-  const size_t total = (size_t)rows * NKV * D;
+  const size_t total = (size_t)(rows - from) * NKV * D;
   for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (size_t)gridDim.x * blockDim.x) {
-    const int pos = (int)(idx / ((size_t)NKV * D));
+    const int pos = from + (int)(idx / ((size_t)NKV * D));
     const int e = (int)(idx % ((size_t)NKV * D));
     const int g = e / D, j = e % D;
     const size_t at = (size_t)layer * layer_stride +
@@ -1456,14 +1456,14 @@ void launch_attn_combine(hipStream_t s, int rows, const StepDims &d, const uint3
 }
 
 void launch_fill_synthetic(hipStream_t s, float *kpool, float *vpool, size_t layer_stride,
-                           int layers, const int32_t *pages, int rows, int NKV, int D,
+                           int layers, const int32_t *pages, int from, int rows, int NKV, int D,
                            uint64_t seed, uint32_t stream) {
-  const size_t total = (size_t)rows * NKV * D;
+  const size_t total = (size_t)(rows - from) * NKV * D;
   int blocks = (int)((total + 255) / 256);
   if (blocks > 1024) blocks = 1024;
   if (blocks < 1) blocks = 1;
   launch_k(k_fill_synthetic, dim3(blocks, layers), dim3(256), 0, s, kpool, vpool,
-                     layer_stride, pages, rows, NKV, D, seed, stream);
+                     layer_stride, pages, from, rows, NKV, D, seed, stream);
 }
 
 void launch_copy_page(hipStream_t s, float *kpool, float *vpool, size_t layer_stride, int layers,

@@ -94,9 +94,11 @@ uint32_t cohx_seq_pages(const cohx_ctx *ctx, uint32_t seq, int32_t *out, uint32_
 /* Copy one layer's K (values=0) or V (values=1) rows [0, length) to host,
  * kv_heads*head_dim floats per row. */
 int cohx_seq_read_kv(cohx_ctx *ctx, uint32_t seq, uint32_t layer, int values, float *out);
-/* Benchmark/test utility with no engine counterpart: fill rows [0, rows) of
- * every layer with seeded values hash(seed, stream, layer, K/V, pos, elem) on
- * the device and set the length to `rows`. */
+/* Benchmark/test utility with no engine counterpart: fill rows [length, rows)
+ * of every layer with seeded values hash(seed, stream, layer, K/V, pos, elem)
+ * on the device and set the length to `rows` (rows >= length; on a fresh
+ * sequence that is rows [0, rows)).  Appending after a fork leaves the
+ * shared prefix pages untouched. */
 int cohx_seq_fill_synthetic(cohx_ctx *ctx, uint32_t seq, uint32_t rows, uint64_t seed,
                             uint32_t stream);
 
