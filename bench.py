@@ -211,6 +211,82 @@ def run_c4(seed, steps, warmup):
             "replay_same_tokens": same}
 
 
+C3_CHUNKS, C3_DECODE, C3_CONTEXT = 8, 56, 4608
+MFMA_F16_PEAK = 2.5e15
+
+
+def run_c3(seed, steps, warmup):
+    """F16 weights; every step packs 8 prompt chunks of
+    U[128,512] tokens (each sequence continuing its prompt) with 56 greedy
+    decode rows over KV U[256,4096].  Linears of packed batches run on the
+    matrix cores (f32 sums; tolerance-checked by the tests).  Reports packed
+    rows/s and the linears' achieved TFLOP/s against the dense fp16 peak."""
+    path = model_file(seed, "f16")
+    meta, tensors = gguf.read(path)
+    cfg = gguf.qwen2_config(meta)
+    n = C3_CHUNKS + C3_DECODE
+    rng = np.random.default_rng(seed + 3)
+    total = warmup + steps
+    chunk_len = rng.integers(128, 513, (total, C3_CHUNKS))
+    max_rows = int(chunk_len.sum(axis=1).max()) + C3_DECODE
+    model = cohx.Model(cfg, tensors, max_lanes=n, max_rows=max_rows, max_seqs=n, max_context=C3_CONTEXT)
+    pre = [model.seq_alloc() for _ in range(C3_CHUNKS)]
+    dec = []
+    kv = [int(v) for v in rng.integers(256, 4097 - total - 8, C3_DECODE)]
+    for i, k in enumerate(kv):
+        s = model.seq_alloc()
+        model.seq_fill_synthetic(s, k, seed, 500 + i)
+        dec.append(s)
+    chunks = [[[int(v) for v in rng.integers(0, cfg["vocabulary"], chunk_len[t, j])]
+               for j in range(C3_CHUNKS)] for t in range(total)]
+    dec_tok = [int(v) for v in rng.integers(0, cfg["vocabulary"], C3_DECODE)]
+
+    def one_step(t, toks):
+        lanes = [dict(seq=s, tokens=chunks[t][j]) for j, s in enumerate(pre)]
+        lanes += [dict(seq=s, tokens=[tk]) for s, tk in zip(dec, toks)]
+        res = model.step(lanes)
+        if any(r["status"] for r in res):
+            raise RuntimeError(f"lane failure {[r['status'] for r in res]}")
+        return [r["argmax"] for r in res[C3_CHUNKS:]]
+
+    for t in range(warmup):
+        dec_tok = one_step(t, dec_tok)
+    lengths = [model.seq_length(s) for s in pre + dec]
+    start, trace = list(dec_tok), []
+    rows = int(sum(chunk_len[t].sum() for t in range(warmup, total))) + C3_DECODE * steps
+    t0 = time.perf_counter()
+    for t in range(warmup, total):
+        dec_tok = one_step(t, dec_tok)
+        trace.append(dec_tok)
+    elapsed = time.perf_counter() - t0
+    for s, k in zip(pre + dec, lengths):
+        model.seq_truncate(s, k)
+    model.profile(True)
+    toks, same = start, True
+    for i, t in enumerate(range(warmup, total)):
+        toks = one_step(t, toks)
+        same &= toks == trace[i]
+    stats = model.profile_read()
+    model.profile(False)
+    lin = [x for x in stats if x["name"] in ("matvec_qkv", "matvec_o_residual", "matvec_gate_up_swiglu",
+                                            "matvec_down_residual")]
+    lin_flops = sum(x["flops"] for x in lin)
+    lin_ms = sum(x["total_ms"] for x in lin)
+    ms = elapsed * 1e3 / steps
+    tflops = lin_flops / (lin_ms / 1e3) / 1e12 if lin_ms else 0.0
+    log(f"[bench] c3: {rows / elapsed:.0f} packed rows/s, {ms:.2f} ms/step, linears "
+        f"{tflops:.0f} TFLOP/s, replay same tokens: {same}")
+    return {"workload": "Qwen2.5-0.5B-shape F16, each step 8 prompt chunks U[128,512] + 56 decode "
+                        "rows over KV U[256,4096]; linears on the matrix cores (f32 sums)",
+            "value": rows / elapsed, "unit": "packed rows/s", "ms_per_step": ms, "steps": steps,
+            "mean_rows_per_step": rows / steps,
+            "roofline": {"bound": "mfma", "kernel": "linears (k_gemm_f16)",
+                         "achieved": tflops, "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
+                         "frac": tflops * 1e12 / MFMA_F16_PEAK},
+            "kernels": {x["name"]: {"ms_per_step": x["total_ms"] / steps} for x in stats if x["launches"]},
+            "replay_same_tokens": same}
+
+
 def measured_traffic(category, lanes):
     """HBM bytes per launch of `category`'s kernel from the committed counter
     summary, or None when it does not cover this kernel and workload."""
@@ -361,6 +437,7 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-c4", action="store_true", help="skip the Q4_0 shared-prefix workload")
+    ap.add_argument("--no-c3", action="store_true", help="skip the F16 packed-prefill workload")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 1 GiB device-to-device 4 times (counter calibration)")
     ap.add_argument("--summarize-counters", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
@@ -427,6 +504,8 @@ def main():
     if not args.no_c4:
         del model
         line["c4"] = run_c4(args.seed, 128, args.warmup)
+    if not args.no_c3:
+        line["c3"] = run_c3(args.seed, 8, 2)
     if not args.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)
         n_cpu = min(16, args.lanes)

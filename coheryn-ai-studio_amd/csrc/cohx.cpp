@@ -217,6 +217,8 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   ctx->device = device;
   // COHX_GRAPHS=0 issues every launch directly (graphs are on by default)
   if (const char *g = std::getenv("COHX_GRAPHS")) ctx->use_graphs = std::strcmp(g, "0") != 0;
+  // COHX_PREFILL_MFMA=0 keeps tall F16 batches on the exact (f64-sum) kernels
+  if (const char *g = std::getenv("COHX_PREFILL_MFMA")) ctx->prefill_mfma = std::strcmp(g, "0") != 0;
   auto bail = [&](int rc) {
     cohx_destroy(ctx);
     return rc;
@@ -818,6 +820,7 @@ extern "C" uint32_t cohx_profile_read(const cohx_ctx *ctx, cohx_kernel_stat *out
 // sizes the attention grids; blocks past a row's length exit at once.
 int enqueue_device_step(cohx_ctx *ctx, const Prepared &p, int kv_grid, bool any_logits) {
   const cohx_model_desc &d = ctx->desc;
+  set_prefill_mfma(ctx->prefill_mfma);
   const int pk = prof_begin(ctx, kCatPack, 0.0, 0.0);
   enqueue_pack(ctx, (int)p.included.size());
   prof_end(ctx, pk);
@@ -907,17 +910,10 @@ int enqueue_device_step(cohx_ctx *ctx, const Prepared &p, int kv_grid, bool any_
   e = prof_begin(ctx, kCatMvHead,
                  matrix_pass_bytes(head.view, NL, 0, false) + (any_logits ? (double)NL * d.vocabulary * 4 : 0.0) + NL * 8.0,
                  2.0 * NL * d.vocabulary * H);
-  if (head.view.dtype != 1) {
-    launch_matvec(s, kEpiArgmax, head.view, act, NL,
-                  MatvecOut{nullptr, 0, w.argmax_part, any_logits ? w.logits : nullptr, w.row_err,
-                            w.lane_last});
-    launch_argmax_reduce(s, NL, w.argmax_part, head.view.mtiles, w.argmax);
-  } else {
-    launch_fill_u64(s, w.argmax, NL, 0ull);
-    launch_matvec(s, kEpiArgmax, head.view, act, NL,
-                  MatvecOut{nullptr, 0, w.argmax, any_logits ? w.logits : nullptr, w.row_err,
-                            w.lane_last});
-  }
+  launch_matvec(s, kEpiArgmax, head.view, act, NL,
+                MatvecOut{nullptr, 0, w.argmax_part, any_logits ? w.logits : nullptr, w.row_err,
+                          w.lane_last});
+  launch_argmax_reduce(s, NL, w.argmax_part, head.view.mtiles, w.argmax);
   prof_end(ctx, e);
   HIP_TRY(hipGetLastError());
   return COHX_OK;

@@ -111,7 +111,8 @@ struct cohx_ctx {
   cohx::Workspace ws;
   cohx::Profiler prof;
   std::vector<void *> allocations;
-  bool use_graphs = true;  // replay each step's launches as one captured graph
+  bool use_graphs = true;    // replay each step's launches as one captured graph
+  bool prefill_mfma = true;  // F16 batches of 128+ rows on the matrix cores
   std::map<cohx::StepKey, hipGraphExec_t> graphs;
 };
 

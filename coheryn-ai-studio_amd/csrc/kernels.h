@@ -38,8 +38,8 @@ enum Epilogue { kEpiStore = 0, kEpiResidual = 1, kEpiSwiglu = 2, kEpiArgmax = 3 
 struct MatvecOut {
   float *out;          // kEpiStore: [rows_b][ld]; kEpiResidual: x [rows_b][ld]; kEpiSwiglu: h
   int ld;
-  unsigned long long *argmax;  // kEpiArgmax: Q8_0 -> per (batch row, tile) partial keys
-                               // [rows_b][mtiles]; F16 -> per batch row key (atomic max)
+  unsigned long long *argmax;  // kEpiArgmax: per (batch row, 16-row tile) partial keys
+                               // [rows_b][mtiles], reduced by launch_argmax_reduce
   float *logits;               // kEpiArgmax: optional [rows_b][V] (nullptr: none)
   uint32_t *row_err;           // per batch row error bits
   const uint32_t *err_rows;    // batch row -> packed row index for error bits (nullptr: same)
@@ -57,6 +57,9 @@ void launch_norm_act(hipStream_t s, int rows, const float *x, const uint32_t *in
                      uint32_t *row_err);
 void launch_quant_act(hipStream_t s, int rows, const float *src, int K, int act_dtype, int nbp,
                       ActView act, uint32_t *row_err);
+// Packed F16 batches of 128+ rows on the matrix cores (f32 sums, within tolerance
+// of the reference's f64 sums) or always on the exact kernels.
+void set_prefill_mfma(bool on);
 // Timing events for the next launches (see the launch helper); both null ends it.
 void set_launch_events(hipEvent_t start, hipEvent_t stop);
 

@@ -27,6 +27,7 @@ namespace cohx {
 // ---------------------------------------------------------------------------
 namespace {
 thread_local hipEvent_t t_ev_start = nullptr, t_ev_stop = nullptr;
+thread_local bool g_prefill_mfma = true;  // set per step from the context
 
 template <typename F, typename... Args>
 void launch_k(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args... args) {
@@ -38,6 +39,8 @@ void launch_k(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args
   }
 }
 }  // namespace
+
+void set_prefill_mfma(bool on) { g_prefill_mfma = on; }
 
 void set_launch_events(hipEvent_t start, hipEvent_t stop) {
   t_ev_start = start;
@@ -321,7 +324,6 @@ __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int r
   const int nt = rem / 8, unit = group * 8 + rem % 8;
   if (unit >= units) return;
   const int nbp = w.nbp, npairs = nbp / 2, nchunks = (nbp + kCB - 1) / kCB;
-  const int rsub = 4 * (lane / 16);
   const v4i zero = {0, 0, 0, 0};
   // phase-2 ownership: thread t < 256 owns the output the matrix-core layout
   // puts in lane t%64, slot t/64: row 4*((t%64)/16) + t/64, batch column t%16.
@@ -863,6 +865,296 @@ __global__ __launch_bounds__(256) void k_mv_f16(MatrixView w, ActView act, int r
 }
 
 // ---------------------------------------------------------------------------
+// F16 matvec for batches of 16..127 rows, in the reference's exact order: lane
+// = batch row, each dot one sequential f64 chain over k from -0.0
+// (cpu.rs:31-35 over round_f16 operands), f32 result.  A wave owns 4 output
+// rows (4 gate + 4 up rows for SwiGLU) and one pass of up to 64 batch rows;
+// the weight rows are wave-uniform loads, the activation rows per lane.  The
+// argmax epilogue leaves one key per (batch row, 16-row tile) for
+// k_argmax_reduce.
+// ---------------------------------------------------------------------------
+template <int kEpi>
+__global__ __launch_bounds__(256) void k_mv_f16s(MatrixView w, ActView act, int rows_b,
+                                                 MatvecOut o) {
+  constexpr int kQ = kEpi == kEpiSwiglu ? 8 : 4;
+  __shared__ unsigned long long s_key[4][kWave];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int out_rows = kEpi == kEpiSwiglu ? w.rows / 2 : w.rows;
+  const int o0 = (blockIdx.x * 4 + wave) * 4;
+  const int r = blockIdx.y * kWave + lane;
+  const int K = w.K;
+  const int rr = min(r, rows_b - 1);
+  const uint16_t *xr = act.f16 + (size_t)rr * K;
+  const uint16_t *wq[kQ];
+#pragma unroll
+  for (int q = 0; q < kQ; q++) {
+    int row = o0 + (q % 4);
+    row = min(row, out_rows - 1);
+    if (kEpi == kEpiSwiglu && q >= 4) row += out_rows;
+    wq[q] = w.f16 + (size_t)row * K;
+  }
+  double acc[kQ];
+#pragma unroll
+  for (int q = 0; q < kQ; q++) acc[q] = -0.0;
+  for (int k0 = 0; k0 < K; k0 += 8) {
+    const uint4 xv = *reinterpret_cast<const uint4 *>(xr + k0);
+    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+    uint4 wv[kQ];
+#pragma unroll
+    for (int q = 0; q < kQ; q++) wv[q] = *reinterpret_cast<const uint4 *>(wq[q] + k0);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float a = h2f((uint16_t)(xw[e / 2] >> (16 * (e % 2))));
+#pragma unroll
+      for (int q = 0; q < kQ; q++) {
+        const uint32_t ww[4] = {wv[q].x, wv[q].y, wv[q].z, wv[q].w};
+        acc[q] += (double)(h2f((uint16_t)(ww[e / 2] >> (16 * (e % 2)))) * a);
+      }
+    }
+  }
+  const bool rvalid = r < rows_b;
+  const int er = (rvalid && o.err_rows) ? (int)o.err_rows[r] : r;
+  bool bad = false;
+  if (kEpi == kEpiArgmax) {
+    unsigned long long best = 0ull;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int row = o0 + q;
+      if (!rvalid || row >= w.rows) continue;
+      const float v = (float)acc[q];
+      bad |= !finitef(v);
+      if (o.logits) o.logits[(size_t)r * w.rows + row] = v;
+      const unsigned long long key = argmax_key(v, row);
+      best = key > best ? key : best;
+    }
+    s_key[wave][lane] = best;
+    __syncthreads();
+    if (wave == 0 && rvalid) {
+      unsigned long long b = s_key[0][lane];
+#pragma unroll
+      for (int i = 1; i < 4; i++) b = s_key[i][lane] > b ? s_key[i][lane] : b;
+      o.argmax[(size_t)r * w.mtiles + blockIdx.x] = b;
+    }
+  } else if (rvalid) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int row = o0 + q;
+      if (row >= out_rows) continue;
+      float v = (float)acc[q];
+      float *p = o.out + (size_t)r * o.ld + row;
+      if (kEpi == kEpiSwiglu) {
+        const float u = (float)acc[q + 4];
+        bad |= !finitef(v) || !finitef(u);
+        *p = (v / (1.0f + exp_f32(-v))) * u;
+      } else {
+        bad |= !finitef(v);
+        *p = kEpi == kEpiResidual ? *p + v : v;
+      }
+    }
+  }
+  if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
+}
+
+// ---------------------------------------------------------------------------
+// F16 LM head with argmax: the same per-output arithmetic as k_mv_f16 (f64
+// per lane in element order, fixed butterfly), 16 vocabulary rows per
+// workgroup (4 per wave); each batch row's best key over the 16 rows goes to
+// part[r][tile] for k_argmax_reduce, so no output contends on an atomic.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_head_f16(MatrixView w, ActView act, int rows_b,
+                                                  MatvecOut o) {
+  __shared__ unsigned long long s_key[4];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int row0 = blockIdx.x * 16 + wave * 4;
+  const int K = w.K, units = w.mtiles;
+  for (int r = 0; r < rows_b; r++) {
+    const uint16_t *ar = act.f16 + (size_t)r * K;
+    double acc[4] = {-0.0, -0.0, -0.0, -0.0};
+    for (int k = lane; k < K; k += kWave) {
+      const float a = h2f(ar[k]);
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        if (row0 + q < w.rows) acc[q] += (double)(h2f(w.f16[(size_t)(row0 + q) * K + k]) * a);
+    }
+    const int er = o.err_rows ? (int)o.err_rows[r] : r;
+    unsigned long long best = 0ull;
+    bool bad = false;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const float v = (float)wave_sum_f64(acc[q]);
+      const int row = row0 + q;
+      if (row >= w.rows) continue;
+      bad |= !finitef(v);
+      if (o.logits && lane == 0) o.logits[(size_t)r * w.rows + row] = v;
+      const unsigned long long key = argmax_key(v, row);
+      best = key > best ? key : best;
+    }
+    if (bad && lane == 0) atomicOr(&o.row_err[er], kErrNonFinite);
+    if (lane == 0) s_key[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      unsigned long long b = s_key[0];
+#pragma unroll
+      for (int i = 1; i < 4; i++) b = s_key[i] > b ? s_key[i] : b;
+      o.argmax[(size_t)r * units + blockIdx.x] = b;
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Packed-prefill F16 linear on the matrix cores: out[r][f] = sum_k x[r][k] *
+// w[f][k] over binary16 operands (the activations already rounded to
+// binary16, as the reference rounds them, cpu.rs:37-48), f32 accumulation in
+// v_mfma_f32_16x16x32_f16 order.  The reference sums these exact products in
+// f64 (cpu.rs:31-35); this regime differs from it by f32 rounding of the
+// partial sums and is held to a tolerance, while decode batches keep the
+// exact kernels.  A workgroup (4 waves) owns 128 features x 128 rows; wave
+// (wf, wr) computes features wf*64.. and rows wr*64.. as 4x4 MFMA tiles.  K is
+// staged through LDS in steps of 32, double-buffered, with the next step's
+// global loads in flight during the MFMAs.  For the SwiGLU epilogue the
+// workgroup's feature tile is 64 gate rows and the 64 matching up rows; the
+// up waves hand their sums to the gate waves through LDS.
+// ---------------------------------------------------------------------------
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+constexpr int kGemmBM = 128, kGemmBK = 32, kGemmLds = 40;  // LDS row: 32 halves + 8 pad
+
+template <int kEpi>
+__global__ __launch_bounds__(256) void k_gemm_f16(MatrixView w, const uint16_t *__restrict__ x,
+                                                  int rows_b, MatvecOut o) {
+  // one LDS block: [weights buf 0 | weights buf 1 | rows buf 0 | rows buf 1];
+  // the SwiGLU exchange reuses it from the start after the K loop
+  constexpr int kTile = kGemmBM * kGemmLds;
+  __shared__ __align__(16) uint16_t s_mem[4 * kTile];
+  static_assert(sizeof(s_mem) >= 2 * 16 * 4 * 64 * sizeof(float), "LDS for the SwiGLU exchange");
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int wf = wave / 2, wr = wave % 2;
+  const int K = w.K, nk = K / kGemmBK;
+  const int out_rows = kEpi == kEpiSwiglu ? w.rows / 2 : w.rows;
+  const int f0 = blockIdx.x * (kEpi == kEpiSwiglu ? kGemmBM / 2 : kGemmBM);
+  const int r0 = blockIdx.y * kGemmBM;
+  // global -> LDS: each thread moves 2 x 16 bytes of each operand per K step
+  int wrow[2], xrow[2], seg[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int idx = tid + 256 * i, row = idx / 4;
+    seg[i] = idx % 4;
+    int f;
+    if (kEpi == kEpiSwiglu)
+      f = row < 64 ? f0 + row : out_rows + f0 + (row - 64);
+    else
+      f = f0 + row;
+    wrow[i] = min(f, w.rows - 1);
+    xrow[i] = min(r0 + row, rows_b - 1);
+  }
+  const uint16_t *wp0 = w.f16 + (size_t)wrow[0] * K + seg[0] * 8;
+  const uint16_t *wp1 = w.f16 + (size_t)wrow[1] * K + seg[1] * 8;
+  const uint16_t *xp0 = x + (size_t)xrow[0] * K + seg[0] * 8;
+  const uint16_t *xp1 = x + (size_t)xrow[1] * K + seg[1] * 8;
+  const int so0 = (tid / 4) * kGemmLds + seg[0] * 8, so1 = ((tid + 256) / 4) * kGemmLds + seg[1] * 8;
+  uint4 gw0, gw1, gx0, gx1;
+#define GEMM_FETCH(ks)                                                         \
+  do {                                                                         \
+    gw0 = *reinterpret_cast<const uint4 *>(wp0 + (size_t)(ks) * kGemmBK);      \
+    gw1 = *reinterpret_cast<const uint4 *>(wp1 + (size_t)(ks) * kGemmBK);      \
+    gx0 = *reinterpret_cast<const uint4 *>(xp0 + (size_t)(ks) * kGemmBK);      \
+    gx1 = *reinterpret_cast<const uint4 *>(xp1 + (size_t)(ks) * kGemmBK);      \
+  } while (0)
+#define GEMM_STASH(buf)                                                        \
+  do {                                                                         \
+    *reinterpret_cast<uint4 *>(&s_mem[(buf) * kTile + so0]) = gw0;                          \
+    *reinterpret_cast<uint4 *>(&s_mem[(buf) * kTile + so1]) = gw1;                          \
+    *reinterpret_cast<uint4 *>(&s_mem[(2 + (buf)) * kTile + so0]) = gx0;                          \
+    *reinterpret_cast<uint4 *>(&s_mem[(2 + (buf)) * kTile + so1]) = gx1;                          \
+  } while (0)
+  float4v acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; a++)
+#pragma unroll
+    for (int b = 0; b < 4; b++) acc[a][b] = float4v{0.f, 0.f, 0.f, 0.f};
+  GEMM_FETCH(0);
+  GEMM_STASH(0);
+  __syncthreads();
+  const int koff = 8 * (lane / 16), lr = lane % 16;
+  for (int ks = 0; ks < nk; ks++) {
+    const int buf = ks & 1;
+    if (ks + 1 < nk) GEMM_FETCH(ks + 1);
+    half8 af[4], bf[4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+      af[a] = *reinterpret_cast<const half8 *>(&s_mem[(buf) * kTile + (wf * 64 + a * 16 + lr) * kGemmLds + koff]);
+#pragma unroll
+    for (int b = 0; b < 4; b++)
+      bf[b] = *reinterpret_cast<const half8 *>(&s_mem[(2 + (buf)) * kTile + (wr * 64 + b * 16 + lr) * kGemmLds + koff]);
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+      for (int b = 0; b < 4; b++)
+        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bf[b], acc[a][b], 0, 0, 0);
+    if (ks + 1 < nk) GEMM_STASH(buf ^ 1);
+    __syncthreads();
+  }
+#undef GEMM_FETCH
+#undef GEMM_STASH
+  // ---- epilogue: lane holds features (tile row) 4*(lane/16)+i of rows (tile col) lane%16
+  if (kEpi == kEpiSwiglu) {
+    float *s_up = reinterpret_cast<float *>(s_mem);  // 2 x 16 x 4 x 64 floats = 32 KiB
+    if (wf == 1) {
+#pragma unroll
+      for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) s_up[((wr * 16 + a * 4 + b) * 4 + i) * 64 + lane] = acc[a][b][i];
+    }
+    __syncthreads();
+    if (wf == 1) return;
+  }
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    const int r = r0 + wr * 64 + b * 16 + lr;
+    if (r >= rows_b) continue;
+    const int er = o.err_rows ? (int)o.err_rows[r] : r;
+    bool bad = false;
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+      const int fb = f0 + wf * 64 + a * 16 + 4 * (lane / 16);
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        v[i] = acc[a][b][i];
+        if (kEpi == kEpiSwiglu) {
+          const float *s_up = reinterpret_cast<const float *>(s_mem);
+          const float g = v[i], u = s_up[((wr * 16 + a * 4 + b) * 4 + i) * 64 + lane];
+          bad |= !finitef(g) || !finitef(u);
+          v[i] = (g / (1.0f + exp_f32(-g))) * u;
+        } else {
+          bad |= !finitef(v[i]);
+        }
+      }
+      if (fb + 3 < out_rows && (o.ld % 4) == 0) {
+        float4 *p = reinterpret_cast<float4 *>(o.out + (size_t)r * o.ld + fb);
+        if (kEpi == kEpiResidual) {
+          const float4 q = *p;
+          *p = make_float4(q.x + v[0], q.y + v[1], q.z + v[2], q.w + v[3]);
+        } else {
+          *p = make_float4(v[0], v[1], v[2], v[3]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          if (fb + i >= out_rows) continue;
+          float *p = o.out + (size_t)r * o.ld + fb + i;
+          *p = kEpi == kEpiResidual ? *p + v[i] : v[i];
+        }
+      }
+    }
+    if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Bias add, NeoX RoPE from the host-built table (cos, sin of the engine's
 // iterative angle, cpu.rs:59-73), K/V append into the paged pool
 // (Kv::append, inference.rs:1019-1043; batch.rs:164-184).
@@ -1324,10 +1616,30 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
   }
 }
 
+// Packed batches at least this tall take the matrix-core F16 linear.
+constexpr int kPrefillRows = 128;
+
 template <int kEpi>
 static void mv_f16(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
                    const MatvecOut &o) {
   const int out_rows = kEpi == kEpiSwiglu ? w.rows / 2 : w.rows;
+  // tall packed batches: matrix cores (f32 sums); the head always stays exact
+  if (kEpi != kEpiArgmax && g_prefill_mfma && rows_b >= kPrefillRows && w.K % kGemmBK == 0 &&
+      (kEpi != kEpiSwiglu || out_rows % (kGemmBM / 2) == 0)) {
+    const int ftile = kEpi == kEpiSwiglu ? kGemmBM / 2 : kGemmBM;
+    launch_k(k_gemm_f16<kEpi>, dim3((out_rows + ftile - 1) / ftile, (rows_b + kGemmBM - 1) / kGemmBM),
+             dim3(256), 0, s, w, (const uint16_t *)act.f16, rows_b, o);
+    return;
+  }
+  if (rows_b >= 16 && w.K % 8 == 0) {  // lane = batch row, sequential f64 chains
+    launch_k(k_mv_f16s<kEpi>, dim3((out_rows + 15) / 16, (rows_b + kWave - 1) / kWave), dim3(256), 0,
+             s, w, act, rows_b, o);
+    return;
+  }
+  if (kEpi == kEpiArgmax) {  // partial keys per 16-row tile, then k_argmax_reduce
+    launch_k(k_head_f16, dim3(w.mtiles), dim3(256), 0, s, w, act, rows_b, o);
+    return;
+  }
   launch_k(k_mv_f16<kEpi>, dim3((out_rows + 3) / 4), dim3(256), 0, s, w, act, rows_b, o);
 }
 

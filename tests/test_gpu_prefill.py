@@ -1,0 +1,100 @@
+"""Packed-prefill regime (F16 weights, 128+ packed rows): the linears run on
+the matrix cores with f32 sums instead of the reference's f64 sums
+(cpu.rs:31-35), so this regime is checked to the north_star tolerance for F16
+logits (max-abs 1e-2), not bit for bit.  Greedy ids must agree wherever the
+reference's top-2 margin exceeds the measured difference.  The same steps
+with the matrix-core path switched off (COHX_PREFILL_MFMA=0) stay bit-exact
+against the oracle."""
+import os
+
+import numpy as np
+import pytest
+
+import cohx
+import orc
+import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def make(cfg, t, mfma, **kw):
+    old = os.environ.get("COHX_PREFILL_MFMA")
+    os.environ["COHX_PREFILL_MFMA"] = "1" if mfma else "0"
+    try:
+        return cohx.Model(cfg, t, **kw)
+    finally:
+        if old is None:
+            del os.environ["COHX_PREFILL_MFMA"]
+        else:
+            os.environ["COHX_PREFILL_MFMA"] = old
+
+
+def close(got, want, what):
+    diff = float(np.abs(got.astype(np.float64) - want).max())
+    order = np.sort(want)
+    margin = float(order[-1] - order[-2])
+    print(f"{what}: max-abs {diff:.3g}, top1-top2 margin {margin:.3g}", flush=True)
+    assert diff <= TOL, what
+    if margin > 2 * diff:
+        assert int(np.argmax(got)) == int(np.argmax(want)), what
+    return diff
+
+
+def test_prefill_chunk_matches_oracle_within_tolerance():
+    print("case: tiny F16 prefill chunk of 150 rows, matrix cores vs oracle", flush=True)
+    cfg = synth.config(layers=2, hidden=128, intermediate=256, heads=4, kv_heads=2,
+                       vocabulary=300, context=512)
+    c, t = synth.in_memory(cfg, "f16", seed=31)
+    kw = dict(max_lanes=4, max_rows=256, max_seqs=4, max_context=256)
+    mm, me = make(c, t, True, **kw), make(c, t, False, **kw)
+    o = orc.Model(c, t, threads=8)
+    rng = np.random.default_rng(5)
+    chunk = [int(v) for v in rng.integers(0, c["vocabulary"], 150)]
+    sm, se = mm.seq_alloc(), me.seq_alloc()
+    rm = mm.step([dict(seq=sm, tokens=chunk, logits=True)])[0]
+    re = me.step([dict(seq=se, tokens=chunk, logits=True)])[0]
+    s = o.session(256)
+    for tok in chunk:
+        o.forward_batch([s], [tok])
+    want = s.logits()
+    assert rm["status"] == 0 and re["status"] == 0
+    assert np.array_equal(re["logits"], want)  # exact kernels: bit for bit
+    close(rm["logits"], want, "matrix-core chunk logits")
+    for layer in range(c["layers"]):
+        kv_diff = float(np.abs(mm.seq_read_kv(sm, layer) - s.kv(layer)).max())
+        assert kv_diff < 1e-3, (layer, kv_diff)
+    # decoding on after the chunk: one-row steps are exact again
+    tok = int(np.argmax(want))
+    r1 = mm.step([dict(seq=sm, tokens=[tok], logits=True)])[0]
+    o.forward_batch([s], [tok])
+    close(r1["logits"], s.logits(), "decode after matrix-core chunk")
+
+
+def test_mixed_prefill_and_decode_full_shape():
+    """Config 3's form at the full shape, shortened: two prefill chunks plus
+    decode rows over seeded KV in one packed step; the matrix-core context
+    against the exact context (itself pinned to the oracle by the other GPU
+    tests)."""
+    print("case: full-shape F16 mixed packed step, matrix cores vs exact", flush=True)
+    c, t = synth.in_memory(synth.config(), "f16", seed=32)
+    kw = dict(max_lanes=8, max_rows=512, max_seqs=8, max_context=1024)
+    mm, me = make(c, t, True, **kw), make(c, t, False, **kw)
+    rng = np.random.default_rng(6)
+    chunks = [[int(v) for v in rng.integers(0, c["vocabulary"], n)] for n in (200, 131)]
+    kv = [300, 900, 64, 512]
+    lanes_m, lanes_e = [], []
+    for m, lanes in ((mm, lanes_m), (me, lanes_e)):
+        for ch in chunks:
+            lanes.append(dict(seq=m.seq_alloc(), tokens=ch, logits=True))
+        for i, n in enumerate(kv):
+            s = m.seq_alloc()
+            m.seq_fill_synthetic(s, n, 8, i)
+            lanes.append(dict(seq=s, tokens=[int(10 + i)], logits=True))
+    rm, re = mm.step(lanes_m), me.step(lanes_e)
+    worst = 0.0
+    for i, (a, b) in enumerate(zip(rm, re)):
+        assert a["status"] == 0 and b["status"] == 0
+        worst = max(worst, close(a["logits"], b["logits"], f"lane {i}"))
+    print(f"worst lane max-abs {worst:.3g}", flush=True)
