@@ -316,6 +316,12 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   if (!rc) rc = dalloc(ctx, &w.scores, (size_t)R * NKV * d->max_context * 8);
   if (!rc) rc = dalloc(ctx, &w.chunk_max, (size_t)R * NH * ((d->max_context + 255) / 256));
   if (!rc) rc = dalloc(ctx, &w.den_part, (size_t)R * NH * ((d->max_context + 255) / 256));
+  w.max_tiles = (R + 15) / 16 + (int)d->max_lanes;
+  if (!rc) rc = dalloc(ctx, &w.tiles, (size_t)w.max_tiles);
+  if (!rc) rc = dalloc(ctx, &w.row_skip, (size_t)R);
+  if (!rc) rc = dalloc(ctx, &w.direct, (size_t)R * H);
+  if (!rc) rc = halloc(ctx, &w.h_tiles, (size_t)w.max_tiles);
+  if (!rc) rc = halloc(ctx, &w.h_row_skip, (size_t)R);
   if (!rc) rc = dalloc(ctx, &w.partial, (size_t)R * NH * ctx->max_chunks * D);
   if (!rc) rc = dalloc(ctx, &w.logits, (size_t)NL * V);
   if (!rc) rc = dalloc(ctx, &w.argmax, NL);
@@ -337,6 +343,8 @@ void cohx_destroy(cohx_ctx *ctx) {
   if (ctx->ws.h_upload) (void)hipHostFree(ctx->ws.h_upload);
   if (ctx->ws.h_row_err) (void)hipHostFree(ctx->ws.h_row_err);
   if (ctx->ws.h_argmax) (void)hipHostFree(ctx->ws.h_argmax);
+  if (ctx->ws.h_tiles) (void)hipHostFree(ctx->ws.h_tiles);
+  if (ctx->ws.h_row_skip) (void)hipHostFree(ctx->ws.h_row_skip);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -640,6 +648,8 @@ struct Prepared {
   uint32_t rows = 0;
   uint32_t max_kv = 0;
   uint64_t kv_rows_read = 0;
+  int n_tiles = 0;            // prefill-chunk attention tiles on the matrix cores
+  bool single_token = true;   // every lane carries one token (a pure decode step)
 };
 
 // Host validation (batch.rs:119-131) and upload of the device batch.
@@ -686,6 +696,7 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
     for (uint32_t j = 0; j < ln.n_tokens; j++)
       p.kv_rows_read += (uint64_t)start + j + 1;
     p.rows += ln.n_tokens;
+    if (ln.n_tokens != 1) p.single_token = false;
     p.max_kv = std::max(p.max_kv, start + ln.n_tokens);
     p.included.push_back((int)i);
   }
@@ -693,6 +704,32 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
   int rc = sync_page_table(ctx);
   if (rc) return rc;
   const size_t n = p.included.size();
+  // prefill regime: F16 linears on the matrix cores, and lanes of 16+ tokens
+  // take the matrix-core chunk attention (both held to a tolerance)
+  const int G = (int)(d.heads / d.kv_heads);
+  const bool regime = ctx->prefill_mfma && d.weight_dtype == COHX_F16 && p.rows >= 128 &&
+                      attention_chunk_supported((int)d.head_dim, G);
+  p.n_tiles = 0;
+  if (regime) {
+    Workspace &w = ctx->ws;
+    std::memset(w.h_row_skip, 0, p.rows * sizeof(uint32_t));
+    for (size_t k = 0; k < n; k++) {
+      const uint32_t nt = info[k * 4 + 0], start = info[k * 4 + 1], seq = info[k * 4 + 2],
+                     row0 = info[k * 4 + 3];
+      if (nt < 16) continue;
+      for (uint32_t t = 0; t < nt; t += 16) {
+        w.h_tiles[p.n_tiles++] = int4{(int)(row0 + t), (int)std::min(16u, nt - t), (int)seq,
+                                      (int)(start + t)};
+        for (uint32_t j = t; j < std::min(nt, t + 16); j++) w.h_row_skip[row0 + j] = 1;
+      }
+    }
+    if (p.n_tiles) {
+      HIP_TRY(hipMemcpyAsync(w.tiles, w.h_tiles, p.n_tiles * sizeof(int4), hipMemcpyHostToDevice,
+                             ctx->stream));
+      HIP_TRY(hipMemcpyAsync(w.row_skip, w.h_row_skip, p.rows * sizeof(uint32_t),
+                             hipMemcpyHostToDevice, ctx->stream));
+    }
+  }
   HIP_TRY(hipMemcpyAsync(ctx->ws.lane_info, info, n * 4 * sizeof(uint32_t), hipMemcpyHostToDevice,
                          ctx->stream));
   HIP_TRY(hipMemcpyAsync(ctx->ws.tokens, toks, p.rows * sizeof(uint32_t), hipMemcpyHostToDevice,
@@ -743,7 +780,7 @@ namespace {
 const char *kCatNames[kCatCount] = {
     "pack", "embed", "rmsnorm_act", "matvec_qkv", "qkv_rope_append", "attn_scores",
     "attn_softmax_stats", "attn_pv", "attn_combine_act", "matvec_o_residual", "matvec_gate_up_swiglu",
-    "swiglu_act", "matvec_down_residual", "matvec_head_argmax"};
+    "swiglu_act", "matvec_down_residual", "matvec_head_argmax", "attn_chunk_mfma"};
 
 int prof_begin(cohx_ctx *ctx, int cat, double bytes, double flops) {
   Profiler &p = ctx->prof;
@@ -833,7 +870,8 @@ int enqueue_device_step(cohx_ctx *ctx, const Prepared &p, int kv_grid, bool any_
   Workspace &w = ctx->ws;
   hipStream_t s = ctx->stream;
   StepDims sd{H, F, (int)d.vocabulary, NH, NKV, D, KVD, NH / NKV, d.norm_epsilon,
-              1.0f / sqrtf((float)D), ctx->max_pages, (int)d.max_context, ctx->max_chunks};
+              1.0f / sqrtf((float)D), ctx->max_pages, (int)d.max_context, ctx->max_chunks,
+              p.n_tiles ? w.row_skip : nullptr, p.n_tiles ? w.direct : nullptr};
   const ActView act = act_view(ctx);
   const double kv_rows = (double)p.kv_rows_read;  // sum over rows of attended positions
   int e;
@@ -865,6 +903,11 @@ int enqueue_device_step(cohx_ctx *ctx, const Prepared &p, int kv_grid, bool any_
     launch_qkv_post(s, R, sd, w.qkv, ly.bqkv, ctx->rope, w.row_pos, w.row_slot, w.q_rot, kp, vp,
                     w.row_err);
     prof_end(ctx, e);
+    if (p.n_tiles) {
+      e = prof_begin(ctx, kCatAttnChunk, b_scores + b_pv, 2.0 * f_attn);
+      launch_attn_chunk(s, p.n_tiles, sd, w.tiles, w.q_rot, kp, vp, ctx->page_table, w.direct);
+      prof_end(ctx, e);
+    }
     e = prof_begin(ctx, kCatAttnScores, b_scores, f_attn);
     launch_attn_scores(s, R, kv_grid, sd, w.q_rot, kp, w.row_pos, w.row_seq,
                        ctx->page_table, w.scores, w.chunk_max, w.row_err);
@@ -950,7 +993,7 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
     if (batch->lanes[p.included[k]].want_logits && out->lanes[p.included[k]].logits)
       any_logits = true;
   const int kv_grid = (int)((p.max_kv + 255) / 256 * 256);
-  if (ctx->prof.on || !ctx->use_graphs) {
+  if (ctx->prof.on || !ctx->use_graphs || !p.single_token) {
     rc = enqueue_device_step(ctx, p, kv_grid, any_logits);
     if (rc) return rc;
   } else {

@@ -44,17 +44,25 @@ struct Workspace {
   float *chunk_max = nullptr, *logits = nullptr;
   double *partial = nullptr;
   double *den_part = nullptr;  // [rows][heads][256-token chunks] softmax denominator partials
+  // prefill chunks on the matrix cores: 16-row tiles, per-row flags, f32 output
+  int4 *tiles = nullptr;
+  uint32_t *row_skip = nullptr;
+  float *direct = nullptr;
+  int max_tiles = 0;
   unsigned long long *argmax = nullptr;
   unsigned long long *argmax_part = nullptr;  // [max_lanes][head m-tiles]
   // pinned host staging
   uint32_t *h_upload = nullptr;  // lane_info then tokens
   uint32_t *h_row_err = nullptr;
+  int4 *h_tiles = nullptr;        // pinned staging for tiles, then row flags
+  uint32_t *h_row_skip = nullptr;
   unsigned long long *h_argmax = nullptr;
 };
 
 enum ProfCat {
   kCatPack, kCatEmbed, kCatNorm, kCatMvQkv, kCatQkvPost, kCatAttnScores, kCatAttnSoftmax,
-  kCatAttnPv, kCatAttnCombine, kCatMvO, kCatMvGateUp, kCatQuant, kCatMvDown, kCatMvHead, kCatCount
+  kCatAttnPv, kCatAttnCombine, kCatMvO, kCatMvGateUp, kCatQuant, kCatMvDown, kCatMvHead,
+  kCatAttnChunk, kCatCount
 };
 
 struct Profiler {

@@ -31,6 +31,10 @@ struct StepDims {
   int max_pages;                     // page-table row stride
   int kv_cap;                        // score row stride (>= max kv length this step)
   int max_chunks;                    // partial-sum stride
+  // rows whose attention the matrix-core chunk kernel computes (nullptr: none);
+  // the exact passes skip them and the combine pass reads their f32 output
+  const uint32_t *row_skip;
+  const float *direct;               // [rows][H]
 };
 
 enum Epilogue { kEpiStore = 0, kEpiResidual = 1, kEpiSwiglu = 2, kEpiArgmax = 3 };
@@ -85,6 +89,12 @@ void launch_attn_exp(hipStream_t s, int rows, int max_kv, const StepDims &d,
 void launch_attn_pv(hipStream_t s, int rows, int max_kv, const StepDims &d, const float *vpool,
                     const uint32_t *row_pos, const uint32_t *row_seq, const int32_t *page_table,
                     const float *escores, const double *den_part, double *partial);
+// Matrix-core attention for prefill chunks (tolerance regime): tiles[i] =
+// {first packed row, rows (<= 16), sequence, position of the first row}.
+bool attention_chunk_supported(int D, int G);
+void launch_attn_chunk(hipStream_t s, int n_tiles, const StepDims &d, const int4 *tiles,
+                       const float *q_rot, const float *kpool, const float *vpool,
+                       const int32_t *page_table, float *direct);
 void launch_attn_combine(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
                          const double *partial, int act_dtype, int nbp, ActView act,
                          uint32_t *row_err);

@@ -1226,7 +1226,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(StepDims d, const float *__
   const int r = blockIdx.x, g = blockIdx.y, c = blockIdx.z;
   const int kv = (int)row_pos[r] + 1;
   const int t0 = c * kT;
-  if (t0 >= kv) return;
+  if (t0 >= kv || (d.row_skip && d.row_skip[r])) return;
   __shared__ float wmax[4][kG];
   const int t = t0 + threadIdx.x;
   const bool valid = t < kv;
@@ -1302,7 +1302,7 @@ __global__ __launch_bounds__(256) void k_attn_exp(StepDims d, const uint32_t *__
   __shared__ double redd[kW][8];
   const int r = blockIdx.x, g = blockIdx.y, c = blockIdx.z;
   const int kv = (int)row_pos[r] + 1, t0 = c * kT;
-  if (t0 >= kv) return;
+  if (t0 >= kv || (d.row_skip && d.row_skip[r])) return;
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
   const int slot = threadIdx.x % 8, tok = threadIdx.x / 8;
   const int nch = (kv + kT - 1) / kT, nsc = (d.kv_cap + kT - 1) / kT;
@@ -1366,7 +1366,7 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
   static_assert(kChunk * 2 == 256, "one float4 of weights per thread");
   const int r = blockIdx.x, g = blockIdx.y, c = blockIdx.z;
   const int kv = (int)row_pos[r] + 1, t0 = c * kChunk;
-  if (t0 >= kv) return;
+  if (t0 >= kv || (d.row_skip && d.row_skip[r])) return;
   __shared__ double red[3][kG][kD];
   __shared__ float s_inv[8];
   __shared__ float4 s_p[kChunk * 2];
@@ -1461,6 +1461,128 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
   }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill chunks on the matrix cores (tolerance regime, used only with the
+// matrix-core linears): a workgroup takes up to 16 consecutive rows of one
+// lane and one KV head; wave h is query head g*kG + h.  Key tiles of 64
+// tokens are staged in LDS; S = Q K^T and O += P V run on
+// v_mfma_f32_16x16x4_f32 (f32 operands and sums) with an online softmax and
+// the causal mask pos(key) <= pos(row).  Row pads make every operand read
+// bank-conflict free (K: 68 floats, V: 80, P: 68).  The reference computes
+// the same attention with f64 dot products and sums (cpu.rs:133-210); rows
+// handled here are flagged in row_skip so the exact passes leave them.
+// ---------------------------------------------------------------------------
+template <int kG>
+__global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *__restrict__ tiles,
+                                                        const float *__restrict__ q_rot,
+                                                        const float *__restrict__ kpool,
+                                                        const float *__restrict__ vpool,
+                                                        const int32_t *__restrict__ pt,
+                                                        float *__restrict__ direct) {
+  constexpr int kD = 64, kKT = 64, kSK = 68, kSV = 80, kSP = 68;
+  __shared__ float s_k[kKT * kSK];
+  __shared__ float s_v[kKT * kSV];
+  __shared__ float s_p[kG][16 * kSP];
+  const int4 tile = tiles[blockIdx.x];  // first row, rows, sequence, position of first row
+  const int g = blockIdx.y, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int h = g * kG + wave, grp = lane / 16, c = lane % 16;
+  const int nr = tile.y, pos0 = tile.w, kv_end = pos0 + nr;
+  const int32_t *ptr = pt + (size_t)tile.z * d.max_pages;
+  // A operand of S: lane supplies Q[row c][dim 4j + grp], j = 0..15
+  float qa[16];
+  {
+    const float *qrow = q_rot + (size_t)(tile.x + min(c, nr - 1)) * d.H + h * kD;
+#pragma unroll
+    for (int j = 0; j < 16; j++) qa[j] = qrow[4 * j + grp];
+  }
+  float4v o[4];
+#pragma unroll
+  for (int n = 0; n < 4; n++) o[n] = float4v{0.f, 0.f, 0.f, 0.f};
+  float m[4], l[4];
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    m[v] = -__builtin_inff();
+    l[v] = 0.0f;
+  }
+  for (int t0 = 0; t0 < kv_end; t0 += kKT) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < kKT * kD / 4; i += blockDim.x) {
+      const int tok = i / (kD / 4), d4 = (i % (kD / 4)) * 4, t = t0 + tok;
+      float4 kk = make_float4(0.f, 0.f, 0.f, 0.f), vv = kk;
+      if (t < kv_end) {
+        const size_t at = ((size_t)(ptr[t / kPage] * d.NKV + g) * kPage + t % kPage) * kD + d4;
+        kk = *reinterpret_cast<const float4 *>(kpool + at);
+        vv = *reinterpret_cast<const float4 *>(vpool + at);
+      }
+      float *pk = s_k + tok * kSK + d4, *pv = s_v + tok * kSV + d4;
+      pk[0] = kk.x; pk[1] = kk.y; pk[2] = kk.z; pk[3] = kk.w;
+      pv[0] = vv.x; pv[1] = vv.y; pv[2] = vv.z; pv[3] = vv.w;
+    }
+    __syncthreads();
+    // S tile: s4[n][v] = S[row 4*grp + v][token t0 + 16n + c]
+    float4v s4[4];
+#pragma unroll
+    for (int n = 0; n < 4; n++) {
+      s4[n] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 16; j++)
+        s4[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[j], s_k[(n * 16 + c) * kSK + 4 * j + grp], s4[n], 0, 0, 0);
+    }
+    float tmax[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int row = 4 * grp + v, prow = pos0 + row;
+      tmax[v] = -__builtin_inff();
+#pragma unroll
+      for (int n = 0; n < 4; n++) {
+        const int t = t0 + n * 16 + c;
+        float sv = s4[n][v] * d.scale;
+        if (row >= nr || t > prow) sv = -__builtin_inff();
+        s4[n][v] = sv;
+        tmax[v] = fmaxf(tmax[v], sv);
+      }
+#pragma unroll
+      for (int x = 1; x < 16; x <<= 1) tmax[v] = fmaxf(tmax[v], __shfl_xor(tmax[v], x, kWave));
+    }
+    float alpha[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const float mn = fmaxf(m[v], tmax[v]);
+      alpha[v] = mn == -__builtin_inff() ? 1.0f : exp_f32(m[v] - mn);
+      float sum = 0.0f;
+#pragma unroll
+      for (int n = 0; n < 4; n++) {
+        const float p = mn == -__builtin_inff() ? 0.0f : exp_f32(s4[n][v] - mn);
+        s_p[wave][(4 * grp + v) * kSP + n * 16 + c] = p;
+        sum += p;
+      }
+#pragma unroll
+      for (int x = 1; x < 16; x <<= 1) sum += __shfl_xor(sum, x, kWave);
+      l[v] = l[v] * alpha[v] + sum;
+      m[v] = mn;
+#pragma unroll
+      for (int n = 0; n < 4; n++) o[n][v] *= alpha[v];
+    }
+    __syncthreads();
+    // O[row 4*grp+v][dim 16n + c] += sum_k P[row][k] V[k][dim]
+#pragma unroll
+    for (int n = 0; n < 4; n++)
+#pragma unroll
+      for (int j = 0; j < 16; j++)
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(s_p[wave][c * kSP + 4 * j + grp],
+                                                    s_v[(4 * j + grp) * kSV + n * 16 + c], o[n], 0, 0, 0);
+  }
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int row = 4 * grp + v;
+    if (row >= nr) continue;
+    const float inv = 1.0f / l[v];
+#pragma unroll
+    for (int n = 0; n < 4; n++)
+      direct[(size_t)(tile.x + row) * d.H + h * kD + n * 16 + c] = o[n][v] * inv;
+  }
+}
+
 // Pass 4: chunks combined in order, rounded to f32, and prepared as the
 // operand of attn_output (each head's D elements hold whole Q8_0 blocks).
 template <int kAct>
@@ -1474,11 +1596,12 @@ __global__ __launch_bounds__(128) void k_attn_combine(StepDims d,
   const double *pp = partial + ((size_t)r * d.NH + h) * d.max_chunks * d.D;
   const bool active = j < d.D;
   double acc = 0.0;
-  if (active) {
+  const bool direct = d.row_skip && d.row_skip[r];
+  if (active && !direct) {
     acc = pp[j];
     for (int c = 1; c < nch; c++) acc += pp[(size_t)c * d.D + j];
   }
-  const float o = (float)acc;
+  const float o = direct ? (active ? d.direct[(size_t)r * d.H + h * d.D + j] : 0.0f) : (float)acc;
   bool bad = active && !finitef(o);
   if (kAct == 8) {
     if (active) o_s[j] = o;
@@ -1753,6 +1876,25 @@ void launch_attn_pv(hipStream_t s, int rows, int max_kv, const StepDims &d, cons
   COHX_DG_DISPATCH(d.D, d.G, L);
 #undef L
   (void)ok;
+}
+
+bool attention_chunk_supported(int D, int G) { return D == 64 && G >= 1 && G <= 8; }
+
+void launch_attn_chunk(hipStream_t s, int n_tiles, const StepDims &d, const int4 *tiles,
+                       const float *q_rot, const float *kpool, const float *vpool,
+                       const int32_t *page_table, float *direct) {
+  if (n_tiles <= 0) return;
+  const dim3 grid(n_tiles, d.NKV);
+  switch (d.G) {
+#define L(GG)                                                                                 \
+  case GG:                                                                                    \
+    launch_k(k_attn_chunk<GG>, grid, dim3(64 * GG), 0, s, d, tiles, q_rot, kpool, vpool,      \
+             page_table, direct);                                                             \
+    break;
+    L(1) L(2) L(4) L(6) L(7) L(8)
+#undef L
+    default: break;
+  }
 }
 
 void launch_attn_combine(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,

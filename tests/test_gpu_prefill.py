@@ -98,3 +98,35 @@ def test_mixed_prefill_and_decode_full_shape():
         assert a["status"] == 0 and b["status"] == 0
         worst = max(worst, close(a["logits"], b["logits"], f"lane {i}"))
     print(f"worst lane max-abs {worst:.3g}", flush=True)
+
+
+def test_chunk_attention_matches_oracle_within_tolerance():
+    """head_dim 64 (the matrix-core chunk attention's shape): a prefill chunk
+    continuing a sequence that already holds 40 tokens, next to a decode lane;
+    logits of both lanes against the oracle."""
+    print("case: D=64 chunk attention, 170-row chunk after 40 tokens + a decode lane", flush=True)
+    cfg = synth.config(layers=2, hidden=256, intermediate=512, heads=4, kv_heads=2,
+                       vocabulary=500, context=512)
+    c, t = synth.in_memory(cfg, "f16", seed=33)
+    kw = dict(max_lanes=4, max_rows=256, max_seqs=4, max_context=512)
+    m = make(c, t, True, **kw)
+    o = orc.Model(c, t, threads=8)
+    rng = np.random.default_rng(7)
+    head = [int(v) for v in rng.integers(0, c["vocabulary"], 40)]
+    chunk = [int(v) for v in rng.integers(0, c["vocabulary"], 170)]
+    a, b = m.seq_alloc(), m.seq_alloc()
+    assert m.step([dict(seq=a, tokens=head)])[0]["status"] == 0
+    m.seq_fill_synthetic(b, 300, 9, 1)
+    sa, sb = o.session(512), o.session(512)
+    for tok in head:
+        o.forward_batch([sa], [tok])
+    sb.fill_synthetic(300, 9, 1)
+    res = m.step([dict(seq=a, tokens=chunk, logits=True), dict(seq=b, tokens=[77], logits=True)])
+    for tok in chunk:
+        o.forward_batch([sa], [tok])
+    o.forward_batch([sb], [77])
+    assert res[0]["status"] == 0 and res[1]["status"] == 0
+    close(res[0]["logits"], sa.logits(), "chunk lane")
+    close(res[1]["logits"], sb.logits(), "decode lane")
+    for layer in range(c["layers"]):
+        assert float(np.abs(m.seq_read_kv(a, layer, True) - sa.kv(layer, True)).max()) < 1e-3
