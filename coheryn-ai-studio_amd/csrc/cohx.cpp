@@ -319,9 +319,11 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   w.max_tiles = (R + 15) / 16 + (int)d->max_lanes;
   if (!rc) rc = dalloc(ctx, &w.tiles, (size_t)w.max_tiles);
   if (!rc) rc = dalloc(ctx, &w.row_skip, (size_t)R);
+  if (!rc) rc = dalloc(ctx, &w.row_map, (size_t)R);
   if (!rc) rc = dalloc(ctx, &w.direct, (size_t)R * H);
   if (!rc) rc = halloc(ctx, &w.h_tiles, (size_t)w.max_tiles);
   if (!rc) rc = halloc(ctx, &w.h_row_skip, (size_t)R);
+  if (!rc) rc = halloc(ctx, &w.h_row_map, (size_t)R);
   if (!rc) rc = dalloc(ctx, &w.partial, (size_t)R * NH * ctx->max_chunks * D);
   if (!rc) rc = dalloc(ctx, &w.logits, (size_t)NL * V);
   if (!rc) rc = dalloc(ctx, &w.argmax, NL);
@@ -345,6 +347,7 @@ void cohx_destroy(cohx_ctx *ctx) {
   if (ctx->ws.h_argmax) (void)hipHostFree(ctx->ws.h_argmax);
   if (ctx->ws.h_tiles) (void)hipHostFree(ctx->ws.h_tiles);
   if (ctx->ws.h_row_skip) (void)hipHostFree(ctx->ws.h_row_skip);
+  if (ctx->ws.h_row_map) (void)hipHostFree(ctx->ws.h_row_map);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -649,6 +652,10 @@ struct Prepared {
   uint32_t max_kv = 0;
   uint64_t kv_rows_read = 0;
   int n_tiles = 0;            // prefill-chunk attention tiles on the matrix cores
+  uint32_t n_exact = 0;       // rows left to the exact attention passes
+  uint64_t kv_rows_chunk = 0; // attended positions of the tiles' rows
+  uint64_t kv_chunk_lanes = 0;// KV rows of the lanes the tiles belong to
+  uint32_t max_kv_exact = 0;  // longest attended length among the exact passes' rows
   bool single_token = true;   // every lane carries one token (a pure decode step)
 };
 
@@ -710,24 +717,43 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
   const bool regime = ctx->prefill_mfma && d.weight_dtype == COHX_F16 && p.rows >= 128 &&
                       attention_chunk_supported((int)d.head_dim, G);
   p.n_tiles = 0;
+  p.n_exact = p.rows;
+  p.max_kv_exact = p.max_kv;
   if (regime) {
     Workspace &w = ctx->ws;
     std::memset(w.h_row_skip, 0, p.rows * sizeof(uint32_t));
     for (size_t k = 0; k < n; k++) {
       const uint32_t nt = info[k * 4 + 0], start = info[k * 4 + 1], seq = info[k * 4 + 2],
                      row0 = info[k * 4 + 3];
-      if (nt < 16) continue;
+      if (nt < 16) {
+        p.max_kv_exact = std::max(p.max_kv_exact, start + nt);
+        continue;
+      }
+      p.kv_chunk_lanes += start + nt;
       for (uint32_t t = 0; t < nt; t += 16) {
         w.h_tiles[p.n_tiles++] = int4{(int)(row0 + t), (int)std::min(16u, nt - t), (int)seq,
                                       (int)(start + t)};
-        for (uint32_t j = t; j < std::min(nt, t + 16); j++) w.h_row_skip[row0 + j] = 1;
+        for (uint32_t j = t; j < std::min(nt, t + 16); j++) {
+          w.h_row_skip[row0 + j] = 1;
+          p.kv_rows_chunk += (uint64_t)start + j + 1;
+        }
       }
     }
+    if (!p.n_tiles) p.max_kv_exact = p.max_kv;
     if (p.n_tiles) {
+      // longest KV first, so the short tiles fill in behind the long ones
+      std::stable_sort(w.h_tiles, w.h_tiles + p.n_tiles,
+                       [](const int4 &a, const int4 &b) { return a.w + a.y > b.w + b.y; });
+      p.n_exact = 0;
+      for (uint32_t r = 0; r < p.rows; r++)
+        if (!w.h_row_skip[r]) w.h_row_map[p.n_exact++] = r;
       HIP_TRY(hipMemcpyAsync(w.tiles, w.h_tiles, p.n_tiles * sizeof(int4), hipMemcpyHostToDevice,
                              ctx->stream));
       HIP_TRY(hipMemcpyAsync(w.row_skip, w.h_row_skip, p.rows * sizeof(uint32_t),
                              hipMemcpyHostToDevice, ctx->stream));
+      if (p.n_exact)
+        HIP_TRY(hipMemcpyAsync(w.row_map, w.h_row_map, p.n_exact * sizeof(uint32_t),
+                               hipMemcpyHostToDevice, ctx->stream));
     }
   }
   HIP_TRY(hipMemcpyAsync(ctx->ws.lane_info, info, n * 4 * sizeof(uint32_t), hipMemcpyHostToDevice,
@@ -871,16 +897,24 @@ int enqueue_device_step(cohx_ctx *ctx, const Prepared &p, int kv_grid, bool any_
   hipStream_t s = ctx->stream;
   StepDims sd{H, F, (int)d.vocabulary, NH, NKV, D, KVD, NH / NKV, d.norm_epsilon,
               1.0f / sqrtf((float)D), ctx->max_pages, (int)d.max_context, ctx->max_chunks,
-              p.n_tiles ? w.row_skip : nullptr, p.n_tiles ? w.direct : nullptr};
+              p.n_tiles ? w.row_skip : nullptr, p.n_tiles ? w.direct : nullptr,
+              p.n_tiles ? w.row_map : nullptr};
+  const int RX = (int)p.n_exact;  // rows of the exact attention passes
+  if (p.n_tiles) kv_grid = (int)((p.max_kv_exact + 255) / 256 * 256);
   const ActView act = act_view(ctx);
-  const double kv_rows = (double)p.kv_rows_read;  // sum over rows of attended positions
+  // attended positions summed over the exact passes' rows and the tiles' rows
+  const double kv_rows = (double)(p.kv_rows_read - p.kv_rows_chunk);
+  const double kv_chunk = (double)p.kv_rows_chunk;
   int e;
   // per-launch algorithmic bytes
   const double b_norm = (double)R * H * 4 + H * 4 + R * act_row;
-  const double b_scores = kv_rows * KVD * 4 + (double)R * H * 4 + kv_rows * NH * 4;
+  const double b_scores = kv_rows * KVD * 4 + (double)RX * H * 4 + kv_rows * NH * 4;
   const double b_softmax = kv_rows * NH * 4 * 2;
-  const double b_pv = kv_rows * KVD * 4 + kv_rows * NH * 4 + (double)R * H * 4;
+  const double b_pv = kv_rows * KVD * 4 + kv_rows * NH * 4 + (double)RX * H * 4;
   const double f_attn = kv_rows * NH * D * 2;
+  // chunk tiles: each lane's K and V once, Q in and O out; QK^T and PV flops
+  const double b_chunk = (double)p.kv_chunk_lanes * KVD * 4 * 2 + (R - RX) * (double)H * 4 * 2;
+  const double f_chunk = kv_chunk * NH * D * 4;
   const double b_combine = (double)R * H * 4 + R * act_row;
   const double b_post = (double)R * (H + 2 * KVD) * 4 * 2 + (H + 2 * KVD) * 4;
   e = prof_begin(ctx, kCatEmbed, (double)R * act_row + (double)R * H * 4, 0);
@@ -904,21 +938,23 @@ int enqueue_device_step(cohx_ctx *ctx, const Prepared &p, int kv_grid, bool any_
                     w.row_err);
     prof_end(ctx, e);
     if (p.n_tiles) {
-      e = prof_begin(ctx, kCatAttnChunk, b_scores + b_pv, 2.0 * f_attn);
+      e = prof_begin(ctx, kCatAttnChunk, b_chunk, f_chunk);
       launch_attn_chunk(s, p.n_tiles, sd, w.tiles, w.q_rot, kp, vp, ctx->page_table, w.direct);
       prof_end(ctx, e);
     }
-    e = prof_begin(ctx, kCatAttnScores, b_scores, f_attn);
-    launch_attn_scores(s, R, kv_grid, sd, w.q_rot, kp, w.row_pos, w.row_seq,
-                       ctx->page_table, w.scores, w.chunk_max, w.row_err);
-    prof_end(ctx, e);
-    e = prof_begin(ctx, kCatAttnSoftmax, b_softmax, 0);
-    launch_attn_exp(s, R, kv_grid, sd, w.row_pos, w.scores, w.chunk_max, w.den_part);
-    prof_end(ctx, e);
-    e = prof_begin(ctx, kCatAttnPv, b_pv, f_attn);
-    launch_attn_pv(s, R, kv_grid, sd, vp, w.row_pos, w.row_seq, ctx->page_table, w.scores,
-                   w.den_part, w.partial);
-    prof_end(ctx, e);
+    if (RX) {
+      e = prof_begin(ctx, kCatAttnScores, b_scores, f_attn);
+      launch_attn_scores(s, RX, kv_grid, sd, w.q_rot, kp, w.row_pos, w.row_seq,
+                         ctx->page_table, w.scores, w.chunk_max, w.row_err);
+      prof_end(ctx, e);
+      e = prof_begin(ctx, kCatAttnSoftmax, b_softmax, 0);
+      launch_attn_exp(s, RX, kv_grid, sd, w.row_pos, w.scores, w.chunk_max, w.den_part);
+      prof_end(ctx, e);
+      e = prof_begin(ctx, kCatAttnPv, b_pv, f_attn);
+      launch_attn_pv(s, RX, kv_grid, sd, vp, w.row_pos, w.row_seq, ctx->page_table, w.scores,
+                     w.den_part, w.partial);
+      prof_end(ctx, e);
+    }
     e = prof_begin(ctx, kCatAttnCombine, b_combine, 0);
     launch_attn_combine(s, R, sd, w.row_pos, w.partial, act_dtype, ctx->nbp_h, act, w.row_err);
     prof_end(ctx, e);

@@ -44,9 +44,11 @@ struct Workspace {
   float *chunk_max = nullptr, *logits = nullptr;
   double *partial = nullptr;
   double *den_part = nullptr;  // [rows][heads][256-token chunks] softmax denominator partials
-  // prefill chunks on the matrix cores: 16-row tiles, per-row flags, f32 output
+  // prefill chunks on the matrix cores: 16-row tiles, per-row flags, f32
+  // output, and the list of rows left to the exact attention passes
   int4 *tiles = nullptr;
   uint32_t *row_skip = nullptr;
+  uint32_t *row_map = nullptr;
   float *direct = nullptr;
   int max_tiles = 0;
   unsigned long long *argmax = nullptr;
@@ -54,8 +56,9 @@ struct Workspace {
   // pinned host staging
   uint32_t *h_upload = nullptr;  // lane_info then tokens
   uint32_t *h_row_err = nullptr;
-  int4 *h_tiles = nullptr;        // pinned staging for tiles, then row flags
+  int4 *h_tiles = nullptr;        // pinned staging for tiles, row flags and the row list
   uint32_t *h_row_skip = nullptr;
+  uint32_t *h_row_map = nullptr;
   unsigned long long *h_argmax = nullptr;
 };
 

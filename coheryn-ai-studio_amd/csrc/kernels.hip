@@ -1223,10 +1223,11 @@ __global__ __launch_bounds__(256) void k_attn_scores(StepDims d, const float *__
                                                      float *__restrict__ chunk_max,
                                                      uint32_t *row_err) {
   constexpr int kT = 256;
-  const int r = blockIdx.x, g = blockIdx.y, c = blockIdx.z;
+  const int r = d.row_map ? (int)d.row_map[blockIdx.x] : (int)blockIdx.x;
+  const int g = blockIdx.y, c = blockIdx.z;
   const int kv = (int)row_pos[r] + 1;
   const int t0 = c * kT;
-  if (t0 >= kv || (d.row_skip && d.row_skip[r])) return;
+  if (t0 >= kv) return;
   __shared__ float wmax[4][kG];
   const int t = t0 + threadIdx.x;
   const bool valid = t < kv;
@@ -1300,9 +1301,10 @@ __global__ __launch_bounds__(256) void k_attn_exp(StepDims d, const uint32_t *__
   constexpr int kT = 256, kW = kT / kWave, kK = kT / 32;
   __shared__ float redf[kW][8];
   __shared__ double redd[kW][8];
-  const int r = blockIdx.x, g = blockIdx.y, c = blockIdx.z;
+  const int r = d.row_map ? (int)d.row_map[blockIdx.x] : (int)blockIdx.x;
+  const int g = blockIdx.y, c = blockIdx.z;
   const int kv = (int)row_pos[r] + 1, t0 = c * kT;
-  if (t0 >= kv || (d.row_skip && d.row_skip[r])) return;
+  if (t0 >= kv) return;
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
   const int slot = threadIdx.x % 8, tok = threadIdx.x / 8;
   const int nch = (kv + kT - 1) / kT, nsc = (d.kv_cap + kT - 1) / kT;
@@ -1364,9 +1366,10 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
                                                  double *__restrict__ partial) {
   constexpr int kE = (kD + kWave - 1) / kWave;  // elements per lane (lanes >= kD idle when kD < 64)
   static_assert(kChunk * 2 == 256, "one float4 of weights per thread");
-  const int r = blockIdx.x, g = blockIdx.y, c = blockIdx.z;
+  const int r = d.row_map ? (int)d.row_map[blockIdx.x] : (int)blockIdx.x;
+  const int g = blockIdx.y, c = blockIdx.z;
   const int kv = (int)row_pos[r] + 1, t0 = c * kChunk;
-  if (t0 >= kv || (d.row_skip && d.row_skip[r])) return;
+  if (t0 >= kv) return;
   __shared__ double red[3][kG][kD];
   __shared__ float s_inv[8];
   __shared__ float4 s_p[kChunk * 2];
@@ -1463,15 +1466,45 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
 
 // ---------------------------------------------------------------------------
 // Prefill chunks on the matrix cores (tolerance regime, used only with the
-// matrix-core linears): a workgroup takes up to 16 consecutive rows of one
-// lane and one KV head; wave h is query head g*kG + h.  Key tiles of 64
-// tokens are staged in LDS; S = Q K^T and O += P V run on
-// v_mfma_f32_16x16x4_f32 (f32 operands and sums) with an online softmax and
-// the causal mask pos(key) <= pos(row).  Row pads make every operand read
-// bank-conflict free (K: 68 floats, V: 80, P: 68).  The reference computes
-// the same attention with f64 dot products and sums (cpu.rs:133-210); rows
-// handled here are flagged in row_skip so the exact passes leave them.
+// matrix-core linears).  A workgroup takes up to 16 consecutive rows of one
+// lane and one KV head; wave w is query head g*kG + w.  Key tiles of 64
+// tokens are staged in LDS as bf16 hi/lo pairs (x = hi + lo + O(2^-17 x)),
+// and every product runs as three v_mfma_f32_16x16x32_bf16 (lo*hi + hi*lo +
+// hi*hi, f32 sums), which keeps scores and outputs within ~2^-16 relative of
+// f32 arithmetic at the bf16 rate and f32 exponent range.
+//   S^T = K Q^T: lane (grp, c) ends up holding S[row c][key 16n + 4grp + i]
+//     for n, i in 0..3, so one lane owns one query row: the row max and sum
+//     need two cross-lane steps, and P never leaves registers.
+//   O^T = V^T P^T: the lane's 16 probabilities are exactly its B operand when
+//     the k-slots of each 32-key step are ordered 16*(j/4) + 4grp + j%4;
+//     V^T is staged in that key order, so each A operand is one 16-byte read.
+// Scores are taken in log2 units (Q pre-scaled by scale*log2(e)) and
+// exponentiated with v_exp_f32; rows are normalized once at the end.  The
+// reference computes the same attention with f64 dot products and sums
+// (cpu.rs:133-210); rows handled here are flagged in row_skip so the exact
+// passes leave them.  Tiles arrive sorted by KV length, longest first.
 // ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+namespace chunk {
+constexpr int kD = 64, kKT = 64, kS = 72;  // head dim, keys per tile, LDS row stride (bf16)
+constexpr int kItems = kKT / 2 * kD / 4;   // staging items: (token pair, 4 dims)
+
+__device__ __forceinline__ void split(float x, __bf16 &hi, __bf16 &lo) {
+  hi = (__bf16)x;
+  lo = (__bf16)(x - (float)hi);
+}
+
+// Position of key k (0..63 within a tile) in the V^T rows: the k-slot order
+// of the P operand (see above).
+__device__ __forceinline__ int vperm(int k) {
+  const int ks = k / 32, r = k % 32, h = r / 16, grp = (r % 16) / 4, j = r % 4;
+  return ks * 32 + grp * 8 + h * 4 + j;
+}
+}  // namespace chunk
+
 template <int kG>
 __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *__restrict__ tiles,
                                                         const float *__restrict__ q_rot,
@@ -1479,108 +1512,176 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
                                                         const float *__restrict__ vpool,
                                                         const int32_t *__restrict__ pt,
                                                         float *__restrict__ direct) {
-  constexpr int kD = 64, kKT = 64, kSK = 68, kSV = 80, kSP = 68;
-  __shared__ float s_k[kKT * kSK];
-  __shared__ float s_v[kKT * kSV];
-  __shared__ float s_p[kG][16 * kSP];
-  const int4 tile = tiles[blockIdx.x];  // first row, rows, sequence, position of first row
-  const int g = blockIdx.y, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  using namespace chunk;
+  constexpr int kThreads = 64 * kG, kPer = (kItems + kThreads - 1) / kThreads;
+  __shared__ __align__(16) __bf16 s_kh[kKT * kS];
+  __shared__ __align__(16) __bf16 s_kl[kKT * kS];
+  __shared__ __align__(16) __bf16 s_vh[kD * kS];
+  __shared__ __align__(16) __bf16 s_vl[kD * kS];
+  const int4 tile = tiles[blockIdx.x / d.NKV];  // first row, rows, sequence, position of first row
+  const int g = blockIdx.x % d.NKV, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int h = g * kG + wave, grp = lane / 16, c = lane % 16;
   const int nr = tile.y, pos0 = tile.w, kv_end = pos0 + nr;
+  const int prow = pos0 + min(c, nr - 1);  // rows past the tile repeat its last row
   const int32_t *ptr = pt + (size_t)tile.z * d.max_pages;
-  // A operand of S: lane supplies Q[row c][dim 4j + grp], j = 0..15
-  float qa[16];
+  // B operand of S^T: Q[row c][dims 32ks + 8grp .. +7] in log2 units, split
+  bf16x8 qh[2], ql[2];
   {
+    const float qs = d.scale * 1.4426950408889634f;
     const float *qrow = q_rot + (size_t)(tile.x + min(c, nr - 1)) * d.H + h * kD;
 #pragma unroll
-    for (int j = 0; j < 16; j++) qa[j] = qrow[4 * j + grp];
+    for (int ks = 0; ks < 2; ks++) {
+      const float4 a = *reinterpret_cast<const float4 *>(qrow + 32 * ks + 8 * grp);
+      const float4 b = *reinterpret_cast<const float4 *>(qrow + 32 * ks + 8 * grp + 4);
+      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        __bf16 hi, lo;
+        split(v[j] * qs, hi, lo);
+        qh[ks][j] = hi;
+        ql[ks][j] = lo;
+      }
+    }
   }
   float4v o[4];
 #pragma unroll
   for (int n = 0; n < 4; n++) o[n] = float4v{0.f, 0.f, 0.f, 0.f};
-  float m[4], l[4];
+  float m = -__builtin_inff(), l = 0.0f;
+  // staging: item i = (token pair i / 16, dims 4 * (i % 16)); every load of
+  // a tile is issued before the first conversion (two resident workgroups
+  // per CU overlap one's staging with the other's matrix work)
+  float4 rk[kPer][2], rv[kPer][2];
+  auto fetch = [&](int t0) {
 #pragma unroll
-  for (int v = 0; v < 4; v++) {
-    m[v] = -__builtin_inff();
-    l[v] = 0.0f;
-  }
-  for (int t0 = 0; t0 < kv_end; t0 += kKT) {
-    __syncthreads();
-    for (int i = threadIdx.x; i < kKT * kD / 4; i += blockDim.x) {
-      const int tok = i / (kD / 4), d4 = (i % (kD / 4)) * 4, t = t0 + tok;
-      float4 kk = make_float4(0.f, 0.f, 0.f, 0.f), vv = kk;
-      if (t < kv_end) {
-        const size_t at = ((size_t)(ptr[t / kPage] * d.NKV + g) * kPage + t % kPage) * kD + d4;
-        kk = *reinterpret_cast<const float4 *>(kpool + at);
-        vv = *reinterpret_cast<const float4 *>(vpool + at);
+    for (int u = 0; u < kPer; u++) {
+      const int i = threadIdx.x + u * kThreads;
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        rk[u][e] = make_float4(0.f, 0.f, 0.f, 0.f);
+        rv[u][e] = rk[u][e];
+        const int t = t0 + 2 * (i / 16) + e;
+        if (i < kItems && t < kv_end) {
+          const size_t at =
+              ((size_t)(ptr[t / kPage] * d.NKV + g) * kPage + t % kPage) * kD + 4 * (i % 16);
+          rk[u][e] = *reinterpret_cast<const float4 *>(kpool + at);
+          rv[u][e] = *reinterpret_cast<const float4 *>(vpool + at);
+        }
       }
-      float *pk = s_k + tok * kSK + d4, *pv = s_v + tok * kSV + d4;
-      pk[0] = kk.x; pk[1] = kk.y; pk[2] = kk.z; pk[3] = kk.w;
-      pv[0] = vv.x; pv[1] = vv.y; pv[2] = vv.z; pv[3] = vv.w;
     }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int u = 0; u < kPer; u++) {
+      const int i = threadIdx.x + u * kThreads;
+      if (i >= kItems) continue;
+      const int k = 2 * (i / 16), d4 = 4 * (i % 16), vp = vperm(k);
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const float kx[4] = {rk[u][e].x, rk[u][e].y, rk[u][e].z, rk[u][e].w};
+        bf16x4 hi, lo;
+#pragma unroll
+        for (int x = 0; x < 4; x++) {
+          __bf16 a, b;
+          split(kx[x], a, b);
+          hi[x] = a;
+          lo[x] = b;
+        }
+        *reinterpret_cast<bf16x4 *>(s_kh + (k + e) * kS + d4) = hi;
+        *reinterpret_cast<bf16x4 *>(s_kl + (k + e) * kS + d4) = lo;
+      }
+      // keys k and k+1 sit side by side in the V^T order (vperm keeps pairs)
+      const float v0[4] = {rv[u][0].x, rv[u][0].y, rv[u][0].z, rv[u][0].w};
+      const float v1[4] = {rv[u][1].x, rv[u][1].y, rv[u][1].z, rv[u][1].w};
+#pragma unroll
+      for (int x = 0; x < 4; x++) {
+        bf16x2 hi, lo;
+        __bf16 a, b;
+        split(v0[x], a, b);
+        hi[0] = a;
+        lo[0] = b;
+        split(v1[x], a, b);
+        hi[1] = a;
+        lo[1] = b;
+        *reinterpret_cast<bf16x2 *>(s_vh + (d4 + x) * kS + vp) = hi;
+        *reinterpret_cast<bf16x2 *>(s_vl + (d4 + x) * kS + vp) = lo;
+      }
+    }
+  };
+  for (int t0 = 0; t0 < kv_end; t0 += kKT) {
+    fetch(t0);
+    __syncthreads();  // every wave is done with the previous tile
+    stash();
     __syncthreads();
-    // S tile: s4[n][v] = S[row 4*grp + v][token t0 + 16n + c]
-    float4v s4[4];
+    // S^T tile: s[n][i] = S[row c][key t0 + 16n + 4grp + i]
+    float4v s[4];
 #pragma unroll
     for (int n = 0; n < 4; n++) {
-      s4[n] = float4v{0.f, 0.f, 0.f, 0.f};
+      s[n] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < 16; j++)
-        s4[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[j], s_k[(n * 16 + c) * kSK + 4 * j + grp], s4[n], 0, 0, 0);
-    }
-    float tmax[4];
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-      const int row = 4 * grp + v, prow = pos0 + row;
-      tmax[v] = -__builtin_inff();
-#pragma unroll
-      for (int n = 0; n < 4; n++) {
-        const int t = t0 + n * 16 + c;
-        float sv = s4[n][v] * d.scale;
-        if (row >= nr || t > prow) sv = -__builtin_inff();
-        s4[n][v] = sv;
-        tmax[v] = fmaxf(tmax[v], sv);
+      for (int ks = 0; ks < 2; ks++) {
+        const int at = (16 * n + c) * kS + 32 * ks + 8 * grp;
+        const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(s_kh + at);
+        const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(s_kl + at);
+        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[ks], s[n], 0, 0, 0);
+        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[ks], s[n], 0, 0, 0);
+        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[ks], s[n], 0, 0, 0);
       }
-#pragma unroll
-      for (int x = 1; x < 16; x <<= 1) tmax[v] = fmaxf(tmax[v], __shfl_xor(tmax[v], x, kWave));
     }
-    float alpha[4];
+    if (t0 + kKT - 1 > pos0) {  // the tile reaches the chunk: causal mask key <= row
 #pragma unroll
-    for (int v = 0; v < 4; v++) {
-      const float mn = fmaxf(m[v], tmax[v]);
-      alpha[v] = mn == -__builtin_inff() ? 1.0f : exp_f32(m[v] - mn);
-      float sum = 0.0f;
+      for (int n = 0; n < 4; n++)
 #pragma unroll
-      for (int n = 0; n < 4; n++) {
-        const float p = mn == -__builtin_inff() ? 0.0f : exp_f32(s4[n][v] - mn);
-        s_p[wave][(4 * grp + v) * kSP + n * 16 + c] = p;
+        for (int i = 0; i < 4; i++)
+          if (t0 + 16 * n + 4 * grp + i > prow) s[n][i] = -__builtin_inff();
+    }
+    float mx = m;
+#pragma unroll
+    for (int n = 0; n < 4; n++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[n][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float alpha = __builtin_amdgcn_exp2f(m - mx);  // 0 on the first tile
+    m = mx;
+    // B operand of O^T: P[row c][k-slot j of step ks], split into hi/lo
+    bf16x8 ph[2], pl[2];
+    float sum = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const float p = __builtin_amdgcn_exp2f(s[2 * ks + j / 4][j % 4] - mx);
         sum += p;
+        __bf16 hi, lo;
+        split(p, hi, lo);
+        ph[ks][j] = hi;
+        pl[ks][j] = lo;
       }
+    l = l * alpha + sum;  // this lane's share of the row sum
 #pragma unroll
-      for (int x = 1; x < 16; x <<= 1) sum += __shfl_xor(sum, x, kWave);
-      l[v] = l[v] * alpha[v] + sum;
-      m[v] = mn;
-#pragma unroll
-      for (int n = 0; n < 4; n++) o[n][v] *= alpha[v];
-    }
-    __syncthreads();
-    // O[row 4*grp+v][dim 16n + c] += sum_k P[row][k] V[k][dim]
+    for (int n = 0; n < 4; n++) o[n] *= alpha;
+    // O^T tile: o[n][i] += sum_k V[k][dim 16n + 4grp + i] P[row c][k]
 #pragma unroll
     for (int n = 0; n < 4; n++)
 #pragma unroll
-      for (int j = 0; j < 16; j++)
-        o[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(s_p[wave][c * kSP + 4 * j + grp],
-                                                    s_v[(4 * j + grp) * kSV + n * 16 + c], o[n], 0, 0, 0);
+      for (int ks = 0; ks < 2; ks++) {
+        const int at = (16 * n + c) * kS + 32 * ks + 8 * grp;
+        const bf16x8 vh = *reinterpret_cast<const bf16x8 *>(s_vh + at);
+        const bf16x8 vl = *reinterpret_cast<const bf16x8 *>(s_vl + at);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph[ks], o[n], 0, 0, 0);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl[ks], o[n], 0, 0, 0);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[ks], o[n], 0, 0, 0);
+      }
   }
+  l += __shfl_xor(l, 16, kWave);
+  l += __shfl_xor(l, 32, kWave);
+  if (c >= nr) return;
+  const float inv = 1.0f / l;
+  float *out = direct + (size_t)(tile.x + c) * d.H + h * kD + 4 * grp;
 #pragma unroll
-  for (int v = 0; v < 4; v++) {
-    const int row = 4 * grp + v;
-    if (row >= nr) continue;
-    const float inv = 1.0f / l[v];
-#pragma unroll
-    for (int n = 0; n < 4; n++)
-      direct[(size_t)(tile.x + row) * d.H + h * kD + n * 16 + c] = o[n][v] * inv;
-  }
+  for (int n = 0; n < 4; n++)
+    *reinterpret_cast<float4 *>(out + 16 * n) =
+        make_float4(o[n][0] * inv, o[n][1] * inv, o[n][2] * inv, o[n][3] * inv);
 }
 
 // Pass 4: chunks combined in order, rounded to f32, and prepared as the
@@ -1878,13 +1979,15 @@ void launch_attn_pv(hipStream_t s, int rows, int max_kv, const StepDims &d, cons
   (void)ok;
 }
 
-bool attention_chunk_supported(int D, int G) { return D == 64 && G >= 1 && G <= 8; }
+bool attention_chunk_supported(int D, int G) {
+  return D == 64 && (G == 1 || G == 2 || G == 4 || G == 6 || G == 7 || G == 8);
+}
 
 void launch_attn_chunk(hipStream_t s, int n_tiles, const StepDims &d, const int4 *tiles,
                        const float *q_rot, const float *kpool, const float *vpool,
                        const int32_t *page_table, float *direct) {
   if (n_tiles <= 0) return;
-  const dim3 grid(n_tiles, d.NKV);
+  const dim3 grid(n_tiles * d.NKV);  // tile-major: the longest tiles of every KV head first
   switch (d.G) {
 #define L(GG)                                                                                 \
   case GG:                                                                                    \

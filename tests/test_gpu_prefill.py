@@ -130,3 +130,11 @@ def test_chunk_attention_matches_oracle_within_tolerance():
     close(res[1]["logits"], sb.logits(), "decode lane")
     for layer in range(c["layers"]):
         assert float(np.abs(m.seq_read_kv(a, layer, True) - sa.kv(layer, True)).max()) < 1e-3
+    # a step of chunk rows only (no row left to the exact passes), 130 rows
+    # ending at a ragged 2-row tile
+    more = [int(v) for v in rng.integers(0, c["vocabulary"], 130)]
+    res = m.step([dict(seq=a, tokens=more, logits=True)])
+    for tok in more:
+        o.forward_batch([sa], [tok])
+    assert res[0]["status"] == 0
+    close(res[0]["logits"], sa.logits(), "chunk-only step")
