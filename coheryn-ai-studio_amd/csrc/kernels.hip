@@ -1204,13 +1204,24 @@ __global__ __launch_bounds__(256) void k_qkv_post(StepDims d, const float *__res
 // three operations: f32 product, widening, f64 add.
 //
 // Pass 1 (scores): one thread per cached token; its K row sits in VGPRs; for
-// each query head the dot is summed in f64 in element order (cpu.rs:31-35),
-// two heads interleaved.  s = f32(dot) * scale, stored per token as 8 floats
-// (scores[row][kv_head][t][8], slot = q head within the group, unused slots 0);
-// per-256-token chunk maxima per head.
+// each query head the dot is summed in f64 in element order (cpu.rs:31-35).
+// All kG heads advance together, kE elements at a time, issued as groups
+// [products][widenings][adds]: a head's consecutive adds are kG instructions
+// apart, so the f64 latency is covered inside the wave (the compiler would
+// otherwise chain every triple through one temporary).  s = f32(dot) * scale,
+// stored per token as 8 floats (scores[row][kv_head][t][8], slot = q head
+// within the group, unused slots 0); per-256-token chunk maxima per head.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float f4get(const float4 &v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// Empty asm that takes each value as a VGPR operand: every value is live and
+// computed at this point, which fixes the issue order of a group.
+template <typename T, int kN>
+__device__ __forceinline__ void pin_vgprs(T (&v)[kN]) {
+#pragma unroll
+  for (int i = 0; i < kN; i++) asm volatile("" : "+v"(v[i]));
 }
 
 template <int kD, int kG>
@@ -1243,21 +1254,33 @@ __global__ __launch_bounds__(256) void k_attn_scores(StepDims d, const float *__
     for (int j = 0; j < kD / 4; j++) k4[j] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   const float *qbase = q_rot + (size_t)r * d.H + (size_t)g * kG * kD;
+  constexpr int kE = kD == 64 ? 4 : 1;  // elements per group (VGPR budget)
+  double acc[kG];
+#pragma unroll
+  for (int h = 0; h < kG; h++) acc[h] = -0.0;
+#pragma unroll
+  for (int j0 = 0; j0 < kD; j0 += kE) {
+    float pr[kE * kG];
+#pragma unroll
+    for (int e = 0; e < kE; e++) {
+      const float kj = f4get(k4[(j0 + e) / 4], (j0 + e) % 4);
+#pragma unroll
+      for (int h = 0; h < kG; h++) pr[e * kG + h] = qbase[h * kD + j0 + e] * kj;
+    }
+    pin_vgprs(pr);
+    double w[kE * kG];
+#pragma unroll
+    for (int i = 0; i < kE * kG; i++) w[i] = (double)pr[i];
+    pin_vgprs(w);
+#pragma unroll
+    for (int e = 0; e < kE; e++)
+#pragma unroll
+      for (int h = 0; h < kG; h++) acc[h] += w[e * kG + h];
+    pin_vgprs(acc);
+  }
   float sc[kG];
 #pragma unroll
-  for (int h0 = 0; h0 < kG; h0 += 2) {
-    const float *q0 = qbase + h0 * kD;
-    const float *q1 = qbase + (h0 + 1 < kG ? h0 + 1 : h0) * kD;
-    double a0 = -0.0, a1 = -0.0;
-#pragma unroll
-    for (int j = 0; j < kD; j++) {
-      const float kj = f4get(k4[j / 4], j % 4);
-      a0 += (double)(q0[j] * kj);
-      if (h0 + 1 < kG) a1 += (double)(q1[j] * kj);
-    }
-    sc[h0] = (float)a0 * d.scale;
-    if (h0 + 1 < kG) sc[h0 + 1] = (float)a1 * d.scale;
-  }
+  for (int h = 0; h < kG; h++) sc[h] = (float)acc[h] * d.scale;
   bool bad = false;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   if (valid) {
