@@ -39,13 +39,16 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_decode128.json")
 # (o and down share one instance and grid, so counters cannot tell them apart)
 CATEGORY_KERNEL = {"attn_scores": "k_attn_scores<64, 7>", "attn_softmax_stats": "k_attn_exp<7>",
                    "attn_pv": "k_attn_pv<64, 7>", "attn_combine_act": "k_attn_combine<8>",
-                   "matvec_gate_up_swiglu": "k_mv_q8s<2, 2>", "matvec_head_argmax": "k_mv_q8w<3, 1>"}
-PMC_CMD = ("rocprofv3 --pmc {counter} --kernel-include-regex \"k_attn|k_mv\" --output-format csv "
+                   "matvec_qkv": "k_mv_q8s<0, 1, 2, 8>", "matvec_o_residual": "k_mv_q8s<1, 1, 2, 8>",
+                   "matvec_gate_up_swiglu": "k_mv_q8c<2, 2, 2, 4, 8>",
+                   "matvec_down_residual": "k_mv_q8s<1, 1, 4, 8>",
+                   "matvec_head_argmax": "k_mv_q8c<3, 1, 2, 4, 8>"}
+PMC_CMD = ("COHX_GRAPHS=0 rocprofv3 --pmc {counter} --kernel-include-regex \"k_attn|k_mv\" --output-format csv "
            "-d <dir> -o <name> -- python3 bench.py --steps 2 --warmup 1 --secondary-lanes 0 "
-           "--no-cpu-baseline")
+           "--no-cpu-baseline --no-c3 --no-c4")
 COPY_CMD = ("rocprofv3 --pmc {counter} --output-format csv -d <dir> -o <name> -- "
             "python3 bench.py --copy-probe")
-TRACE_CMD = ("rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o <name> -- "
+TRACE_CMD = ("COHX_GRAPHS=0 rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o <name> -- "
              "python3 bench.py")
 
 
@@ -382,15 +385,18 @@ def summarize_counters(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, lan
 
 def summarize_trace(trace_csv, bench_json):
     """Markdown summary of a rocprofv3 --kernel-trace run of the default bench
-    command: per kernel instance and grid width (which tells the 32- and
-    128-lane workloads apart) the dispatch count and mean duration, next to
-    the dispatch-event means of a plain run of the same command on the same
-    machine (under the tracer those events also time the tracer's work)."""
+    command: per kernel instance and grid shape (x tells the 32- and 128-lane
+    workloads apart, z the KV depth of the attention passes, which separates
+    the 128-lane decode from the longer-context workloads) the dispatch count
+    and mean duration, next to the dispatch-event means of a plain run of the
+    same command on the same machine (under the tracer those events also time
+    the tracer's work)."""
     import csv
     groups = {}
     with open(trace_csv) as f:
         for row in csv.DictReader(f):
-            k = (kernel_instance(row["Kernel_Name"]), int(row["Grid_Size_X"]))
+            k = (kernel_instance(row["Kernel_Name"]),
+                 f'{row["Grid_Size_X"]}x{row["Grid_Size_Y"]}x{row["Grid_Size_Z"]}')
             g = groups.setdefault(k, [])
             g.append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
     with open(bench_json) as f:
@@ -402,7 +408,7 @@ def summarize_trace(trace_csv, bench_json):
     print("Plain-run dispatch-event means, 128 lanes (us per launch):\n")
     for name, v in line["kernels"].items():
         print(f"- {name}: {v['ms_per_step'] * 1e3 / v['launches_per_step']:.2f}")
-    print("\n| kernel | grid x | dispatches | mean us | min us | max us | total ms |")
+    print("\n| kernel | grid (threads) | dispatches | mean us | min us | max us | total ms |")
     print("|---|---:|---:|---:|---:|---:|---:|")
     for (name, gx), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
         if sum(d) < 1000:
