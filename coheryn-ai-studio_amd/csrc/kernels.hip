@@ -448,139 +448,6 @@ __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int r
 }
 
 // ---------------------------------------------------------------------------
-// Wave-chain Q8_0 matvec for short K: one wave owns kNM m-tiles x one n-tile
-// and runs the reference block chain in registers (no LDS, no barriers); the
-// operands of the next kDepth block pairs are in flight in a register ring.
-// A workgroup is the n_tiles waves of one weight tile (A loads shared in L1).
-// ---------------------------------------------------------------------------
-template <int kNM>
-struct Q8Pair {
-  uint4 a[kNM];
-  uint4 b;
-  uint2 dw[kNM][2];  // the lane's 4 output rows, blocks 2p and 2p+1
-  uint32_t da;       // the lane's batch column, blocks 2p (low) and 2p+1 (high)
-};
-
-template <int kNM>
-__device__ __forceinline__ void q8_pair_load(Q8Pair<kNM> &r, const MatrixView &w,
-                                             const ActView &act, int unit, int nt, int pair,
-                                             int lane, int rsub) {
-  const int nbp = w.nbp;
-#pragma unroll
-  for (int m = 0; m < kNM; m++) {
-    r.a[m] = *reinterpret_cast<const uint4 *>(w.qs + q8_byte(unit * kNM + m, nbp, pair * 2, lane, 0));
-    r.dw[m][0] = *reinterpret_cast<const uint2 *>(w.ds + q8_scale(unit * kNM + m, nbp, pair * 2, rsub));
-    r.dw[m][1] = *reinterpret_cast<const uint2 *>(w.ds + q8_scale(unit * kNM + m, nbp, pair * 2 + 1, rsub));
-  }
-  r.b = *reinterpret_cast<const uint4 *>(act.qs + q8_byte(nt, nbp, pair * 2, lane, 0));
-  r.da = (uint32_t)act.ds[q8_scale(nt, nbp, pair * 2, lane % 16)] |
-         ((uint32_t)act.ds[q8_scale(nt, nbp, pair * 2 + 1, lane % 16)] << 16);
-}
-
-template <int kNM>
-__device__ __forceinline__ void q8_pair_chain(const Q8Pair<kNM> &r, float (&acc)[kNM][4]) {
-  const v4i zero = {0, 0, 0, 0};
-#pragma unroll
-  for (int h = 0; h < 2; h++) {
-    const long bop = h ? hi64(r.b) : lo64(r.b);
-    const float da = h2f((uint16_t)(h ? (r.da >> 16) : (r.da & 0xffffu)));
-#pragma unroll
-    for (int m = 0; m < kNM; m++) {
-      const v4i sum = __builtin_amdgcn_mfma_i32_16x16x32_i8(h ? hi64(r.a[m]) : lo64(r.a[m]), bop,
-                                                            zero, 0, 0, 0);
-      const uint2 s2 = r.dw[m][h];
-      const float dw[4] = {h2f((uint16_t)(s2.x & 0xffffu)), h2f((uint16_t)(s2.x >> 16)),
-                           h2f((uint16_t)(s2.y & 0xffffu)), h2f((uint16_t)(s2.y >> 16))};
-#pragma unroll
-      for (int i = 0; i < 4; i++) acc[m][i] = fmaf((float)sum[i], dw[i] * da, acc[m][i]);
-    }
-  }
-}
-
-template <int kEpi, int kNM>
-__global__ __launch_bounds__(512) void k_mv_q8w(MatrixView w, ActView act, int rows_b,
-                                                int n_tiles, MatvecOut o) {
-  constexpr int kDepth = 4;
-  const int lane = threadIdx.x % kWave;
-  const int nt = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int unit = blockIdx.x;
-  const int units = w.mtiles / kNM;
-  if (unit >= units || nt >= n_tiles) return;
-  const int npairs = w.nbp / 2, rsub = 4 * (lane / 16);
-  float acc[kNM][4];
-#pragma unroll
-  for (int m = 0; m < kNM; m++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) acc[m][i] = 0.0f;
-  Q8Pair<kNM> ring[kDepth];
-#pragma unroll
-  for (int i = 0; i < kDepth; i++)
-    if (i < npairs) q8_pair_load(ring[i], w, act, unit, nt, i, lane, rsub);
-  for (int p0 = 0; p0 < npairs; p0 += kDepth) {
-#pragma unroll
-    for (int u = 0; u < kDepth; u++) {
-      const int pr = p0 + u;
-      if (pr < npairs) {
-        q8_pair_chain(ring[u], acc);
-        if (pr + kDepth < npairs) q8_pair_load(ring[u], w, act, unit, nt, pr + kDepth, lane, rsub);
-      }
-    }
-  }
-  // ---- epilogue: lane holds rows unit*16 + rsub + i (per m-tile), batch row nt*16 + lane%16
-  const int r = nt * 16 + lane % 16;
-  const bool rvalid = r < rows_b;
-  const int er = (rvalid && o.err_rows) ? (int)o.err_rows[r] : r;
-  bool bad = false;
-  if (kEpi == kEpiArgmax) {
-    float best = 0.0f;
-    int best_row = 0;
-    bool have = false;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int row = unit * 16 + rsub + i;
-      if (!rvalid || row >= w.rows) continue;
-      const float v = acc[0][i];
-      bad |= !finitef(v);
-      if (o.logits) o.logits[(size_t)r * w.rows + row] = v;
-      if (!have || v > best) {
-        best = v;
-        best_row = row;
-        have = true;
-      }
-    }
-    unsigned long long key = have ? argmax_key(best, best_row) : 0ull;
-    unsigned long long x = __shfl_xor(key, 16, kWave);
-    key = x > key ? x : key;
-    x = __shfl_xor(key, 32, kWave);
-    key = x > key ? x : key;
-    if (lane < 16 && rvalid) o.argmax[(size_t)r * units + unit] = key;
-  } else if (kEpi == kEpiSwiglu) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int row = unit * 16 + rsub + i;
-      if (!rvalid || row >= w.rows / 2) continue;
-      const float g = acc[0][i], u = acc[kNM - 1][i];
-      bad |= !finitef(g) || !finitef(u);
-      o.out[(size_t)r * o.ld + row] = (g / (1.0f + exp_f32(-g))) * u;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int row = unit * 16 + rsub + i;
-      if (!rvalid || row >= w.rows) continue;
-      const float v = acc[0][i];
-      bad |= !finitef(v);
-      float *q = o.out + (size_t)r * o.ld + row;
-      if (kEpi == kEpiResidual)
-        *q = *q + v;
-      else
-        *q = v;
-    }
-  }
-  if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
-}
-
-// ---------------------------------------------------------------------------
 // Register-chain Q8_0 matvec for short K.  A wave owns kNM weight tiles x kNN
 // batch tiles and walks the blocks in order, as the reference chain does
 // (quant.rs:265-272): per block one int8 MFMA gives the exact isum of every
