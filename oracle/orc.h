@@ -22,6 +22,11 @@
  *                            token-0 closed form, EOS stop, tiny-model
  *                            brute-force re-derivation in numpy (f64)
  *   pack                     closed-form prefix sums / page arithmetic
+ *   q35 delta step           fixtures/qwen35/operations-v1.json (3 steps, 2e-6)
+ *   q35 conv / norm / gates  closed forms from qwen35/kernels.rs tests
+ *   q35 partial rope         identity at position 0, untouched tail, f64 closed form
+ *   q35 forward              batched == individual, float64 numpy textbook hybrid
+ *                            step within tolerance, planted-mistake check
  */
 #ifndef ORC_H
 #define ORC_H
@@ -127,6 +132,53 @@ int orc_forward_row(const orc_model *m, orc_session *s, uint32_t token, int logi
 /* Optional observer: x after each block, per lane (layers*hidden floats). */
 int orc_forward_batch_trace(const orc_model *m, orc_session **sessions, const uint32_t *tokens,
                             size_t n, int32_t *errors, float *trace);
+
+/* ---- Qwen3.5 hybrid text model: qwen35/execution.rs, qwen35/kernels.rs ---- */
+typedef struct {
+  uint32_t layers, hidden, intermediate, vocabulary, heads, kv_heads, head_dim;
+  uint32_t key_heads, value_heads, key_dim, value_dim, conv_kernel, rotary_dim, context;
+  float epsilon, rope_base;
+  uint8_t full[128]; /* 1: full attention, 0: linear attention (config.rs layer_types) */
+} orc_q35_config;
+
+/* Tensor slots per layer (unused slots of the other mixer kind stay empty). */
+enum {
+  ORC_Q35_INPUT_NORM = 0, ORC_Q35_POST_NORM, ORC_Q35_GATE, ORC_Q35_UP, ORC_Q35_DOWN,
+  ORC_Q35_Q, ORC_Q35_K, ORC_Q35_V, ORC_Q35_O, ORC_Q35_QNORM, ORC_Q35_KNORM,
+  ORC_Q35_QKV, ORC_Q35_Z, ORC_Q35_A, ORC_Q35_B, ORC_Q35_OUT, ORC_Q35_CONV, ORC_Q35_ALOG,
+  ORC_Q35_DT, ORC_Q35_NORM, ORC_Q35_LAYER_TENSORS
+};
+
+typedef struct orc_q35_model orc_q35_model;
+typedef struct orc_q35_session orc_q35_session;
+
+float orc_q35_sigmoid(float x);
+float orc_q35_silu(float x);
+float orc_q35_softplus(float x);
+int orc_q35_norm(const float *in, const float *w, float eps, int zero_centered, float *out,
+                 size_t n);
+int orc_q35_conv_step(float *history, uint32_t *cursor, size_t channels, size_t kernel,
+                      const float *in, const float *w, float *out);
+int orc_q35_delta_step(float *memory, size_t heads, size_t key, size_t value, const float *q,
+                       const float *k, const float *v, const float *log_decay,
+                       const float *beta, float *out);
+int orc_q35_partial_rope(float *values, size_t n, size_t head, size_t rotary, size_t position,
+                         float base);
+/* globals: embed_tokens, final norm, lm_head (data == NULL: tied to embed_tokens).
+ * Matrices: dtype 0 (F32) or 30 (BF16), ne0 = input width, ne1 = output rows. */
+int orc_q35_model_new(const orc_q35_config *c, const orc_tensor *globals,
+                      const orc_tensor *layers, int threads, orc_q35_model **out);
+void orc_q35_model_free(orc_q35_model *m);
+int orc_q35_session_new(const orc_q35_model *m, uint32_t context, orc_q35_session **out);
+void orc_q35_session_free(orc_q35_session *s);
+uint32_t orc_q35_session_position(const orc_q35_session *s);
+const float *orc_q35_session_logits(const orc_q35_session *s);
+int orc_q35_session_state(const orc_q35_model *m, const orc_q35_session *s, uint32_t layer,
+                          int which, float *out);
+/* One token per lane (logits[i]: compute the vocabulary projection). */
+int orc_q35_forward_batch(const orc_q35_model *m, orc_q35_session **sessions,
+                          const uint32_t *tokens, const uint8_t *logits, size_t n,
+                          int32_t *errors);
 
 /* ---- ragged packer (host restatement of the GPU packing contract) --------- */
 /* lanes: n_tokens[i] >= 1, start[i] = first position, page tables row-major

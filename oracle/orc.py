@@ -340,3 +340,204 @@ def pack(n_tokens, start, pages, page_size):
                       page_size, ptr(cu, _u32p), ptr(pos, _u32p), ptr(slot, _i64p),
                       ptr(lane, _u32p))
     return rc, cu, pos, slot, lane
+
+# ---- Qwen3.5 hybrid text model -------------------------------------------------
+
+class OrcQ35Config(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in
+                ("layers", "hidden", "intermediate", "vocabulary", "heads", "kv_heads",
+                 "head_dim", "key_heads", "value_heads", "key_dim", "value_dim", "conv_kernel",
+                 "rotary_dim", "context")] + [("epsilon", ctypes.c_float),
+                                              ("rope_base", ctypes.c_float),
+                                              ("full", ctypes.c_uint8 * 128)]
+
+
+Q35_SLOTS = ["input_layernorm.weight", "post_attention_layernorm.weight", "mlp.gate_proj.weight",
+             "mlp.up_proj.weight", "mlp.down_proj.weight", "self_attn.q_proj.weight",
+             "self_attn.k_proj.weight", "self_attn.v_proj.weight", "self_attn.o_proj.weight",
+             "self_attn.q_norm.weight", "self_attn.k_norm.weight",
+             "linear_attn.in_proj_qkv.weight", "linear_attn.in_proj_z.weight",
+             "linear_attn.in_proj_a.weight", "linear_attn.in_proj_b.weight",
+             "linear_attn.out_proj.weight", "linear_attn.conv1d.weight", "linear_attn.A_log",
+             "linear_attn.dt_bias", "linear_attn.norm.weight"]
+
+_q35_sig = {
+    "orc_q35_sigmoid": (ctypes.c_float, [ctypes.c_float]),
+    "orc_q35_silu": (ctypes.c_float, [ctypes.c_float]),
+    "orc_q35_softplus": (ctypes.c_float, [ctypes.c_float]),
+    "orc_q35_norm": (ctypes.c_int, [_f32p, _f32p, ctypes.c_float, ctypes.c_int, _f32p, _sz]),
+    "orc_q35_conv_step": (ctypes.c_int, [_f32p, _u32p, _sz, _sz, _f32p, _f32p, _f32p]),
+    "orc_q35_delta_step": (ctypes.c_int, [_f32p, _sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p,
+                                          _f32p, _f32p]),
+    "orc_q35_partial_rope": (ctypes.c_int, [_f32p, _sz, _sz, _sz, _sz, ctypes.c_float]),
+    "orc_q35_model_new": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                         ctypes.c_int, ctypes.POINTER(ctypes.c_void_p)]),
+    "orc_q35_model_free": (None, [ctypes.c_void_p]),
+    "orc_q35_session_new": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32,
+                                           ctypes.POINTER(ctypes.c_void_p)]),
+    "orc_q35_session_free": (None, [ctypes.c_void_p]),
+    "orc_q35_session_position": (ctypes.c_uint32, [ctypes.c_void_p]),
+    "orc_q35_session_logits": (_f32p, [ctypes.c_void_p]),
+    "orc_q35_session_state": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32,
+                                             ctypes.c_int, _f32p]),
+    "orc_q35_forward_batch": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _u32p, _u8p, _sz,
+                                             _i32p]),
+}
+for _name, (_res, _args) in _q35_sig.items():
+    _fn = getattr(lib, _name)
+    _fn.restype, _fn.argtypes = _res, _args
+
+
+def q35_sigmoid(x):
+    return float(lib.orc_q35_sigmoid(x))
+
+
+def q35_silu(x):
+    return float(lib.orc_q35_silu(x))
+
+
+def q35_softplus(x):
+    return float(lib.orc_q35_softplus(x))
+
+
+def q35_norm(x, w, eps, zero_centered):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.zeros_like(x)
+    rc = lib.orc_q35_norm(ptr(x, _f32p), ptr(w, _f32p), eps, int(zero_centered), ptr(out, _f32p),
+                          x.size)
+    return rc, out
+
+
+class ConvState:
+    """kernels.rs:54-120 ConvState over [channels][kernel]."""
+
+    def __init__(self, channels, kernel):
+        self.history = np.zeros(channels * kernel, np.float32)
+        self.cursor = np.zeros(1, np.uint32)
+        self.channels, self.kernel = channels, kernel
+
+    def step(self, x, w):
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        out = np.zeros(self.channels, np.float32)
+        rc = lib.orc_q35_conv_step(ptr(self.history, _f32p), ptr(self.cursor, _u32p),
+                                   self.channels, self.kernel, ptr(x, _f32p), ptr(w, _f32p),
+                                   ptr(out, _f32p))
+        return rc, out
+
+
+class DeltaState:
+    """kernels.rs:122-214 DeltaState over [heads][key][value]."""
+
+    def __init__(self, heads, key, value):
+        self.memory = np.zeros(heads * key * value, np.float32)
+        self.shape = (heads, key, value)
+
+    def step(self, q, k, v, log_decay, beta):
+        h, kd, vd = self.shape
+        a = [np.ascontiguousarray(x, np.float32) for x in (q, k, v, log_decay, beta)]
+        out = np.zeros(h * vd, np.float32)
+        rc = lib.orc_q35_delta_step(ptr(self.memory, _f32p), h, kd, vd, *[ptr(x, _f32p) for x in a],
+                                    ptr(out, _f32p))
+        return rc, out
+
+
+def q35_partial_rope(x, head, rotary, position, base):
+    x = np.array(x, np.float32)
+    rc = lib.orc_q35_partial_rope(ptr(x, _f32p), x.size, head, rotary, position, base)
+    return rc, x
+
+
+class Qwen35Model:
+    """Oracle Qwen3.5 hybrid model over in-memory tensors (dict name -> Tensor)."""
+
+    def __init__(self, config, tensors, threads=None):
+        self.config = config
+        self.tensors = tensors
+        c = OrcQ35Config()
+        for k in ("layers", "hidden", "intermediate", "vocabulary", "heads", "kv_heads",
+                  "head_dim", "key_heads", "value_heads", "key_dim", "value_dim", "conv_kernel",
+                  "rotary_dim", "context"):
+            setattr(c, k, config[k])
+        c.epsilon, c.rope_base = config["epsilon"], config["rope_base"]
+        for i, f in enumerate(config["full"]):
+            c.full[i] = 1 if f else 0
+
+        def ot(name):
+            t = tensors.get(name)
+            if t is None:
+                return OrcTensor(0, 0, 0, None, 0)
+            n = int(np.prod(t.shape))
+            ne0 = t.shape[0]
+            return OrcTensor(t.dtype, ne0, n // ne0, t.data.ctypes.data, t.data.nbytes)
+
+        g = (OrcTensor * 3)(ot("model.language_model.embed_tokens.weight"),
+                            ot("model.language_model.norm.weight"), ot("lm_head.weight"))
+        L = config["layers"]
+        lt = (OrcTensor * (L * len(Q35_SLOTS)))()
+        for i in range(L):
+            for j, slot in enumerate(Q35_SLOTS):
+                lt[i * len(Q35_SLOTS) + j] = ot(f"model.language_model.layers.{i}.{slot}")
+        h = ctypes.c_void_p()
+        threads = threads or min(16, os.cpu_count() or 1)
+        rc = lib.orc_q35_model_new(ctypes.byref(c), g, lt, threads, ctypes.byref(h))
+        if rc:
+            raise ValueError(f"oracle Qwen3.5 model rejected ({rc})")
+        self.h = h
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib.orc_q35_model_free(self.h)
+            self.h = None
+
+    def session(self, context):
+        return Qwen35Session(self, context)
+
+    def forward_batch(self, sessions, tokens, logits=None):
+        n = len(sessions)
+        arr = (ctypes.c_void_p * n)(*[s.h for s in sessions])
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        want = np.ascontiguousarray([1] * n if logits is None else logits, np.uint8)
+        errs = np.array([s.error for s in sessions], np.int32)
+        lib.orc_q35_forward_batch(self.h, arr, ptr(toks, _u32p), ptr(want, _u8p), n,
+                                  ptr(errs, _i32p))
+        for s, e in zip(sessions, errs):
+            s.error = int(e)
+        return errs
+
+
+class Qwen35Session:
+    def __init__(self, model, context):
+        self.model = model
+        h = ctypes.c_void_p()
+        rc = lib.orc_q35_session_new(model.h, context, ctypes.byref(h))
+        if rc:
+            raise ValueError(f"oracle session rejected ({rc})")
+        self.h = h
+        self.error = 0
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib.orc_q35_session_free(self.h)
+            self.h = None
+
+    def position(self):
+        return int(lib.orc_q35_session_position(self.h))
+
+    def logits(self):
+        p = lib.orc_q35_session_logits(self.h)
+        return np.ctypeslib.as_array(p, (self.model.config["vocabulary"],)).copy()
+
+    def state(self, layer, which):
+        """0/1: K/V rows [0, position); 2: conv ring; 3: delta memory; 4: conv cursor."""
+        c = self.model.config
+        kw = c["kv_heads"] * c["head_dim"]
+        ch = 2 * c["key_heads"] * c["key_dim"] + c["value_heads"] * c["value_dim"]
+        n = {0: self.position() * kw, 1: self.position() * kw, 2: ch * c["conv_kernel"],
+             3: c["value_heads"] * c["key_dim"] * c["value_dim"], 4: 1}[which]
+        out = np.zeros(max(n, 1), np.float32)
+        rc = lib.orc_q35_session_state(self.model.h, self.h, layer, which, ptr(out, _f32p))
+        if rc:
+            raise ValueError(f"state {which} of layer {layer}: {rc}")
+        return out[:n]
