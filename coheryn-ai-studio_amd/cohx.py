@@ -77,6 +77,17 @@ class StepOut(ctypes.Structure):
                 ("kv_bytes", ctypes.c_uint64), ("elapsed_ns", ctypes.c_uint64)]
 
 
+class Qwen35Desc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "layers", "hidden", "intermediate", "vocabulary", "heads", "kv_heads", "head_dim",
+        "linear_key_heads", "linear_value_heads", "linear_key_dim", "linear_value_dim",
+        "conv_kernel", "rotary_dim", "context", "tied")] + [
+        ("epsilon", ctypes.c_float), ("rope_base", ctypes.c_float),
+        ("full_attention", ctypes.c_uint8 * 128)] + [(n, ctypes.c_uint32) for n in (
+            "max_lanes", "max_rows", "max_seqs", "max_context", "n_eog")] + [
+        ("eog", ctypes.c_uint32 * 4)]
+
+
 class GenOptions(ctypes.Structure):
     _fields_ = [("max_tokens", ctypes.c_uint32), ("temperature", ctypes.c_float),
                 ("top_k", ctypes.c_uint32), ("top_p", ctypes.c_float), ("seed", ctypes.c_uint64),
@@ -99,6 +110,8 @@ class BatchStepC(ctypes.Structure):
 EXPORTS = {
     "cohx_create": (ctypes.c_int, [ctypes.POINTER(ModelDesc), ctypes.c_int,
                                    ctypes.POINTER(ctypes.c_void_p)]),
+    "cohx_create_qwen35": (ctypes.c_int, [ctypes.POINTER(Qwen35Desc), ctypes.c_int,
+                                          ctypes.POINTER(ctypes.c_void_p)]),
     "cohx_destroy": (None, [ctypes.c_void_p]),
     "cohx_last_error": (ctypes.c_char_p, [ctypes.c_void_p]),
     "cohx_upload_tensor": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_uint32,
@@ -444,3 +457,66 @@ def generate(model, prompt, options):
             model.step_generation(st)
         st.sample()
     return st
+
+
+class Qwen35(Model):
+    """An MI355X context holding one Qwen3.5 hybrid text model (qwen35::Model,
+    qwen35/mod.rs:103-193): tensors by their safetensors names, BF16
+    matrices.  Steps, sequences and errors behave as for Model; a fork is a
+    full snapshot copy, and read_state exposes the recurrent state."""
+
+    def __init__(self, config, tensors, max_lanes=16, max_rows=None, max_seqs=None,
+                 max_context=None, device=0, eog=None):
+        self.config = dict(config)
+        L = lib()
+        d = Qwen35Desc()
+        for k, v in (("layers", "layers"), ("hidden", "hidden"), ("intermediate", "intermediate"),
+                     ("vocabulary", "vocabulary"), ("heads", "heads"), ("kv_heads", "kv_heads"),
+                     ("head_dim", "head_dim"), ("linear_key_heads", "key_heads"),
+                     ("linear_value_heads", "value_heads"), ("linear_key_dim", "key_dim"),
+                     ("linear_value_dim", "value_dim"), ("conv_kernel", "conv_kernel"),
+                     ("rotary_dim", "rotary_dim"), ("context", "context")):
+            setattr(d, k, int(config[v]))
+        d.tied = 1 if config.get("tied", True) else 0
+        d.epsilon = float(config["epsilon"])
+        d.rope_base = float(config["rope_base"])
+        for i, f in enumerate(config["full"]):
+            d.full_attention[i] = 1 if f else 0
+        d.max_lanes = max_lanes
+        d.max_rows = max_rows or max_lanes
+        d.max_seqs = max_seqs or max_lanes
+        d.max_context = max_context or min(int(config["context"]), 4096)
+        eog = list(eog or [])
+        d.n_eog = len(eog)
+        for i, e in enumerate(eog):
+            d.eog[i] = e
+        self.desc = d
+        h = ctypes.c_void_p()
+        rc = L.cohx_create_qwen35(ctypes.byref(d), device, ctypes.byref(h))
+        if rc:
+            raise CohxError(rc, "cohx_create_qwen35")
+        self.h = h
+        self.max_lanes = max_lanes
+        self.max_context = d.max_context
+        for name, t in tensors.items():
+            data = np.ascontiguousarray(t.data)
+            n = int(np.prod(t.shape))
+            rc = L.cohx_upload_tensor(h, name.encode(), t.dtype, t.shape[0], n // t.shape[0],
+                                      data.ctypes.data, data.nbytes)
+            self._check(rc)
+        self._check(L.cohx_finalize(h))
+
+    def read_state(self, seq, layer, which):
+        """0/1: K/V rows [0, length) of a full-attention layer; 2: conv ring
+        [channels * kernel]; 3: delta memory [value_heads * key_dim * value_dim]."""
+        c = self.config
+        n = {0: self.seq_length(seq) * c["kv_heads"] * c["head_dim"],
+             1: self.seq_length(seq) * c["kv_heads"] * c["head_dim"],
+             2: (2 * c["key_heads"] * c["key_dim"] + c["value_heads"] * c["value_dim"])
+             * c["conv_kernel"],
+             3: c["value_heads"] * c["key_dim"] * c["value_dim"]}[which]
+        out = np.zeros(max(n, 1), np.float32)
+        self._check(lib().cohx_seq_read_kv(self.h, seq, layer, which,
+                                           out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+        return out[:n]
+

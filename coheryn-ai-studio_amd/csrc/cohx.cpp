@@ -348,6 +348,7 @@ void cohx_destroy(cohx_ctx *ctx) {
   if (ctx->ws.h_tiles) (void)hipHostFree(ctx->ws.h_tiles);
   if (ctx->ws.h_row_skip) (void)hipHostFree(ctx->ws.h_row_skip);
   if (ctx->ws.h_row_map) (void)hipHostFree(ctx->ws.h_row_map);
+  q35_free(ctx);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -355,6 +356,11 @@ void cohx_destroy(cohx_ctx *ctx) {
 // compat.rs:161-221: names and shapes of the Qwen2 graph.
 int cohx_upload_tensor(cohx_ctx *ctx, const char *name, uint32_t dtype, uint64_t ne0,
                        uint64_t ne1, const void *data, size_t bytes) {
+  if (ctx && ctx->q35 && name && data) {
+    if (ctx->finalized) return fail(ctx, COHX_INVALID_REQUEST, "context already finalized");
+    (void)hipSetDevice(ctx->device);
+    return q35_upload(ctx, name, dtype, ne0, ne1, data, bytes);
+  }
   if (!ctx || !name || !data) return COHX_INVALID_REQUEST;
   if (hipSetDevice(ctx->device) != hipSuccess) return fail(ctx, COHX_DEVICE, "hipSetDevice");
   const cohx_model_desc &d = ctx->desc;
@@ -427,6 +433,7 @@ int cohx_upload_tensor(cohx_ctx *ctx, const char *name, uint32_t dtype, uint64_t
 }
 
 int cohx_finalize(cohx_ctx *ctx) {
+  if (ctx && ctx->q35) return q35_finalize(ctx);
   if (!ctx) return COHX_INVALID_REQUEST;
   const cohx_model_desc &d = ctx->desc;
   std::vector<std::string> need = {"token_embd.weight", "output_norm.weight"};
@@ -529,6 +536,10 @@ int cohx_seq_alloc(cohx_ctx *ctx, uint32_t capacity, uint32_t *seq) {
   q.capacity = capacity;
   q.pages.clear();
   *seq = s;
+  if (ctx->q35) {
+    (void)hipSetDevice(ctx->device);
+    return q35_seq_reset(ctx, s);
+  }
   return COHX_OK;
 }
 
@@ -548,8 +559,16 @@ int cohx_seq_fork(cohx_ctx *ctx, uint32_t src, uint32_t rows, uint32_t capacity,
   if (!ctx || !valid_seq(ctx, src) || !seq) return COHX_INVALID_REQUEST;
   if (rows > ctx->seqs[src].length || rows > capacity)
     return fail(ctx, COHX_INVALID_REQUEST, "fork longer than the source or the capacity");
+  if (ctx->q35 && rows != ctx->seqs[src].length)
+    return fail(ctx, COHX_UNSUPPORTED, "recurrent state forks only at the source length");
   int rc = cohx_seq_alloc(ctx, capacity, seq);
   if (rc) return rc;
+  if (ctx->q35) {
+    rc = q35_seq_copy(ctx, src, *seq, rows);
+    if (rc) return rc;
+    ctx->seqs[*seq].length = rows;
+    return COHX_OK;
+  }
   Sequence &d = ctx->seqs[*seq];
   const Sequence &s = ctx->seqs[src];
   const size_t pages = (rows + kPage - 1) / kPage;
@@ -567,6 +586,8 @@ int cohx_seq_truncate(cohx_ctx *ctx, uint32_t seq, uint32_t rows) {
   if (!ctx || !valid_seq(ctx, seq)) return COHX_INVALID_REQUEST;
   Sequence &q = ctx->seqs[seq];
   if (rows > q.length) return fail(ctx, COHX_INVALID_REQUEST, "truncate beyond length");
+  if (ctx->q35 && rows != q.length)
+    return fail(ctx, COHX_UNSUPPORTED, "recurrent state cannot be rewound");
   const size_t keep = (rows + kPage - 1) / kPage;
   for (size_t i = keep; i < q.pages.size(); i++) {
     drop_page(ctx, q.pages[i]);
@@ -584,6 +605,7 @@ int cohx_seq_length(const cohx_ctx *ctx, uint32_t seq, uint32_t *rows) {
 }
 
 uint32_t cohx_seq_pages(const cohx_ctx *ctx, uint32_t seq, int32_t *out, uint32_t cap) {
+  if (ctx && ctx->q35) return 0;  // no KV pages: contiguous per-sequence state
   if (!ctx || !valid_seq(ctx, seq)) return 0;
   const Sequence &q = ctx->seqs[seq];
   const uint32_t n = (uint32_t)q.pages.size();
@@ -594,6 +616,10 @@ uint32_t cohx_seq_pages(const cohx_ctx *ctx, uint32_t seq, int32_t *out, uint32_
 int cohx_seq_read_kv(cohx_ctx *ctx, uint32_t seq, uint32_t layer, int values, float *out) {
   if (!ctx || !valid_seq(ctx, seq) || layer >= ctx->desc.layers || !out)
     return COHX_INVALID_REQUEST;
+  if (ctx->q35) {
+    (void)hipSetDevice(ctx->device);
+    return q35_read_state(ctx, seq, layer, values, out);
+  }
   HIP_TRY(hipSetDevice(ctx->device));
   const Sequence &q = ctx->seqs[seq];
   const int NKV = ctx->desc.kv_heads, D = ctx->desc.head_dim;
@@ -613,6 +639,7 @@ int cohx_seq_read_kv(cohx_ctx *ctx, uint32_t seq, uint32_t layer, int values, fl
 
 int cohx_seq_fill_synthetic(cohx_ctx *ctx, uint32_t seq, uint32_t rows, uint64_t seed,
                             uint32_t stream) {
+  if (ctx && ctx->q35) return fail(ctx, COHX_UNSUPPORTED, "no synthetic fill for Qwen3.5");
   if (!ctx || !valid_seq(ctx, seq)) return COHX_INVALID_REQUEST;
   Sequence &q = ctx->seqs[seq];
   if (rows > q.capacity) return fail(ctx, COHX_RESOURCE, "rows exceed the sequence capacity");
@@ -778,6 +805,7 @@ ActView act_view(cohx_ctx *ctx) {
 
 extern "C" int cohx_pack(cohx_ctx *ctx, const cohx_batch *batch, uint32_t *cu, uint32_t *positions,
                          int64_t *slots, uint32_t *lanes) {
+  if (ctx && ctx->q35) return fail(ctx, COHX_UNSUPPORTED, "no paged packer for Qwen3.5");
   if (!ctx) return COHX_INVALID_REQUEST;
   HIP_TRY(hipSetDevice(ctx->device));
   Prepared p;
@@ -857,6 +885,7 @@ double matrix_pass_bytes(const MatrixView &w, int rows_b, int out_rows, bool res
 }  // namespace
 
 extern "C" int cohx_profile(cohx_ctx *ctx, int enable) {
+  if (ctx && ctx->q35) return fail(ctx, COHX_UNSUPPORTED, "no kernel profile for Qwen3.5");
   if (!ctx) return COHX_INVALID_REQUEST;
   Profiler &p = ctx->prof;
   if (enable) {
@@ -999,6 +1028,7 @@ int enqueue_device_step(cohx_ctx *ctx, const Prepared &p, int kv_grid, bool any_
 }
 
 extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
+  if (ctx && ctx->q35) return q35_step(ctx, batch, out);
   if (!ctx || !out || !out->lanes) return COHX_INVALID_REQUEST;
   const auto t_start = std::chrono::steady_clock::now();
   HIP_TRY(hipSetDevice(ctx->device));

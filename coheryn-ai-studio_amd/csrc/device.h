@@ -76,6 +76,24 @@ __device__ __forceinline__ uint16_t f2h(float f) {
 }
 __device__ __forceinline__ bool finitef(float v) { return __builtin_isfinite(v); }
 
+// Orderable key of (value, row): larger value wins, then the lower row
+// (greedy sampling keeps the first maximum, sampling.rs:160-173); -0 ties +0.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
+  if (v == 0.0f) v = 0.0f;
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)row);
+}
+
+// Empty asm that takes each value as a VGPR operand: every value is live and
+// computed at this point, which fixes the issue order of a group (the
+// scheduler would otherwise chain every f64 triple through one temporary).
+template <typename T, int kN>
+__device__ __forceinline__ void pin_vgprs(T (&v)[kN]) {
+#pragma unroll
+  for (int i = 0; i < kN; i++) asm volatile("" : "+v"(v[i]));
+}
+
 // Rust `f as i8` (saturating; NaN -> 0).
 __device__ __forceinline__ int8_t sat_i8(float v) {
   if (v != v) return 0;

@@ -93,6 +93,8 @@ struct StepKey {
 };
 constexpr size_t kMaxGraphs = 64;
 
+struct Q35Model;  // Qwen3.5 hybrid model state (q35.cpp)
+
 }  // namespace cohx
 
 struct cohx_ctx {
@@ -125,9 +127,19 @@ struct cohx_ctx {
   bool use_graphs = true;    // replay each step's launches as one captured graph
   bool prefill_mfma = true;  // F16 batches of 128+ rows on the matrix cores
   std::map<cohx::StepKey, hipGraphExec_t> graphs;
+  cohx::Q35Model *q35 = nullptr;  // set for Qwen3.5 contexts (cohx_create_qwen35)
 };
 
 namespace cohx {
 int fail(cohx_ctx *ctx, int code, const std::string &msg);
 void drop_graphs(cohx_ctx *ctx);
+// Qwen3.5 contexts: the C entry points hand over to these (q35.cpp).
+void q35_free(cohx_ctx *ctx);
+int q35_upload(cohx_ctx *ctx, const char *name, uint32_t dtype, uint64_t ne0, uint64_t ne1,
+               const void *data, size_t bytes);
+int q35_finalize(cohx_ctx *ctx);
+int q35_seq_reset(cohx_ctx *ctx, uint32_t seq);
+int q35_seq_copy(cohx_ctx *ctx, uint32_t src, uint32_t dst, uint32_t rows);
+int q35_read_state(cohx_ctx *ctx, uint32_t seq, uint32_t layer, int which, float *out);
+int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out);
 }

@@ -240,13 +240,6 @@ __global__ __launch_bounds__(256) void k_quant_act(const float *__restrict__ src
 // ---------------------------------------------------------------------------
 // Epilogues
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
-  if (v == 0.0f) v = 0.0f;  // -0 ties +0 (sampling.rs:163 compares with >)
-  uint32_t u = __float_as_uint(v);
-  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((unsigned long long)u << 32) | (unsigned long long)(0xffffffffu - (uint32_t)row);
-}
-
 // Best (value, lowest row) of one batch column over the four lanes that hold
 // it (lanes c, c+16, c+32, c+48), then one atomic per column.
 __device__ __forceinline__ void argmax_commit(float best, int best_row, bool valid, int r,
@@ -1083,13 +1076,6 @@ __device__ __forceinline__ float f4get(const float4 &v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
 
-// Empty asm that takes each value as a VGPR operand: every value is live and
-// computed at this point, which fixes the issue order of a group.
-template <typename T, int kN>
-__device__ __forceinline__ void pin_vgprs(T (&v)[kN]) {
-#pragma unroll
-  for (int i = 0; i < kN; i++) asm volatile("" : "+v"(v[i]));
-}
 
 template <int kD, int kG>
 __global__ __launch_bounds__(256) void k_attn_scores(StepDims d, const float *__restrict__ q_rot,

@@ -1,0 +1,625 @@
+// Qwen3.5 hybrid text step on the GPU, exact: every kernel reproduces the
+// engine's float arithmetic (crates/coheryn-engine/src/qwen35/execution.rs:
+// 257-608, qwen35/kernels.rs:11-269, cpu.rs:31-35,74-124) bit for bit:
+// f32 products, f64 sums in the reference's element order, glibc expf and
+// log1pf restated (exp_f32, log1p_f32), no contraction.
+//
+// Layout: activations are row-major f32 per packed row; matrices are BF16
+// tiles of 16 outputs (q35_tiled_index); the sequence state lives in slabs
+// indexed by sequence slot: K/V rows of the full-attention layers, the
+// causal-conv ring and the delta-rule memory of the linear layers.
+#include <hip/hip_runtime.h>
+
+#include "device.h"
+#include "log1pf.h"
+#include "q35.h"
+
+namespace cohx {
+namespace {
+
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// kernels.rs:11-24
+__device__ __forceinline__ float sigmoid_f32(float x) {
+  if (x >= 0.0f) return 1.0f / (1.0f + exp_f32(-x));
+  const float e = exp_f32(x);
+  return e / (1.0f + e);
+}
+__device__ __forceinline__ float silu_f32(float x) { return x * sigmoid_f32(x); }
+__device__ __forceinline__ float softplus_f32(float x) {
+  return fmaxf(x, 0.0f) + log1p_f32(exp_f32(-fabsf(x)));
+}
+
+// ---------------------------------------------------------------------------
+// Token embedding (tensor.rs read_row over BF16: exact widening).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_q35_embed(const uint16_t *__restrict__ embed,
+                                                   const uint32_t *__restrict__ tokens, int H,
+                                                   float *__restrict__ x) {
+  const int r = blockIdx.x;
+  const uint16_t *src = embed + (size_t)tokens[r] * H;
+  for (int i = threadIdx.x; i < H; i += 256) x[(size_t)r * H + i] = bf_lo(src[i]);
+}
+
+// ---------------------------------------------------------------------------
+// Norm (kernels.rs:26-52): mean of f32 squares summed in f64 in element
+// order, scale = 1/sqrt(f32(mean) + eps), y = (x*scale)*(w + zc).  The
+// squares are formed in parallel; one lane runs the ordered sum.
+// ---------------------------------------------------------------------------
+constexpr int kNormMax = kQ35MaxHidden;
+__global__ __launch_bounds__(256) void k_q35_norm(const float *__restrict__ x, int ldx,
+                                                  const uint32_t *__restrict__ src,
+                                                  const float *__restrict__ w, int n, float eps,
+                                                  int zc, float *__restrict__ out, int ldo,
+                                                  uint32_t *row_err,
+                                                  const uint32_t *__restrict__ err_row) {
+  __shared__ float sq[kNormMax];
+  __shared__ float s_scale;
+  __shared__ int s_bad;
+  const int r = blockIdx.x;
+  const float *xr = x + (size_t)(src ? src[r] : r) * ldx;
+  bool bad = false;
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const float v = xr[i];
+    sq[i] = v * v;
+    bad |= !finitef(v);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double sum = -0.0;
+    for (int i = 0; i < n; i++) sum += (double)sq[i];
+    const double mean = sum / (double)n;
+    s_bad = !(__builtin_isfinite(mean) && finitef((float)mean));
+    s_scale = 1.0f / sqrtf((float)mean + eps);
+  }
+  __syncthreads();
+  const float scale = s_scale, add = zc ? 1.0f : 0.0f;
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const float y = (xr[i] * scale) * (w[i] + add);
+    out[(size_t)r * ldo + i] = y;
+    bad |= !finitef(y);
+  }
+  if (bad || (threadIdx.x == 0 && s_bad)) atomicOr(&row_err[err_row ? err_row[r] : r], kErrRequest);
+}
+
+// ---------------------------------------------------------------------------
+// BF16 matvec (tensor.rs:380-406 -> cpu::dot): out[r][o] = f32(sum_k
+// f64(w[o][k] * x[r][k])), k in order from -0.0.  A workgroup owns 64
+// outputs (4 tiles of 16, one per wave) x 16 batch rows staged in LDS; lane
+// (o16, g) runs rows 4g..4g+3 of output o16 as four chains, issued as pinned
+// groups of products, widenings and adds.
+// ---------------------------------------------------------------------------
+constexpr int kMvRows = 16, kMvKC = 256;
+template <int kEpi>
+__global__ __launch_bounds__(256) void k_q35_mv(const uint16_t *__restrict__ w, int rows_w,
+                                                int valid_rows, int K,
+                                                const float *__restrict__ x, int ldx, int R,
+                                                float *out, int ldo,
+                                                unsigned long long *__restrict__ part,
+                                                uint32_t *row_err,
+                                                const uint32_t *__restrict__ err_row) {
+  __shared__ __align__(16) float xs[kMvRows][kMvKC];
+  __shared__ unsigned long long keys[kMvRows][64];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int o16 = lane % 16, g = lane / 16;
+  const int tile = blockIdx.x * 4 + wave, r0 = blockIdx.y * kMvRows;
+  const int o = tile * 16 + o16;
+  const bool live_tile = tile * 16 < rows_w;
+  const uint4 *wt = reinterpret_cast<const uint4 *>(w) + (size_t)tile * (K / 8) * 16 + o16;
+  double acc[4] = {-0.0, -0.0, -0.0, -0.0};
+  for (int k0 = 0; k0 < K; k0 += kMvKC) {
+    const int kc = min(kMvKC, K - k0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < kMvRows * (kMvKC / 4); i += 256) {
+      const int rr = i / (kMvKC / 4), c4 = (i % (kMvKC / 4)) * 4;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (r0 + rr < R && c4 < kc)
+        v = *reinterpret_cast<const float4 *>(x + (size_t)(r0 + rr) * ldx + k0 + c4);
+      *reinterpret_cast<float4 *>(&xs[rr][c4]) = v;
+    }
+    __syncthreads();
+    if (!live_tile) continue;
+    for (int kk = 0; kk < kc; kk += 8) {
+      const uint4 wv = wt[(size_t)((k0 + kk) / 8) * 16];
+      const float wf[8] = {bf_lo(wv.x), bf_hi(wv.x), bf_lo(wv.y), bf_hi(wv.y),
+                           bf_lo(wv.z), bf_hi(wv.z), bf_lo(wv.w), bf_hi(wv.w)};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        float pr[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) pr[rr] = wf[e] * xs[g * 4 + rr][kk + e];
+        pin_vgprs(pr);
+        double wd[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) wd[rr] = (double)pr[rr];
+        pin_vgprs(wd);
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) acc[rr] += wd[rr];
+        pin_vgprs(acc);
+      }
+    }
+  }
+#pragma unroll
+  for (int rr = 0; rr < 4; rr++) {
+    const int br = g * 4 + rr, r = r0 + br;
+    const float v = (float)acc[rr];
+    const bool ok = live_tile && r < R && o < valid_rows;
+    if (kEpi == kQ35Argmax) {
+      keys[br][wave * 16 + o16] = ok ? argmax_key(v, o) : 0ull;
+      if (ok && out) out[(size_t)r * ldo + o] = v;
+    } else if (ok) {
+      float *p = out + (size_t)r * ldo + o;
+      *p = kEpi == kQ35Residual ? *p + v : v;
+    }
+    if (ok && !finitef(v)) atomicOr(&row_err[err_row ? err_row[r] : r], kErrNonFinite);
+  }
+  if (kEpi == kQ35Argmax) {
+    __syncthreads();
+    if (threadIdx.x < kMvRows && r0 + (int)threadIdx.x < R) {
+      unsigned long long best = 0;
+      for (int i = 0; i < 64; i++) best = keys[threadIdx.x][i] > best ? keys[threadIdx.x][i] : best;
+      part[(size_t)(r0 + threadIdx.x) * gridDim.x + blockIdx.x] = best;
+    }
+  }
+}
+
+// cpu.rs:74-78 swiglu
+__global__ __launch_bounds__(256) void k_q35_swiglu(const float *__restrict__ gu, int ldgu, int F,
+                                                    int up_off, float *__restrict__ h, int ldh) {
+  const int r = blockIdx.y;
+  for (int f = blockIdx.x * 256 + threadIdx.x; f < F; f += gridDim.x * 256) {
+    const float g = gu[(size_t)r * ldgu + f], u = gu[(size_t)r * ldgu + up_off + f];
+    h[(size_t)r * ldh + f] = (g / (1.0f + exp_f32(-g))) * u;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Causal depthwise conv (kernels.rs:54-120), one thread per channel walking
+// its lane's tokens in order.  The ring is kept in time order in registers
+// (oldest first), which is exactly the reference's slot order
+// (cursor + 1 + i) % kernel after the new input is written; the cursor of a
+// sequence is position % kernel, since every layer steps once per token.
+// ---------------------------------------------------------------------------
+constexpr int kMaxConv = 8;
+__global__ __launch_bounds__(256) void k_q35_conv(Q35Lanes L, const float *__restrict__ mix,
+                                                  int ldm, const float *__restrict__ w, int C,
+                                                  int K, float *hist, size_t hist_seq,
+                                                  float *__restrict__ out, int ldo,
+                                                  uint32_t *row_err) {
+  const int ln = blockIdx.x, ch = blockIdx.y * 256 + threadIdx.x;
+  if (ch >= C) return;
+  const uint32_t first = L.first[ln], n = L.n[ln], start = L.start[ln];
+  float *h = hist + (size_t)L.seq[ln] * hist_seq + (size_t)ch * K;
+  const int c0 = (int)(start % (uint32_t)K);
+  float tap[kMaxConv], wv[kMaxConv];
+#pragma unroll
+  for (int i = 0; i < kMaxConv; i++) {
+    tap[i] = i < K ? h[(c0 + i) % K] : 0.0f;
+    wv[i] = i < K ? w[(size_t)ch * K + i] : 0.0f;
+  }
+  for (uint32_t t = 0; t < n; t++) {
+    const uint32_t row = first + t;
+    const float in = mix[(size_t)row * ldm + ch];
+#pragma unroll
+    for (int i = 0; i < kMaxConv - 1; i++)
+      if (i < K - 1) tap[i] = tap[i + 1];
+#pragma unroll
+    for (int i = 0; i < kMaxConv; i++)
+      if (i == K - 1) tap[i] = in;
+    double sum = -0.0;
+#pragma unroll
+    for (int i = 0; i < kMaxConv; i++)
+      if (i < K) sum += (double)(tap[i] * wv[i]);
+    const float y = silu_f32((float)sum);
+    out[(size_t)row * ldo + ch] = y;
+    if (!finitef(in) || !finitef(y)) atomicOr(&row_err[row], kErrRequest);
+  }
+  const int c1 = (int)((start + n) % (uint32_t)K);
+#pragma unroll
+  for (int i = 0; i < kMaxConv; i++)
+    if (i < K) h[(c1 + i) % K] = tap[i];
+}
+
+// ---------------------------------------------------------------------------
+// Gated delta rule (kernels.rs:122-214) in three passes.
+// Gates, per (row, value head): the q/k norms (ordered f64 sums of f32
+// squares), q_scale = (1/sqrt(qn + 1e-6))/sqrt(key_dim), k_scale =
+// 1/sqrt(kn + 1e-6), decay = exp(log_decay) with log_decay = -exp(A_log) *
+// softplus(a + dt_bias), beta = sigmoid(b) (execution.rs:376-388).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_q35_gates(const float *__restrict__ conv, int ldc,
+                                                   int keys, const float *__restrict__ mix,
+                                                   int ldm, int a_off, int b_off,
+                                                   const float *__restrict__ a_log,
+                                                   const float *__restrict__ dt, int KH, int VH,
+                                                   int KD, float4 *__restrict__ gates,
+                                                   uint32_t *row_err) {
+  __shared__ float sq[2][512];
+  __shared__ float norms[2];
+  const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int src = (h / (VH / KH)) * KD;
+  const float *cr = conv + (size_t)row * ldc;
+  for (int i = tid; i < KD; i += blockDim.x) {
+    const float q = cr[src + i], k = cr[keys + src + i];
+    sq[0][i] = q * q;
+    sq[1][i] = k * k;
+  }
+  __syncthreads();
+  if (tid % kWave == 0 && tid / kWave < 2) {  // one lane of each of two waves
+    const int which = tid / kWave;
+    double a = -0.0;
+    for (int i = 0; i < KD; i++) a += (double)sq[which][i];
+    norms[which] = (float)a;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const float qn = norms[0], kn = norms[1];
+    const float *mr = mix + (size_t)row * ldm;
+    const float ld = -exp_f32(a_log[h]) * softplus_f32(mr[a_off + h] + dt[h]);
+    const float beta = sigmoid_f32(mr[b_off + h]);
+    gates[(size_t)row * VH + h] = make_float4((1.0f / sqrtf(qn + 1e-6f)) / sqrtf((float)KD),
+                                              1.0f / sqrtf(kn + 1e-6f), exp_f32(ld), beta);
+    if (!finitef(qn) || !finitef(kn) || !finitef(ld) || !finitef(beta) || ld > 0.0f ||
+        !(beta >= 0.0f && beta <= 1.0f))
+      atomicOr(&row_err[row], kErrRequest);
+  }
+}
+
+// The recurrence: one workgroup per (lane, value head); thread j keeps state
+// column j (kKD cells) in registers across the lane's tokens.  Per token the
+// cells decay, the prediction chain sum_i f64(cell * k_i*k_scale) runs in key
+// order from +0.0, corr = (v_j - f32(pred)) * beta, then the cells take
+// k_i*k_scale*corr and the read chain sum_i f64(cell * q_i*q_scale) gives
+// the head's raw output.
+template <int kKD>
+__global__ __launch_bounds__(256) void k_q35_delta(Q35Lanes L, const float *__restrict__ conv,
+                                                   int ldc, int keys,
+                                                   const float4 *__restrict__ gates, int KH,
+                                                   int VH, int VD, float *state, size_t state_seq,
+                                                   float *__restrict__ o_out, int ldo,
+                                                   uint32_t *row_err) {
+  __shared__ float s_qq[kKD], s_kk[kKD];
+  const int ln = blockIdx.x, h = blockIdx.y, j = threadIdx.x;
+  const uint32_t first = L.first[ln], n = L.n[ln];
+  const int src = (h / (VH / KH)) * kKD;
+  float *S = state + (size_t)L.seq[ln] * state_seq + (size_t)h * kKD * VD;
+  const bool active = j < VD;
+  // the column moves through a buffer resource: lane offset j*4 in one VGPR,
+  // key offset i*VD*4 as a scalar, so no per-key address stays live
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(S, (short)0, (int)(kKD * VD * 4), 0x00020000);
+  const int voff = active ? j * 4 : 0;
+  float col[kKD];
+#pragma unroll
+  for (int i = 0; i < kKD; i++)
+    col[i] = active ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff, i * VD * 4, 0))
+                    : 0.0f;
+  for (uint32_t t = 0; t < n; t++) {
+    const uint32_t row = first + t;
+    const float *cr = conv + (size_t)row * ldc;
+    const float4 gt = gates[(size_t)row * VH + h];
+    __syncthreads();
+    for (int i = j; i < kKD; i += blockDim.x) {
+      s_qq[i] = cr[src + i] * gt.x;
+      s_kk[i] = cr[keys + src + i] * gt.y;
+    }
+    __syncthreads();
+    if (!active) continue;
+    const float decay = gt.z, beta = gt.w, v = cr[2 * keys + h * VD + j];
+    double pred = 0.0;
+#pragma unroll
+    for (int i0 = 0; i0 < kKD; i0 += 4) {
+      asm volatile("" ::: "memory");
+      float p[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        col[i0 + e] *= decay;
+        p[e] = col[i0 + e] * s_kk[i0 + e];
+      }
+      pin_vgprs(p);
+      double wd[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) wd[e] = (double)p[e];
+      pin_vgprs(wd);
+#pragma unroll
+      for (int e = 0; e < 4; e++) pred += wd[e];
+    }
+    const float corr = (v - (float)pred) * beta;
+    double rd = 0.0;
+#pragma unroll
+    for (int i0 = 0; i0 < kKD; i0 += 4) {
+      asm volatile("" ::: "memory");
+      float p[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        col[i0 + e] += s_kk[i0 + e] * corr;
+        p[e] = col[i0 + e] * s_qq[i0 + e];
+      }
+      pin_vgprs(p);
+      double wd[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) wd[e] = (double)p[e];
+      pin_vgprs(wd);
+#pragma unroll
+      for (int e = 0; e < 4; e++) rd += wd[e];
+    }
+    const float o = (float)rd;
+    bool bad = !finitef(o) || !finitef(v);
+#pragma unroll
+    for (int i = 0; i < kKD; i++) bad |= !finitef(col[i]);
+    o_out[(size_t)row * ldo + h * VD + j] = o;
+    if (bad) atomicOr(&row_err[row], kErrRequest);
+  }
+  if (active) {
+#pragma unroll
+    for (int i = 0; i < kKD; i++)
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, col[i]), rs, voff,
+                                            i * VD * 4, 0);
+  }
+}
+
+// Per value head: the output norm (zero_centered false) times SiLU(z)
+// (execution.rs:397-411).
+__global__ __launch_bounds__(256) void k_q35_headnorm(const float *__restrict__ o_in, int ldo,
+                                                      const float *__restrict__ mix, int ldm,
+                                                      int z_off, const float *__restrict__ w,
+                                                      int VD, float eps, float *__restrict__ tgt,
+                                                      int ldt, uint32_t *row_err) {
+  __shared__ float sq[256];
+  __shared__ float s_scale;
+  __shared__ int s_bad;
+  const int row = blockIdx.x, h = blockIdx.y, j = threadIdx.x;
+  const float o = j < VD ? o_in[(size_t)row * ldo + h * VD + j] : 0.0f;
+  if (j < VD) sq[j] = o * o;
+  __syncthreads();
+  if (j == 0) {
+    double sum = -0.0;
+    for (int i = 0; i < VD; i++) sum += (double)sq[i];
+    const double mean = sum / (double)VD;
+    s_bad = !(__builtin_isfinite(mean) && finitef((float)mean));
+    s_scale = 1.0f / sqrtf((float)mean + eps);
+  }
+  __syncthreads();
+  bool bad = false;
+  if (j < VD) {
+    const float z = mix[(size_t)row * ldm + z_off + h * VD + j];
+    const float y = ((o * s_scale) * (w[j] + 0.0f)) * silu_f32(z);
+    tgt[(size_t)row * ldt + h * VD + j] = y;
+    bad = !finitef(y);
+  }
+  if (bad || (j == 0 && s_bad)) atomicOr(&row_err[row], kErrRequest);
+}
+
+// ---------------------------------------------------------------------------
+// Full-attention q/k preparation (execution.rs:436-497): per head the
+// zero-centred norm, then the partial rotary embedding (kernels.rs:226-268)
+// from the host table (cos, sin) of angle pos * base^(-2i/rotary); q and its
+// gate to the q/z buffers, k and v appended to the sequence's cache rows.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(576) void k_q35_qk(Q35Rows Rw, const float *__restrict__ mix,
+                                                int ldm, int k_off, int v_off,
+                                                const float *__restrict__ q_norm,
+                                                const float *__restrict__ k_norm, int NH, int NKV,
+                                                int D, int rotary, float eps,
+                                                const float2 *__restrict__ rope, float *q,
+                                                float *z, int ldq, float *kc, float *vc,
+                                                size_t cache_seq, uint32_t *row_err) {
+  __shared__ float y[512], sq[512];
+  __shared__ float s_scale;
+  __shared__ int s_bad;
+  const int row = blockIdx.x, hh = blockIdx.y, d = threadIdx.x;
+  const uint32_t pos = Rw.pos[row], seq = Rw.seq[row];
+  const bool is_q = hh < NH;
+  const int kh = hh - NH, kvw = NKV * D;
+  const float *srcp = mix + (size_t)row * ldm + (is_q ? hh * 2 * D : k_off + kh * D);
+  const float xv = d < D ? srcp[d] : 0.0f;
+  if (d < D) sq[d] = xv * xv;
+  __syncthreads();
+  if (d == 0) {
+    double sum = -0.0;
+    for (int i = 0; i < D; i++) sum += (double)sq[i];
+    const double mean = sum / (double)D;
+    s_bad = !(__builtin_isfinite(mean) && finitef((float)mean));
+    s_scale = 1.0f / sqrtf((float)mean + eps);
+  }
+  __syncthreads();
+  bool bad = d < D && !finitef(xv);
+  if (d < D) {
+    y[d] = (xv * s_scale) * ((is_q ? q_norm : k_norm)[d] + 1.0f);
+    bad |= !finitef(y[d]);
+  }
+  __syncthreads();
+  float *dst = is_q ? q + (size_t)row * ldq + hh * D
+                    : kc + (size_t)seq * cache_seq + (size_t)pos * kvw + kh * D;
+  const int half = rotary / 2;
+  if (d < half) {
+    const float a = y[d], b = y[d + half];
+    const float2 cs = rope[(size_t)pos * half + d];
+    const float ra = a * cs.x - b * cs.y, rb = b * cs.x + a * cs.y;
+    dst[d] = ra;
+    dst[d + half] = rb;
+    bad |= !finitef(ra) || !finitef(rb);
+  } else if (d >= rotary && d < D) {
+    dst[d] = y[d];
+  }
+  if (d < D) {
+    if (is_q)
+      z[(size_t)row * ldq + hh * D + d] = mix[(size_t)row * ldm + hh * 2 * D + D + d];
+    else
+      vc[(size_t)seq * cache_seq + (size_t)pos * kvw + kh * D + d] =
+          mix[(size_t)row * ldm + v_off + kh * D + d];
+  }
+  if (bad || (d == 0 && s_bad)) atomicOr(&row_err[row], kErrRequest);
+}
+
+// ---------------------------------------------------------------------------
+// Online-softmax attention (cpu.rs:80-124) in the reference's exact order.
+// The running maximum m_t is a prefix maximum (exact in any order), so the
+// scores, the maxima and both exponentials old_t = exp(m_{t-1} - m_t),
+// new_t = exp(s_t - m_t) are formed in parallel; the two f32 recurrences
+// den = den*old + new and o_d = o_d*old + new*v_d then run in key order,
+// one thread per output element (and one for the denominator).  The output
+// is o/den times sigmoid(gate) (execution.rs:506-508).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(576) void k_q35_attn(Q35Rows Rw, const float *__restrict__ q,
+                                                  const float *__restrict__ z, int ldq,
+                                                  const float *__restrict__ kc,
+                                                  const float *__restrict__ vc, size_t cache_seq,
+                                                  int NH, int NKV, int D, int maxc,
+                                                  float *__restrict__ out, int ldo) {
+  extern __shared__ float sm[];
+  float *sq = sm, *sc = sq + 512, *mx = sc + maxc, *old = mx + maxc, *seg = old + maxc;
+  __shared__ float s_den;
+  const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
+  const int dthreads = nt - kWave;  // the last wave runs the denominator
+  const uint32_t pos = Rw.pos[row], seq = Rw.seq[row];
+  const int kv = (int)pos + 1, kvh = h / (NH / NKV), kvw = NKV * D;
+  const float *K = kc + (size_t)seq * cache_seq + kvh * D;
+  const float *V = vc + (size_t)seq * cache_seq + kvh * D;
+  for (int i = tid; i < D; i += nt) sq[i] = q[(size_t)row * ldq + h * D + i];
+  __syncthreads();
+  const float root = sqrtf((float)D);
+  for (int t = tid; t < kv; t += nt) {
+    const float *kr = K + (size_t)t * kvw;
+    double a = -0.0;
+    for (int i = 0; i < D; i++) a += (double)(sq[i] * kr[i]);
+    sc[t] = (float)a / root;
+  }
+  __syncthreads();
+  // prefix maxima: contiguous segments, then an exclusive scan of segment maxima
+  const int per = (kv + nt - 1) / nt, lo = min(kv, tid * per), hi = min(kv, lo + per);
+  float m = -__builtin_inff();
+  for (int t = lo; t < hi; t++) {
+    m = fmaxf(m, sc[t]);
+    mx[t] = m;
+  }
+  seg[tid] = m;
+  __syncthreads();
+  if (tid == 0) {
+    float run = -__builtin_inff();
+    for (int i = 0; i < nt; i++) {
+      const float s = seg[i];
+      seg[i] = run;
+      run = fmaxf(run, s);
+    }
+  }
+  __syncthreads();
+  const float base = seg[tid];
+  for (int t = lo; t < hi; t++) mx[t] = fmaxf(base, mx[t]);
+  __syncthreads();
+  for (int t = lo; t < hi; t++) {
+    const float prev = t ? mx[t - 1] : -__builtin_inff();
+    old[t] = exp_f32(prev - mx[t]);
+  }
+  __syncthreads();
+  for (int t = lo; t < hi; t++) sc[t] = exp_f32(sc[t] - mx[t]);  // new_t
+  __syncthreads();
+  if (tid == dthreads) {
+    float den = 0.0f;
+    for (int t = 0; t < kv; t++) den = den * old[t] + sc[t];
+    s_den = den;
+  }
+  float o = 0.0f;
+  if (tid < D) {
+    for (int t = 0; t < kv; t++) o = o * old[t] + sc[t] * V[(size_t)t * kvw + tid];
+  }
+  __syncthreads();
+  if (tid < D) {
+    const float gate = z[(size_t)row * ldq + h * D + tid];
+    out[(size_t)row * ldo + h * D + tid] = (o / s_den) * sigmoid_f32(gate);
+  }
+}
+
+}  // namespace
+
+// ---- launchers ---------------------------------------------------------------
+
+void q35_embed(hipStream_t s, int rows, const uint16_t *embed, const uint32_t *tokens, int H,
+               float *x) {
+  hipLaunchKernelGGL(k_q35_embed, dim3(rows), dim3(256), 0, s, embed, tokens, H, x);
+}
+
+void q35_norm(hipStream_t s, int rows, const float *x, int ldx, const uint32_t *src,
+              const float *w, int n, float eps, int zc, float *out, int ldo, uint32_t *row_err,
+              const uint32_t *err_row) {
+  hipLaunchKernelGGL(k_q35_norm, dim3(rows), dim3(256), 0, s, x, ldx, src, w, n, eps, zc, out,
+                     ldo, row_err, err_row);
+}
+
+int q35_matvec_blocks(int rows_w) { return (rows_w + 63) / 64; }
+
+void q35_matvec(hipStream_t s, int epi, const uint16_t *w, int rows_w, int valid_rows, int K,
+                const float *x, int ldx, int R, float *out, int ldo, unsigned long long *part,
+                uint32_t *row_err, const uint32_t *err_row) {
+  const dim3 grid(q35_matvec_blocks(rows_w), (R + kMvRows - 1) / kMvRows);
+  if (epi == kQ35Store)
+    hipLaunchKernelGGL(k_q35_mv<kQ35Store>, grid, dim3(256), 0, s, w, rows_w, valid_rows, K, x,
+                       ldx, R, out, ldo, part, row_err, err_row);
+  else if (epi == kQ35Residual)
+    hipLaunchKernelGGL(k_q35_mv<kQ35Residual>, grid, dim3(256), 0, s, w, rows_w, valid_rows, K,
+                       x, ldx, R, out, ldo, part, row_err, err_row);
+  else
+    hipLaunchKernelGGL(k_q35_mv<kQ35Argmax>, grid, dim3(256), 0, s, w, rows_w, valid_rows, K, x,
+                       ldx, R, out, ldo, part, row_err, err_row);
+}
+
+void q35_swiglu(hipStream_t s, int rows, const float *gu, int ldgu, int F, int up_off, float *h,
+                int ldh) {
+  hipLaunchKernelGGL(k_q35_swiglu, dim3((F + 255) / 256, rows), dim3(256), 0, s, gu, ldgu, F,
+                     up_off, h, ldh);
+}
+
+void q35_conv(hipStream_t s, int lanes, Q35Lanes L, const float *mix, int ldm, const float *w,
+              int C, int K, float *hist, size_t hist_seq, float *out, int ldo, uint32_t *row_err) {
+  hipLaunchKernelGGL(k_q35_conv, dim3(lanes, (C + 255) / 256), dim3(256), 0, s, L, mix, ldm, w, C,
+                     K, hist, hist_seq, out, ldo, row_err);
+}
+
+bool q35_delta_supported(int key_dim, int value_dim) {
+  return (key_dim == 16 || key_dim == 32 || key_dim == 64 || key_dim == 128) && value_dim >= 1 &&
+         value_dim <= 256;
+}
+
+void q35_delta(hipStream_t s, int rows, int lanes, Q35Lanes L, const float *conv, int ldc, int keys,
+               const float *mix, int ldm, int z_off, int a_off, int b_off, const float *a_log,
+               const float *dt, const float *norm_w, int key_heads, int value_heads, int key_dim,
+               int value_dim, float eps, float *state, size_t state_seq, float4 *gates,
+               float *o_raw, float *tgt, int ldt, uint32_t *row_err) {
+  hipLaunchKernelGGL(k_q35_gates, dim3(rows, value_heads), dim3(128), 0, s, conv, ldc, keys, mix,
+                     ldm, a_off, b_off, a_log, dt, key_heads, value_heads, key_dim, gates, row_err);
+  const dim3 grid(lanes, value_heads), block(((value_dim + kWave - 1) / kWave) * kWave);
+#define L_(KD)                                                                                 \
+  case KD:                                                                                     \
+    hipLaunchKernelGGL(k_q35_delta<KD>, grid, block, 0, s, L, conv, ldc, keys, gates, key_heads, \
+                       value_heads, value_dim, state, state_seq, o_raw, ldt, row_err);         \
+    break;
+  switch (key_dim) {
+    L_(16) L_(32) L_(64) L_(128)
+    default: break;
+  }
+#undef L_
+  hipLaunchKernelGGL(k_q35_headnorm, dim3(rows, value_heads), block, 0, s, o_raw, ldt, mix, ldm,
+                     z_off, norm_w, value_dim, eps, tgt, ldt, row_err);
+}
+
+void q35_qk(hipStream_t s, int rows, Q35Rows Rw, const float *mix, int ldm, int k_off, int v_off,
+            const float *q_norm, const float *k_norm, int heads, int kv_heads, int D, int rotary,
+            float eps, const float2 *rope, float *q, float *z, int ldq, float *kc, float *vc,
+            size_t cache_seq, uint32_t *row_err) {
+  const int threads = ((D + kWave - 1) / kWave) * kWave;
+  hipLaunchKernelGGL(k_q35_qk, dim3(rows, heads + kv_heads), dim3(threads), 0, s, Rw, mix, ldm,
+                     k_off, v_off, q_norm, k_norm, heads, kv_heads, D, rotary, eps, rope, q, z,
+                     ldq, kc, vc, cache_seq, row_err);
+}
+
+void q35_attention(hipStream_t s, int rows, Q35Rows Rw, const float *q, const float *z, int ldq,
+                   const float *kc, const float *vc, size_t cache_seq, int heads, int kv_heads,
+                   int D, int max_context, float *out, int ldo) {
+  const int threads = ((D + kWave - 1) / kWave) * kWave + kWave;
+  const size_t lds = (size_t)(512 + 3 * max_context + threads) * sizeof(float);
+  hipLaunchKernelGGL(k_q35_attn, dim3(rows, heads), dim3(threads), lds, s, Rw, q, z, ldq, kc, vc,
+                     cache_seq, heads, kv_heads, D, max_context, out, ldo);
+}
+
+}  // namespace cohx

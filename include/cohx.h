@@ -40,8 +40,8 @@ enum {
   COHX_DEVICE = 7           /* HIP runtime failure */
 };
 
-/* GGML dtypes accepted for matrices (gguf.rs:104-128). */
-enum { COHX_F32 = 0, COHX_F16 = 1, COHX_Q4_0 = 2, COHX_Q8_0 = 8 };
+/* GGML dtypes accepted for matrices (gguf.rs:104-128; BF16 for Qwen3.5). */
+enum { COHX_F32 = 0, COHX_F16 = 1, COHX_Q4_0 = 2, COHX_Q8_0 = 8, COHX_BF16 = 30 };
 
 typedef struct cohx_ctx cohx_ctx;
 
@@ -164,6 +164,39 @@ typedef struct {
 } cohx_kernel_stat;
 int cohx_profile(cohx_ctx *ctx, int enable);
 uint32_t cohx_profile_read(const cohx_ctx *ctx, cohx_kernel_stat *out, uint32_t cap);
+
+/* ---- Qwen3.5 hybrid text model ------------------------------------------- */
+
+/* qwen35/config.rs:6-25 Config plus capacities.  Linear-attention layers carry
+ * a causal-conv ring and a gated delta-rule memory per sequence; full-attention
+ * layers carry K/V rows. */
+typedef struct {
+  uint32_t layers, hidden, intermediate, vocabulary;
+  uint32_t heads, kv_heads, head_dim; /* full-attention layers */
+  uint32_t linear_key_heads, linear_value_heads, linear_key_dim, linear_value_dim;
+  uint32_t conv_kernel, rotary_dim, context, tied;
+  float epsilon, rope_base;
+  uint8_t full_attention[128]; /* layer_types: 1 full_attention, 0 linear_attention */
+  uint32_t max_lanes, max_rows, max_seqs, max_context;
+  uint32_t n_eog, eog[4];
+} cohx_qwen35_desc;
+
+/* qwen35::Model::load counterpart (qwen35/mod.rs:103-193, execution.rs:168-219):
+ * HBM for the weights, the per-sequence recurrent state and K/V rows
+ * (max_context at most 4096 rows per sequence).  The context then takes:
+ *   cohx_upload_tensor: the safetensors tensor set of config.rs:193-309 by name;
+ *     matrices BF16 (COHX_BF16), vectors F32 or BF16; conv1d.weight [C][1][K]
+ *     as ne0 = K, ne1 = C;
+ *   cohx_finalize; cohx_seq_alloc / free / length;
+ *   cohx_seq_fork: a full snapshot copy at the source's length (recurrent state
+ *     cannot be shared; execution.rs:117-133);
+ *   cohx_seq_read_kv: values 0/1 = K/V rows [0, length) of a full-attention
+ *     layer, 2 = conv ring [channels][kernel], 3 = delta memory
+ *     [value_heads][key_dim][value_dim] of a linear-attention layer;
+ *   cohx_step: Graph::forward_batch (execution.rs:257-608) over a ragged batch,
+ *     exact; a lane may carry several tokens, processed in order.
+ * Other entry points return COHX_UNSUPPORTED on such a context. */
+int cohx_create_qwen35(const cohx_qwen35_desc *desc, int device, cohx_ctx **out);
 
 /* ---- host mirror of the engine's generation API ------------------------- */
 

@@ -14,13 +14,14 @@ HEADER = os.path.join(ROOT, "include", "cohx.h")
 def declared():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(cohx_[a-z_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(cohx_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_header_declares_the_boundary():
     names = declared()
     for must in ("cohx_create", "cohx_upload_tensor", "cohx_seq_alloc", "cohx_seq_free",
-                 "cohx_step", "cohx_destroy", "cohx_step_batch", "cohx_gen_sample"):
+                 "cohx_step", "cohx_destroy", "cohx_step_batch", "cohx_gen_sample",
+                 "cohx_create_qwen35"):
         assert must in names
 
 

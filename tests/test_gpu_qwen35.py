@@ -1,0 +1,149 @@
+"""Qwen3.5 hybrid step on the GPU against the oracle (oracle/orc_qwen35.c),
+bit for bit: logits of every lane's last row, greedy ids, and the recurrent
+state (K/V rows, causal-conv ring, delta-rule memory) after each step.  A lane
+may carry a prompt chunk of several tokens; the oracle steps the same tokens
+one at a time (Graph::forward_batch, qwen35/execution.rs:257-608)."""
+import numpy as np
+import pytest
+
+import cohx
+import orc
+import synth35
+
+pytestmark = pytest.mark.gpu
+
+
+def tiny(**kw):
+    return synth35.config(layers=4, hidden=64, intermediate=96, vocabulary=300, heads=2,
+                          kv_heads=1, head_dim=32, key_heads=2, value_heads=4, key_dim=16,
+                          value_dim=8, rotary_dim=16, context=256, **kw)
+
+
+class Pair:
+    """A GPU context and an oracle model over the same tensors, with one oracle
+    session per GPU sequence."""
+
+    def __init__(self, cfg, t, threads=8, **kw):
+        self.cfg = cfg
+        self.gpu = cohx.Qwen35(cfg, t, **kw)
+        self.orc = orc.Qwen35Model(cfg, t, threads=threads)
+        self.sessions = {}
+
+    def alloc(self):
+        s = self.gpu.seq_alloc()
+        self.sessions[s] = self.orc.session(self.gpu.max_context)
+        return s
+
+    def step(self, lanes):
+        """lanes: [(seq, tokens)]; every lane asks for logits.  Checks each lane
+        against the oracle and returns the GPU argmax per lane."""
+        res = self.gpu.step([dict(seq=s, tokens=toks, logits=True) for s, toks in lanes])
+        width = max(len(toks) for _, toks in lanes)
+        for j in range(width):
+            live = [(s, toks[j]) for s, toks in lanes if j < len(toks)]
+            errs = self.orc.forward_batch([self.sessions[s] for s, _ in live],
+                                          [tok for _, tok in live])
+            assert not any(errs), errs
+        out = []
+        for (s, toks), r in zip(lanes, res):
+            assert r["status"] == 0, (s, r["status"])
+            want = self.sessions[s].logits()
+            got = r["logits"]
+            if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
+                bad = np.nonzero(got.view(np.uint32) != want.view(np.uint32))[0]
+                raise AssertionError(f"seq {s}: {bad.size} logits differ, first {bad[:4]}, "
+                                     f"max-abs {np.abs(got - want).max():.3g}")
+            assert r["argmax"] == int(np.argmax(want)), (s, r["argmax"], int(np.argmax(want)))
+            assert self.gpu.seq_length(s) == self.sessions[s].position()
+            out.append(r["argmax"])
+        return out
+
+    def check_state(self, seq):
+        ses = self.sessions[seq]
+        for layer, full in enumerate(self.cfg["full"]):
+            for which in ((0, 1) if full else (2, 3)):
+                got = self.gpu.read_state(seq, layer, which)
+                want = ses.state(layer, which).reshape(-1)
+                assert got.size == want.size, (layer, which)
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (seq, layer, which)
+
+
+def test_tiny_prefill_decode_and_state_bit_exact():
+    print("case: tiny Qwen3.5, 3 lanes prefill (7, 3, 1 tokens) then 5 greedy steps", flush=True)
+    cfg, t = synth35.in_memory(tiny(), seed=3)
+    p = Pair(cfg, t, max_lanes=4, max_rows=32, max_context=64)
+    seqs = [p.alloc() for _ in range(3)]
+    prompts = [[5, 17, 3, 99, 250, 7, 7], [1, 2, 3], [299]]
+    nxt = p.step(list(zip(seqs, prompts)))
+    for s in seqs:
+        p.check_state(s)
+    for _ in range(5):
+        nxt = p.step([(s, [tok]) for s, tok in zip(seqs, nxt)])
+    for s in seqs:
+        p.check_state(s)
+
+
+def test_tiny_ragged_chunks_across_steps():
+    print("case: tiny Qwen3.5, one prompt in chunks 8/1/11 beside a decoding lane", flush=True)
+    cfg, t = synth35.in_memory(tiny(), seed=4)
+    p = Pair(cfg, t, max_lanes=4, max_rows=24, max_context=64)
+    a, b = p.alloc(), p.alloc()
+    rng = np.random.default_rng(9)
+    prompt = [int(v) for v in rng.integers(0, cfg["vocabulary"], 20)]
+    (tok_b,) = p.step([(b, [4, 8, 15])])
+    for chunk in (prompt[:8], prompt[8:9], prompt[9:]):
+        _, tok_b = p.step([(a, chunk), (b, [tok_b])])
+    p.check_state(a)
+    p.check_state(b)
+
+
+def test_tiny_fork_snapshot_then_diverge():
+    print("case: tiny Qwen3.5, fork at the source length, both branches step", flush=True)
+    cfg, t = synth35.in_memory(tiny(), seed=5)
+    p = Pair(cfg, t, max_lanes=4, max_rows=16, max_context=64)
+    a = p.alloc()
+    prompt = [11, 22, 33, 44, 55, 66]
+    p.step([(a, prompt)])
+    f = p.gpu.seq_fork(a, len(prompt))
+    # the oracle branch replays the prompt in a fresh session
+    p.sessions[f] = p.orc.session(p.gpu.max_context)
+    for tok in prompt:
+        assert p.orc.forward_batch([p.sessions[f]], [tok])[0] == 0
+    p.check_state(f)
+    p.step([(a, [1]), (f, [2])])
+    p.step([(a, [3, 4]), (f, [5])])
+    p.check_state(a)
+    p.check_state(f)
+    with pytest.raises(cohx.CohxError):
+        p.gpu.seq_fork(a, 2)           # recurrent state cannot be forked mid-sequence
+    with pytest.raises(cohx.CohxError):
+        p.gpu.seq_truncate(a, 3)       # nor rewound
+
+
+def test_tiny_request_errors():
+    print("case: tiny Qwen3.5, invalid lanes rejected without touching the others", flush=True)
+    cfg, t = synth35.in_memory(tiny(), seed=6)
+    p = Pair(cfg, t, max_lanes=4, max_rows=8, max_context=16)
+    a, b = p.alloc(), p.alloc()
+    res = p.gpu.step([dict(seq=a, tokens=[cfg["vocabulary"]], logits=True),
+                      dict(seq=b, tokens=[1, 2], logits=True)])
+    assert res[0]["status"] == cohx.INVALID_REQUEST
+    assert res[1]["status"] == 0
+    assert p.gpu.seq_length(a) == 0 and p.gpu.seq_length(b) == 2
+    res = p.gpu.step([dict(seq=b, tokens=list(range(15)), logits=True)])  # past capacity
+    assert res[0]["status"] == cohx.INVALID_REQUEST
+    res = p.gpu.step([dict(seq=a, tokens=list(range(9)), logits=True)])   # past max_rows
+    assert res[0]["status"] == cohx.RESOURCE
+
+
+def test_full_shape_prefill_and_decode_bit_exact():
+    print("case: Qwen3.5-0.8B shape (random weights), 2 lanes prefill 5/3 then 2 steps",
+          flush=True)
+    cfg, t = synth35.in_memory(synth35.config(), seed=7)
+    p = Pair(cfg, t, threads=16, max_lanes=4, max_rows=16, max_context=64)
+    a, b = p.alloc(), p.alloc()
+    nxt = p.step([(a, [100, 2000, 30000, 248000, 5]), (b, [7, 77, 777])])
+    for _ in range(2):
+        nxt = p.step([(a, [nxt[0]]), (b, [nxt[1]])])
+    p.check_state(a)
+    p.check_state(b)
