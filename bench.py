@@ -45,7 +45,7 @@ CATEGORY_KERNEL = {"attn_scores": "k_attn_scores<64, 7>", "attn_softmax_stats": 
                    "matvec_head_argmax": "k_mv_q8c<3, 1, 2, 4, 8>"}
 PMC_CMD = ("COHX_GRAPHS=0 rocprofv3 --pmc {counter} --kernel-include-regex \"k_attn|k_mv\" --output-format csv "
            "-d <dir> -o <name> -- python3 bench.py --steps 2 --warmup 1 --secondary-lanes 0 "
-           "--no-cpu-baseline --no-c3 --no-c4")
+           "--no-cpu-baseline --no-c3 --no-c4 --no-c5")
 COPY_CMD = ("rocprofv3 --pmc {counter} --output-format csv -d <dir> -o <name> -- "
             "python3 bench.py --copy-probe")
 TRACE_CMD = ("COHX_GRAPHS=0 rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o <name> -- "
@@ -432,6 +432,109 @@ def copy_probe():
           flush=True)
 
 
+C5_SEQS, C5_PROMPT, C5_GEN, C5_CHUNK = 16, (64, 1024), 64, 256
+
+
+def c5_generate(model, prompts, chunk, head_every_row=False):
+    """Continuous batching of the hybrid graph (qwen35/generation.rs:335-406):
+    every step gives each unfinished sequence its next `chunk` prompt tokens
+    (prompt rows that do not end the prompt skip the head, generation.rs:368)
+    or its last greedy token; the step on a prompt's last row yields the first
+    greedy token, and a sequence stops after C5_GEN tokens.  chunk=1 is the
+    engine's own schedule (one token per state per step_batch call)."""
+    seqs = [model.seq_alloc() for _ in prompts]
+    cursor = [0] * len(prompts)
+    out = [[] for _ in prompts]
+    steps = rows = 0
+    while any(len(o) < C5_GEN for o in out):
+        lanes, idx = [], []
+        for i, p in enumerate(prompts):
+            if len(out[i]) >= C5_GEN:
+                continue
+            if cursor[i] < len(p):
+                toks = p[cursor[i]:cursor[i] + chunk]
+                ends = cursor[i] + len(toks) == len(p)
+                lanes.append(dict(seq=seqs[i], tokens=toks,
+                                  skip_head=not ends and not head_every_row))
+            else:
+                toks = [out[i][-1]]
+                lanes.append(dict(seq=seqs[i], tokens=toks))
+            idx.append((i, len(toks)))
+        res = model.step(lanes)
+        for (i, n), r in zip(idx, res):
+            if r["status"]:
+                raise RuntimeError(f"c5 lane {i} failed with status {r['status']}")
+            if cursor[i] < len(prompts[i]):
+                cursor[i] += n
+                if cursor[i] == len(prompts[i]):
+                    out[i].append(int(r["argmax"]))
+            else:
+                out[i].append(int(r["argmax"]))
+        steps += 1
+        rows += sum(n for _, n in idx)
+    for s in seqs:
+        model.seq_free(s)
+    return out, steps, rows
+
+
+def run_c5(seed, cpu_steps, threads, with_cpu=True):
+    """the Qwen3.5-0.8B hybrid shape (bf16 N(0,0.02)
+    weights), 16 sequences with prompts U[64,1024] of random ids, 64 greedy
+    tokens each, exact arithmetic (bit-exact against the oracle).  Timed twice
+    from fresh sequences: with prompts in chunks of C5_CHUNK rows per lane per
+    step, and in the engine's one-token-per-step schedule; both must generate
+    the same tokens.  The CPU baseline steps the oracle over the first
+    prompt tokens of all 16 sequences (one token per sequence per step)."""
+    import synth35
+    t0 = time.perf_counter()
+    cfg, tensors = synth35.in_memory(synth35.config(), seed=seed + 5)
+    log(f"[bench] c5: synthetic Qwen3.5-0.8B weights in {time.perf_counter() - t0:.1f}s")
+    rng = np.random.default_rng(seed + 5)
+    plen = [int(v) for v in rng.integers(C5_PROMPT[0], C5_PROMPT[1] + 1, C5_SEQS)]
+    prompts = [[int(v) for v in rng.integers(0, cfg["vocabulary"], n)] for n in plen]
+    ctx = C5_PROMPT[1] + C5_GEN + 8
+    model = cohx.Qwen35(cfg, tensors, max_lanes=C5_SEQS, max_rows=C5_SEQS * C5_CHUNK,
+                        max_seqs=C5_SEQS, max_context=ctx)
+    c5_generate(model, [p[:C5_CHUNK + 3] for p in prompts[:4]], C5_CHUNK)  # warm-up
+    res = {}
+    for name, chunk in (("chunked", C5_CHUNK), ("engine_schedule", 1)):
+        t0 = time.perf_counter()
+        toks, steps, rows = c5_generate(model, prompts, chunk)
+        el = time.perf_counter() - t0
+        res[name] = dict(tokens=toks, steps=steps, rows=rows, elapsed=el)
+        log(f"[bench] c5 {name}: {C5_SEQS * C5_GEN / el:.0f} generated tok/s, {rows / el:.0f} rows/s, "
+            f"{steps} steps, {el:.2f}s")
+    ch, es = res["chunked"], res["engine_schedule"]
+    same = ch["tokens"] == es["tokens"]
+    line = {"workload": f"Qwen3.5-0.8B-shape hybrid (bf16 weights, f32 state), {C5_SEQS} sequences, "
+                        f"prompts U[{C5_PROMPT[0]},{C5_PROMPT[1]}], {C5_GEN} greedy tokens each; exact",
+            "value": C5_SEQS * C5_GEN / ch["elapsed"], "unit": "generated tok/s (whole job)",
+            "rows_per_s": ch["rows"] / ch["elapsed"], "elapsed_s": ch["elapsed"],
+            "steps": ch["steps"], "prompt_chunk": C5_CHUNK, "prompt_rows": sum(plen),
+            "matrix_bytes": model.matrix_bytes,
+            "engine_schedule": {"value": C5_SEQS * C5_GEN / es["elapsed"],
+                                "rows_per_s": es["rows"] / es["elapsed"], "steps": es["steps"],
+                                "ms_per_step": es["elapsed"] * 1e3 / es["steps"],
+                                "elapsed_s": es["elapsed"]},
+            "same_tokens_both_schedules": same, "seed": seed + 5}
+    del model
+    if with_cpu:
+        import orc
+        m = orc.Qwen35Model(cfg, tensors, threads=threads)
+        sess = [m.session(ctx) for _ in prompts]
+        t0 = time.perf_counter()
+        for j in range(cpu_steps):
+            errs = m.forward_batch(sess, [p[j] for p in prompts], logits=[0] * C5_SEQS)
+            assert not errs.any()
+        el = time.perf_counter() - t0
+        line["cpu_baseline"] = {
+            "value": C5_SEQS * cpu_steps / el, "unit": "rows/s", "cores": threads, "kind": "port",
+            "sample": f"oracle, the first {cpu_steps} prompt tokens of all {C5_SEQS} sequences, "
+                      f"one token per sequence per step, no head (prompt rows); {el:.1f}s",
+            "gpu_engine_schedule_rows_per_s": es["rows"] / es["elapsed"]}
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -444,6 +547,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-c4", action="store_true", help="skip the Q4_0 shared-prefix workload")
     ap.add_argument("--no-c3", action="store_true", help="skip the F16 packed-prefill workload")
+    ap.add_argument("--no-c5", action="store_true", help="skip the Qwen3.5 hybrid workload")
+    ap.add_argument("--c5-only", action="store_true",
+                    help="run only the Qwen3.5 hybrid workload and print its JSON")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 1 GiB device-to-device 4 times (counter calibration)")
     ap.add_argument("--summarize-counters", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
@@ -464,6 +570,11 @@ def main():
         print("bench.py measures one MI355X: this build has no multi-GPU path "
               "(the step shards by sequence with no collectives; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
+    threads = min(16, os.cpu_count() or 1)
+    if args.c5_only:
+        print(json.dumps(run_c5(args.seed, args.cpu_steps // 2, threads,
+                                with_cpu=not args.no_cpu_baseline)), flush=True)
+        return
     path = model_file(args.seed)
     meta, tensors = gguf.read(path)
     cfg = gguf.qwen2_config(meta)
@@ -512,8 +623,9 @@ def main():
         line["c4"] = run_c4(args.seed, 128, args.warmup)
     if not args.no_c3:
         line["c3"] = run_c3(args.seed, 8, 2)
+    if not args.no_c5:
+        line["c5"] = run_c5(args.seed, args.cpu_steps // 2, threads, with_cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
         n_cpu = min(16, args.lanes)
         log(f"[bench] cpu baseline: oracle, {n_cpu} lanes x {args.cpu_steps} steps, {threads} threads")
         first, tps, el = cpu_baseline(cfg, tensors, main_r["kv"], main_r["start_tokens"], args.seed,

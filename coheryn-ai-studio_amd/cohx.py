@@ -61,6 +61,8 @@ class LaneOut(ctypes.Structure):
 
 
 AT_END = 0xFFFFFFFF  # COHX_AT_END: the sequence's current length
+SKIP_HEAD = 2        # COHX_SKIP_HEAD: rows only advance the state (Qwen3.5 prompt chunks)
+NO_TOKEN = 0xFFFFFFFF  # COHX_NO_TOKEN: argmax of a lane that skipped the head
 
 # numpy views of the same layouts, for building a whole step without per-lane Python work
 LANE_DTYPE = np.dtype({"names": ["seq", "n_tokens", "tokens", "start_position", "want_logits"],
@@ -296,11 +298,12 @@ class Model:
             arr[i].n_tokens = toks.size
             arr[i].tokens = _u32p(toks)
             arr[i].start_position = ln.get("start", AT_END)
-            arr[i].want_logits = 1 if ln.get("logits") else 0
+            arr[i].want_logits = 1 if ln.get("logits") else (SKIP_HEAD if ln.get("skip_head") else 0)
         return Batch(len(lanes), arr), keep
 
     def step(self, lanes):
-        """lanes: [{"seq", "tokens", "start"?, "logits"?: bool}] -> list of dicts."""
+        """lanes: [{"seq", "tokens", "start"?, "logits"?: bool, "skip_head"?: bool}] -> list
+        of dicts (status, argmax, logits)."""
         batch, keep = self._batch(lanes)
         outs = (LaneOut * len(lanes))()
         bufs = []

@@ -1056,7 +1056,7 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
   hipStream_t s = ctx->stream;
   bool any_logits = false;
   for (int k = 0; k < NL; k++)
-    if (batch->lanes[p.included[k]].want_logits && out->lanes[p.included[k]].logits)
+    if (batch->lanes[p.included[k]].want_logits == 1u && out->lanes[p.included[k]].logits)
       any_logits = true;
   const int kv_grid = (int)((p.max_kv + 255) / 256 * 256);
   if (ctx->prof.on || !ctx->use_graphs || !p.single_token) {
@@ -1089,7 +1089,7 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
   for (int k = 0; k < NL; k++) {
     const cohx_lane &ln = batch->lanes[p.included[k]];
     float *dst = out->lanes[p.included[k]].logits;
-    if (ln.want_logits && dst)
+    if (ln.want_logits == 1u && dst)
       HIP_TRY(hipMemcpyAsync(dst, w.logits + (size_t)k * d.vocabulary, d.vocabulary * sizeof(float),
                              hipMemcpyDeviceToHost, s));
   }

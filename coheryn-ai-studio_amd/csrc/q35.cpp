@@ -487,8 +487,8 @@ int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
            *lane_start = lane_seq + NLmax, *lane_last = lane_start + NLmax;
   uint32_t *row_lane = lane_last + NLmax, *row_pos = row_lane + Rmax, *row_seq = row_pos + Rmax,
            *tokens = row_seq + Rmax;
-  std::vector<int> included;
-  uint32_t R = 0;
+  std::vector<int> included, head_of;  // head_of: row of the lane in the head pass, or -1
+  uint32_t R = 0, n_head = 0;
   for (uint32_t i = 0; i < batch->n_lanes; i++) {
     const cohx_lane &ln = batch->lanes[i];
     int32_t st = COHX_OK;
@@ -504,14 +504,19 @@ int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
       if (!st && R + ln.n_tokens > d.max_rows) st = COHX_RESOURCE;
     }
     out->lanes[i].status = st;
-    out->lanes[i].argmax = 0;
+    out->lanes[i].argmax = COHX_NO_TOKEN;
     if (st) continue;
     const uint32_t k = (uint32_t)included.size();
     lane_first[k] = R;
     lane_n[k] = ln.n_tokens;
     lane_seq[k] = ln.seq;
     lane_start[k] = start;
-    lane_last[k] = R + ln.n_tokens - 1;
+    if (ln.want_logits != COHX_SKIP_HEAD) {
+      lane_last[n_head] = R + ln.n_tokens - 1;
+      head_of.push_back((int)n_head++);
+    } else {
+      head_of.push_back(-1);
+    }
     for (uint32_t j = 0; j < ln.n_tokens; j++) {
       row_lane[R + j] = k;
       row_pos[R + j] = start + j;
@@ -571,21 +576,26 @@ int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
     q35_matvec(s, kQ35Residual, Ly.down, q->h_rows, H, q->F, q->hb, q->F, (int)R, q->x, H, nullptr,
                q->row_err, nullptr);
   }
-  // final norm and head over each lane's last row (execution.rs:586-594)
+  // final norm and head over the last row of each lane that needs them
+  // (execution.rs:586-594); d_last lists those rows in head order
   bool any_logits = false;
-  for (int k = 0; k < NL; k++) any_logits |= batch->lanes[included[k]].want_logits != 0;
-  q35_norm(s, NL, q->x, H, d_last, q->final_norm, H, eps, 1, q->fin, H, q->row_err, d_last);
-  q35_matvec(s, kQ35Argmax, q->head, q->head_rows, q->V, H, q->fin, H, NL,
-             any_logits ? q->logits : nullptr, q->V, q->part, q->row_err, d_last);
-  launch_argmax_reduce(s, NL, q->part, q35_matvec_blocks(q->head_rows), q->argmax);
+  for (int k = 0; k < NL; k++) any_logits |= batch->lanes[included[k]].want_logits == 1u;
+  const int NH = (int)n_head;
+  if (NH) {
+    q35_norm(s, NH, q->x, H, d_last, q->final_norm, H, eps, 1, q->fin, H, q->row_err, d_last);
+    q35_matvec(s, kQ35Argmax, q->head, q->head_rows, q->V, H, q->fin, H, NH,
+               any_logits ? q->logits : nullptr, q->V, q->part, q->row_err, d_last);
+    launch_argmax_reduce(s, NH, q->part, q35_matvec_blocks(q->head_rows), q->argmax);
+  }
   Q35_TRY(hipGetLastError());
-  Q35_TRY(hipMemcpyAsync(q->h_argmax, q->argmax, NL * 8, hipMemcpyDeviceToHost, s));
+  if (NH) Q35_TRY(hipMemcpyAsync(q->h_argmax, q->argmax, NH * 8, hipMemcpyDeviceToHost, s));
   Q35_TRY(hipMemcpyAsync(q->h_row_err, q->row_err, R * 4, hipMemcpyDeviceToHost, s));
   for (int k = 0; k < NL; k++) {
     const cohx_lane &ln = batch->lanes[included[k]];
     float *dst = out->lanes[included[k]].logits;
-    if (ln.want_logits && dst)
-      Q35_TRY(hipMemcpyAsync(dst, q->logits + (size_t)k * q->V, q->V * 4, hipMemcpyDeviceToHost, s));
+    if (ln.want_logits == 1u && dst && head_of[k] >= 0)
+      Q35_TRY(hipMemcpyAsync(dst, q->logits + (size_t)head_of[k] * q->V, q->V * 4,
+                             hipMemcpyDeviceToHost, s));
   }
   Q35_TRY(hipStreamSynchronize(s));
   uint32_t width = 0;
@@ -596,7 +606,8 @@ int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
     uint32_t bits = 0;
     for (uint32_t j = 0; j < ln.n_tokens; j++) bits |= q->h_row_err[lane_first[k] + j];
     cohx_lane_out &o = out->lanes[i];
-    o.argmax = 0xffffffffu - (uint32_t)(q->h_argmax[k] & 0xffffffffull);
+    o.argmax = head_of[k] < 0 ? COHX_NO_TOKEN
+                              : 0xffffffffu - (uint32_t)(q->h_argmax[head_of[k]] & 0xffffffffull);
     if (bits & kErrRequest)
       o.status = COHX_INVALID_REQUEST;
     else if (bits)

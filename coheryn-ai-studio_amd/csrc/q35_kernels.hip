@@ -164,6 +164,106 @@ __global__ __launch_bounds__(256) void k_q35_mv(const uint16_t *__restrict__ w, 
   }
 }
 
+// The same product for a few rows (decode steps): a workgroup owns one tile
+// of 16 outputs x 16 rows, a wave 4 rows, a lane one (output, row) chain, so
+// a 1024-output matrix still spreads over 256 waves.  The tile's weights and
+// the rows' activations pass through LDS in chunks of 512 inputs, double
+// buffered: each thread holds its share of the next chunk in registers while
+// the current chunk is summed, so a whole chunk of work covers the memory
+// latency.  The k order of each chain is the reference's.
+constexpr int kMvdChunk = 512;                 // inputs per chunk
+constexpr int kMvdXld = kMvdChunk + 4;         // padded LDS row (floats)
+constexpr int kMvdW4 = kMvdChunk / 8 * 16;     // uint4 words of a weight chunk
+constexpr int kMvdX4 = 16 * kMvdChunk / 4;     // float4 words of an activation chunk
+template <int kEpi>
+__global__ __launch_bounds__(256) void k_q35_mvd(const uint16_t *__restrict__ w, int valid_rows,
+                                                 int K, const float *__restrict__ x, int ldx,
+                                                 int R, float *out, int ldo,
+                                                 unsigned long long *__restrict__ part,
+                                                 uint32_t *row_err,
+                                                 const uint32_t *__restrict__ err_row) {
+  __shared__ __align__(16) uint4 ws[2][kMvdW4];
+  __shared__ __align__(16) float xs[2][16 * kMvdXld];
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int o16 = lane % 16, tile = blockIdx.x, r0 = blockIdx.y * 16;
+  const int br = wave * 4 + lane / 16, r = r0 + br;
+  const int o = tile * 16 + o16;
+  const bool live = r < R;
+  const int nk8 = K / 8;
+  const uint4 *wt = reinterpret_cast<const uint4 *>(w) + (size_t)tile * nk8 * 16;
+  uint4 wr[kMvdW4 / 256];
+  float4 xr[kMvdX4 / 256];
+  auto fetch = [&](int k0) {
+    const int n4 = min(kMvdChunk, K - k0) / 8 * 16;  // weight words in this chunk
+    const int kc = min(kMvdChunk, K - k0);
+#pragma unroll
+    for (int i = 0; i < kMvdW4 / 256; i++) {
+      const int idx = tid + 256 * i;
+      wr[i] = idx < n4 ? wt[(size_t)k0 / 8 * 16 + idx] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < kMvdX4 / 256; i++) {
+      const int idx = tid + 256 * i, row = idx / (kMvdChunk / 4), c = (idx % (kMvdChunk / 4)) * 4;
+      xr[i] = (r0 + row < R && c < kc)
+                  ? *reinterpret_cast<const float4 *>(x + (size_t)(r0 + row) * ldx + k0 + c)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < kMvdW4 / 256; i++) ws[buf][tid + 256 * i] = wr[i];
+#pragma unroll
+    for (int i = 0; i < kMvdX4 / 256; i++) {
+      const int idx = tid + 256 * i, row = idx / (kMvdChunk / 4), c = (idx % (kMvdChunk / 4)) * 4;
+      *reinterpret_cast<float4 *>(&xs[buf][row * kMvdXld + c]) = xr[i];
+    }
+  };
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  double acc = -0.0;
+  int buf = 0;
+  for (int k0 = 0; k0 < K; k0 += kMvdChunk) {
+    const bool more = k0 + kMvdChunk < K;
+    if (more) fetch(k0 + kMvdChunk);
+    const int n8 = min(kMvdChunk, K - k0) / 8;
+    const uint4 *wl = ws[buf] + o16;
+    const float *xl = xs[buf] + br * kMvdXld;
+    for (int k8 = 0; k8 < n8; k8++) {
+      const uint4 v = wl[k8 * 16];
+      const float4 p = *reinterpret_cast<const float4 *>(xl + k8 * 8);
+      const float4 q = *reinterpret_cast<const float4 *>(xl + k8 * 8 + 4);
+      acc += (double)(bf_lo(v.x) * p.x);
+      acc += (double)(bf_hi(v.x) * p.y);
+      acc += (double)(bf_lo(v.y) * p.z);
+      acc += (double)(bf_hi(v.y) * p.w);
+      acc += (double)(bf_lo(v.z) * q.x);
+      acc += (double)(bf_hi(v.z) * q.y);
+      acc += (double)(bf_lo(v.w) * q.z);
+      acc += (double)(bf_hi(v.w) * q.w);
+    }
+    if (more) stash(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+  const float v = (float)acc;
+  const bool ok = live && o < valid_rows;
+  if (kEpi == kQ35Argmax) {
+    unsigned long long key = ok ? argmax_key(v, o) : 0ull;
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) {
+      const unsigned long long other = __shfl_xor(key, m, 16);
+      key = other > key ? other : key;
+    }
+    if (ok && out) out[(size_t)r * ldo + o] = v;
+    if (live && o16 == 0) part[(size_t)r * gridDim.x + tile] = key;
+  } else if (ok) {
+    float *p = out + (size_t)r * ldo + o;
+    *p = kEpi == kQ35Residual ? *p + v : v;
+  }
+  if (ok && !finitef(v)) atomicOr(&row_err[err_row ? err_row[r] : r], kErrNonFinite);
+}
+
 // cpu.rs:74-78 swiglu
 __global__ __launch_bounds__(256) void k_q35_swiglu(const float *__restrict__ gu, int ldgu, int F,
                                                     int up_off, float *__restrict__ h, int ldh) {
@@ -547,12 +647,29 @@ void q35_norm(hipStream_t s, int rows, const float *x, int ldx, const uint32_t *
                      ldo, row_err, err_row);
 }
 
-int q35_matvec_blocks(int rows_w) { return (rows_w + 63) / 64; }
+int q35_matvec_blocks(int rows_w) { return (rows_w + 15) / 16; }
+
+// Up to this many rows the one-chain-per-lane form runs (and always for the
+// argmax head, whose partials are per 16-output tile).
+constexpr int kMvdMaxRows = 64;
 
 void q35_matvec(hipStream_t s, int epi, const uint16_t *w, int rows_w, int valid_rows, int K,
                 const float *x, int ldx, int R, float *out, int ldo, unsigned long long *part,
                 uint32_t *row_err, const uint32_t *err_row) {
-  const dim3 grid(q35_matvec_blocks(rows_w), (R + kMvRows - 1) / kMvRows);
+  if (R <= kMvdMaxRows || epi == kQ35Argmax) {
+    const dim3 grid(rows_w / 16, (R + 15) / 16);
+    if (epi == kQ35Store)
+      hipLaunchKernelGGL(k_q35_mvd<kQ35Store>, grid, dim3(256), 0, s, w, valid_rows, K, x, ldx, R,
+                         out, ldo, part, row_err, err_row);
+    else if (epi == kQ35Residual)
+      hipLaunchKernelGGL(k_q35_mvd<kQ35Residual>, grid, dim3(256), 0, s, w, valid_rows, K, x, ldx,
+                         R, out, ldo, part, row_err, err_row);
+    else
+      hipLaunchKernelGGL(k_q35_mvd<kQ35Argmax>, grid, dim3(256), 0, s, w, valid_rows, K, x, ldx,
+                         R, out, ldo, part, row_err, err_row);
+    return;
+  }
+  const dim3 grid((rows_w + 63) / 64, (R + kMvRows - 1) / kMvRows);
   if (epi == kQ35Store)
     hipLaunchKernelGGL(k_q35_mv<kQ35Store>, grid, dim3(256), 0, s, w, rows_w, valid_rows, K, x,
                        ldx, R, out, ldo, part, row_err, err_row);

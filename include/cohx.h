@@ -112,8 +112,17 @@ typedef struct {
   uint32_t n_tokens;
   const uint32_t *tokens;
   uint32_t start_position;
-  uint32_t want_logits; /* copy the last row's logits to cohx_lane_out.logits */
+  uint32_t want_logits; /* 1: copy the last row's logits to cohx_lane_out.logits;
+                         * COHX_SKIP_HEAD: see below; 0: argmax only */
 } cohx_lane;
+/* want_logits value for a lane whose rows only advance its state: no final
+ * norm, head or argmax (cohx_lane_out.argmax reads COHX_NO_TOKEN).  Honoured
+ * by Qwen3.5 contexts, whose engine computes the head only where
+ * cursor + 1 >= len (qwen35/generation.rs:368, execution.rs:586-594);
+ * Qwen2 contexts compute the head for every lane (batch.rs:250-266) and treat
+ * it as 0. */
+#define COHX_SKIP_HEAD 2u
+#define COHX_NO_TOKEN 0xFFFFFFFFu
 
 typedef struct {
   uint32_t n_lanes;

@@ -34,10 +34,12 @@ class Pair:
         self.sessions[s] = self.orc.session(self.gpu.max_context)
         return s
 
-    def step(self, lanes):
-        """lanes: [(seq, tokens)]; every lane asks for logits.  Checks each lane
-        against the oracle and returns the GPU argmax per lane."""
-        res = self.gpu.step([dict(seq=s, tokens=toks, logits=True) for s, toks in lanes])
+    def step(self, lanes, skip=()):
+        """lanes: [(seq, tokens)]; every lane asks for logits except the seqs in
+        `skip`, whose rows only advance the state.  Checks each lane against
+        the oracle and returns the GPU argmax per lane."""
+        res = self.gpu.step([dict(seq=s, tokens=toks, logits=s not in skip, skip_head=s in skip)
+                             for s, toks in lanes])
         width = max(len(toks) for _, toks in lanes)
         for j in range(width):
             live = [(s, toks[j]) for s, toks in lanes if j < len(toks)]
@@ -47,6 +49,11 @@ class Pair:
         out = []
         for (s, toks), r in zip(lanes, res):
             assert r["status"] == 0, (s, r["status"])
+            if s in skip:
+                assert r["argmax"] == cohx.NO_TOKEN and r["logits"] is None
+                assert self.gpu.seq_length(s) == self.sessions[s].position()
+                out.append(None)
+                continue
             want = self.sessions[s].logits()
             got = r["logits"]
             if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
@@ -95,6 +102,20 @@ def test_tiny_ragged_chunks_across_steps():
         _, tok_b = p.step([(a, chunk), (b, [tok_b])])
     p.check_state(a)
     p.check_state(b)
+
+
+def test_tiny_prompt_chunks_without_head():
+    print("case: tiny Qwen3.5, prompt chunks that skip the head, then the last chunk with it",
+          flush=True)
+    cfg, t = synth35.in_memory(tiny(), seed=8)
+    p = Pair(cfg, t, max_lanes=4, max_rows=24, max_context=64)
+    a, b, c = p.alloc(), p.alloc(), p.alloc()
+    p.step([(a, [1, 2, 3, 4, 5]), (b, [6]), (c, [7, 8])], skip={a, c})
+    p.step([(a, [9, 10]), (b, [11]), (c, [12])], skip={b})
+    p.step([(a, [13]), (b, [14, 15, 16]), (c, [17])], skip={a, b, c})
+    p.step([(a, [18]), (b, [19]), (c, [20])])
+    for s in (a, b, c):
+        p.check_state(s)
 
 
 def test_tiny_fork_snapshot_then_diverge():
