@@ -42,10 +42,34 @@ __global__ __launch_bounds__(256) void k_q35_embed(const uint16_t *__restrict__ 
   for (int i = threadIdx.x; i < H; i += 256) x[(size_t)r * H + i] = bf_lo(src[i]);
 }
 
+// Sum of v[0..n) in f64, in index order from `init`, by one lane: the
+// terms stream from LDS in batches of 16, the next batch loading while the
+// current one is added, so the dependent add chain sets the pace.
+__device__ __forceinline__ double ordered_sum_f64(const double *v, int n, double init) {
+  double sum = init;
+  const int n16 = n / 16;
+  double cur[16], nxt[16];
+  if (n16) {
+#pragma unroll
+    for (int j = 0; j < 16; j++) cur[j] = v[j];
+  }
+  for (int b = 0; b < n16; b++) {
+    const int nb = min(b + 1, n16 - 1) * 16;
+#pragma unroll
+    for (int j = 0; j < 16; j++) nxt[j] = v[nb + j];
+#pragma unroll
+    for (int j = 0; j < 16; j++) sum += cur[j];
+#pragma unroll
+    for (int j = 0; j < 16; j++) cur[j] = nxt[j];
+  }
+  for (int i = n16 * 16; i < n; i++) sum += v[i];
+  return sum;
+}
+
 // ---------------------------------------------------------------------------
 // Norm (kernels.rs:26-52): mean of f32 squares summed in f64 in element
 // order, scale = 1/sqrt(f32(mean) + eps), y = (x*scale)*(w + zc).  The
-// squares are formed in parallel; one lane runs the ordered sum.
+// squares are formed and widened in parallel; one lane runs the ordered sum.
 // ---------------------------------------------------------------------------
 constexpr int kNormMax = kQ35MaxHidden;
 __global__ __launch_bounds__(256) void k_q35_norm(const float *__restrict__ x, int ldx,
@@ -54,7 +78,7 @@ __global__ __launch_bounds__(256) void k_q35_norm(const float *__restrict__ x, i
                                                   int zc, float *__restrict__ out, int ldo,
                                                   uint32_t *row_err,
                                                   const uint32_t *__restrict__ err_row) {
-  __shared__ float sq[kNormMax];
+  __shared__ double sq[kNormMax];
   __shared__ float s_scale;
   __shared__ int s_bad;
   const int r = blockIdx.x;
@@ -62,13 +86,12 @@ __global__ __launch_bounds__(256) void k_q35_norm(const float *__restrict__ x, i
   bool bad = false;
   for (int i = threadIdx.x; i < n; i += 256) {
     const float v = xr[i];
-    sq[i] = v * v;
+    sq[i] = (double)(v * v);
     bad |= !finitef(v);
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    double sum = -0.0;
-    for (int i = 0; i < n; i++) sum += (double)sq[i];
+    const double sum = ordered_sum_f64(sq, n, -0.0);
     const double mean = sum / (double)n;
     s_bad = !(__builtin_isfinite(mean) && finitef((float)mean));
     s_scale = 1.0f / sqrtf((float)mean + eps);
@@ -164,46 +187,46 @@ __global__ __launch_bounds__(256) void k_q35_mv(const uint16_t *__restrict__ w, 
   }
 }
 
-// The same product for a few rows (decode steps): a workgroup owns one tile
-// of 16 outputs x 16 rows, a wave 4 rows, a lane one (output, row) chain, so
-// a 1024-output matrix still spreads over 256 waves.  The tile's weights and
-// the rows' activations pass through LDS in chunks of 512 inputs, double
-// buffered: each thread holds its share of the next chunk in registers while
-// the current chunk is summed, so a whole chunk of work covers the memory
-// latency.  The k order of each chain is the reference's.
-constexpr int kMvdChunk = 512;                 // inputs per chunk
-constexpr int kMvdXld = kMvdChunk + 4;         // padded LDS row (floats)
-constexpr int kMvdW4 = kMvdChunk / 8 * 16;     // uint4 words of a weight chunk
-constexpr int kMvdX4 = 16 * kMvdChunk / 4;     // float4 words of an activation chunk
-template <int kEpi>
-__global__ __launch_bounds__(256) void k_q35_mvd(const uint16_t *__restrict__ w, int valid_rows,
-                                                 int K, const float *__restrict__ x, int ldx,
-                                                 int R, float *out, int ldo,
-                                                 unsigned long long *__restrict__ part,
-                                                 uint32_t *row_err,
-                                                 const uint32_t *__restrict__ err_row) {
-  __shared__ __align__(16) uint4 ws[2][kMvdW4];
-  __shared__ __align__(16) float xs[2][16 * kMvdXld];
+// The same product for a few rows (decode steps): a workgroup of kWaves
+// waves owns one tile of 16 outputs x 4*kWaves rows, a wave 4 rows, a lane
+// one (output, row) chain, so a 1024-output matrix still spreads over 256
+// waves.  The tile's weights and the rows' activations pass through LDS in
+// chunks of kChunk inputs, double buffered: each thread holds its share of
+// the next chunk in registers while the current chunk is summed, so a whole
+// chunk of work covers the memory latency.  The k order of each chain is the
+// reference's.
+template <int kEpi, int kChunk, int kWaves>
+__global__ __launch_bounds__(kWaves * 64) void k_q35_mvd(
+    const uint16_t *__restrict__ w, int valid_rows, int K, const float *__restrict__ x, int ldx,
+    int R, float *out, int ldo, unsigned long long *__restrict__ part, uint32_t *row_err,
+    const uint32_t *__restrict__ err_row) {
+  constexpr int kT = kWaves * 64, kRows = 4 * kWaves;
+  constexpr int kXld = kChunk + 4;            // padded LDS row (floats)
+  constexpr int kW4 = kChunk / 8 * 16;        // uint4 words of a weight chunk
+  constexpr int kX4 = kRows * kChunk / 4;     // float4 words of an activation chunk
+  static_assert(kW4 % kT == 0 && kX4 % kT == 0, "chunk must split evenly over the threads");
+  __shared__ __align__(16) uint4 ws[2][kW4];
+  __shared__ __align__(16) float xs[2][kRows * kXld];
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int o16 = lane % 16, tile = blockIdx.x, r0 = blockIdx.y * 16;
+  const int o16 = lane % 16, tile = blockIdx.x, r0 = blockIdx.y * kRows;
   const int br = wave * 4 + lane / 16, r = r0 + br;
   const int o = tile * 16 + o16;
   const bool live = r < R;
   const int nk8 = K / 8;
   const uint4 *wt = reinterpret_cast<const uint4 *>(w) + (size_t)tile * nk8 * 16;
-  uint4 wr[kMvdW4 / 256];
-  float4 xr[kMvdX4 / 256];
+  uint4 wr[kW4 / kT];
+  float4 xr[kX4 / kT];
   auto fetch = [&](int k0) {
-    const int n4 = min(kMvdChunk, K - k0) / 8 * 16;  // weight words in this chunk
-    const int kc = min(kMvdChunk, K - k0);
+    const int kc = min(kChunk, K - k0);
+    const int n4 = kc / 8 * 16;  // weight words in this chunk
 #pragma unroll
-    for (int i = 0; i < kMvdW4 / 256; i++) {
-      const int idx = tid + 256 * i;
+    for (int i = 0; i < kW4 / kT; i++) {
+      const int idx = tid + kT * i;
       wr[i] = idx < n4 ? wt[(size_t)k0 / 8 * 16 + idx] : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < kMvdX4 / 256; i++) {
-      const int idx = tid + 256 * i, row = idx / (kMvdChunk / 4), c = (idx % (kMvdChunk / 4)) * 4;
+    for (int i = 0; i < kX4 / kT; i++) {
+      const int idx = tid + kT * i, row = idx / (kChunk / 4), c = (idx % (kChunk / 4)) * 4;
       xr[i] = (r0 + row < R && c < kc)
                   ? *reinterpret_cast<const float4 *>(x + (size_t)(r0 + row) * ldx + k0 + c)
                   : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -211,11 +234,11 @@ __global__ __launch_bounds__(256) void k_q35_mvd(const uint16_t *__restrict__ w,
   };
   auto stash = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < kMvdW4 / 256; i++) ws[buf][tid + 256 * i] = wr[i];
+    for (int i = 0; i < kW4 / kT; i++) ws[buf][tid + kT * i] = wr[i];
 #pragma unroll
-    for (int i = 0; i < kMvdX4 / 256; i++) {
-      const int idx = tid + 256 * i, row = idx / (kMvdChunk / 4), c = (idx % (kMvdChunk / 4)) * 4;
-      *reinterpret_cast<float4 *>(&xs[buf][row * kMvdXld + c]) = xr[i];
+    for (int i = 0; i < kX4 / kT; i++) {
+      const int idx = tid + kT * i, row = idx / (kChunk / 4), c = (idx % (kChunk / 4)) * 4;
+      *reinterpret_cast<float4 *>(&xs[buf][row * kXld + c]) = xr[i];
     }
   };
   fetch(0);
@@ -223,12 +246,12 @@ __global__ __launch_bounds__(256) void k_q35_mvd(const uint16_t *__restrict__ w,
   __syncthreads();
   double acc = -0.0;
   int buf = 0;
-  for (int k0 = 0; k0 < K; k0 += kMvdChunk) {
-    const bool more = k0 + kMvdChunk < K;
-    if (more) fetch(k0 + kMvdChunk);
-    const int n8 = min(kMvdChunk, K - k0) / 8;
+  for (int k0 = 0; k0 < K; k0 += kChunk) {
+    const bool more = k0 + kChunk < K;
+    if (more) fetch(k0 + kChunk);
+    const int n8 = min(kChunk, K - k0) / 8;
     const uint4 *wl = ws[buf] + o16;
-    const float *xl = xs[buf] + br * kMvdXld;
+    const float *xl = xs[buf] + br * kXld;
     for (int k8 = 0; k8 < n8; k8++) {
       const uint4 v = wl[k8 * 16];
       const float4 p = *reinterpret_cast<const float4 *>(xl + k8 * 8);
@@ -245,6 +268,126 @@ __global__ __launch_bounds__(256) void k_q35_mvd(const uint16_t *__restrict__ w,
     if (more) stash(buf ^ 1);
     __syncthreads();
     buf ^= 1;
+  }
+  const float v = (float)acc;
+  const bool ok = live && o < valid_rows;
+  if (kEpi == kQ35Argmax) {
+    unsigned long long key = ok ? argmax_key(v, o) : 0ull;
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) {
+      const unsigned long long other = __shfl_xor(key, m, 16);
+      key = other > key ? other : key;
+    }
+    if (ok && out) out[(size_t)r * ldo + o] = v;
+    if (live && o16 == 0) part[(size_t)r * gridDim.x + tile] = key;
+  } else if (ok) {
+    float *p = out + (size_t)r * ldo + o;
+    *p = kEpi == kQ35Residual ? *p + v : v;
+  }
+  if (ok && !finitef(v)) atomicOr(&row_err[err_row ? err_row[r] : r], kErrNonFinite);
+}
+
+// Broadcast lane J of each 16-lane row to the whole row; folded into the
+// consuming multiply as a DPP operand (row_newbcast).
+template <int J>
+__device__ __forceinline__ float row_bcast(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x150 + J, 0xf, 0xf, false));
+}
+
+// Few-rows product split between waves: one wave issues at most one
+// vector instruction every few clocks, so a lane that forms, widens and adds
+// its own products runs its chain at a quarter of the SIMD's pace.  Here the
+// consumer wave (wave 0) owns 64 chains, 16 outputs (lane % 16) x 4 rows
+// (lane / 16), and only adds: per 64-input chunk it reads its 64 widened
+// products from LDS, two per read, in k order.  Producer waves 1..4 each form
+// 16 of the chunk's products per chain (f32 product, widened to f64) for the
+// next chunk, taking the activation for input j from lane j of the 16-lane
+// row and the weights from registers loaded kDepth chunks ahead.  The
+// consumer's adds are the reference's chain exactly.  K % 16 == 0.
+constexpr int kPcChunk = 64;
+template <int kEpi, int kDepth>
+__global__ __launch_bounds__(320) void k_q35_mvpc(
+    const uint16_t *__restrict__ w, int valid_rows, int K, const float *__restrict__ x, int ldx,
+    int R, float *out, int ldo, unsigned long long *__restrict__ part, uint32_t *row_err,
+    const uint32_t *__restrict__ err_row) {
+  __shared__ __align__(16) double2 pb[2][kPcChunk / 2][64];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int o16 = lane % 16, tile = blockIdx.x;
+  const int r = blockIdx.y * 4 + lane / 16;
+  const int o = tile * 16 + o16;
+  const bool live = r < R;
+  const int nc = (K + kPcChunk - 1) / kPcChunk, ng = K / 16;
+  double acc = -0.0;
+  // producer state: group g = 4 * chunk + (wave - 1) of 16 inputs
+  const int pg = wave - 1;
+  const uint4 *wt = reinterpret_cast<const uint4 *>(w) + (size_t)tile * (K / 8) * 16 + o16;
+  const float *xr = x + (size_t)(live ? r : 0) * ldx + o16;
+  float xv[kDepth];
+  uint4 wa[kDepth], wb[kDepth];
+  if (wave > 0) {
+#pragma unroll
+    for (int j = 0; j < kDepth; j++) {
+      const int g = min(4 * j + pg, ng - 1);
+      xv[j] = xr[g * 16];
+      wa[j] = wt[(size_t)(2 * g) * 16];
+      wb[j] = wt[(size_t)(2 * g + 1) * 16];
+    }
+  }
+  for (int c0 = 0; c0 < nc; c0 += kDepth) {
+#pragma unroll
+    for (int j = 0; j < kDepth; j++) {
+      const int c = c0 + j;
+      if (c < nc) {
+        if (wave > 0) {
+          const int g = 4 * c + pg;
+          const float xc = xv[j];
+          const uint4 a = wa[j], b = wb[j];
+          const int gn = min(4 * (c + kDepth) + pg, ng - 1);
+          xv[j] = xr[gn * 16];
+          wa[j] = wt[(size_t)(2 * gn) * 16];
+          wb[j] = wt[(size_t)(2 * gn + 1) * 16];
+          if (g < ng) {
+            float pr[16] = {bf_lo(a.x) * row_bcast<0>(xc),  bf_hi(a.x) * row_bcast<1>(xc),
+                            bf_lo(a.y) * row_bcast<2>(xc),  bf_hi(a.y) * row_bcast<3>(xc),
+                            bf_lo(a.z) * row_bcast<4>(xc),  bf_hi(a.z) * row_bcast<5>(xc),
+                            bf_lo(a.w) * row_bcast<6>(xc),  bf_hi(a.w) * row_bcast<7>(xc),
+                            bf_lo(b.x) * row_bcast<8>(xc),  bf_hi(b.x) * row_bcast<9>(xc),
+                            bf_lo(b.y) * row_bcast<10>(xc), bf_hi(b.y) * row_bcast<11>(xc),
+                            bf_lo(b.z) * row_bcast<12>(xc), bf_hi(b.z) * row_bcast<13>(xc),
+                            bf_lo(b.w) * row_bcast<14>(xc), bf_hi(b.w) * row_bcast<15>(xc)};
+            double2 *dst = &pb[c & 1][pg * 8][lane];
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+              dst[e * 64] = make_double2((double)pr[2 * e], (double)pr[2 * e + 1]);
+          }
+        } else if (c > 0) {
+          // every chunk before the last is full: all 32 reads go out before
+          // the adds start
+          const double2 *src = &pb[(c - 1) & 1][0][lane];
+          double2 d[kPcChunk / 2];
+#pragma unroll
+          for (int e = 0; e < kPcChunk / 2; e++) d[e] = src[e * 64];
+#pragma unroll
+          for (int e = 0; e < kPcChunk / 2; e++) {
+            acc += d[e].x;
+            acc += d[e].y;
+          }
+        }
+        __syncthreads();
+      }
+    }
+  }
+  if (wave > 0) return;
+  {
+    const int c = nc - 1;
+    const int n2 = min(kPcChunk, K - c * kPcChunk) / 2;
+    const double2 *src = &pb[c & 1][0][lane];
+    for (int e = 0; e < n2; e++) {
+      const double2 d = src[e * 64];
+      acc += d.x;
+      acc += d.y;
+    }
   }
   const float v = (float)acc;
   const bool ok = live && o < valid_rows;
@@ -335,22 +478,20 @@ __global__ __launch_bounds__(256) void k_q35_gates(const float *__restrict__ con
                                                    const float *__restrict__ dt, int KH, int VH,
                                                    int KD, float4 *__restrict__ gates,
                                                    uint32_t *row_err) {
-  __shared__ float sq[2][512];
+  __shared__ double sq[2][128];
   __shared__ float norms[2];
   const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   const int src = (h / (VH / KH)) * KD;
   const float *cr = conv + (size_t)row * ldc;
   for (int i = tid; i < KD; i += blockDim.x) {
     const float q = cr[src + i], k = cr[keys + src + i];
-    sq[0][i] = q * q;
-    sq[1][i] = k * k;
+    sq[0][i] = (double)(q * q);
+    sq[1][i] = (double)(k * k);
   }
   __syncthreads();
   if (tid % kWave == 0 && tid / kWave < 2) {  // one lane of each of two waves
     const int which = tid / kWave;
-    double a = -0.0;
-    for (int i = 0; i < KD; i++) a += (double)sq[which][i];
-    norms[which] = (float)a;
+    norms[which] = (float)ordered_sum_f64(sq[which], KD, -0.0);
   }
   __syncthreads();
   if (tid == 0) {
@@ -466,16 +607,15 @@ __global__ __launch_bounds__(256) void k_q35_headnorm(const float *__restrict__ 
                                                       int z_off, const float *__restrict__ w,
                                                       int VD, float eps, float *__restrict__ tgt,
                                                       int ldt, uint32_t *row_err) {
-  __shared__ float sq[256];
+  __shared__ double sq[256];
   __shared__ float s_scale;
   __shared__ int s_bad;
   const int row = blockIdx.x, h = blockIdx.y, j = threadIdx.x;
   const float o = j < VD ? o_in[(size_t)row * ldo + h * VD + j] : 0.0f;
-  if (j < VD) sq[j] = o * o;
+  if (j < VD) sq[j] = (double)(o * o);
   __syncthreads();
   if (j == 0) {
-    double sum = -0.0;
-    for (int i = 0; i < VD; i++) sum += (double)sq[i];
+    const double sum = ordered_sum_f64(sq, VD, -0.0);
     const double mean = sum / (double)VD;
     s_bad = !(__builtin_isfinite(mean) && finitef((float)mean));
     s_scale = 1.0f / sqrtf((float)mean + eps);
@@ -505,7 +645,8 @@ __global__ __launch_bounds__(576) void k_q35_qk(Q35Rows Rw, const float *__restr
                                                 const float2 *__restrict__ rope, float *q,
                                                 float *z, int ldq, float *kc, float *vc,
                                                 size_t cache_seq, uint32_t *row_err) {
-  __shared__ float y[512], sq[512];
+  __shared__ float y[512];
+  __shared__ double sq[512];
   __shared__ float s_scale;
   __shared__ int s_bad;
   const int row = blockIdx.x, hh = blockIdx.y, d = threadIdx.x;
@@ -514,11 +655,10 @@ __global__ __launch_bounds__(576) void k_q35_qk(Q35Rows Rw, const float *__restr
   const int kh = hh - NH, kvw = NKV * D;
   const float *srcp = mix + (size_t)row * ldm + (is_q ? hh * 2 * D : k_off + kh * D);
   const float xv = d < D ? srcp[d] : 0.0f;
-  if (d < D) sq[d] = xv * xv;
+  if (d < D) sq[d] = (double)(xv * xv);
   __syncthreads();
   if (d == 0) {
-    double sum = -0.0;
-    for (int i = 0; i < D; i++) sum += (double)sq[i];
+    const double sum = ordered_sum_f64(sq, D, -0.0);
     const double mean = sum / (double)D;
     s_bad = !(__builtin_isfinite(mean) && finitef((float)mean));
     s_scale = 1.0f / sqrtf((float)mean + eps);
@@ -657,16 +797,31 @@ void q35_matvec(hipStream_t s, int epi, const uint16_t *w, int rows_w, int valid
                 const float *x, int ldx, int R, float *out, int ldo, unsigned long long *part,
                 uint32_t *row_err, const uint32_t *err_row) {
   if (R <= kMvdMaxRows || epi == kQ35Argmax) {
-    const dim3 grid(rows_w / 16, (R + 15) / 16);
+    const int tiles = rows_w / 16;
+    // Few (16-output tile, 4-row group) pairs: one chain per lane leaves most
+    // SIMDs with a single wave, so the chains' adds go to consumer waves fed
+    // by producer waves.  Otherwise the one-wave-per-chain-set form, four
+    // waves per workgroup, three workgroups per CU.
+    if (epi != kQ35Argmax && K % 16 == 0 && tiles * ((R + 3) / 4) <= 512) {
+      const dim3 grid(tiles, (R + 3) / 4);
+      if (epi == kQ35Store)
+        hipLaunchKernelGGL((k_q35_mvpc<kQ35Store, 4>), grid, dim3(320), 0, s, w, valid_rows, K, x,
+                           ldx, R, out, ldo, part, row_err, err_row);
+      else
+        hipLaunchKernelGGL((k_q35_mvpc<kQ35Residual, 4>), grid, dim3(320), 0, s, w, valid_rows, K,
+                           x, ldx, R, out, ldo, part, row_err, err_row);
+      return;
+    }
+    const dim3 grid(tiles, (R + 15) / 16);
     if (epi == kQ35Store)
-      hipLaunchKernelGGL(k_q35_mvd<kQ35Store>, grid, dim3(256), 0, s, w, valid_rows, K, x, ldx, R,
-                         out, ldo, part, row_err, err_row);
+      hipLaunchKernelGGL((k_q35_mvd<kQ35Store, 128, 4>), grid, dim3(256), 0, s, w, valid_rows, K, x,
+                         ldx, R, out, ldo, part, row_err, err_row);
     else if (epi == kQ35Residual)
-      hipLaunchKernelGGL(k_q35_mvd<kQ35Residual>, grid, dim3(256), 0, s, w, valid_rows, K, x, ldx,
-                         R, out, ldo, part, row_err, err_row);
+      hipLaunchKernelGGL((k_q35_mvd<kQ35Residual, 128, 4>), grid, dim3(256), 0, s, w, valid_rows,
+                         K, x, ldx, R, out, ldo, part, row_err, err_row);
     else
-      hipLaunchKernelGGL(k_q35_mvd<kQ35Argmax>, grid, dim3(256), 0, s, w, valid_rows, K, x, ldx,
-                         R, out, ldo, part, row_err, err_row);
+      hipLaunchKernelGGL((k_q35_mvd<kQ35Argmax, 128, 4>), grid, dim3(256), 0, s, w, valid_rows, K,
+                         x, ldx, R, out, ldo, part, row_err, err_row);
     return;
   }
   const dim3 grid((rows_w + 63) / 64, (R + kMvRows - 1) / kMvRows);
