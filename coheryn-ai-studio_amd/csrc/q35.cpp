@@ -79,6 +79,7 @@ struct Q35Model {
         *q = nullptr, *z = nullptr, *att = nullptr, *gu_out = nullptr, *hb = nullptr,
         *fin = nullptr, *logits = nullptr;
   float4 *gates = nullptr;  // [rows][value_heads]: q_scale, k_scale, decay, beta
+  float *scores = nullptr;  // [rows][heads][max_context] attention scores
   unsigned long long *part = nullptr, *argmax = nullptr;
   uint32_t *row_err = nullptr, *tables = nullptr;
   uint32_t *h_tables = nullptr, *h_row_err = nullptr;
@@ -138,11 +139,15 @@ int cohx_create_qwen35(const cohx_qwen35_desc *dd, int device, cohx_ctx **out) {
   *out = nullptr;
   const cohx_qwen35_desc &d = *dd;
   if (!d.layers || d.layers > 128 || !d.hidden || !d.heads || !d.kv_heads || d.heads % d.kv_heads ||
-      !d.head_dim || d.head_dim > 512 || !d.linear_key_heads ||
+      !d.head_dim || !d.linear_key_heads ||
       d.linear_value_heads % d.linear_key_heads || !d.rotary_dim || d.rotary_dim % 2 ||
       d.rotary_dim > d.head_dim || !d.conv_kernel || !d.vocabulary || !d.intermediate ||
       !(d.epsilon > 0.0f) || !(d.rope_base > 1.0f))
     return COHX_INVALID_GGUF;
+  const uint32_t group = d.heads / d.kv_heads;
+  if (d.head_dim > (uint32_t)kQ35MaxHeadDim || d.head_dim % 4 || group > (uint32_t)kQ35MaxGroup ||
+      (group & (group - 1)))
+    return COHX_UNSUPPORTED;
   if (d.hidden % 8 || d.intermediate % 8 || (d.heads * d.head_dim) % 8 ||
       (d.linear_value_heads * d.linear_value_dim) % 8 || d.hidden > (uint32_t)kQ35MaxHidden ||
       d.conv_kernel > 8 || !q35_delta_supported((int)d.linear_key_dim, (int)d.linear_value_dim))
@@ -289,6 +294,7 @@ int cohx_create_qwen35(const cohx_qwen35_desc *dd, int device, cohx_ctx **out) {
   if (!rc) rc = q35_alloc(ctx, &q->hb, R * q->F);
   if (!rc) rc = q35_alloc(ctx, &q->fin, NL * H);
   if (!rc) rc = q35_alloc(ctx, &q->gates, R * q->VH);
+  if (!rc && q->n_full) rc = q35_alloc(ctx, &q->scores, R * q->NH * (size_t)d.max_context);
   if (!rc) rc = q35_alloc(ctx, &q->logits, NL * q->V);
   if (!rc) rc = q35_alloc(ctx, &q->part, NL * q35_matvec_blocks(q->head_rows));
   if (!rc) rc = q35_alloc(ctx, &q->argmax, NL);
@@ -565,7 +571,7 @@ int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
              q->kc + Ly.slot * q->kv_layer, q->vc + Ly.slot * q->kv_layer, q->kv_seq, q->row_err);
       q35_attention(s, (int)R, Rw, q->q, q->z, q->qw, q->kc + Ly.slot * q->kv_layer,
                     q->vc + Ly.slot * q->kv_layer, q->kv_seq, q->NH, q->NKV, q->D,
-                    (int)d.max_context, q->att, q->ld_att);
+                    (int)d.max_context, q->scores, q->att, q->ld_att);
       q35_matvec(s, kQ35Residual, Ly.out, q->h_rows, H, q->qw, q->att, q->ld_att, (int)R, q->x, H,
                  nullptr, q->row_err, nullptr);
     }

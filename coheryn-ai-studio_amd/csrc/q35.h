@@ -18,6 +18,10 @@ constexpr int kQ35MaxHidden = 8192;
 // maxima and rescale factors in LDS (3 floats per key, under 64 KiB).
 constexpr int kQ35MaxContext = 4096;
 
+// Attention shapes the kernels stage: heads per KV group (a power of two) and
+// head width.
+constexpr int kQ35MaxGroup = 16, kQ35MaxHeadDim = 256;
+
 // Lane tables of one step: lane i owns rows [first[i], first[i] + n[i]) of
 // sequence seq[i], the first at position start[i].
 struct Q35Lanes {
@@ -65,8 +69,9 @@ void q35_qk(hipStream_t s, int rows, Q35Rows Rw, const float *mix, int ldm, int 
             const float *q_norm, const float *k_norm, int heads, int kv_heads, int D, int rotary,
             float eps, const float2 *rope, float *q, float *z, int ldq, float *kc, float *vc,
             size_t cache_seq, uint32_t *row_err);
+// Scores into scores[rows][heads][max_context], then softmax and output.
 void q35_attention(hipStream_t s, int rows, Q35Rows Rw, const float *q, const float *z, int ldq,
                    const float *kc, const float *vc, size_t cache_seq, int heads, int kv_heads,
-                   int D, int max_context, float *out, int ldo);
+                   int D, int max_context, float *scores, float *out, int ldo);
 
 }  // namespace cohx

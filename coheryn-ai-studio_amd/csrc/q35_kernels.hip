@@ -694,38 +694,75 @@ __global__ __launch_bounds__(576) void k_q35_qk(Q35Rows Rw, const float *__restr
 }
 
 // ---------------------------------------------------------------------------
+// Attention scores s_t = f32(sum_i f64(q_i * k_t,i)) / sqrt(D) (cpu.rs:80-124
+// dot products), every (row, head, key) an independent ordered chain: a
+// workgroup takes one row, one KV group and 256/G keys, the G heads of the
+// group side by side so each K load serves them all.  Scores go to
+// sc[row][head][key].
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_q35_scores(Q35Rows Rw, const float *__restrict__ q,
+                                                    int ldq, const float *__restrict__ kc,
+                                                    size_t cache_seq, int NH, int NKV, int D,
+                                                    float *__restrict__ sc, int ldsc) {
+  __shared__ __align__(16) float qs[kQ35MaxGroup * kQ35MaxHeadDim];
+  const int row = blockIdx.x, kvh = blockIdx.y, G = NH / NKV, kb = 256 / G;
+  const int kv = (int)Rw.pos[row] + 1, t0 = blockIdx.z * kb;
+  if (t0 >= kv) return;
+  const uint32_t seq = Rw.seq[row];
+  const int kvw = NKV * D;
+  const float *qg = q + (size_t)row * ldq + (size_t)kvh * G * D;
+  for (int i = threadIdx.x; i < G * D; i += 256) qs[i] = qg[i];
+  __syncthreads();
+  const int hg = threadIdx.x % G, t = t0 + (int)threadIdx.x / G;
+  if (t >= kv || (int)threadIdx.x >= kb * G) return;
+  const float4 *kr =
+      reinterpret_cast<const float4 *>(kc + (size_t)seq * cache_seq + (size_t)t * kvw + kvh * D);
+  const float4 *qh = reinterpret_cast<const float4 *>(qs + hg * D);
+  double a = -0.0;
+  const int n4 = D / 4;
+  for (int i0 = 0; i0 < n4; i0 += 8) {
+    float4 kk[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) kk[j] = i0 + j < n4 ? kr[i0 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      if (i0 + j < n4) {
+        const float4 qq = qh[i0 + j];
+        a += (double)(qq.x * kk[j].x);
+        a += (double)(qq.y * kk[j].y);
+        a += (double)(qq.z * kk[j].z);
+        a += (double)(qq.w * kk[j].w);
+      }
+    }
+  }
+  sc[((size_t)row * NH + kvh * G + hg) * ldsc + t] = (float)a / sqrtf((float)D);
+}
+
+// ---------------------------------------------------------------------------
 // Online-softmax attention (cpu.rs:80-124) in the reference's exact order.
 // The running maximum m_t is a prefix maximum (exact in any order), so the
-// scores, the maxima and both exponentials old_t = exp(m_{t-1} - m_t),
-// new_t = exp(s_t - m_t) are formed in parallel; the two f32 recurrences
-// den = den*old + new and o_d = o_d*old + new*v_d then run in key order,
-// one thread per output element (and one for the denominator).  The output
-// is o/den times sigmoid(gate) (execution.rs:506-508).
+// maxima and both exponentials old_t = exp(m_{t-1} - m_t), new_t =
+// exp(s_t - m_t) are formed in parallel from the scores; the two f32
+// recurrences den = den*old + new and o_d = o_d*old + new*v_d then run in key
+// order, one thread per output element (and one for the denominator), V
+// loads running eight keys ahead.  The output is o/den times sigmoid(gate)
+// (execution.rs:506-508).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(576) void k_q35_attn(Q35Rows Rw, const float *__restrict__ q,
-                                                  const float *__restrict__ z, int ldq,
-                                                  const float *__restrict__ kc,
+__global__ __launch_bounds__(576) void k_q35_attn(Q35Rows Rw, const float *__restrict__ scores,
+                                                  int ldsc, const float *__restrict__ z, int ldq,
                                                   const float *__restrict__ vc, size_t cache_seq,
-                                                  int NH, int NKV, int D, int maxc,
+                                                  int NH, int NKV, int D, int maxc4,
                                                   float *__restrict__ out, int ldo) {
-  extern __shared__ float sm[];
-  float *sq = sm, *sc = sq + 512, *mx = sc + maxc, *old = mx + maxc, *seg = old + maxc;
+  extern __shared__ __align__(16) float sm[];
+  float *sc = sm, *mx = sc + maxc4, *old = mx + maxc4, *seg = old + maxc4;
   __shared__ float s_den;
   const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
   const int dthreads = nt - kWave;  // the last wave runs the denominator
   const uint32_t pos = Rw.pos[row], seq = Rw.seq[row];
   const int kv = (int)pos + 1, kvh = h / (NH / NKV), kvw = NKV * D;
-  const float *K = kc + (size_t)seq * cache_seq + kvh * D;
   const float *V = vc + (size_t)seq * cache_seq + kvh * D;
-  for (int i = tid; i < D; i += nt) sq[i] = q[(size_t)row * ldq + h * D + i];
-  __syncthreads();
-  const float root = sqrtf((float)D);
-  for (int t = tid; t < kv; t += nt) {
-    const float *kr = K + (size_t)t * kvw;
-    double a = -0.0;
-    for (int i = 0; i < D; i++) a += (double)(sq[i] * kr[i]);
-    sc[t] = (float)a / root;
-  }
+  const float *srow = scores + ((size_t)row * NH + h) * ldsc;
+  for (int t = tid; t < kv; t += nt) sc[t] = srow[t];
   __syncthreads();
   // prefix maxima: contiguous segments, then an exclusive scan of segment maxima
   const int per = (kv + nt - 1) / nt, lo = min(kv, tid * per), hi = min(kv, lo + per);
@@ -762,7 +799,33 @@ __global__ __launch_bounds__(576) void k_q35_attn(Q35Rows Rw, const float *__res
   }
   float o = 0.0f;
   if (tid < D) {
-    for (int t = 0; t < kv; t++) o = o * old[t] + sc[t] * V[(size_t)t * kvw + tid];
+    // whole groups of 8 keys without branches, the next group's V values
+    // loading while the current group is folded in; then the tail
+    const float *vp = V + tid;
+    const int full = kv / 8;
+    float cur[8], nxt[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) cur[j] = full ? vp[(size_t)j * kvw] : 0.0f;
+    for (int g = 0; g < full; g++) {
+      const int tn = min(g + 1, full - 1) * 8;
+#pragma unroll
+      for (int j = 0; j < 8; j++) nxt[j] = vp[(size_t)(tn + j) * kvw];
+      const float4 o0 = *reinterpret_cast<const float4 *>(old + 8 * g);
+      const float4 o1 = *reinterpret_cast<const float4 *>(old + 8 * g + 4);
+      const float4 n0 = *reinterpret_cast<const float4 *>(sc + 8 * g);
+      const float4 n1 = *reinterpret_cast<const float4 *>(sc + 8 * g + 4);
+      o = o * o0.x + n0.x * cur[0];
+      o = o * o0.y + n0.y * cur[1];
+      o = o * o0.z + n0.z * cur[2];
+      o = o * o0.w + n0.w * cur[3];
+      o = o * o1.x + n1.x * cur[4];
+      o = o * o1.y + n1.y * cur[5];
+      o = o * o1.z + n1.z * cur[6];
+      o = o * o1.w + n1.w * cur[7];
+#pragma unroll
+      for (int j = 0; j < 8; j++) cur[j] = nxt[j];
+    }
+    for (int t = full * 8; t < kv; t++) o = o * old[t] + sc[t] * vp[(size_t)t * kvw];
   }
   __syncthreads();
   if (tid < D) {
@@ -887,11 +950,15 @@ void q35_qk(hipStream_t s, int rows, Q35Rows Rw, const float *mix, int ldm, int 
 
 void q35_attention(hipStream_t s, int rows, Q35Rows Rw, const float *q, const float *z, int ldq,
                    const float *kc, const float *vc, size_t cache_seq, int heads, int kv_heads,
-                   int D, int max_context, float *out, int ldo) {
+                   int D, int max_context, float *scores, float *out, int ldo) {
+  const int G = heads / kv_heads, kb = 256 / G;
+  hipLaunchKernelGGL(k_q35_scores, dim3(rows, kv_heads, (max_context + kb - 1) / kb), dim3(256), 0,
+                     s, Rw, q, ldq, kc, cache_seq, heads, kv_heads, D, scores, max_context);
   const int threads = ((D + kWave - 1) / kWave) * kWave + kWave;
-  const size_t lds = (size_t)(512 + 3 * max_context + threads) * sizeof(float);
-  hipLaunchKernelGGL(k_q35_attn, dim3(rows, heads), dim3(threads), lds, s, Rw, q, z, ldq, kc, vc,
-                     cache_seq, heads, kv_heads, D, max_context, out, ldo);
+  const int maxc4 = (max_context + 3) / 4 * 4;
+  const size_t lds = (size_t)(3 * maxc4 + threads) * sizeof(float);
+  hipLaunchKernelGGL(k_q35_attn, dim3(rows, heads), dim3(threads), lds, s, Rw, scores, max_context,
+                     z, ldq, vc, cache_seq, heads, kv_heads, D, maxc4, out, ldo);
 }
 
 }  // namespace cohx
