@@ -338,7 +338,7 @@ def cpu_baseline(cfg, tensors, kv, start_tokens, seed, lanes, steps, threads):
 
 def kernel_instance(name):
     import re
-    m = re.search(r"cohx::(k_\w+)(<[^>]*>)?", name)
+    m = re.search(r"\b(k_\w+)(<[^>]*>)?\(", name)
     return m.group(1) + (m.group(2) or "") if m else name
 
 
@@ -412,6 +412,41 @@ def summarize_trace(trace_csv, bench_json):
     print("|---|---:|---:|---:|---:|---:|---:|")
     for (name, gx), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
         if sum(d) < 1000:
+            continue
+        print(f"| {name} | {gx} | {len(d)} | {sum(d) / len(d):.2f} | {min(d):.2f} | {max(d):.2f} | "
+              f"{sum(d) / 1e3:.2f} |")
+
+
+C5_TRACE_CMD = ("rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o <name> -- "
+                "python3 bench.py --c5-only --no-cpu-baseline")
+
+
+def summarize_c5_trace(trace_csv, bench_json):
+    """Markdown summary of a rocprofv3 --kernel-trace run of the C5 workload:
+    per kernel and grid shape (the grid's y extent counts row groups, so the
+    one-token schedule's 16-row steps separate from the prompt chunks) the
+    dispatch count and mean duration, and the per-step time of the 16-row
+    decode steps by kernel."""
+    import csv
+    groups = {}
+    with open(trace_csv) as f:
+        for row in csv.DictReader(f):
+            k = (kernel_instance(row["Kernel_Name"]),
+                 f'{row["Grid_Size_X"]}x{row["Grid_Size_Y"]}x{row["Grid_Size_Z"]}')
+            groups.setdefault(k, []).append(
+                (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+    with open(bench_json) as f:
+        line = json.loads(f.read().strip().splitlines()[-1])
+    es = line["engine_schedule"]
+    print(f"Command: `{C5_TRACE_CMD}`\n")
+    print(f"Plain run of the same command: prompts in chunks of {line['prompt_chunk']}: "
+          f"{line['value']:.0f} generated tok/s ({line['rows_per_s']:.0f} rows/s); one token per "
+          f"sequence per step: {es['ms_per_step']:.3f} ms/step ({es['rows_per_s']:.0f} rows/s); "
+          f"same tokens: {line['same_tokens_both_schedules']}.\n")
+    print("| kernel | grid (threads) | dispatches | mean us | min us | max us | total ms |")
+    print("|---|---:|---:|---:|---:|---:|---:|")
+    for (name, gx), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        if sum(d) < 2000:
             continue
         print(f"| {name} | {gx} | {len(d)} | {sum(d) / len(d):.2f} | {min(d):.2f} | {max(d):.2f} | "
               f"{sum(d) / 1e3:.2f} |")
@@ -554,6 +589,8 @@ def main():
                     help="only copy 1 GiB device-to-device 4 times (counter calibration)")
     ap.add_argument("--summarize-counters", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
                     help="write the traffic summary from rocprofv3 --pmc csv files (no GPU)")
+    ap.add_argument("--summarize-c5-trace", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_JSON"),
+                    help="print a markdown summary of a rocprofv3 --kernel-trace run of --c5-only")
     ap.add_argument("--summarize-trace", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_JSON"),
                     help="print a markdown summary of a rocprofv3 --kernel-trace run (no GPU)")
     args = ap.parse_args()
@@ -562,6 +599,9 @@ def main():
         return
     if args.summarize_counters:
         summarize_counters(*args.summarize_counters, lanes=args.lanes)
+        return
+    if args.summarize_c5_trace:
+        summarize_c5_trace(*args.summarize_c5_trace)
         return
     if args.summarize_trace:
         summarize_trace(*args.summarize_trace)

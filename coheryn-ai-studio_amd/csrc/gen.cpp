@@ -240,13 +240,18 @@ int cohx_gen_begin(cohx_ctx *ctx, const uint32_t *prompt, uint32_t n_prompt,
   // Prefix reuse (generation.rs:189-202): take over a finished generation's
   // KV, keep the longest common token prefix, capped at prompt_len-1 so the
   // last prompt token is always recomputed.
-  if (prior && prior->ctx == ctx && prior->has_seq && prior->done &&
-      ctx->seqs[prior->seq].capacity >= context) {
-    size_t common = 0;
+  // A hybrid (Qwen3.5) context's recurrent state cannot be rewound, so there
+  // the prior sequence is taken over only when all of it is such a prefix.
+  size_t common = 0;
+  if (prior && prior->ctx == ctx && prior->has_seq && prior->done) {
     while (common < prior->kv_tokens.size() && common < g->prompt.size() &&
            prior->kv_tokens[common] == g->prompt[common])
       common++;
     common = std::min(common, g->prompt.size() - 1);
+  }
+  if (prior && prior->ctx == ctx && prior->has_seq && prior->done &&
+      ctx->seqs[prior->seq].capacity >= context &&
+      (!ctx->q35 || common == prior->kv_tokens.size())) {
     g->seq = prior->seq;
     g->has_seq = true;
     prior->has_seq = false;
@@ -298,8 +303,12 @@ int cohx_step_batch(cohx_ctx *ctx, cohx_gen *const *states, uint32_t n, cohx_bat
     uint32_t len = 0;
     cohx_seq_length(ctx, g->seq, &len);
     ln.start_position = len;
-    ln.want_logits = (sampled_next && g->sampler.needs_logits()) ? 1u : 0u;
-    if (ln.want_logits) g->logits.resize(ctx->desc.vocabulary);
+    // Rows that do not end the prompt need no head on a hybrid context
+    // (qwen35/generation.rs:368); the Qwen2 graph computes it for every lane.
+    ln.want_logits = (sampled_next && g->sampler.needs_logits()) ? 1u
+                     : (!sampled_next && ctx->q35)              ? COHX_SKIP_HEAD
+                                                                 : 0u;
+    if (ln.want_logits == 1u) g->logits.resize(ctx->desc.vocabulary);
     lanes.push_back(ln);
     lane_of.push_back(i);
   }
@@ -308,7 +317,7 @@ int cohx_step_batch(cohx_ctx *ctx, cohx_gen *const *states, uint32_t n, cohx_bat
   if (lanes.empty()) return COHX_OK;
   std::vector<cohx_lane_out> outs(lanes.size());
   for (size_t k = 0; k < lanes.size(); k++)
-    outs[k].logits = lanes[k].want_logits ? states[lane_of[k]]->logits.data() : nullptr;
+    outs[k].logits = lanes[k].want_logits == 1u ? states[lane_of[k]]->logits.data() : nullptr;
   cohx_batch batch{(uint32_t)lanes.size(), lanes.data()};
   cohx_step_out so{};
   so.lanes = outs.data();

@@ -168,3 +168,56 @@ def test_full_shape_prefill_and_decode_bit_exact():
         nxt = p.step([(a, [nxt[0]]), (b, [nxt[1]])])
     p.check_state(a)
     p.check_state(b)
+
+
+def _oracle_greedy(o, cfg, prompt, n, context):
+    s = o.session(context)
+    out = []
+    for tok in prompt:
+        assert o.forward_batch([s], [tok])[0] == 0
+    for _ in range(n):
+        nxt = int(np.argmax(s.logits()))
+        out.append(nxt)
+        if len(out) == n:
+            break
+        assert o.forward_batch([s], [nxt])[0] == 0
+    return out
+
+
+def test_tiny_generation_api_greedy_and_prefix_takeover():
+    print("case: tiny Qwen3.5 through the generation mirror: greedy vs oracle, batched == alone, "
+          "prefix takeover", flush=True)
+    cfg, t = synth35.in_memory(tiny(), seed=9)
+    m = cohx.Qwen35(cfg, t, max_lanes=4, max_rows=8, max_seqs=16, max_context=48)
+    o = orc.Qwen35Model(cfg, t, threads=8)
+    prompts = [[3, 1, 4, 1, 5], [9, 2, 6], [5, 3, 5, 8, 9, 7, 9]]
+    opts = cohx.GenerationOptions(max_tokens=6)
+    states = [m.begin_generation(p, opts) for p in prompts]
+    while not all(s.is_finished() for s in states):
+        live = [s for s in states if s.needs_forward()]
+        if live:
+            m.step_batch(live)
+        for s in states:
+            s.sample()
+    for p, s in zip(prompts, states):
+        assert s.token_ids() == _oracle_greedy(o, cfg, p, 6, 48), p
+    # seeded sampling: batched == alone
+    sopts = cohx.GenerationOptions(max_tokens=5, temperature=0.8, top_k=20, top_p=0.9, seed=11)
+    together = [m.begin_generation(p, sopts) for p in prompts[:2]]
+    while not all(s.is_finished() for s in together):
+        live = [s for s in together if s.needs_forward()]
+        if live:
+            m.step_batch(live)
+        for s in together:
+            s.sample()
+    for p, s in zip(prompts[:2], together):
+        assert cohx.generate(m, p, sopts).token_ids() == s.token_ids()
+    # a finished generation whose whole history prefixes the next prompt is taken over
+    first = states[0]
+    hist = prompts[0] + first.token_ids()[:-1]
+    nxt = m.begin_generation(hist + [7, 7], opts, prior=first)
+    while not nxt.is_finished():
+        if nxt.needs_forward():
+            m.step_generation(nxt)
+        nxt.sample()
+    assert nxt.token_ids() == _oracle_greedy(o, cfg, hist + [7, 7], 6, 48)
