@@ -305,12 +305,12 @@ __device__ __forceinline__ float row_bcast(float v) {
 // next chunk, taking the activation for input j from lane j of the 16-lane
 // row and the weights from registers loaded kDepth chunks ahead.  The
 // consumer's adds are the reference's chain exactly.  K % 16 == 0.
-constexpr int kPcChunk = 64;
-template <int kEpi, int kDepth>
-__global__ __launch_bounds__(320) void k_q35_mvpc(
+template <int kEpi, int kDepth, int kProducers = 4, int kConsumers = 1>
+__global__ __launch_bounds__(64 * (kProducers + kConsumers)) void k_q35_mvpc(
     const uint16_t *__restrict__ w, int valid_rows, int K, const float *__restrict__ x, int ldx,
     int R, float *out, int ldo, unsigned long long *__restrict__ part, uint32_t *row_err,
     const uint32_t *__restrict__ err_row) {
+  constexpr int kPcChunk = 16 * kProducers;
   __shared__ __align__(16) double2 pb[2][kPcChunk / 2][64];
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int o16 = lane % 16, tile = blockIdx.x;
@@ -319,66 +319,85 @@ __global__ __launch_bounds__(320) void k_q35_mvpc(
   const bool live = r < R;
   const int nc = (K + kPcChunk - 1) / kPcChunk, ng = K / 16;
   double acc = -0.0;
-  // producer state: group g = 4 * chunk + (wave - 1) of 16 inputs
-  const int pg = wave - 1;
+  // consumer wave c (< kConsumers) adds the chains of lanes
+  // [c * 64/kConsumers, (c + 1) * 64/kConsumers); producer p = wave -
+  // kConsumers forms group kProducers * chunk + p of 16 inputs for all 64
+  const bool producer = wave >= kConsumers;
+  const bool mine = !producer && lane / (64 / kConsumers) == wave;
+  const int pg = wave - kConsumers;
   const uint4 *wt = reinterpret_cast<const uint4 *>(w) + (size_t)tile * (K / 8) * 16 + o16;
   const float *xr = x + (size_t)(live ? r : 0) * ldx + o16;
-  float xv[kDepth];
-  uint4 wa[kDepth], wb[kDepth];
-  if (wave > 0) {
+  // two register batches of kDepth chunks each: while one batch is turned
+  // into products, the other is loading (no copies between them, so no load
+  // is waited for before a whole batch of work has passed)
+  float xa[kDepth], xb[kDepth];
+  uint4 wa0[kDepth], wa1[kDepth], wb0[kDepth], wb1[kDepth];
+  auto load = [&](float (&xv)[kDepth], uint4 (&w0)[kDepth], uint4 (&w1)[kDepth], int c0) {
 #pragma unroll
     for (int j = 0; j < kDepth; j++) {
-      const int g = min(4 * j + pg, ng - 1);
+      const int g = min(kProducers * (c0 + j) + pg, ng - 1);
       xv[j] = xr[g * 16];
-      wa[j] = wt[(size_t)(2 * g) * 16];
-      wb[j] = wt[(size_t)(2 * g + 1) * 16];
+      w0[j] = wt[(size_t)(2 * g) * 16];
+      w1[j] = wt[(size_t)(2 * g + 1) * 16];
     }
-  }
-  for (int c0 = 0; c0 < nc; c0 += kDepth) {
+  };
+  auto produce = [&](float xc, uint4 a, uint4 b, int c) {
+    const int g = kProducers * c + pg;
+    if (g >= ng) return;
+    float wf[16] = {bf_lo(a.x), bf_hi(a.x), bf_lo(a.y), bf_hi(a.y), bf_lo(a.z), bf_hi(a.z),
+                    bf_lo(a.w), bf_hi(a.w), bf_lo(b.x), bf_hi(b.x), bf_lo(b.y), bf_hi(b.y),
+                    bf_lo(b.z), bf_hi(b.z), bf_lo(b.w), bf_hi(b.w)};
+    pin_vgprs(wf);
+    float pr[16] = {wf[0] * row_bcast<0>(xc),   wf[1] * row_bcast<1>(xc),
+                    wf[2] * row_bcast<2>(xc),   wf[3] * row_bcast<3>(xc),
+                    wf[4] * row_bcast<4>(xc),   wf[5] * row_bcast<5>(xc),
+                    wf[6] * row_bcast<6>(xc),   wf[7] * row_bcast<7>(xc),
+                    wf[8] * row_bcast<8>(xc),   wf[9] * row_bcast<9>(xc),
+                    wf[10] * row_bcast<10>(xc), wf[11] * row_bcast<11>(xc),
+                    wf[12] * row_bcast<12>(xc), wf[13] * row_bcast<13>(xc),
+                    wf[14] * row_bcast<14>(xc), wf[15] * row_bcast<15>(xc)};
+    double2 *dst = &pb[c & 1][pg * 8][lane];
+#pragma unroll
+    for (int e = 0; e < 8; e++) dst[e * 64] = make_double2((double)pr[2 * e], (double)pr[2 * e + 1]);
+  };
+  auto consume = [&](int c) {  // chunk c is full (not the last)
+    const double2 *src = &pb[c & 1][0][lane];
+#pragma unroll
+    for (int e0 = 0; e0 < kPcChunk / 2; e0 += 16) {
+      double2 d[16];
+#pragma unroll
+      for (int e = 0; e < 16; e++) d[e] = src[(e0 + e) * 64];
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        acc += d[e].x;
+        acc += d[e].y;
+      }
+    }
+  };
+  if (producer) load(xa, wa0, wa1, 0);
+  // whole turns of 2*kDepth chunks; steps past the last chunk only keep the
+  // barrier count uniform.  Step c: producers fill chunk c, the consumer adds
+  // chunk c-1.
+  const int ncp = (nc + 2 * kDepth - 1) / (2 * kDepth) * (2 * kDepth);
+  for (int c0 = 0; c0 < ncp; c0 += 2 * kDepth) {
+    if (producer) load(xb, wb0, wb1, c0 + kDepth);
 #pragma unroll
     for (int j = 0; j < kDepth; j++) {
       const int c = c0 + j;
-      if (c < nc) {
-        if (wave > 0) {
-          const int g = 4 * c + pg;
-          const float xc = xv[j];
-          const uint4 a = wa[j], b = wb[j];
-          const int gn = min(4 * (c + kDepth) + pg, ng - 1);
-          xv[j] = xr[gn * 16];
-          wa[j] = wt[(size_t)(2 * gn) * 16];
-          wb[j] = wt[(size_t)(2 * gn + 1) * 16];
-          if (g < ng) {
-            float pr[16] = {bf_lo(a.x) * row_bcast<0>(xc),  bf_hi(a.x) * row_bcast<1>(xc),
-                            bf_lo(a.y) * row_bcast<2>(xc),  bf_hi(a.y) * row_bcast<3>(xc),
-                            bf_lo(a.z) * row_bcast<4>(xc),  bf_hi(a.z) * row_bcast<5>(xc),
-                            bf_lo(a.w) * row_bcast<6>(xc),  bf_hi(a.w) * row_bcast<7>(xc),
-                            bf_lo(b.x) * row_bcast<8>(xc),  bf_hi(b.x) * row_bcast<9>(xc),
-                            bf_lo(b.y) * row_bcast<10>(xc), bf_hi(b.y) * row_bcast<11>(xc),
-                            bf_lo(b.z) * row_bcast<12>(xc), bf_hi(b.z) * row_bcast<13>(xc),
-                            bf_lo(b.w) * row_bcast<14>(xc), bf_hi(b.w) * row_bcast<15>(xc)};
-            double2 *dst = &pb[c & 1][pg * 8][lane];
+      if (producer) produce(xa[j], wa0[j], wa1[j], c);
+      else if (mine && c > 0 && c < nc) consume(c - 1);
+      __syncthreads();
+    }
+    if (producer) load(xa, wa0, wa1, c0 + 2 * kDepth);
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-              dst[e * 64] = make_double2((double)pr[2 * e], (double)pr[2 * e + 1]);
-          }
-        } else if (c > 0) {
-          // every chunk before the last is full: all 32 reads go out before
-          // the adds start
-          const double2 *src = &pb[(c - 1) & 1][0][lane];
-          double2 d[kPcChunk / 2];
-#pragma unroll
-          for (int e = 0; e < kPcChunk / 2; e++) d[e] = src[e * 64];
-#pragma unroll
-          for (int e = 0; e < kPcChunk / 2; e++) {
-            acc += d[e].x;
-            acc += d[e].y;
-          }
-        }
-        __syncthreads();
-      }
+    for (int j = 0; j < kDepth; j++) {
+      const int c = c0 + kDepth + j;
+      if (producer) produce(xb[j], wb0[j], wb1[j], c);
+      else if (mine && c > 0 && c < nc) consume(c - 1);
+      __syncthreads();
     }
   }
-  if (wave > 0) return;
+  if (!mine) return;
   {
     const int c = nc - 1;
     const int n2 = min(kPcChunk, K - c * kPcChunk) / 2;
