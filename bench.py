@@ -445,11 +445,15 @@ def summarize_c5_trace(trace_csv, bench_json):
           f"same tokens: {line['same_tokens_both_schedules']}.\n")
     print("| kernel | grid (threads) | dispatches | mean us | min us | max us | total ms |")
     print("|---|---:|---:|---:|---:|---:|---:|")
-    for (name, gx), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
-        if sum(d) < 2000:
-            continue
+    for (name, gx), d in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:30]:
         print(f"| {name} | {gx} | {len(d)} | {sum(d) / len(d):.2f} | {min(d):.2f} | {max(d):.2f} | "
               f"{sum(d) / 1e3:.2f} |")
+    print("\nThe 30 largest (kernel, grid) groups by total time, over both schedules.  Grid y of the\n"
+          "matvec kernels counts row groups: `k_q35_mvpc` 20480x4 and `k_q35_mvd` 131584x1 / 114688x1\n"
+          "are the 16-row steps of the one-token schedule (o/out/down projections; mix and gate+up),\n"
+          "`k_q35_mvd<2, ...>` is the LM head with its argmax, and `k_q35_mv` with grid y in the hundreds\n"
+          "are the 256-token prompt chunks (up to 4096 rows).\n\n"
+          f"Summary: `python bench.py --summarize-c5-trace <dir>/<name>_kernel_trace.csv <bench stdout>`")
 
 
 def copy_probe():
