@@ -122,7 +122,8 @@ __global__ __launch_bounds__(256) void k_q35_mv(const uint16_t *__restrict__ w, 
                                                 unsigned long long *__restrict__ part,
                                                 uint32_t *row_err,
                                                 const uint32_t *__restrict__ err_row) {
-  __shared__ __align__(16) float xs[kMvRows][kMvKC];
+  // rows padded by 4 floats: the four row groups of a wave read different banks
+  __shared__ __align__(16) float xs[kMvRows][kMvKC + 4];
   __shared__ unsigned long long keys[kMvRows][64];
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int o16 = lane % 16, g = lane / 16;
@@ -147,11 +148,19 @@ __global__ __launch_bounds__(256) void k_q35_mv(const uint16_t *__restrict__ w, 
       const uint4 wv = wt[(size_t)((k0 + kk) / 8) * 16];
       const float wf[8] = {bf_lo(wv.x), bf_hi(wv.x), bf_lo(wv.y), bf_hi(wv.y),
                            bf_lo(wv.z), bf_hi(wv.z), bf_lo(wv.w), bf_hi(wv.w)};
+      float xv[4][8];
+#pragma unroll
+      for (int rr = 0; rr < 4; rr++) {
+        const float4 lo = *reinterpret_cast<const float4 *>(&xs[g * 4 + rr][kk]);
+        const float4 hi = *reinterpret_cast<const float4 *>(&xs[g * 4 + rr][kk + 4]);
+        xv[rr][0] = lo.x; xv[rr][1] = lo.y; xv[rr][2] = lo.z; xv[rr][3] = lo.w;
+        xv[rr][4] = hi.x; xv[rr][5] = hi.y; xv[rr][6] = hi.z; xv[rr][7] = hi.w;
+      }
 #pragma unroll
       for (int e = 0; e < 8; e++) {
         float pr[4];
 #pragma unroll
-        for (int rr = 0; rr < 4; rr++) pr[rr] = wf[e] * xs[g * 4 + rr][kk + e];
+        for (int rr = 0; rr < 4; rr++) pr[rr] = wf[e] * xv[rr][e];
         pin_vgprs(pr);
         double wd[4];
 #pragma unroll

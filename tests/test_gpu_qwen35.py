@@ -104,6 +104,36 @@ def test_tiny_ragged_chunks_across_steps():
     p.check_state(b)
 
 
+def test_tiny_large_packed_step_bit_exact():
+    print("case: tiny Qwen3.5, 141 packed rows (chunks of 100 and 40 plus a decode row): the "
+          "many-rows matvec form", flush=True)
+    cfg, t = synth35.in_memory(tiny(), seed=12)
+    p = Pair(cfg, t, max_lanes=4, max_rows=160, max_context=160)
+    a, b, c = p.alloc(), p.alloc(), p.alloc()
+    rng = np.random.default_rng(13)
+    pa = [int(v) for v in rng.integers(0, cfg["vocabulary"], 100)]
+    pb = [int(v) for v in rng.integers(0, cfg["vocabulary"], 40)]
+    (tc,) = p.step([(c, [5, 6])])
+    ta, tb, tc = p.step([(a, pa), (b, pb), (c, [tc])])
+    p.step([(a, [ta]), (b, [tb]), (c, [tc])])
+    for s_ in (a, b, c):
+        p.check_state(s_)
+
+
+def test_full_shape_large_packed_step_bit_exact():
+    print("case: Qwen3.5-0.8B shape, one step of 96 + 1 packed rows (many-rows matvec form)",
+          flush=True)
+    cfg, t = synth35.in_memory(synth35.config(), seed=14)
+    p = Pair(cfg, t, threads=16, max_lanes=2, max_rows=128, max_context=128)
+    a, b = p.alloc(), p.alloc()
+    rng = np.random.default_rng(15)
+    pa = [int(v) for v in rng.integers(0, cfg["vocabulary"], 96)]
+    (tb,) = p.step([(b, [11])])
+    p.step([(a, pa), (b, [tb])])
+    p.check_state(a)
+    p.check_state(b)
+
+
 def test_tiny_prompt_chunks_without_head():
     print("case: tiny Qwen3.5, prompt chunks that skip the head, then the last chunk with it",
           flush=True)
