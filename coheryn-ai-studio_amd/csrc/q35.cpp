@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <set>
 #include <string>
@@ -84,6 +85,7 @@ struct Q35Model {
   uint32_t *row_err = nullptr, *tables = nullptr;
   uint32_t *h_tables = nullptr, *h_row_err = nullptr;
   unsigned long long *h_argmax = nullptr;
+  bool split_linear = false;  // COHX_Q35_SPLIT_LINEAR=1: the four-kernel mixer (tests)
   std::set<std::string> uploaded;
   size_t expected = 0;
   uint64_t matrix_bytes = 0;
@@ -213,6 +215,7 @@ int cohx_create_qwen35(const cohx_qwen35_desc *dd, int device, cohx_ctx **out) {
   q->head_rows = pad16(q->V);
   q->max_rows = (int)d.max_rows;
   q->max_lanes = (int)d.max_lanes;
+  if (const char *e = std::getenv("COHX_Q35_SPLIT_LINEAR")) q->split_linear = std::atoi(e) != 0;
   int rc = 0;
   const hipError_t e0 = hipSetDevice(device);
   if (e0 == hipSuccess) {
@@ -538,6 +541,8 @@ int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
   out->kv_bytes = 0;
   if (included.empty()) return COHX_OK;
   const int NL = (int)included.size();
+  uint32_t max_lane_tokens = 0;
+  for (int k = 0; k < NL; k++) max_lane_tokens = std::max(max_lane_tokens, lane_n[k]);
   Q35_TRY(hipSetDevice(ctx->device));
   hipStream_t s = ctx->stream;
   uint32_t *dt = q->tables;
@@ -555,12 +560,24 @@ int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
     if (!Ly.full) {
       q35_matvec(s, kQ35Store, Ly.mix, q->lin_rows, q->lin_rows, H, q->nrm, H, (int)R, q->mix_out,
                  q->ld_mix, nullptr, q->row_err, nullptr);
-      q35_conv(s, NL, L, q->mix_out, q->ld_mix, Ly.conv, q->C, q->K,
-               q->conv_state + (size_t)Ly.slot * q->C * q->K, q->conv_seq, q->cv, q->C, q->row_err);
-      q35_delta(s, (int)R, NL, L, q->cv, q->C, q->keys, q->mix_out, q->ld_mix, q->lin_z, q->lin_a,
-                q->lin_b, Ly.a_log, Ly.dt, Ly.norm, q->KH, q->VH, q->KD, q->VD, eps,
-                q->delta_state + (size_t)Ly.slot * q->VH * q->KD * q->VD, q->delta_seq, q->gates,
-                q->att, q->tgt, q->ld_att, q->row_err);
+      // one launch for the mixer when every lane is a decode row or a short
+      // chunk; long prompt chunks gain from forming conv and gates for all
+      // rows in parallel
+      if (q35_linear_fused(q->K, q->KH, q->VH) && !q->split_linear && max_lane_tokens <= 4) {
+        q35_linear(s, NL, L, q->mix_out, q->ld_mix, q->keys, q->lin_z, q->lin_a, q->lin_b, Ly.conv,
+                   q->K, q->conv_state + (size_t)Ly.slot * q->C * q->K, q->conv_seq, Ly.a_log,
+                   Ly.dt, Ly.norm, q->KH, q->VH, q->KD, q->VD, eps,
+                   q->delta_state + (size_t)Ly.slot * q->VH * q->KD * q->VD, q->delta_seq, q->tgt,
+                   q->ld_att, q->row_err);
+      } else {
+        q35_conv(s, NL, L, q->mix_out, q->ld_mix, Ly.conv, q->C, q->K,
+                 q->conv_state + (size_t)Ly.slot * q->C * q->K, q->conv_seq, q->cv, q->C,
+                 q->row_err);
+        q35_delta(s, (int)R, NL, L, q->cv, q->C, q->keys, q->mix_out, q->ld_mix, q->lin_z,
+                  q->lin_a, q->lin_b, Ly.a_log, Ly.dt, Ly.norm, q->KH, q->VH, q->KD, q->VD, eps,
+                  q->delta_state + (size_t)Ly.slot * q->VH * q->KD * q->VD, q->delta_seq,
+                  q->gates, q->att, q->tgt, q->ld_att, q->row_err);
+      }
       q35_matvec(s, kQ35Residual, Ly.out, q->h_rows, H, q->vals, q->tgt, q->ld_att, (int)R, q->x, H,
                  nullptr, q->row_err, nullptr);
     } else {

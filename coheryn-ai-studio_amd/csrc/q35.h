@@ -58,6 +58,16 @@ void q35_swiglu(hipStream_t s, int rows, const float *gu, int ldgu, int F, int u
 void q35_conv(hipStream_t s, int lanes, Q35Lanes L, const float *mix, int ldm, const float *w,
               int C, int K, float *hist, size_t hist_seq, float *out, int ldo, uint32_t *row_err);
 bool q35_delta_supported(int key_dim, int value_dim);
+// The whole linear-attention mixer (conv, gates, delta rule, output norm x
+// SiLU(z)) in one launch per (lane, value head), for conv kernels of at most
+// four taps and one key head per value head; hist is the layer's conv ring
+// (per-sequence stride hist_seq).
+bool q35_linear_fused(int conv_kernel, int key_heads, int value_heads);
+void q35_linear(hipStream_t s, int lanes, Q35Lanes L, const float *mix, int ldm, int keys,
+                int z_off, int a_off, int b_off, const float *conv_w, int K, float *hist,
+                size_t hist_seq, const float *a_log, const float *dt, const float *norm_w,
+                int key_heads, int value_heads, int key_dim, int value_dim, float eps,
+                float *state, size_t state_seq, float *tgt, int ldt, uint32_t *row_err);
 // Gates, the recurrence over each lane's tokens, then the per-head output
 // norm times SiLU(z) into tgt (gates: [rows][value_heads], o_raw like tgt).
 void q35_delta(hipStream_t s, int rows, int lanes, Q35Lanes L, const float *conv, int ldc, int keys,

@@ -10,6 +10,8 @@
 // causal-conv ring and the delta-rule memory of the linear layers.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "device.h"
 #include "log1pf.h"
 #include "q35.h"
@@ -628,6 +630,207 @@ __global__ __launch_bounds__(256) void k_q35_delta(Q35Lanes L, const float *__re
   }
 }
 
+// ---------------------------------------------------------------------------
+// The whole linear-attention mixer of one (lane, value head) in one
+// workgroup, token after token (execution.rs:357-411): the causal conv of the
+// head's q, k (its key head's channels) and v channels, the q/k norms and
+// gates, the delta-rule column updates, and the output norm times SiLU(z).
+// Thread j owns q/k channel j of the key head (j < kKD), v channel and state
+// column j of the value head (j < VD).  The arithmetic of each stage is the
+// one the separate kernels above restate; only the launches are merged.
+// Used when every value head has its own key head: a workgroup then owns all
+// the conv channels it reads and writes back (with shared key heads the ring
+// would be read by one workgroup after another had advanced it).  Conv
+// kernels up to kFusedConv taps.
+// ---------------------------------------------------------------------------
+constexpr int kFusedConv = 4;
+struct ConvTaps {
+  float tap[kFusedConv], w[kFusedConv];
+};
+__device__ __forceinline__ void conv_load(ConvTaps &c, const float *h, const float *w, int K,
+                                          int c0) {
+#pragma unroll
+  for (int i = 0; i < kFusedConv; i++) {
+    c.tap[i] = i < K ? h[(c0 + i) % K] : 0.0f;
+    c.w[i] = i < K ? w[i] : 0.0f;
+  }
+}
+__device__ __forceinline__ float conv_step(ConvTaps &c, float in, int K) {
+#pragma unroll
+  for (int i = 0; i < kFusedConv - 1; i++)
+    if (i < K - 1) c.tap[i] = c.tap[i + 1];
+#pragma unroll
+  for (int i = 0; i < kFusedConv; i++)
+    if (i == K - 1) c.tap[i] = in;
+  double sum = -0.0;
+#pragma unroll
+  for (int i = 0; i < kFusedConv; i++)
+    if (i < K) sum += (double)(c.tap[i] * c.w[i]);
+  return silu_f32((float)sum);
+}
+__device__ __forceinline__ void conv_store(const ConvTaps &c, float *h, int K, int c1) {
+#pragma unroll
+  for (int i = 0; i < kFusedConv; i++)
+    if (i < K) h[(c1 + i) % K] = c.tap[i];
+}
+
+template <int kKD>
+__global__ __launch_bounds__(256) void k_q35_linear(
+    Q35Lanes L, const float *__restrict__ mix, int ldm, int keys, int z_off, int a_off, int b_off,
+    const float *__restrict__ conv_w, int K, float *hist, size_t hist_seq,
+    const float *__restrict__ a_log, const float *__restrict__ dt,
+    const float *__restrict__ norm_w, int KH, int VH, int VD, float eps, float *state,
+    size_t state_seq, float *__restrict__ tgt, int ldt, uint32_t *row_err) {
+  __shared__ float qv[kKD], kv[kKD], s_qq[kKD], s_kk[kKD];
+  __shared__ double qsq[kKD], ksq[kKD], osq[256];
+  __shared__ float s_qn, s_kn, s_scale;
+  __shared__ float4 s_gate;
+  __shared__ int s_bad;
+  const int ln = blockIdx.x, h = blockIdx.y, j = threadIdx.x;
+  const int rep = VH / KH, src = (h / rep) * kKD;
+  const uint32_t first = L.first[ln], n = L.n[ln], start = L.start[ln];
+  const uint32_t seq = L.seq[ln];
+  const bool has_qk = j < kKD, has_v = j < VD;
+  float *hs = hist + (size_t)seq * hist_seq;
+  const int c0 = (int)(start % (uint32_t)K);
+  const int qc = src + j, kc = keys + src + j, vc = 2 * keys + h * VD + j;
+  ConvTaps cq, ck, cv;
+  if (has_qk) {
+    conv_load(cq, hs + (size_t)qc * K, conv_w + (size_t)qc * K, K, c0);
+    conv_load(ck, hs + (size_t)kc * K, conv_w + (size_t)kc * K, K, c0);
+  }
+  if (has_v) conv_load(cv, hs + (size_t)vc * K, conv_w + (size_t)vc * K, K, c0);
+  float *S = state + (size_t)seq * state_seq + (size_t)h * kKD * VD;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(S, (short)0, (int)(kKD * VD * 4), 0x00020000);
+  const int voff = has_v ? j * 4 : 0;
+  float col[kKD];
+#pragma unroll
+  for (int i = 0; i < kKD; i++)
+    col[i] = has_v ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff, i * VD * 4, 0))
+                   : 0.0f;
+  const int T = blockDim.x;
+  const float nw = has_v ? norm_w[j] : 0.0f;
+  for (uint32_t t = 0; t < n; t++) {
+    const uint32_t row = first + t;
+    const float *mr = mix + (size_t)row * ldm;
+    bool bad = false;
+    // causal conv + SiLU (kernels.rs:54-120)
+    if (has_qk) {
+      const float iq = mr[qc], ik = mr[kc];
+      const float q = conv_step(cq, iq, K), k = conv_step(ck, ik, K);
+      qv[j] = q;
+      kv[j] = k;
+      qsq[j] = (double)(q * q);
+      ksq[j] = (double)(k * k);
+      bad |= !finitef(iq) || !finitef(ik) || !finitef(q) || !finitef(k);
+    }
+    float v = 0.0f;
+    if (has_v) {
+      const float iv = mr[vc];
+      v = conv_step(cv, iv, K);
+      bad |= !finitef(iv) || !finitef(v);
+    }
+    __syncthreads();
+    // q/k norms: ordered f64 sums of the f32 squares, in two waves when there are two
+    if (j == 0) s_qn = (float)ordered_sum_f64(qsq, kKD, -0.0);
+    if (j == (T > kWave ? kWave : 0)) s_kn = (float)ordered_sum_f64(ksq, kKD, -0.0);
+    __syncthreads();
+    if (j == 0) {
+      const float qn = s_qn, kn = s_kn;
+      const float ld = -exp_f32(a_log[h]) * softplus_f32(mr[a_off + h] + dt[h]);
+      const float beta = sigmoid_f32(mr[b_off + h]);
+      s_gate = make_float4((1.0f / sqrtf(qn + 1e-6f)) / sqrtf((float)kKD), 1.0f / sqrtf(kn + 1e-6f),
+                           exp_f32(ld), beta);
+      s_bad = !finitef(qn) || !finitef(kn) || !finitef(ld) || !finitef(beta) || ld > 0.0f ||
+              !(beta >= 0.0f && beta <= 1.0f);
+    }
+    __syncthreads();
+    const float4 gt = s_gate;
+    if (has_qk) {
+      s_qq[j] = qv[j] * gt.x;
+      s_kk[j] = kv[j] * gt.y;
+    }
+    __syncthreads();
+    // the delta rule on state column j (kernels.rs:122-214)
+    float o = 0.0f;
+    if (has_v) {
+      const float decay = gt.z, beta = gt.w;
+      double pred = 0.0;
+#pragma unroll
+      for (int i0 = 0; i0 < kKD; i0 += 4) {
+        asm volatile("" ::: "memory");
+        float p[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          col[i0 + e] *= decay;
+          p[e] = col[i0 + e] * s_kk[i0 + e];
+        }
+        pin_vgprs(p);
+        double wd[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) wd[e] = (double)p[e];
+        pin_vgprs(wd);
+#pragma unroll
+        for (int e = 0; e < 4; e++) pred += wd[e];
+      }
+      const float corr = (v - (float)pred) * beta;
+      double rd = 0.0;
+#pragma unroll
+      for (int i0 = 0; i0 < kKD; i0 += 4) {
+        asm volatile("" ::: "memory");
+        float p[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          col[i0 + e] += s_kk[i0 + e] * corr;
+          p[e] = col[i0 + e] * s_qq[i0 + e];
+        }
+        pin_vgprs(p);
+        double wd[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) wd[e] = (double)p[e];
+        pin_vgprs(wd);
+#pragma unroll
+        for (int e = 0; e < 4; e++) rd += wd[e];
+      }
+      o = (float)rd;
+      bad |= !finitef(o);
+#pragma unroll
+      for (int i = 0; i < kKD; i++) bad |= !finitef(col[i]);
+      osq[j] = (double)(o * o);
+    }
+    __syncthreads();
+    // output norm over the head (zero_centered false) times SiLU(z) (execution.rs:397-411)
+    if (j == 0) {
+      const double sum = ordered_sum_f64(osq, VD, -0.0);
+      const double mean = sum / (double)VD;
+      s_bad |= !(__builtin_isfinite(mean) && finitef((float)mean));
+      s_scale = 1.0f / sqrtf((float)mean + eps);
+    }
+    __syncthreads();
+    if (has_v) {
+      const float z = mr[z_off + h * VD + j];
+      const float y = ((o * s_scale) * (nw + 0.0f)) * silu_f32(z);
+      tgt[(size_t)row * ldt + h * VD + j] = y;
+      bad |= !finitef(y);
+    }
+    if (bad || (j == 0 && s_bad)) atomicOr(&row_err[row], kErrRequest);
+    __syncthreads();  // the LDS stages are rewritten by the next token
+  }
+  const int c1 = (int)((start + n) % (uint32_t)K);
+  if (has_qk) {
+    conv_store(cq, hs + (size_t)qc * K, K, c1);
+    conv_store(ck, hs + (size_t)kc * K, K, c1);
+  }
+  if (has_v) {
+    conv_store(cv, hs + (size_t)vc * K, K, c1);
+#pragma unroll
+    for (int i = 0; i < kKD; i++)
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, col[i]), rs, voff,
+                                            i * VD * 4, 0);
+  }
+}
+
 // Per value head: the output norm (zero_centered false) times SiLU(z)
 // (execution.rs:397-411).
 __global__ __launch_bounds__(256) void k_q35_headnorm(const float *__restrict__ o_in, int ldo,
@@ -937,6 +1140,30 @@ void q35_conv(hipStream_t s, int lanes, Q35Lanes L, const float *mix, int ldm, c
               int C, int K, float *hist, size_t hist_seq, float *out, int ldo, uint32_t *row_err) {
   hipLaunchKernelGGL(k_q35_conv, dim3(lanes, (C + 255) / 256), dim3(256), 0, s, L, mix, ldm, w, C,
                      K, hist, hist_seq, out, ldo, row_err);
+}
+
+bool q35_linear_fused(int conv_kernel, int key_heads, int value_heads) {
+  return conv_kernel <= kFusedConv && key_heads == value_heads;
+}
+
+void q35_linear(hipStream_t s, int lanes, Q35Lanes L, const float *mix, int ldm, int keys,
+                int z_off, int a_off, int b_off, const float *conv_w, int K, float *hist,
+                size_t hist_seq, const float *a_log, const float *dt, const float *norm_w,
+                int key_heads, int value_heads, int key_dim, int value_dim, float eps,
+                float *state, size_t state_seq, float *tgt, int ldt, uint32_t *row_err) {
+  const dim3 grid(lanes, value_heads);
+  const dim3 block(((std::max(key_dim, value_dim) + kWave - 1) / kWave) * kWave);
+#define LIN_(KD)                                                                               \
+  case KD:                                                                                     \
+    hipLaunchKernelGGL(k_q35_linear<KD>, grid, block, 0, s, L, mix, ldm, keys, z_off, a_off,  \
+                       b_off, conv_w, K, hist, hist_seq, a_log, dt, norm_w, key_heads,           \
+                       value_heads, value_dim, eps, state, state_seq, tgt, ldt, row_err);      \
+    break;
+  switch (key_dim) {
+    LIN_(16) LIN_(32) LIN_(64) LIN_(128)
+    default: break;
+  }
+#undef LIN_
 }
 
 bool q35_delta_supported(int key_dim, int value_dim) {

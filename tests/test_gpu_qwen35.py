@@ -3,6 +3,8 @@ bit for bit: logits of every lane's last row, greedy ids, and the recurrent
 state (K/V rows, causal-conv ring, delta-rule memory) after each step.  A lane
 may carry a prompt chunk of several tokens; the oracle steps the same tokens
 one at a time (Graph::forward_batch, qwen35/execution.rs:257-608)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -14,9 +16,11 @@ pytestmark = pytest.mark.gpu
 
 
 def tiny(**kw):
-    return synth35.config(layers=4, hidden=64, intermediate=96, vocabulary=300, heads=2,
-                          kv_heads=1, head_dim=32, key_heads=2, value_heads=4, key_dim=16,
-                          value_dim=8, rotary_dim=16, context=256, **kw)
+    c = dict(layers=4, hidden=64, intermediate=96, vocabulary=300, heads=2, kv_heads=1,
+             head_dim=32, key_heads=2, value_heads=4, key_dim=16, value_dim=8, rotary_dim=16,
+             context=256)
+    c.update(kw)
+    return synth35.config(**c)
 
 
 class Pair:
@@ -132,6 +136,41 @@ def test_full_shape_large_packed_step_bit_exact():
     p.step([(a, pa), (b, [tb])])
     p.check_state(a)
     p.check_state(b)
+
+
+def test_tiny_fused_mixer_matches_oracle_and_split_kernels():
+    print("case: tiny Qwen3.5 with one key head per value head (the fused linear mixer) against "
+          "the oracle and against the four-kernel mixer", flush=True)
+    cfg, t = synth35.in_memory(tiny(key_heads=4, value_heads=4, key_dim=16, value_dim=16),
+                               seed=16)
+    p = Pair(cfg, t, max_lanes=4, max_rows=96, max_context=96)
+    a, b = p.alloc(), p.alloc()
+    rng = np.random.default_rng(17)
+    pa = [int(v) for v in rng.integers(0, cfg["vocabulary"], 70)]
+    ta, tb = p.step([(a, pa[:4]), (b, [1, 2, 3])])          # short chunks: fused
+    ta, tb = p.step([(a, pa[4:]), (b, [tb])])               # a long chunk: split
+    for _ in range(3):
+        ta, tb = p.step([(a, [ta]), (b, [tb])])              # decode: fused
+    p.check_state(a)
+    p.check_state(b)
+    old = os.environ.get("COHX_Q35_SPLIT_LINEAR")
+    os.environ["COHX_Q35_SPLIT_LINEAR"] = "1"
+    try:
+        split = cohx.Qwen35(cfg, t, max_lanes=4, max_rows=96, max_context=96)
+    finally:
+        if old is None:
+            del os.environ["COHX_Q35_SPLIT_LINEAR"]
+        else:
+            os.environ["COHX_Q35_SPLIT_LINEAR"] = old
+    sa, fused = split.seq_alloc(), p.gpu.seq_alloc()
+    for chunk in (pa[:3], pa[3:7], pa[7:8]):
+        r = split.step([dict(seq=sa, tokens=chunk, logits=True)])[0]
+        f = p.gpu.step([dict(seq=fused, tokens=chunk, logits=True)])[0]
+        assert np.array_equal(r["logits"].view(np.uint32), f["logits"].view(np.uint32))
+    for layer, full in enumerate(cfg["full"]):
+        for which in ((0, 1) if full else (2, 3)):
+            assert np.array_equal(split.read_state(sa, layer, which).view(np.uint32),
+                                  p.gpu.read_state(fused, layer, which).view(np.uint32))
 
 
 def test_tiny_prompt_chunks_without_head():
