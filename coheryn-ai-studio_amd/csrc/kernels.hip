@@ -264,14 +264,24 @@ __device__ __forceinline__ void argmax_commit(float best, int best_row, bool val
 // Block -> (tile, n-tile) mapping keeps all n-tiles of a weight tile on one
 // XCD (blockIdx % 8), so the tile is fetched into that XCD's L2 once.
 // ---------------------------------------------------------------------------
+// The scales of a block pair: kNM weight tiles x 2 blocks x 16 rows, then
+// 2 blocks x 16 batch rows, (kNM + 1) * 32 values spread over the wave's
+// lanes, one 16-bit load per lane per 64 values.  Slot s = v * 64 + lane:
+// s < kNM * 32 is weight tile s / 32, block 2p + (s % 32) / 16, row s % 16;
+// the next 32 are the batch tile's, block 2p + (s % 32) / 16, batch row s % 16.
 template <int kNM>
 struct Q8Regs {
+  static constexpr int kSV = (kNM + 2) / 2;  // scale values per lane
   uint4 a[kNM];
   uint4 b;
-  uint32_t dw[kNM];
-  uint32_t da;
+  uint16_t sc[kSV];
 };
 
+// Branch-free, so the compiler can count the loads in flight and wait only
+// for the ones it needs: the caller clamps `pair` to the last valid pair and
+// ignores what a clamped load returns.  Each scale stays in its own register
+// until phase 1 stores it: combining two right after the load would make the
+// wave wait for every load in flight (vmcnt counts in order).
 template <int kNM, int kFmt>
 __device__ __forceinline__ void q8_load(Q8Regs<kNM> &r, const MatrixView &w, const ActView &act,
                                         int unit, int nt, int pair, int lane) {
@@ -286,13 +296,13 @@ __device__ __forceinline__ void q8_load(Q8Regs<kNM> &r, const MatrixView &w, con
     }
   }
   r.b = *reinterpret_cast<const uint4 *>(act.qs + q8_byte(nt, nbp, pair * 2, lane, 0));
-  if (lane < 16) {
 #pragma unroll
-    for (int m = 0; m < kNM; m++)
-      r.dw[m] = (uint32_t)w.ds[q8_scale(unit * kNM + m, nbp, pair * 2, lane)] |
-                ((uint32_t)w.ds[q8_scale(unit * kNM + m, nbp, pair * 2 + 1, lane)] << 16);
-    r.da = (uint32_t)act.ds[q8_scale(nt, nbp, pair * 2, lane)] |
-           ((uint32_t)act.ds[q8_scale(nt, nbp, pair * 2 + 1, lane)] << 16);
+  for (int v = 0; v < Q8Regs<kNM>::kSV; v++) {
+    const int sl = v * 64 + lane;
+    const int blk = pair * 2 + (sl % 32) / 16, row = sl % 16;
+    const uint16_t *src = sl < kNM * 32 ? w.ds + q8_scale(unit * kNM + min(sl / 32, kNM - 1), nbp, blk, row)
+                                        : act.ds + q8_scale(nt, nbp, blk, row);
+    r.sc[v] = *src;
   }
 }
 
@@ -329,15 +339,13 @@ __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int r
   Q8Regs<kNM> cur[kP], nxt[kP];
 #pragma unroll
   for (int pp = 0; pp < kP; pp++)
-    if (pp * kW + wave < npairs) q8_load<kNM, kFmt>(cur[pp], w, act, unit, nt, pp * kW + wave, lane);
+    q8_load<kNM, kFmt>(cur[pp], w, act, unit, nt, min(pp * kW + wave, npairs - 1), lane);
   for (int c = 0; c < nchunks; c++) {
-    if (c + 1 < nchunks) {
+    // the last chunk prefetches a clamped (valid, unused) pair rather than branch
 #pragma unroll
-      for (int pp = 0; pp < kP; pp++) {
-        const int pair = (c + 1) * kW * kP + pp * kW + wave;
-        if (pair < npairs) q8_load<kNM, kFmt>(nxt[pp], w, act, unit, nt, pair, lane);
-      }
-    }
+    for (int pp = 0; pp < kP; pp++)
+      q8_load<kNM, kFmt>(nxt[pp], w, act, unit, nt, min((c + 1) * kW * kP + pp * kW + wave, npairs - 1),
+                         lane);
 #pragma unroll
     for (int pp = 0; pp < kP; pp++) {
       const int cp = pp * kW + wave;  // pair index within the chunk
@@ -359,14 +367,13 @@ __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int r
               s_isum[blk][m * 256 + i * 64 + lane] = (float)s4[i];
           }
         }
-        if (lane < 16) {
 #pragma unroll
-          for (int m = 0; m < kNM; m++) {
-            s_dw[2 * cp][m * 16 + lane] = h2f((uint16_t)(cur[pp].dw[m] & 0xffffu));
-            s_dw[2 * cp + 1][m * 16 + lane] = h2f((uint16_t)(cur[pp].dw[m] >> 16));
-          }
-          s_da[2 * cp][lane] = h2f((uint16_t)(cur[pp].da & 0xffffu));
-          s_da[2 * cp + 1][lane] = h2f((uint16_t)(cur[pp].da >> 16));
+        for (int v = 0; v < Q8Regs<kNM>::kSV; v++) {
+          const int sl = v * 64 + lane, blk = 2 * cp + (sl % 32) / 16;
+          if (sl < kNM * 32)
+            s_dw[blk][(sl / 32) * 16 + sl % 16] = h2f(cur[pp].sc[v]);
+          else if (sl < kNM * 32 + 32)
+            s_da[blk][sl % 16] = h2f(cur[pp].sc[v]);
         }
       }
     }
@@ -1229,9 +1236,11 @@ __global__ __launch_bounds__(256) void k_attn_exp(StepDims d, const uint32_t *__
 // fixed order (lane-strided, then butterfly), inv = f32(1/den), and the
 // block's 128 tokens of weights p = e * inv (cpu.rs:196-201) staged in LDS.
 // Then wave w takes pages 2w and 2w+1 of the block's 128 tokens (16 tokens
-// each), lane = element j: one base address per page, one V load per token,
-// acc[h] += f64(p_t[h] * v_t[j]) in token order; the 4 waves' sums are
-// combined in a fixed order into the chunk's f64 partial.
+// each), lane = element j: acc[h] += f64(p_t[h] * v_t[j]) in token order; the
+// 4 waves' sums are combined in a fixed order into the chunk's f64 partial.
+// Every global load the block needs (denominator partials, exponentials and
+// the wave's 32 V rows) is issued before the first wait, so the prologue and
+// the V stream share one memory latency.
 template <int kD, int kG>
 __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__restrict__ vpool,
                                                  const uint32_t *__restrict__ row_pos,
@@ -1242,6 +1251,7 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
                                                  double *__restrict__ partial) {
   constexpr int kE = (kD + kWave - 1) / kWave;  // elements per lane (lanes >= kD idle when kD < 64)
   static_assert(kChunk * 2 == 256, "one float4 of weights per thread");
+  static_assert(kG <= 8, "a wave sums the denominators of at most two heads");
   const int r = d.row_map ? (int)d.row_map[blockIdx.x] : (int)blockIdx.x;
   const int g = blockIdx.y, c = blockIdx.z;
   const int kv = (int)row_pos[r] + 1, t0 = c * kChunk;
@@ -1252,70 +1262,79 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int nch = (kv + 255) / 256, nsc = (d.kv_cap + 255) / 256;
-  for (int hh = wave; hh < kG; hh += 4) {
-    const double *dp = den_part + ((size_t)r * d.NH + g * kG + hh) * nsc;
-    double v = 0.0;
-    for (int i = lane; i < nch; i += kWave) v += dp[i];
-    v = wave_sum_f64(v);
-    if (lane == 0) s_inv[hh] = (float)(1.0 / v);
+  // (1) denominator partials of heads `wave` and `wave + 4`: the first 64
+  // chunks now, any further ones in the loop below
+  double dsum[2] = {0.0, 0.0};
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int hh = wave + 4 * i;
+    if (hh < kG && lane < nch) dsum[i] = den_part[((size_t)r * d.NH + g * kG + hh) * nsc + lane];
+  }
+  // (2) this thread's 4 exponentials
+  const int et = t0 + threadIdx.x / 2, ehalf = threadIdx.x % 2;
+  float4 e = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (et < kv)
+    e = reinterpret_cast<const float4 *>(escores + (((size_t)r * d.NKV + g) * d.kv_cap + et) * 8)[ehalf];
+  // (3) the wave's two pages of V, zero past the sequence's end.  Addresses
+  // are clamped into the last valid page so the loads need no branch.
+  const int32_t *ptr = pt + (size_t)row_seq[r] * d.max_pages;
+  float vr[2][kPage][kE];
+#pragma unroll
+  for (int pg = 0; pg < 2; pg++) {
+    const int tp = t0 + (wave * 2 + pg) * kPage;  // first token of the page
+    const int n = min(kPage, kv - tp);             // <= 0 when the page is past the end
+    const float *vbase = vpool + (size_t)(ptr[min(tp, kv - 1) / kPage] * d.NKV + g) * kPage * kD;
+#pragma unroll
+    for (int i = 0; i < kPage; i++)
+#pragma unroll
+      for (int el = 0; el < kE; el++) {
+        const int j = min(lane + el * kWave, kD - 1);
+        const float x = vbase[max(min(i, n - 1), 0) * kD + j];
+        vr[pg][i][el] = (i < n && lane + el * kWave < kD) ? x : 0.0f;
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int hh = wave + 4 * i;
+    if (hh < kG) {
+      const double *dp = den_part + ((size_t)r * d.NH + g * kG + hh) * nsc;
+      double v = dsum[i];
+      for (int j = lane + kWave; j < nch; j += kWave) v += dp[j];
+      v = wave_sum_f64(v);
+      if (lane == 0) s_inv[hh] = (float)(1.0 / v);
+    }
   }
   __syncthreads();
   {
-    const int t = t0 + threadIdx.x / 2, half = threadIdx.x % 2;
-    float4 e = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (t < kv) {
-      e = reinterpret_cast<const float4 *>(escores + (((size_t)r * d.NKV + g) * d.kv_cap + t) * 8)[half];
-      const int b = half * 4;
-      e.x = b + 0 < kG ? e.x * s_inv[b + 0] : 0.0f;
-      e.y = b + 1 < kG ? e.y * s_inv[b + 1] : 0.0f;
-      e.z = b + 2 < kG ? e.z * s_inv[b + 2] : 0.0f;
-      e.w = b + 3 < kG ? e.w * s_inv[b + 3] : 0.0f;
-    }
+    const int b = ehalf * 4;
+    e.x = b + 0 < kG ? e.x * s_inv[b + 0] : 0.0f;
+    e.y = b + 1 < kG ? e.y * s_inv[b + 1] : 0.0f;
+    e.z = b + 2 < kG ? e.z * s_inv[b + 2] : 0.0f;
+    e.w = b + 3 < kG ? e.w * s_inv[b + 3] : 0.0f;
     s_p[threadIdx.x] = e;
   }
   __syncthreads();
-  const int32_t *ptr = pt + (size_t)row_seq[r] * d.max_pages;
+  // Tokens past the end carry p = 0 and v = 0: their products are +-0, and
+  // adding +-0 leaves the accumulator unchanged (it starts at +0 and a sum
+  // that cancels rounds to +0, so it is never -0).  Both pages therefore run
+  // in full, without branches.
   const float *pl = reinterpret_cast<const float *>(s_p);
   double acc[kG][kE];
 #pragma unroll
   for (int hh = 0; hh < kG; hh++)
 #pragma unroll
-    for (int e = 0; e < kE; e++) acc[hh][e] = 0.0;
+    for (int el = 0; el < kE; el++) acc[hh][el] = 0.0;
 #pragma unroll
   for (int pg = 0; pg < 2; pg++) {
-    const int tp = t0 + (wave * 2 + pg) * kPage;  // first token of the page
-    if (tp >= kv) break;
-    const int n = min(kPage, kv - tp);
-    const float *vbase = vpool + (size_t)(ptr[tp / kPage] * d.NKV + g) * kPage * kD;
-    const float *pbase = pl + (tp - t0) * 8;
-    if (n == kPage) {
+    const float *pbase = pl + (wave * 2 + pg) * kPage * 8;
 #pragma unroll
-      for (int i = 0; i < kPage; i++) {
-        float v[kE];
+    for (int i = 0; i < kPage; i++)
 #pragma unroll
-        for (int e = 0; e < kE; e++)
-          v[e] = (lane + e * kWave < kD) ? vbase[i * kD + lane + e * kWave] : 0.0f;
+      for (int hh = 0; hh < kG; hh++) {
+        const float ph = pbase[i * 8 + hh];
 #pragma unroll
-        for (int hh = 0; hh < kG; hh++) {
-          const float ph = pbase[i * 8 + hh];
-#pragma unroll
-          for (int e = 0; e < kE; e++) acc[hh][e] += (double)(ph * v[e]);
-        }
+        for (int el = 0; el < kE; el++) acc[hh][el] += (double)(ph * vr[pg][i][el]);
       }
-    } else {
-      for (int i = 0; i < n; i++) {
-        float v[kE];
-#pragma unroll
-        for (int e = 0; e < kE; e++)
-          v[e] = (lane + e * kWave < kD) ? vbase[i * kD + lane + e * kWave] : 0.0f;
-#pragma unroll
-        for (int hh = 0; hh < kG; hh++) {
-          const float ph = pbase[i * 8 + hh];
-#pragma unroll
-          for (int e = 0; e < kE; e++) acc[hh][e] += (double)(ph * v[e]);
-        }
-      }
-    }
   }
   if (wave > 0) {
 #pragma unroll
