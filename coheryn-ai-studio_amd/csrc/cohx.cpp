@@ -631,8 +631,9 @@ int cohx_seq_read_kv(cohx_ctx *ctx, uint32_t seq, uint32_t layer, int values, fl
                       page.size() * sizeof(float), hipMemcpyDeviceToHost));
     for (int o = 0; o < kPage && i * kPage + o < q.length; o++)
       for (int g = 0; g < NKV; g++)
-        std::memcpy(out + ((i * kPage + o) * NKV + g) * D, page.data() + ((size_t)g * kPage + o) * D,
-                    D * sizeof(float));
+        for (int j = 0; j < D; j++)
+          out[((i * kPage + o) * NKV + g) * D + j] =
+              page[values ? v_at(0, g, NKV, o, j, D) : k_at(0, (uint32_t)i, g, NKV, o, j, D)];
   }
   return COHX_OK;
 }

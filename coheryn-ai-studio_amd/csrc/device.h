@@ -158,6 +158,34 @@ __device__ __forceinline__ float block_max_f32(float v, float *scratch) {
 // of v_mfma_i32_16x16x32_i8, two blocks per 16-byte lane load.
 // Block scales (binary16) sit at (t*nbp + b)*16 + row%16.
 // ---------------------------------------------------------------------------
+// KV pages.  A page holds kPage consecutive tokens of one sequence; per layer
+// the pool is [page][kv_head][...] with kPage * D floats per (page, head).
+// V rows are token-major: token o of the page, element j at o * D + j, so a
+// wave with lane = element reads one row per instruction.  K is stored
+// element-quad-major: [D/4][kPage][4], so with one thread per token the
+// float4 of elements 4q..4q+3 of a page's 16 tokens are 256 contiguous bytes,
+// and each wave-wide K load covers whole cache lines exactly once.  The quads
+// are rotated by the page's place in its sequence (lpage = position / kPage)
+// and the head: quad q at slot (q + lpage * NKV + head) % (D/4), so waves
+// that read quad q of different pages at the same time spread over all cache
+// channels instead of one 256-byte offset.  The rotation depends on the
+// logical page, not the physical one, so copying a page (copy-on-write) or
+// sharing it between sequences at the same positions keeps its meaning.
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ uint32_t k_rot(uint32_t lpage, int g, int NKV, int D) {
+  return (lpage * (uint32_t)NKV + (uint32_t)g) % (uint32_t)(D / 4);
+}
+__host__ __device__ __forceinline__ size_t k_at(size_t page, uint32_t lpage, int g, int NKV, int off, int j,
+                                                int D) {
+  const size_t slot = ((size_t)(j / 4) + k_rot(lpage, g, NKV, D)) % (size_t)(D / 4);
+  return (page * (size_t)NKV + (size_t)g) * (size_t)(kPage * D) + slot * (kPage * 4) + (size_t)off * 4 +
+         (size_t)(j % 4);
+}
+__host__ __device__ __forceinline__ size_t v_at(size_t page, int g, int NKV, int off, int j, int D) {
+  return ((page * (size_t)NKV + (size_t)g) * kPage + (size_t)off) * (size_t)D + (size_t)j;
+}
+
+// ---------------------------------------------------------------------------
 __host__ __device__ __forceinline__ size_t q8_byte(size_t tile, int nbp, int b, int lane, int j) {
   return ((tile * (size_t)(nbp / 2) + (size_t)(b / 2)) * 64 + (size_t)lane) * 16 +
          (size_t)(b % 2) * 8 + (size_t)j;

@@ -1053,13 +1053,12 @@ __global__ __launch_bounds__(256) void k_qkv_post(StepDims d, const float *__res
     const int g = p / half, i = p % half, e = d.H + g * d.D + i;
     const float a = src[e] + bias[e], b = src[e + half] + bias[e + half];
     const float2 cs = rp[i];
-    float *dst = kpool + ((size_t)(page * d.NKV + g) * kPage + off) * d.D;
-    dst[i] = fmaf(a, cs.x, -(b * cs.y));
-    dst[i + half] = fmaf(a, cs.y, b * cs.x);
+    kpool[k_at(page, pos / kPage, g, d.NKV, off, i, d.D)] = fmaf(a, cs.x, -(b * cs.y));
+    kpool[k_at(page, pos / kPage, g, d.NKV, off, i + half, d.D)] = fmaf(a, cs.y, b * cs.x);
   }
   for (int e = threadIdx.x; e < d.KVD; e += 256) {
     const int g = e / d.D, j = e % d.D, s = d.H + d.KVD + e;
-    vpool[((size_t)(page * d.NKV + g) * kPage + off) * d.D + j] = src[s] + bias[s];
+    vpool[v_at(page, g, d.NKV, off, j, d.D)] = src[s] + bias[s];
   }
 }
 
@@ -1105,10 +1104,11 @@ __global__ __launch_bounds__(256) void k_attn_scores(StepDims d, const float *__
   float4 k4[kD / 4];
   if (valid) {
     const int32_t phys = pt[(size_t)row_seq[r] * d.max_pages + t / kPage];
-    const float4 *krow = reinterpret_cast<const float4 *>(
-        kpool + ((size_t)(phys * d.NKV + g) * kPage + t % kPage) * kD);
+    const uint32_t rot = k_rot((uint32_t)t / kPage, g, d.NKV, kD);
+    const float *kq = kpool + (size_t)(phys * d.NKV + g) * (kPage * kD) + (t % kPage) * 4;
 #pragma unroll
-    for (int j = 0; j < kD / 4; j++) k4[j] = krow[j];
+    for (int j = 0; j < kD / 4; j++)
+      k4[j] = *reinterpret_cast<const float4 *>(kq + ((j + rot) % (kD / 4)) * (kPage * 4));
   } else {
 #pragma unroll
     for (int j = 0; j < kD / 4; j++) k4[j] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1456,10 +1456,9 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
         rv[u][e] = rk[u][e];
         const int t = t0 + 2 * (i / 16) + e;
         if (i < kItems && t < kv_end) {
-          const size_t at =
-              ((size_t)(ptr[t / kPage] * d.NKV + g) * kPage + t % kPage) * kD + 4 * (i % 16);
-          rk[u][e] = *reinterpret_cast<const float4 *>(kpool + at);
-          rv[u][e] = *reinterpret_cast<const float4 *>(vpool + at);
+          const int32_t phys = ptr[t / kPage];
+          rk[u][e] = *reinterpret_cast<const float4 *>(kpool + k_at(phys, t / kPage, g, d.NKV, t % kPage, 4 * (i % 16), kD));
+          rv[u][e] = *reinterpret_cast<const float4 *>(vpool + v_at(phys, g, d.NKV, t % kPage, 4 * (i % 16), kD));
         }
       }
     }
@@ -1643,10 +1642,9 @@ __global__ void k_fill_synthetic(float *kpool, float *vpool, size_t layer_stride
     const int pos = from + (int)(idx / ((size_t)NKV * D));
     const int e = (int)(idx % ((size_t)NKV * D));
     const int g = e / D, j = e % D;
-    const size_t at = (size_t)layer * layer_stride +
-                      ((size_t)(pages[pos / kPage] * NKV + g) * kPage + pos % kPage) * D + j;
-    kpool[at] = synthetic_kv(seed, stream, layer, 0, pos, e);
-    vpool[at] = synthetic_kv(seed, stream, layer, 1, pos, e);
+    const size_t base = (size_t)layer * layer_stride;
+    kpool[base + k_at(pages[pos / kPage], pos / kPage, g, NKV, pos % kPage, j, D)] = synthetic_kv(seed, stream, layer, 0, pos, e);
+    vpool[base + v_at(pages[pos / kPage], g, NKV, pos % kPage, j, D)] = synthetic_kv(seed, stream, layer, 1, pos, e);
   }
 }
 
