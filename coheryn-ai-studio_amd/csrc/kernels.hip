@@ -657,6 +657,145 @@ __global__ __launch_bounds__(64 * kChainWaves) void k_mv_q8c(MatrixView w, ActVi
   }
 }
 
+// ---------------------------------------------------------------------------
+// Short-K Q8_0/Q4_0 matvec with the weight unit in LDS.  A workgroup owns one
+// unit (kNM weight tiles of 16 rows; 2 = a gate tile and its up tile) and up
+// to 8 batch tiles, one per wave.  At the start every thread issues its share
+// of one cooperative copy into LDS (the unit's quantized tiles, their block
+// scales and the batch tiles' block scales), and each wave issues the loads
+// of its batch tile's whole B operand into registers, so the kernel waits on
+// memory once.  Then every wave walks the blocks in order, as the reference
+// chain does (quant.rs:265-292): per block one int8 MFMA gives the exact isum
+// of every (row, batch row) pair, then acc = fmaf((float)isum, dw*da, acc)
+// for Q8_0 (dw*da exact in f32, formed by v_fma_mix_f32 with a +0 addend) or
+// acc = fmaf((float)isum*dw, da, acc) for Q4_0.  K is limited to
+// 64 * kMaxPairs inputs (the B operand lives in registers).
+// ---------------------------------------------------------------------------
+template <int kEpi, int kNM, int kFmt, int kMaxPairs>
+__global__ __launch_bounds__(512) void k_mv_q8w(MatrixView w, ActView act, int rows_b, int n_tiles,
+                                                MatvecOut o) {
+  constexpr int kPairBytes = kFmt == 8 ? 1024 : 512;  // weight bytes per tile per block pair
+  constexpr int kCopy = 8;                            // 16-byte copy items per thread (<= 64 KB)
+  extern __shared__ uint4 smem[];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int nthreads = blockDim.x, unit = blockIdx.x;
+  const int tile0 = blockIdx.y * 8, nt = tile0 + wave;
+  const int nbt = min(8, n_tiles - tile0);
+  const int npairs = w.nbp / 2, nbp = w.nbp;
+  const int nw = kNM * npairs * kPairBytes / 16;  // copy items: weights, weight scales, batch scales
+  const int ns = kNM * nbp * 32 / 16;
+  const int nd = nbt * nbp * 32 / 16;
+  const uint4 *gw = reinterpret_cast<const uint4 *>(w.qs + (size_t)unit * kNM * npairs * kPairBytes);
+  const uint4 *gs = reinterpret_cast<const uint4 *>(w.ds + (size_t)unit * kNM * nbp * 16);
+  const uint4 *gd = reinterpret_cast<const uint4 *>(act.ds + (size_t)tile0 * nbp * 16);
+  const bool live = nt < n_tiles;
+  uint4 b[kMaxPairs];
+#pragma unroll
+  for (int p = 0; p < kMaxPairs; p++)
+    if (live && p < npairs) b[p] = *reinterpret_cast<const uint4 *>(act.qs + q8_byte(nt, nbp, 2 * p, lane, 0));
+  // one round covers 64 KB with 8 waves; fewer waves (few batch rows) take more
+  const int total = nw + ns + nd;
+  for (int base = 0; base < total; base += kCopy * nthreads) {
+    uint4 cp[kCopy];
+#pragma unroll
+    for (int k = 0; k < kCopy; k++) {  // past the end: reload the last item, not stored
+      const int i = min(base + (int)threadIdx.x + k * nthreads, total - 1);
+      const uint4 *src = i < nw ? gw + i : i < nw + ns ? gs + (i - nw) : gd + (i - nw - ns);
+      cp[k] = *src;
+    }
+#pragma unroll
+    for (int k = 0; k < kCopy; k++) {
+      const int i = base + (int)threadIdx.x + k * nthreads;
+      if (i < total) smem[i] = cp[k];
+    }
+  }
+  __syncthreads();
+  if (!live) return;
+  const uint8_t *sw = reinterpret_cast<const uint8_t *>(smem);
+  const uint16_t *ssc = reinterpret_cast<const uint16_t *>(smem + nw);  // [m][block][16 rows]
+  const uint16_t *sda = ssc + kNM * nbp * 16;                           // [wave][block][16 batch rows]
+  const int rsub = 4 * (lane / 16), col = lane % 16;
+  const v4i zero = {0, 0, 0, 0};
+  float acc[kNM][4];
+#pragma unroll
+  for (int m = 0; m < kNM; m++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[m][i] = 0.0f;
+#pragma unroll
+  for (int p = 0; p < kMaxPairs; p++) {
+    if (p < npairs) {
+      uint4 a[kNM];
+#pragma unroll
+      for (int m = 0; m < kNM; m++) {
+        if constexpr (kFmt == 8) {
+          a[m] = *reinterpret_cast<const uint4 *>(sw + (m * npairs + p) * kPairBytes + lane * 16);
+        } else {
+          const uint2 v = *reinterpret_cast<const uint2 *>(sw + (m * npairs + p) * kPairBytes + lane * 8);
+          a[m] = make_uint4(v.x, v.y, 0u, 0u);
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int blk = 2 * p + h;
+        const long bop = h ? hi64(b[p]) : lo64(b[p]);
+        const uint32_t da = sda[(wave * nbp + blk) * 16 + col];
+#pragma unroll
+        for (int m = 0; m < kNM; m++) {
+          long aop;
+          if constexpr (kFmt == 8)
+            aop = h ? hi64(a[m]) : lo64(a[m]);
+          else
+            aop = q4_operand(h ? a[m].y : a[m].x);
+          const v4i sum = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, zero, 0, 0, 0);
+          const uint2 s2 = *reinterpret_cast<const uint2 *>(ssc + (m * nbp + blk) * 16 + rsub);
+          if constexpr (kFmt == 8) {
+            const float sc[4] = {scale_mul<0, 0>(s2.x, da), scale_mul<1, 0>(s2.x, da), scale_mul<0, 0>(s2.y, da),
+                                 scale_mul<1, 0>(s2.y, da)};
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[m][i] = fmaf((float)sum[i], sc[i], acc[m][i]);
+          } else {
+            const float t[4] = {mul_half<0>((float)sum[0], s2.x), mul_half<1>((float)sum[1], s2.x),
+                                mul_half<0>((float)sum[2], s2.y), mul_half<1>((float)sum[3], s2.y)};
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[m][i] = fma_half(t[i], da, acc[m][i]);
+          }
+        }
+      }
+    }
+  }
+  // ---- epilogue: lane holds rows (unit*kNM + m)*16 + rsub + i of batch row nt*16 + col
+  const int r = nt * 16 + col;
+  const bool rvalid = r < rows_b;
+  const int er = (rvalid && o.err_rows) ? (int)o.err_rows[r] : r;
+  bool bad = false;
+  if (kEpi == kEpiSwiglu) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = unit * 16 + rsub + i;
+      if (!rvalid || row >= w.rows / 2) continue;
+      const float g = acc[0][i], u = acc[kNM - 1][i];
+      bad |= !finitef(g) || !finitef(u);
+      o.out[(size_t)r * o.ld + row] = (g / (1.0f + exp_f32(-g))) * u;
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < kNM; m++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int row = (unit * kNM + m) * 16 + rsub + i;
+        if (!rvalid || row >= w.rows) continue;
+        const float v = acc[m][i];
+        bad |= !finitef(v);
+        float *q = o.out + (size_t)r * o.ld + row;
+        if (kEpi == kEpiResidual)
+          *q = *q + v;
+        else
+          *q = v;
+      }
+  }
+  if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
+}
+
 // Final argmax over the per-tile partial keys of each batch row.
 __global__ __launch_bounds__(256) void k_argmax_reduce(const unsigned long long *__restrict__ part,
                                                        int units, unsigned long long *out) {
@@ -1710,7 +1849,16 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
                   const MatvecOut &o) {
   const int units = w.mtiles / kNM;
   const int n_tiles = (rows_b + 15) / 16;
-  if ((kEpi == kEpiArgmax || kEpi == kEpiSwiglu) && w.nbp <= 64) {
+  constexpr int kWPairs = 16;  // k_mv_q8w: K <= 1024
+  if (kEpi == kEpiSwiglu && w.nbp <= 2 * kWPairs) {
+    // gate+up at short K: the unit's weights in LDS, B operands in registers
+    const int by = (n_tiles + 7) / 8;
+    const int nthreads = 64 * (n_tiles < 8 ? n_tiles : 8);
+    const size_t lds = (size_t)kNM * (w.nbp / 2) * (kFmt == 8 ? 1024 : 512) + (size_t)kNM * w.nbp * 32 +
+                       (size_t)8 * w.nbp * 32;
+    launch_k((k_mv_q8w<kEpi, kNM, kFmt, kWPairs>), dim3(units, by), dim3(nthreads), lds, s, w, act, rows_b,
+             n_tiles, o);
+  } else if ((kEpi == kEpiArgmax || kEpi == kEpiSwiglu) && w.nbp <= 64) {
     // short K, many weight tiles (the LM head, gate+up): register chains,
     // 2 batch tiles per wave, 4 waves per workgroup
     constexpr int kNN = 2;
