@@ -1859,9 +1859,10 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
     launch_k((k_mv_q8w<kEpi, kNM, kFmt, kWPairs>), dim3(units, by), dim3(nthreads), lds, s, w, act, rows_b,
              n_tiles, o);
   } else if ((kEpi == kEpiArgmax || kEpi == kEpiSwiglu) && w.nbp <= 64) {
-    // short K, many weight tiles (the LM head, gate+up): register chains,
-    // 2 batch tiles per wave, 4 waves per workgroup
-    constexpr int kNN = 2;
+    // short K, many weight tiles (the LM head, gate+up beyond k_mv_q8w's K):
+    // register chains, 4 waves per workgroup; the head takes 4 batch tiles
+    // per wave (each weight pair loaded once feeds 8 MFMAs)
+    constexpr int kNN = kEpi == kEpiArgmax ? 4 : 2;
     const int groups = (n_tiles + kNN - 1) / kNN;
     const int waves = groups < kChainWaves ? groups : kChainWaves;
     launch_k((k_mv_q8c<kEpi, kNM, kNN, 4, kFmt>), dim3(units, (groups + kChainWaves - 1) / kChainWaves),
