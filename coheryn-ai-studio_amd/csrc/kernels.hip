@@ -174,15 +174,34 @@ __global__ __launch_bounds__(256) void k_norm_act(const float *__restrict__ x,
   const int ob = blockIdx.x;
   const int ib = in_rows ? (int)in_rows[ob] : ob;
   const float *xr = x + (size_t)ib * H;
+  // the thread's first kPer elements of x and of the weight are requested at
+  // once and held (H <= 1024 needs no more); the per-thread sum of squares
+  // runs in element order as before
+  constexpr int kPer = 4;
+  float xv[kPer], wv[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; i++) {
+    const int k = min((int)threadIdx.x + i * 256, H - 1);
+    xv[i] = xr[k];
+    wv[i] = w[k];
+  }
   double ss = -0.0;
-  for (int k = threadIdx.x; k < H; k += 256) {
+#pragma unroll
+  for (int i = 0; i < kPer; i++)
+    if ((int)threadIdx.x + i * 256 < H) ss += (double)(xv[i] * xv[i]);
+  for (int k = threadIdx.x + kPer * 256; k < H; k += 256) {
     const float v = xr[k];
     ss += (double)(v * v);
   }
   const double total = block_sum_f64<256>(ss, red);
   const float mean = (float)(total / (double)H);
   const float scale = 1.0f / sqrtf(mean + eps);
-  for (int k = threadIdx.x; k < H; k += 256) y[k] = xr[k] * scale * w[k];
+#pragma unroll
+  for (int i = 0; i < kPer; i++) {
+    const int k = (int)threadIdx.x + i * 256;
+    if (k < H) y[k] = xv[i] * scale * wv[i];
+  }
+  for (int k = threadIdx.x + kPer * 256; k < H; k += 256) y[k] = xr[k] * scale * w[k];
   __syncthreads();
   bool bad = false;
   if (kAct == 8) {
@@ -212,20 +231,30 @@ __global__ __launch_bounds__(256) void k_quant_act(const float *__restrict__ src
   const float *s = src + (size_t)r * K;
   bool bad = false;
   if (kAct == 8) {
-    for (int base = 0; base < nbp * 4; base += 256) {
-      const int kg = base + threadIdx.x;
-      const bool active = kg < nbp * 4;
-      float v[8];
-      if (active && kg * 8 + 8 <= K) {
-        const float4 a = reinterpret_cast<const float4 *>(s)[kg * 2];
-        const float4 c = reinterpret_cast<const float4 *>(s)[kg * 2 + 1];
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
-      } else {
+    // up to kIt rounds of 256 groups: every round's values are requested
+    // before the first is quantized
+    constexpr int kIt = 4;
+    for (int base0 = 0; base0 < nbp * 4; base0 += kIt * 256) {
+      float v[kIt][8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = (active && kg * 8 + i < K) ? s[kg * 8 + i] : 0.0f;
+      for (int it = 0; it < kIt; it++) {
+        const int kg = base0 + it * 256 + threadIdx.x;
+        const bool active = kg < nbp * 4;
+        if (active && kg * 8 + 8 <= K) {
+          const float4 a = reinterpret_cast<const float4 *>(s)[kg * 2];
+          const float4 c = reinterpret_cast<const float4 *>(s)[kg * 2 + 1];
+          v[it][0] = a.x; v[it][1] = a.y; v[it][2] = a.z; v[it][3] = a.w;
+          v[it][4] = c.x; v[it][5] = c.y; v[it][6] = c.z; v[it][7] = c.w;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; i++) v[it][i] = (active && kg * 8 + i < K) ? s[kg * 8 + i] : 0.0f;
+        }
       }
-      bad |= quant_group_q8(v, active, r, kg, nbp, act);
+#pragma unroll
+      for (int it = 0; it < kIt; it++) {
+        const int kg = base0 + it * 256 + threadIdx.x;
+        if (base0 + it * 256 < nbp * 4) bad |= quant_group_q8(v[it], kg < nbp * 4, r, kg, nbp, act);
+      }
     }
   } else {
     for (int k = threadIdx.x; k < K; k += 256) {
@@ -1179,12 +1208,27 @@ __global__ __launch_bounds__(256) void k_qkv_post(StepDims d, const float *__res
   const int half = d.D / 2, width = d.H + 2 * d.KVD;
   const float *src = qkv + (size_t)r * width;
   const float2 *rp = rope + (size_t)pos * half;
-  for (int p = threadIdx.x; p < d.NH * half; p += 256) {
-    const int h = p / half, i = p % half, e = h * d.D + i;
-    const float a = src[e] + bias[e], b = src[e + half] + bias[e + half];
-    const float2 cs = rp[i];
-    q_rot[(size_t)r * d.H + e] = fmaf(a, cs.x, -(b * cs.y));
-    q_rot[(size_t)r * d.H + e + half] = fmaf(a, cs.y, b * cs.x);
+  // query pairs: kQ per thread requested at once, then rotated and stored
+  constexpr int kQ = 2;
+  for (int p0 = 0; p0 < d.NH * half; p0 += kQ * 256) {
+    float qa[kQ], qb[kQ];
+    float2 qcs[kQ];
+#pragma unroll
+    for (int u = 0; u < kQ; u++) {
+      const int pc = min(p0 + u * 256 + (int)threadIdx.x, d.NH * half - 1);
+      const int e = (pc / half) * d.D + pc % half;
+      qa[u] = src[e] + bias[e];
+      qb[u] = src[e + half] + bias[e + half];
+      qcs[u] = rp[pc % half];
+    }
+#pragma unroll
+    for (int u = 0; u < kQ; u++) {
+      const int p = p0 + u * 256 + (int)threadIdx.x;
+      if (p >= d.NH * half) continue;
+      const int e = (p / half) * d.D + p % half;
+      q_rot[(size_t)r * d.H + e] = fmaf(qa[u], qcs[u].x, -(qb[u] * qcs[u].y));
+      q_rot[(size_t)r * d.H + e + half] = fmaf(qa[u], qcs[u].y, qb[u] * qcs[u].x);
+    }
   }
   if (slot < 0) return;
   const int page = slot / kPage, off = slot % kPage;
@@ -1732,8 +1776,17 @@ __global__ __launch_bounds__(128) void k_attn_combine(StepDims d,
   double acc = 0.0;
   const bool direct = d.row_skip && d.row_skip[r];
   if (active && !direct) {
-    acc = pp[j];
-    for (int c = 1; c < nch; c++) acc += pp[(size_t)c * d.D + j];
+    // chunk partials summed in chunk order; each batch of up to 16 is
+    // requested at once (clamped into range, past-the-end values unused)
+    constexpr int kB = 16;
+    for (int c0 = 0; c0 < nch; c0 += kB) {
+      double v[kB];
+#pragma unroll
+      for (int i = 0; i < kB; i++) v[i] = pp[(size_t)min(c0 + i, nch - 1) * d.D + j];
+#pragma unroll
+      for (int i = 0; i < kB; i++)
+        if (c0 + i < nch) acc = (c0 + i == 0) ? v[i] : acc + v[i];
+    }
   }
   const float o = direct ? (active ? d.direct[(size_t)r * d.H + h * d.D + j] : 0.0f) : (float)acc;
   bool bad = active && !finitef(o);
