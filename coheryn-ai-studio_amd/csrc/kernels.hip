@@ -231,33 +231,23 @@ __global__ __launch_bounds__(256) void k_quant_act(const float *__restrict__ src
   const float *s = src + (size_t)r * K;
   bool bad = false;
   if (kAct == 8) {
-    // up to kIt rounds of 256 groups: every round's values are requested
-    // before the first is quantized
-    constexpr int kIt = 4;
-    for (int base0 = 0; base0 < nbp * 4; base0 += kIt * 256) {
-      float v[kIt][8];
+    // block y takes groups [256 y, 256 y + 256) of the row: one group of 8
+    // values per thread, 64 whole 32-element blocks per workgroup
+    const int kg = blockIdx.y * 256 + threadIdx.x;
+    const bool active = kg < nbp * 4;
+    float v[8];
+    if (active && kg * 8 + 8 <= K) {
+      const float4 a = reinterpret_cast<const float4 *>(s)[kg * 2];
+      const float4 c = reinterpret_cast<const float4 *>(s)[kg * 2 + 1];
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+    } else {
 #pragma unroll
-      for (int it = 0; it < kIt; it++) {
-        const int kg = base0 + it * 256 + threadIdx.x;
-        const bool active = kg < nbp * 4;
-        if (active && kg * 8 + 8 <= K) {
-          const float4 a = reinterpret_cast<const float4 *>(s)[kg * 2];
-          const float4 c = reinterpret_cast<const float4 *>(s)[kg * 2 + 1];
-          v[it][0] = a.x; v[it][1] = a.y; v[it][2] = a.z; v[it][3] = a.w;
-          v[it][4] = c.x; v[it][5] = c.y; v[it][6] = c.z; v[it][7] = c.w;
-        } else {
-#pragma unroll
-          for (int i = 0; i < 8; i++) v[it][i] = (active && kg * 8 + i < K) ? s[kg * 8 + i] : 0.0f;
-        }
-      }
-#pragma unroll
-      for (int it = 0; it < kIt; it++) {
-        const int kg = base0 + it * 256 + threadIdx.x;
-        if (base0 + it * 256 < nbp * 4) bad |= quant_group_q8(v[it], kg < nbp * 4, r, kg, nbp, act);
-      }
+      for (int i = 0; i < 8; i++) v[i] = (active && kg * 8 + i < K) ? s[kg * 8 + i] : 0.0f;
     }
+    bad |= quant_group_q8(v, active, r, kg, nbp, act);
   } else {
-    for (int k = threadIdx.x; k < K; k += 256) {
+    for (int k = blockIdx.y * 256 + threadIdx.x; k < K; k += 256 * gridDim.y) {
       const uint16_t h = f2h(s[k]);
       bad |= !finitef(h2f(h));
       act.f16[(size_t)r * K + k] = h;
@@ -1891,10 +1881,11 @@ void launch_norm_act(hipStream_t s, int rows, const float *x, const uint32_t *in
 
 void launch_quant_act(hipStream_t s, int rows, const float *src, int K, int act_dtype, int nbp,
                       ActView act, uint32_t *row_err) {
+  const int splits = (nbp * 4 + 255) / 256;  // 256 groups of 8 values per workgroup
   if (act_dtype == 8)
-    launch_k(k_quant_act<8>, dim3(rows), dim3(256), 0, s, src, K, nbp, act, row_err);
+    launch_k(k_quant_act<8>, dim3(rows, splits), dim3(256), 0, s, src, K, nbp, act, row_err);
   else
-    launch_k(k_quant_act<1>, dim3(rows), dim3(256), 0, s, src, K, nbp, act, row_err);
+    launch_k(k_quant_act<1>, dim3(rows, splits), dim3(256), 0, s, src, K, nbp, act, row_err);
 }
 
 template <int kEpi, int kNM, int kFmt>
