@@ -1912,13 +1912,13 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
     launch_k((k_mv_q8c<kEpi, kNM, kNN, 4, kFmt>), dim3(units, (groups + kChainWaves - 1) / kChainWaves),
              dim3(64 * waves), 0, s, w, act, rows_b, n_tiles, o);
   } else {
-    // blocks per LDS chunk: 32 covers K <= 1024 in one chunk, 64 keeps long K to few chunks
+    // chunks of 16 blocks: 18 KB of LDS per workgroup, so several workgroups
+    // per CU overlap one's chain with another's loads (128-row down
+    // projection 13.3 -> 11.6 us against chunks of 64; qkv and o 0.2 us
+    // faster than one chunk of 32)
     const int groups = (units + 7) / 8;
-    if (kNM == 1 && w.nbp > 32)
-      launch_k((k_mv_q8s<kEpi, kNM, 4, kFmt>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
-               rows_b, n_tiles, o);
-    else if (kNM == 1)
-      launch_k((k_mv_q8s<kEpi, kNM, 2, kFmt>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
+    if (kNM == 1)
+      launch_k((k_mv_q8s<kEpi, kNM, 1, kFmt>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
                rows_b, n_tiles, o);
     else
       launch_k((k_mv_q8s<kEpi, kNM, 1, kFmt>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
