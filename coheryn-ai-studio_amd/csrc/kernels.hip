@@ -815,6 +815,147 @@ __global__ __launch_bounds__(512) void k_mv_q8w(MatrixView w, ActView act, int r
   if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
 }
 
+// ---------------------------------------------------------------------------
+// LM head (Q8_0/Q4_0, many weight tiles, short K) with per-tile argmax keys.
+// Persistent workgroups of up to 8 waves, wave w = batch tile w: each wave
+// loads its batch tile's B operand into registers once, and the workgroup
+// streams weight tiles unit = blockIdx.x, + gridDim.x, ... through two LDS
+// buffers (the next tile's copy is requested before the current one is
+// consumed; one barrier per tile), so a weight tile is read from memory once
+// per workgroup and the activations once per wave, instead of once per
+// (tile, wave).  The chain per (row, batch row) is the reference's
+// (quant.rs:265-292), as in k_mv_q8w.  K <= 64 * kMaxPairs, n_tiles <= 8.
+// ---------------------------------------------------------------------------
+template <int kFmt, int kMaxPairs>
+__global__ __launch_bounds__(512, 4) void k_mv_q8h(MatrixView w, ActView act, int rows_b, int n_tiles,
+                                                   MatvecOut o) {
+  constexpr int kPairBytes = kFmt == 8 ? 1024 : 512;
+  constexpr int kCopy = 4;  // 16-byte items per thread per tile copy (<= 32 KB: 512 threads)
+  static_assert(kCopy == 4, "the loop's copy registers are cp0..cp3");
+  extern __shared__ uint4 smem[];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, nthreads = blockDim.x;
+  const int units = w.mtiles, npairs = w.nbp / 2, nbp = w.nbp;
+  const int nw = npairs * kPairBytes / 16, ns = nbp * 32 / 16, nd = n_tiles * nbp * 32 / 16;
+  const int tile_items = nw + ns;  // one weight tile and its scales, in 16-byte items (<= 2048)
+  const uint16_t *sda = reinterpret_cast<const uint16_t *>(smem + 2 * tile_items);  // [tile][block][16]
+  const int nt = wave;
+  const bool live = nt < n_tiles;
+  uint4 b[kMaxPairs];
+#pragma unroll
+  for (int p = 0; p < kMaxPairs; p++)
+    if (live && p < npairs) b[p] = *reinterpret_cast<const uint4 *>(act.qs + q8_byte(nt, nbp, 2 * p, lane, 0));
+  // batch scales (once) and the first weight tile
+  const uint4 *gd = reinterpret_cast<const uint4 *>(act.ds);
+  for (int i = threadIdx.x; i < nd; i += nthreads) smem[2 * tile_items + i] = gd[i];
+  // tile item i: the tile's quantized pairs, then its block scales
+  const uint4 *gq = reinterpret_cast<const uint4 *>(w.qs);
+  const uint4 *gs = reinterpret_cast<const uint4 *>(w.ds);
+  int unit = blockIdx.x;
+  {
+    uint4 c0[kCopy];
+#pragma unroll
+    for (int k = 0; k < kCopy; k++) {
+      const int i = min((int)threadIdx.x + k * nthreads, tile_items - 1);
+      c0[k] = i < nw ? gq[(size_t)unit * nw + i] : gs[(size_t)unit * ns + (i - nw)];
+    }
+#pragma unroll
+    for (int k = 0; k < kCopy; k++)
+      if ((int)threadIdx.x + k * nthreads < tile_items) smem[threadIdx.x + k * nthreads] = c0[k];
+  }
+  __syncthreads();
+  const int rsub = 4 * (lane / 16), col = lane % 16;
+  const v4i zero = {0, 0, 0, 0};
+  const int r = nt * 16 + col;
+  const bool rvalid = live && r < rows_b;
+  const int er = (rvalid && o.err_rows) ? (int)o.err_rows[r] : r;
+  bool bad = false;
+  for (int it = 0; unit < units; it++, unit += gridDim.x) {
+    const int next = unit + gridDim.x;
+    // the next tile's share of this thread (kCopy == 4 items), requested now;
+    // the last tile refetches itself (never stored) rather than branch
+    const int nu = min(next, units - 1);
+    auto item = [&](int k) {
+      const int i = min((int)threadIdx.x + k * nthreads, tile_items - 1);
+      return i < nw ? gq[(size_t)nu * nw + i] : gs[(size_t)nu * ns + (i - nw)];
+    };
+    const uint4 cp0 = item(0), cp1 = item(1), cp2 = item(2), cp3 = item(3);
+    const uint4 *cur = smem + (it & 1) * tile_items;  // the two tile buffers alternate
+    const uint8_t *sw = reinterpret_cast<const uint8_t *>(cur);
+    const uint16_t *ssc = reinterpret_cast<const uint16_t *>(cur + nw);  // [block][16 rows]
+    if (live) {
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int p = 0; p < kMaxPairs; p++) {
+        if (p < npairs) {
+          uint4 a;
+          if constexpr (kFmt == 8) {
+            a = *reinterpret_cast<const uint4 *>(sw + p * kPairBytes + lane * 16);
+          } else {
+            const uint2 v = *reinterpret_cast<const uint2 *>(sw + p * kPairBytes + lane * 8);
+            a = make_uint4(v.x, v.y, 0u, 0u);
+          }
+#pragma unroll
+          for (int h = 0; h < 2; h++) {
+            const int blk = 2 * p + h;
+            long aop;
+            if constexpr (kFmt == 8)
+              aop = h ? hi64(a) : lo64(a);
+            else
+              aop = q4_operand(h ? a.y : a.x);
+            const v4i sum = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, h ? hi64(b[p]) : lo64(b[p]), zero, 0, 0, 0);
+            const uint32_t da = sda[(nt * nbp + blk) * 16 + col];
+            const uint2 s2 = *reinterpret_cast<const uint2 *>(ssc + blk * 16 + rsub);
+            if constexpr (kFmt == 8) {
+              const float sc[4] = {scale_mul<0, 0>(s2.x, da), scale_mul<1, 0>(s2.x, da),
+                                   scale_mul<0, 0>(s2.y, da), scale_mul<1, 0>(s2.y, da)};
+#pragma unroll
+              for (int i = 0; i < 4; i++) acc[i] = fmaf((float)sum[i], sc[i], acc[i]);
+            } else {
+              const float t[4] = {mul_half<0>((float)sum[0], s2.x), mul_half<1>((float)sum[1], s2.x),
+                                  mul_half<0>((float)sum[2], s2.y), mul_half<1>((float)sum[3], s2.y)};
+#pragma unroll
+              for (int i = 0; i < 4; i++) acc[i] = fma_half(t[i], da, acc[i]);
+            }
+          }
+        }
+      }
+      // per-tile argmax key of batch row r over the tile's rows (lowest row wins ties)
+      float best = 0.0f;
+      int best_row = 0;
+      bool have = false;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int row = unit * 16 + rsub + i;
+        if (!rvalid || row >= w.rows) continue;
+        const float v = acc[i];
+        bad |= !finitef(v);
+        if (o.logits) o.logits[(size_t)r * w.rows + row] = v;
+        if (!have || v > best) {
+          best = v;
+          best_row = row;
+          have = true;
+        }
+      }
+      unsigned long long key = have ? argmax_key(best, best_row) : 0ull;
+      unsigned long long x = __shfl_xor(key, 16, kWave);
+      key = x > key ? x : key;
+      x = __shfl_xor(key, 32, kWave);
+      key = x > key ? x : key;
+      if (lane < 16 && rvalid) o.argmax[(size_t)r * units + unit] = key;
+    }
+    if (next < units) {
+      uint4 *dst = smem + ((it + 1) & 1) * tile_items;
+      const int i0 = threadIdx.x;
+      if (i0 < tile_items) dst[i0] = cp0;
+      if (i0 + nthreads < tile_items) dst[i0 + nthreads] = cp1;
+      if (i0 + 2 * nthreads < tile_items) dst[i0 + 2 * nthreads] = cp2;
+      if (i0 + 3 * nthreads < tile_items) dst[i0 + 3 * nthreads] = cp3;
+    }
+    __syncthreads();
+  }
+  if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
+}
+
 // Final argmax over the per-tile partial keys of each batch row.
 __global__ __launch_bounds__(256) void k_argmax_reduce(const unsigned long long *__restrict__ part,
                                                        int units, unsigned long long *out) {
@@ -1902,6 +2043,18 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
                        (size_t)8 * w.nbp * 32;
     launch_k((k_mv_q8w<kEpi, kNM, kFmt, kWPairs>), dim3(units, by), dim3(nthreads), lds, s, w, act, rows_b,
              n_tiles, o);
+  } else if (kEpi == kEpiArgmax && kNM == 1 && n_tiles <= 8 && w.nbp <= 2 * kWPairs) {
+    // LM head: persistent workgroups streaming weight tiles through LDS, two
+    // per CU (4 waves per SIMD); always 8 waves, since the tile copy needs
+    // them all (waves past the last batch tile only copy)
+    const int nthreads = 512;
+    const int blocks = units < 512 ? units : 512;
+    const size_t tile = (size_t)(w.nbp / 2) * (kFmt == 8 ? 1024 : 512) + (size_t)w.nbp * 32;
+    const size_t lds = 2 * tile + (size_t)n_tiles * w.nbp * 32;
+    if (w.nbp <= 28)  // K <= 896: 14 register pairs of B operand
+      launch_k((k_mv_q8h<kFmt, 14>), dim3(blocks), dim3(nthreads), lds, s, w, act, rows_b, n_tiles, o);
+    else
+      launch_k((k_mv_q8h<kFmt, kWPairs>), dim3(blocks), dim3(nthreads), lds, s, w, act, rows_b, n_tiles, o);
   } else if ((kEpi == kEpiArgmax || kEpi == kEpiSwiglu) && w.nbp <= 64) {
     // short K, many weight tiles (the LM head, gate+up beyond k_mv_q8w's K):
     // register chains, 4 waves per workgroup; the head takes 4 batch tiles
