@@ -1186,20 +1186,24 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 constexpr int kGemmBM = 128, kGemmBK = 32, kGemmLds = 40;  // LDS row: 32 halves + 8 pad
 
-template <int kEpi>
+template <int kEpi, int kNB>
 __global__ __launch_bounds__(256) void k_gemm_f16(MatrixView w, const uint16_t *__restrict__ x,
                                                   int rows_b, MatvecOut o) {
-  // one LDS block: [weights buf 0 | weights buf 1 | rows buf 0 | rows buf 1];
-  // the SwiGLU exchange reuses it from the start after the K loop
-  constexpr int kTile = kGemmBM * kGemmLds;
-  __shared__ __align__(16) uint16_t s_mem[4 * kTile];
-  static_assert(sizeof(s_mem) >= 2 * 16 * 4 * 64 * sizeof(float), "LDS for the SwiGLU exchange");
+  // kNB MFMA row tiles per wave: a workgroup covers 32 * kNB rows (128 or 64;
+  // 64 doubles the workgroups of the narrow linears, whose 128-row grid
+  // leaves CUs idle).  One LDS block: [weights buf 0 | weights buf 1 | rows
+  // buf 0 | rows buf 1]; the SwiGLU exchange reuses it after the K loop.
+  constexpr int kBR = 32 * kNB;
+  constexpr int kTile = kGemmBM * kGemmLds, kTileX = kBR * kGemmLds;
+  constexpr int kXI = kBR * 4 / 256;  // 16-byte row items per thread per K step
+  __shared__ __align__(16) uint16_t s_mem[2 * kTile + 2 * kTileX];
+  static_assert(sizeof(s_mem) >= 2 * 4 * kNB * 4 * 64 * sizeof(float), "LDS for the SwiGLU exchange");
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int wf = wave / 2, wr = wave % 2;
   const int K = w.K, nk = K / kGemmBK;
   const int out_rows = kEpi == kEpiSwiglu ? w.rows / 2 : w.rows;
   const int f0 = blockIdx.x * (kEpi == kEpiSwiglu ? kGemmBM / 2 : kGemmBM);
-  const int r0 = blockIdx.y * kGemmBM;
+  const int r0 = blockIdx.y * kBR;
   // global -> LDS: each thread moves 2 x 16 bytes of each operand per K step
   int wrow[2], xrow[2], seg[2];
 #pragma unroll
@@ -1212,7 +1216,7 @@ __global__ __launch_bounds__(256) void k_gemm_f16(MatrixView w, const uint16_t *
     else
       f = f0 + row;
     wrow[i] = min(f, w.rows - 1);
-    xrow[i] = min(r0 + row, rows_b - 1);
+    xrow[i] = min(r0 + min(row, kBR - 1), rows_b - 1);
   }
   const uint16_t *wp0 = w.f16 + (size_t)wrow[0] * K + seg[0] * 8;
   const uint16_t *wp1 = w.f16 + (size_t)wrow[1] * K + seg[1] * 8;
@@ -1225,20 +1229,20 @@ __global__ __launch_bounds__(256) void k_gemm_f16(MatrixView w, const uint16_t *
     gw0 = *reinterpret_cast<const uint4 *>(wp0 + (size_t)(ks) * kGemmBK);      \
     gw1 = *reinterpret_cast<const uint4 *>(wp1 + (size_t)(ks) * kGemmBK);      \
     gx0 = *reinterpret_cast<const uint4 *>(xp0 + (size_t)(ks) * kGemmBK);      \
-    gx1 = *reinterpret_cast<const uint4 *>(xp1 + (size_t)(ks) * kGemmBK);      \
+    if (kXI > 1) gx1 = *reinterpret_cast<const uint4 *>(xp1 + (size_t)(ks) * kGemmBK); \
   } while (0)
 #define GEMM_STASH(buf)                                                        \
   do {                                                                         \
     *reinterpret_cast<uint4 *>(&s_mem[(buf) * kTile + so0]) = gw0;                          \
     *reinterpret_cast<uint4 *>(&s_mem[(buf) * kTile + so1]) = gw1;                          \
-    *reinterpret_cast<uint4 *>(&s_mem[(2 + (buf)) * kTile + so0]) = gx0;                          \
-    *reinterpret_cast<uint4 *>(&s_mem[(2 + (buf)) * kTile + so1]) = gx1;                          \
+    *reinterpret_cast<uint4 *>(&s_mem[2 * kTile + (buf) * kTileX + so0]) = gx0;                   \
+    if (kXI > 1) *reinterpret_cast<uint4 *>(&s_mem[2 * kTile + (buf) * kTileX + so1]) = gx1;      \
   } while (0)
-  float4v acc[4][4];
+  float4v acc[4][kNB];
 #pragma unroll
   for (int a = 0; a < 4; a++)
 #pragma unroll
-    for (int b = 0; b < 4; b++) acc[a][b] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < kNB; b++) acc[a][b] = float4v{0.f, 0.f, 0.f, 0.f};
   GEMM_FETCH(0);
   GEMM_STASH(0);
   __syncthreads();
@@ -1246,17 +1250,18 @@ __global__ __launch_bounds__(256) void k_gemm_f16(MatrixView w, const uint16_t *
   for (int ks = 0; ks < nk; ks++) {
     const int buf = ks & 1;
     if (ks + 1 < nk) GEMM_FETCH(ks + 1);
-    half8 af[4], bf[4];
+    half8 af[4], bf[kNB];
 #pragma unroll
     for (int a = 0; a < 4; a++)
       af[a] = *reinterpret_cast<const half8 *>(&s_mem[(buf) * kTile + (wf * 64 + a * 16 + lr) * kGemmLds + koff]);
 #pragma unroll
-    for (int b = 0; b < 4; b++)
-      bf[b] = *reinterpret_cast<const half8 *>(&s_mem[(2 + (buf)) * kTile + (wr * 64 + b * 16 + lr) * kGemmLds + koff]);
+    for (int b = 0; b < kNB; b++)
+      bf[b] = *reinterpret_cast<const half8 *>(
+          &s_mem[2 * kTile + (buf) * kTileX + (wr * 16 * kNB + b * 16 + lr) * kGemmLds + koff]);
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
-      for (int b = 0; b < 4; b++)
+      for (int b = 0; b < kNB; b++)
         acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bf[b], acc[a][b], 0, 0, 0);
     if (ks + 1 < nk) GEMM_STASH(buf ^ 1);
     __syncthreads();
@@ -1265,21 +1270,21 @@ __global__ __launch_bounds__(256) void k_gemm_f16(MatrixView w, const uint16_t *
 #undef GEMM_STASH
   // ---- epilogue: lane holds features (tile row) 4*(lane/16)+i of rows (tile col) lane%16
   if (kEpi == kEpiSwiglu) {
-    float *s_up = reinterpret_cast<float *>(s_mem);  // 2 x 16 x 4 x 64 floats = 32 KiB
+    float *s_up = reinterpret_cast<float *>(s_mem);  // 2 x 4 kNB x 4 x 64 floats
     if (wf == 1) {
 #pragma unroll
       for (int a = 0; a < 4; a++)
 #pragma unroll
-        for (int b = 0; b < 4; b++)
+        for (int b = 0; b < kNB; b++)
 #pragma unroll
-          for (int i = 0; i < 4; i++) s_up[((wr * 16 + a * 4 + b) * 4 + i) * 64 + lane] = acc[a][b][i];
+          for (int i = 0; i < 4; i++) s_up[((wr * 4 * kNB + a * kNB + b) * 4 + i) * 64 + lane] = acc[a][b][i];
     }
     __syncthreads();
     if (wf == 1) return;
   }
 #pragma unroll
-  for (int b = 0; b < 4; b++) {
-    const int r = r0 + wr * 64 + b * 16 + lr;
+  for (int b = 0; b < kNB; b++) {
+    const int r = r0 + wr * 16 * kNB + b * 16 + lr;
     if (r >= rows_b) continue;
     const int er = o.err_rows ? (int)o.err_rows[r] : r;
     bool bad = false;
@@ -1292,7 +1297,7 @@ __global__ __launch_bounds__(256) void k_gemm_f16(MatrixView w, const uint16_t *
         v[i] = acc[a][b][i];
         if (kEpi == kEpiSwiglu) {
           const float *s_up = reinterpret_cast<const float *>(s_mem);
-          const float g = v[i], u = s_up[((wr * 16 + a * 4 + b) * 4 + i) * 64 + lane];
+          const float g = v[i], u = s_up[((wr * 4 * kNB + a * kNB + b) * 4 + i) * 64 + lane];
           bad |= !finitef(g) || !finitef(u);
           v[i] = (g / (1.0f + exp_f32(-g))) * u;
         } else {
@@ -1324,7 +1329,8 @@ __global__ __launch_bounds__(256) void k_gemm_f16(MatrixView w, const uint16_t *
 // Bias add, NeoX RoPE from the host-built table (cos, sin of the engine's
 // iterative angle, cpu.rs:59-73), K/V append into the paged pool
 // (Kv::append, inference.rs:1019-1043; batch.rs:164-184).
-// Pool layout per layer: [page][kv_head][16][head_dim] f32.
+// Pool layout per layer: [page][kv_head][16 tokens x head_dim] f32, K rows
+// through k_at (element-quad-major, rotated), V rows through v_at.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_qkv_post(StepDims d, const float *__restrict__ qkv,
                                                   const float *__restrict__ bias,
@@ -2090,8 +2096,14 @@ static void mv_f16(hipStream_t s, const MatrixView &w, const ActView &act, int r
   if (kEpi != kEpiArgmax && g_prefill_mfma && rows_b >= kPrefillRows && w.K % kGemmBK == 0 &&
       (kEpi != kEpiSwiglu || out_rows % (kGemmBM / 2) == 0)) {
     const int ftile = kEpi == kEpiSwiglu ? kGemmBM / 2 : kGemmBM;
-    launch_k(k_gemm_f16<kEpi>, dim3((out_rows + ftile - 1) / ftile, (rows_b + kGemmBM - 1) / kGemmBM),
-             dim3(256), 0, s, w, (const uint16_t *)act.f16, rows_b, o);
+    const int fblocks = (out_rows + ftile - 1) / ftile;
+    // 128-row workgroups unless that leaves CUs idle; then 64-row ones
+    if (fblocks * ((rows_b + 127) / 128) >= 512)
+      launch_k(k_gemm_f16<kEpi, 4>, dim3(fblocks, (rows_b + 127) / 128), dim3(256), 0, s, w,
+               (const uint16_t *)act.f16, rows_b, o);
+    else
+      launch_k(k_gemm_f16<kEpi, 2>, dim3(fblocks, (rows_b + 63) / 64), dim3(256), 0, s, w,
+               (const uint16_t *)act.f16, rows_b, o);
     return;
   }
   if (rows_b >= 16 && w.K % 8 == 0) {  // lane = batch row, sequential f64 chains
