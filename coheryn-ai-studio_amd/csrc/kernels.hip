@@ -1182,92 +1182,106 @@ __global__ __launch_bounds__(256) void k_head_f16(MatrixView w, ActView act, int
 // workgroup's feature tile is 64 gate rows and the 64 matching up rows; the
 // up waves hand their sums to the gate waves through LDS.
 // ---------------------------------------------------------------------------
+// 16 bytes per lane straight from global memory into LDS: lane l's bytes
+// land at l * 16 past `lds` (the same for the whole wave).  Completion counts
+// in vmcnt.
+__device__ __forceinline__ void lds_load16(const void *global, void *lds) {
+  __builtin_amdgcn_global_load_lds(global, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+}
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
-constexpr int kGemmBM = 128, kGemmBK = 32, kGemmLds = 40;  // LDS row: 32 halves + 8 pad
+constexpr int kGemmBM = 128, kGemmBK = 32;
+// LDS ring depth of the 128-row and the 64-row workgroups
+constexpr int kGemmStages4 = 2, kGemmStages2 = 4;
 
-template <int kEpi, int kNB>
+template <int kEpi, int kNB, int kStages>
 __global__ __launch_bounds__(256) void k_gemm_f16(MatrixView w, const uint16_t *__restrict__ x,
                                                   int rows_b, MatvecOut o) {
   // kNB MFMA row tiles per wave: a workgroup covers 32 * kNB rows (128 or 64;
   // 64 doubles the workgroups of the narrow linears, whose 128-row grid
-  // leaves CUs idle).  One LDS block: [weights buf 0 | weights buf 1 | rows
-  // buf 0 | rows buf 1]; the SwiGLU exchange reuses it after the K loop.
+  // leaves CUs idle).  K steps of 32 go through a ring of kStages LDS stages
+  // filled by direct-to-LDS loads issued kStages - 1 steps ahead.  A stage
+  // holds 128 weight rows and the workgroup's 32 * kNB activation rows, 64
+  // bytes each, as 16-byte segments: segment s of row R sits at slot
+  // 4 R + (s ^ ((R >> 2) & 3)), so a wave's operand read (16 rows x 4
+  // segments) touches every bank once.  The SwiGLU exchange reuses the LDS
+  // after the K loop.
   constexpr int kBR = 32 * kNB;
-  constexpr int kTile = kGemmBM * kGemmLds, kTileX = kBR * kGemmLds;
-  constexpr int kXI = kBR * 4 / 256;  // 16-byte row items per thread per K step
-  __shared__ __align__(16) uint16_t s_mem[2 * kTile + 2 * kTileX];
-  static_assert(sizeof(s_mem) >= 2 * 4 * kNB * 4 * 64 * sizeof(float), "LDS for the SwiGLU exchange");
+  static_assert(kStages >= 2 && kStages <= 4, "LDS ring of 2 to 4 K steps");
+  constexpr int kWSlots = kGemmBM * 4, kXSlots = kBR * 4, kSlots = kWSlots + kXSlots;
+  constexpr int kPerStage = kSlots / 256;  // direct-to-LDS loads per wave per stage
+  extern __shared__ __align__(16) uint4 g_smem[];
+  uint16_t *s_mem = reinterpret_cast<uint16_t *>(g_smem);
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int wf = wave / 2, wr = wave % 2;
   const int K = w.K, nk = K / kGemmBK;
   const int out_rows = kEpi == kEpiSwiglu ? w.rows / 2 : w.rows;
   const int f0 = blockIdx.x * (kEpi == kEpiSwiglu ? kGemmBM / 2 : kGemmBM);
   const int r0 = blockIdx.y * kBR;
-  // global -> LDS: each thread moves 2 x 16 bytes of each operand per K step
-  int wrow[2], xrow[2], seg[2];
+  // this lane's source row and segment for each of its kPerStage loads
+  const uint16_t *src[kPerStage];
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    const int idx = tid + 256 * i, row = idx / 4;
-    seg[i] = idx % 4;
-    int f;
-    if (kEpi == kEpiSwiglu)
-      f = row < 64 ? f0 + row : out_rows + f0 + (row - 64);
-    else
-      f = f0 + row;
-    wrow[i] = min(f, w.rows - 1);
-    xrow[i] = min(r0 + min(row, kBR - 1), rows_b - 1);
+  for (int i = 0; i < kPerStage; i++) {
+    const int slot = (wave * kPerStage + i) * kWave + lane;
+    if (slot < kWSlots) {
+      const int row = slot >> 2, seg = (slot & 3) ^ ((row >> 2) & 3);
+      int f;
+      if (kEpi == kEpiSwiglu)
+        f = row < 64 ? f0 + row : out_rows + f0 + (row - 64);
+      else
+        f = f0 + row;
+      src[i] = w.f16 + (size_t)min(f, w.rows - 1) * K + seg * 8;
+    } else {
+      const int row = (slot - kWSlots) >> 2, seg = (slot & 3) ^ ((row >> 2) & 3);
+      src[i] = x + (size_t)min(r0 + row, rows_b - 1) * K + seg * 8;
+    }
   }
-  const uint16_t *wp0 = w.f16 + (size_t)wrow[0] * K + seg[0] * 8;
-  const uint16_t *wp1 = w.f16 + (size_t)wrow[1] * K + seg[1] * 8;
-  const uint16_t *xp0 = x + (size_t)xrow[0] * K + seg[0] * 8;
-  const uint16_t *xp1 = x + (size_t)xrow[1] * K + seg[1] * 8;
-  const int so0 = (tid / 4) * kGemmLds + seg[0] * 8, so1 = ((tid + 256) / 4) * kGemmLds + seg[1] * 8;
-  uint4 gw0, gw1, gx0, gx1;
-#define GEMM_FETCH(ks)                                                         \
-  do {                                                                         \
-    gw0 = *reinterpret_cast<const uint4 *>(wp0 + (size_t)(ks) * kGemmBK);      \
-    gw1 = *reinterpret_cast<const uint4 *>(wp1 + (size_t)(ks) * kGemmBK);      \
-    gx0 = *reinterpret_cast<const uint4 *>(xp0 + (size_t)(ks) * kGemmBK);      \
-    if (kXI > 1) gx1 = *reinterpret_cast<const uint4 *>(xp1 + (size_t)(ks) * kGemmBK); \
-  } while (0)
-#define GEMM_STASH(buf)                                                        \
-  do {                                                                         \
-    *reinterpret_cast<uint4 *>(&s_mem[(buf) * kTile + so0]) = gw0;                          \
-    *reinterpret_cast<uint4 *>(&s_mem[(buf) * kTile + so1]) = gw1;                          \
-    *reinterpret_cast<uint4 *>(&s_mem[2 * kTile + (buf) * kTileX + so0]) = gx0;                   \
-    if (kXI > 1) *reinterpret_cast<uint4 *>(&s_mem[2 * kTile + (buf) * kTileX + so1]) = gx1;      \
-  } while (0)
+  auto issue = [&](int ks) {  // K step ks (clamped to the last) into stage ks % kStages
+    const int kc = min(ks, nk - 1);
+    uint4 *stage = g_smem + (ks % kStages) * kSlots;
+#pragma unroll
+    for (int i = 0; i < kPerStage; i++)
+      lds_load16(src[i] + (size_t)kc * kGemmBK, stage + (wave * kPerStage + i) * kWave);
+  };
   float4v acc[4][kNB];
 #pragma unroll
   for (int a = 0; a < 4; a++)
 #pragma unroll
     for (int b = 0; b < kNB; b++) acc[a][b] = float4v{0.f, 0.f, 0.f, 0.f};
-  GEMM_FETCH(0);
-  GEMM_STASH(0);
-  __syncthreads();
-  const int koff = 8 * (lane / 16), lr = lane % 16;
+#pragma unroll
+  for (int st = 0; st < kStages - 1; st++) issue(st);
+  const int seg = lane / 16, lr = lane % 16;
   for (int ks = 0; ks < nk; ks++) {
-    const int buf = ks & 1;
-    if (ks + 1 < nk) GEMM_FETCH(ks + 1);
+    // this wave's loads of step ks are done once at most kStages - 2 later
+    // steps are in flight; the barrier makes every wave's visible and frees
+    // the stage read in step ks - 1 for step ks + kStages - 1
+    constexpr int kInFlight = (kStages - 2) * kPerStage;  // loads of later steps still allowed
+    static_assert(kInFlight < 16, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | kInFlight);  // vmcnt(kInFlight)
+    __builtin_amdgcn_s_barrier();
+    issue(ks + kStages - 1);
+    const uint4 *stage = g_smem + (ks % kStages) * kSlots;
     half8 af[4], bf[kNB];
 #pragma unroll
-    for (int a = 0; a < 4; a++)
-      af[a] = *reinterpret_cast<const half8 *>(&s_mem[(buf) * kTile + (wf * 64 + a * 16 + lr) * kGemmLds + koff]);
+    for (int a = 0; a < 4; a++) {
+      const int R = wf * 64 + a * 16 + lr;
+      af[a] = *reinterpret_cast<const half8 *>(stage + R * 4 + (seg ^ ((R >> 2) & 3)));
+    }
 #pragma unroll
-    for (int b = 0; b < kNB; b++)
-      bf[b] = *reinterpret_cast<const half8 *>(
-          &s_mem[2 * kTile + (buf) * kTileX + (wr * 16 * kNB + b * 16 + lr) * kGemmLds + koff]);
+    for (int b = 0; b < kNB; b++) {
+      const int R = wr * 16 * kNB + b * 16 + lr;
+      bf[b] = *reinterpret_cast<const half8 *>(stage + kWSlots + R * 4 + (seg ^ ((R >> 2) & 3)));
+    }
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
       for (int b = 0; b < kNB; b++)
         acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bf[b], acc[a][b], 0, 0, 0);
-    if (ks + 1 < nk) GEMM_STASH(buf ^ 1);
-    __syncthreads();
   }
-#undef GEMM_FETCH
-#undef GEMM_STASH
+  // every load (the clamped ones past the end included) lands before the
+  // LDS is reused
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
   // ---- epilogue: lane holds features (tile row) 4*(lane/16)+i of rows (tile col) lane%16
   if (kEpi == kEpiSwiglu) {
     float *s_up = reinterpret_cast<float *>(s_mem);  // 2 x 4 kNB x 4 x 64 floats
@@ -2098,12 +2112,13 @@ static void mv_f16(hipStream_t s, const MatrixView &w, const ActView &act, int r
     const int ftile = kEpi == kEpiSwiglu ? kGemmBM / 2 : kGemmBM;
     const int fblocks = (out_rows + ftile - 1) / ftile;
     // 128-row workgroups unless that leaves CUs idle; then 64-row ones
+    // LDS: kStages stages of (128 weight rows + the workgroup's rows) x 64 bytes
     if (fblocks * ((rows_b + 127) / 128) >= 512)
-      launch_k(k_gemm_f16<kEpi, 4>, dim3(fblocks, (rows_b + 127) / 128), dim3(256), 0, s, w,
-               (const uint16_t *)act.f16, rows_b, o);
+      launch_k(k_gemm_f16<kEpi, 4, kGemmStages4>, dim3(fblocks, (rows_b + 127) / 128), dim3(256),
+               kGemmStages4 * (128 + 128) * 64, s, w, (const uint16_t *)act.f16, rows_b, o);
     else
-      launch_k(k_gemm_f16<kEpi, 2>, dim3(fblocks, (rows_b + 63) / 64), dim3(256), 0, s, w,
-               (const uint16_t *)act.f16, rows_b, o);
+      launch_k(k_gemm_f16<kEpi, 2, kGemmStages2>, dim3(fblocks, (rows_b + 63) / 64), dim3(256),
+               kGemmStages2 * (128 + 64) * 64, s, w, (const uint16_t *)act.f16, rows_b, o);
     return;
   }
   if (rows_b >= 16 && w.K % 8 == 0) {  // lane = batch row, sequential f64 chains
