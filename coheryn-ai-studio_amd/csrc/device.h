@@ -42,7 +42,10 @@ __constant__ static const uint64_t kExp2Tab[32] = {
     0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
     0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
 
-__device__ __forceinline__ float exp_f32(float x) {
+// expf with the 2^(i/32) table read from `tab`: kExp2Tab itself, or a copy
+// a kernel has staged in LDS (a per-lane indexed constant load is a memory
+// round trip per call; an LDS read is not).
+__device__ __forceinline__ float exp_f32_tab(float x, const uint64_t *tab) {
   uint32_t ux = __float_as_uint(x);
   uint32_t abstop = (ux >> 20) & 0x7ffu;
   if (abstop >= 0x42bu) {  // |x| >= 88 or nan
@@ -59,13 +62,14 @@ __device__ __forceinline__ float exp_f32(float x) {
   uint64_t ki = (uint64_t)__double_as_longlong(kd);
   kd -= shift;
   double r = __fma_rn(inv_ln2_n, xd, -kd);
-  uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+  uint64_t t = tab[ki % 32] + (ki << 47);
   double s = __longlong_as_double((long long)t);
   double z = __fma_rn(c0, r, c1), r2 = r * r, y = __fma_rn(c2, r, 1.0);
   y = __fma_rn(z, r2, y);
   y = y * s;
   return (float)y;
 }
+__device__ __forceinline__ float exp_f32(float x) { return exp_f32_tab(x, kExp2Tab); }
 
 // binary16 <-> binary32 (round to nearest even; the `half` crate contract).
 __device__ __forceinline__ float h2f(uint16_t h) {

@@ -728,6 +728,8 @@ __global__ __launch_bounds__(512) void k_mv_q8w(MatrixView w, ActView act, int r
       if (i < total) smem[i] = cp[k];
     }
   }
+  __shared__ uint64_t s_tab[32];  // expf's table for the SwiGLU epilogue
+  if (kEpi == kEpiSwiglu && threadIdx.x < 32) s_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
   __syncthreads();
   if (!live) return;
   const uint8_t *sw = reinterpret_cast<const uint8_t *>(smem);
@@ -794,7 +796,7 @@ __global__ __launch_bounds__(512) void k_mv_q8w(MatrixView w, ActView act, int r
       if (!rvalid || row >= w.rows / 2) continue;
       const float g = acc[0][i], u = acc[kNM - 1][i];
       bad |= !finitef(g) || !finitef(u);
-      o.out[(size_t)r * o.ld + row] = (g / (1.0f + exp_f32(-g))) * u;
+      o.out[(size_t)r * o.ld + row] = (g / (1.0f + exp_f32_tab(-g, s_tab))) * u;
     }
   } else {
 #pragma unroll
@@ -1518,6 +1520,8 @@ __global__ __launch_bounds__(256) void k_attn_exp(StepDims d, const uint32_t *__
   constexpr int kT = 256, kW = kT / kWave, kK = kT / 32;
   __shared__ float redf[kW][8];
   __shared__ double redd[kW][8];
+  __shared__ uint64_t s_tab[32];  // expf's table, read per lane below
+  if (threadIdx.x < 32) s_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
   const int r = d.row_map ? (int)d.row_map[blockIdx.x] : (int)blockIdx.x;
   const int g = blockIdx.y, c = blockIdx.z;
   const int kv = (int)row_pos[r] + 1, t0 = c * kT;
@@ -1549,7 +1553,7 @@ __global__ __launch_bounds__(256) void k_attn_exp(StepDims d, const uint32_t *__
   for (int k = 0; k < kK; k++) {
     const int t = t0 + tok + 32 * k;
     if (t < kv && live) {
-      const float e = exp_f32(sv[k] - m);
+      const float e = exp_f32_tab(sv[k] - m, s_tab);
       base[k * kT] = e;
       den += (double)e;
     }
