@@ -993,6 +993,8 @@ __global__ __launch_bounds__(576) void k_q35_attn(Q35Rows Rw, const float *__res
   const int kv = (int)pos + 1, kvh = h / (NH / NKV), kvw = NKV * D;
   const float *V = vc + (size_t)seq * cache_seq + kvh * D;
   const float *srow = scores + ((size_t)row * NH + h) * ldsc;
+  __shared__ uint64_t s_tab[32];  // expf's table, read per lane in the exponent loops
+  if (tid < 32) s_tab[tid] = kExp2Tab[tid];
   for (int t = tid; t < kv; t += nt) sc[t] = srow[t];
   __syncthreads();
   // prefix maxima: contiguous segments, then an exclusive scan of segment maxima
@@ -1018,10 +1020,10 @@ __global__ __launch_bounds__(576) void k_q35_attn(Q35Rows Rw, const float *__res
   __syncthreads();
   for (int t = lo; t < hi; t++) {
     const float prev = t ? mx[t - 1] : -__builtin_inff();
-    old[t] = exp_f32(prev - mx[t]);
+    old[t] = exp_f32_tab(prev - mx[t], s_tab);
   }
   __syncthreads();
-  for (int t = lo; t < hi; t++) sc[t] = exp_f32(sc[t] - mx[t]);  // new_t
+  for (int t = lo; t < hi; t++) sc[t] = exp_f32_tab(sc[t] - mx[t], s_tab);  // new_t
   __syncthreads();
   if (tid == dthreads) {
     float den = 0.0f;
