@@ -43,7 +43,7 @@ CATEGORY_KERNEL = {"attn_scores": "k_attn_scores<64, 7>", "attn_softmax_stats": 
                    "matvec_qkv": "k_mv_q8s<0, 1, 1, 8>", "matvec_o_residual": "k_mv_q8s<1, 1, 1, 8>",
                    "matvec_gate_up_swiglu": "k_mv_q8w<2, 2, 8, 16>",
                    "matvec_down_residual": "k_mv_q8s<1, 1, 1, 8>",
-                   "matvec_head_argmax": "k_mv_q8c<3, 1, 4, 4, 8>"}
+                   "matvec_head_argmax": "k_mv_q8h<8, 14>"}
 PMC_CMD = ("COHX_GRAPHS=0 rocprofv3 --pmc {counter} --kernel-include-regex \"k_attn|k_mv\" --output-format csv "
            "-d <dir> -o <name> -- python3 bench.py --steps 2 --warmup 1 --secondary-lanes 0 "
            "--no-cpu-baseline --no-c3 --no-c4 --no-c5")
