@@ -110,17 +110,28 @@ int make_f16(cohx_ctx *ctx, DeviceMatrix &m, int rows, int K) {
   return rc;
 }
 
+// Device row of source row r when the rows are query or key heads of
+// rope_d elements (0: identity): element i of a head lands on row 2i and
+// element i + rope_d/2 on row 2i + 1, so the two halves NeoX RoPE rotates
+// together are adjacent rows of one 16-row tile (the fused qkv epilogue
+// reads them from one workgroup).  Each row's dot product is unchanged.
+int rope_row(int r, int rope_d) {
+  if (!rope_d) return r;
+  const int head = r / rope_d, i = r % rope_d, half = rope_d / 2;
+  return head * rope_d + (i < half ? 2 * i : 2 * (i - half) + 1);
+}
+
 // GGUF Q8_0 rows -> tiles [tile_first, ...) of the device layout, tile i of the
-// source landing on tile tile_first + i*tile_step.
+// source landing on tile tile_first + i*tile_step; rows reordered by rope_row.
 int upload_q8(cohx_ctx *ctx, DeviceMatrix &m, const uint8_t *src, int rows, int tile_first,
-              int tile_step) {
+              int tile_step, int rope_d) {
   const int nb = m.view.nb, nbp = m.view.nbp;
   const int tiles = (rows + 15) / 16;
   const size_t tile_bytes = (size_t)nbp * 512, tile_scales = (size_t)nbp * 16;
   std::vector<int8_t> qs(tiles * tile_bytes, 0);
   std::vector<uint16_t> ds(tiles * tile_scales, 0);
   for (int r = 0; r < rows; r++) {
-    const int t = r / 16, c = r % 16;
+    const int dr = rope_row(r, rope_d), t = dr / 16, c = dr % 16;
     for (int b = 0; b < nb; b++) {
       const uint8_t *blk = src + ((size_t)r * nb + b) * 34;
       ds[q8_scale(t, nbp, b, c)] = (uint16_t)(blk[0] | (blk[1] << 8));
@@ -139,14 +150,14 @@ int upload_q8(cohx_ctx *ctx, DeviceMatrix &m, const uint8_t *src, int rows, int 
 // GGUF Q4_0 rows (quant.rs:97-101: value j = low nibble of byte j, value
 // j+16 = high nibble) -> Q4 tiles, tile i of the source at tile_first + i*tile_step.
 int upload_q4(cohx_ctx *ctx, DeviceMatrix &m, const uint8_t *src, int rows, int tile_first,
-              int tile_step) {
+              int tile_step, int rope_d) {
   const int nb = m.view.nb, nbp = m.view.nbp;
   const int tiles = (rows + 15) / 16;
   const size_t tile_bytes = (size_t)nbp * 256, tile_scales = (size_t)nbp * 16;
   std::vector<uint8_t> qs(tiles * tile_bytes, 0);
   std::vector<uint16_t> ds(tiles * tile_scales, 0);
   for (int r = 0; r < rows; r++) {
-    const int t = r / 16, c = r % 16;
+    const int dr = rope_row(r, rope_d), t = dr / 16, c = dr % 16;
     for (int b = 0; b < nb; b++) {
       const uint8_t *blk = src + ((size_t)r * nb + b) * 18;
       ds[q8_scale(t, nbp, b, c)] = (uint16_t)(blk[0] | (blk[1] << 8));
@@ -171,12 +182,14 @@ int upload_f16(cohx_ctx *ctx, DeviceMatrix &m, const void *src, int rows, int ro
   return COHX_OK;
 }
 
+// Q8_0/Q4_0: `first` and `step` count 16-row tiles and rope_d reorders the
+// rows (rope_row); F16: `first` counts rows and the order is the source's.
 int upload_matrix(cohx_ctx *ctx, DeviceMatrix &m, uint32_t dtype, const void *data, int rows,
-                  int first, int step) {
+                  int first, int step, int rope_d = 0) {
   if (dtype != (uint32_t)m.view.dtype)
     return fail(ctx, COHX_UNSUPPORTED, "matrix dtype differs from the context's weight dtype");
-  if (dtype == 8) return upload_q8(ctx, m, (const uint8_t *)data, rows, first, step);
-  if (dtype == 2) return upload_q4(ctx, m, (const uint8_t *)data, rows, first, step);
+  if (dtype == 8) return upload_q8(ctx, m, (const uint8_t *)data, rows, first, step, rope_d);
+  if (dtype == 2) return upload_q4(ctx, m, (const uint8_t *)data, rows, first, step, rope_d);
   return upload_f16(ctx, m, data, rows, first);
 }
 
@@ -405,8 +418,10 @@ int cohx_upload_tensor(cohx_ctx *ctx, const char *name, uint32_t dtype, uint64_t
       const uint64_t rows = s == "attn_q.weight" ? H : KVD;
       const uint64_t first = s == "attn_q.weight" ? 0 : s == "attn_k.weight" ? H : H + KVD;
       if (!expect(H, rows)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
+      // Q8_0/Q4_0 query and key rows pair each head's RoPE halves (rope_row)
       rc = upload_matrix(ctx, ly.qkv, dtype, data, (int)rows,
-                         (int)(dtype == 8 || dtype == 2 ? first / 16 : first), 1);
+                         (int)(dtype == 8 || dtype == 2 ? first / 16 : first), 1,
+                         s == "attn_v.weight" ? 0 : (int)d.head_dim);
       ly.qkv.gguf_bytes += bytes;
     } else if (s == "attn_output.weight") {
       if (!expect(H, H)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
@@ -958,15 +973,29 @@ int enqueue_device_step(cohx_ctx *ctx, const Prepared &p, int kv_grid, bool any_
     launch_norm_act(s, R, w.x, nullptr, ly.attn_norm, H, d.norm_epsilon, act_dtype, ctx->nbp_h, act,
                     w.row_err);
     prof_end(ctx, e);
-    e = prof_begin(ctx, kCatMvQkv, matrix_pass_bytes(ly.qkv.view, R, H + 2 * KVD, false),
-                   2.0 * R * (H + 2 * KVD) * H);
-    launch_matvec(s, kEpiStore, ly.qkv.view, act, R,
-                  MatvecOut{w.qkv, H + 2 * KVD, nullptr, nullptr, w.row_err, nullptr});
-    prof_end(ctx, e);
-    e = prof_begin(ctx, kCatQkvPost, b_post, 0);
-    launch_qkv_post(s, R, sd, w.qkv, ly.bqkv, ctx->rope, w.row_pos, w.row_slot, w.q_rot, kp, vp,
-                    w.row_err);
-    prof_end(ctx, e);
+    if (ly.qkv.view.dtype == 1) {
+      e = prof_begin(ctx, kCatMvQkv, matrix_pass_bytes(ly.qkv.view, R, H + 2 * KVD, false),
+                     2.0 * R * (H + 2 * KVD) * H);
+      launch_matvec(s, kEpiStore, ly.qkv.view, act, R,
+                    MatvecOut{w.qkv, H + 2 * KVD, nullptr, nullptr, w.row_err, nullptr});
+      prof_end(ctx, e);
+      e = prof_begin(ctx, kCatQkvPost, b_post, 0);
+      launch_qkv_post(s, R, sd, w.qkv, ly.bqkv, ctx->rope, w.row_pos, w.row_slot, w.q_rot, kp, vp,
+                      w.row_err);
+      prof_end(ctx, e);
+    } else {
+      // Q8_0/Q4_0: bias, RoPE and the K/V append run in the matvec's epilogue
+      // (rows uploaded in rope_row order); the bytes are the matrix pass plus
+      // the post pass's writes
+      e = prof_begin(ctx, kCatMvQkv,
+                     matrix_pass_bytes(ly.qkv.view, R, 0, false) + (double)R * (H + 2 * KVD) * 4 +
+                         (H + 2 * KVD) * 4,
+                     2.0 * R * (H + 2 * KVD) * H);
+      launch_matvec_qkv(s, ly.qkv.view, act, R,
+                        MatvecOut{nullptr, 0, nullptr, nullptr, w.row_err, nullptr},
+                        QkvEpi{ly.bqkv, ctx->rope, w.row_pos, w.row_slot, w.q_rot, kp, vp, H, KVD, D, NKV});
+      prof_end(ctx, e);
+    }
     if (p.n_tiles) {
       e = prof_begin(ctx, kCatAttnChunk, b_chunk, f_chunk);
       launch_attn_chunk(s, p.n_tiles, sd, w.tiles, w.q_rot, kp, vp, ctx->page_table, w.direct);

@@ -73,6 +73,21 @@ void launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActVi
                    int rows_b, const MatvecOut &o);
 void launch_argmax_reduce(hipStream_t s, int rows, const unsigned long long *part, int units,
                           unsigned long long *out);
+// Q8_0/Q4_0 qkv projection with launch_qkv_post's work in its epilogue (bias,
+// NeoX RoPE, K/V append into the paged pool), for weights whose query and key
+// rows were uploaded in rope_row order.  Gives the same bits as the matvec and
+// launch_qkv_post in sequence; out.out is unused.
+struct QkvEpi {
+  const float *bias;         // [H + 2 KVD], the source row order
+  const float2 *rope;        // [position][D/2] (cos, sin)
+  const uint32_t *row_pos;   // [rows_b]
+  const int32_t *row_slot;   // [rows_b] KV slot (< 0: no append)
+  float *q_rot;              // [rows_b][H]
+  float *kpool, *vpool;      // the layer's pools
+  int H, KVD, D, NKV;
+};
+void launch_matvec_qkv(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
+                       const MatvecOut &o, const QkvEpi &q);
 void launch_qkv_post(hipStream_t s, int rows, const StepDims &d, const float *qkv,
                      const float *bias, const float2 *rope, const uint32_t *row_pos,
                      const int32_t *row_slot, float *q_rot, float *kpool, float *vpool,

@@ -332,9 +332,13 @@ __device__ __forceinline__ long hi64(uint4 v) {
   return (long)(((unsigned long)v.w << 32) | v.z);
 }
 
+// Epilogue of the fused qkv projection (launch_matvec_qkv); the generic
+// launch_matvec never selects it.
+constexpr int kEpiQkv = 4;
+
 template <int kEpi, int kNM, int kP, int kFmt>
 __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int rows_b,
-                                                int n_tiles, MatvecOut o) {
+                                                int n_tiles, MatvecOut o, QkvEpi qe) {
   constexpr int kW = 8, kCB = 2 * kW * kP;  // blocks per chunk: kP pairs per wave
   __shared__ float s_isum[kCB][kNM * 256];
   __shared__ float s_dw[kCB][kNM * 16];
@@ -420,7 +424,49 @@ __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int r
   const bool rvalid = t < 256 && r < rows_b;
   const int er = (rvalid && o.err_rows) ? (int)o.err_rows[r] : r;
   bool bad = false;
-  if (kEpi == kEpiArgmax) {
+  if constexpr (kEpi == kEpiQkv) {
+    // The tile's 16 x 16 outputs meet in LDS (the block sums' space is free
+    // after the chain's last barrier), so that one thread holds both rows of
+    // a RoPE pair: with rows in rope_row order, rows 2i and 2i + 1 of a query
+    // or key head are its elements i and i + D/2.  Then k_qkv_post's
+    // arithmetic, operation for operation.
+    float *s_out = &s_isum[0][0];
+    if (t < 256) {
+      const float v = acc[0];
+      s_out[prow * 16 + pcol] = v;
+      bad = rvalid && unit * 16 + prow < w.rows && !finitef(v);
+    }
+    __syncthreads();
+    const int pi = t / 16, c = t % 16, rb = nt * 16 + c, row0 = unit * 16 + 2 * pi;
+    if (t < 128 && rb < rows_b && row0 + 1 < w.rows) {
+      const float va = s_out[2 * pi * 16 + c], vb = s_out[(2 * pi + 1) * 16 + c];
+      const uint32_t pos = qe.row_pos[rb];
+      const int32_t slot = qe.row_slot[rb];
+      const int half = qe.D / 2, page = slot / kPage, off = slot % kPage;
+      if (row0 < qe.H + qe.KVD) {
+        const bool isq = row0 < qe.H;
+        const int e0 = isq ? row0 : row0 - qe.H;
+        const int head = e0 / qe.D, i = (e0 % qe.D) / 2;
+        const int e = (isq ? 0 : qe.H) + head * qe.D + i;  // source row of element i
+        const float a = va + qe.bias[e], b = vb + qe.bias[e + half];
+        const float2 cs = qe.rope[(size_t)pos * half + i];
+        const float ya = fmaf(a, cs.x, -(b * cs.y)), yb = fmaf(a, cs.y, b * cs.x);
+        if (isq) {
+          float *q = qe.q_rot + (size_t)rb * qe.H + head * qe.D + i;
+          q[0] = ya;
+          q[half] = yb;
+        } else if (slot >= 0) {
+          qe.kpool[k_at(page, pos / kPage, head, qe.NKV, off, i, qe.D)] = ya;
+          qe.kpool[k_at(page, pos / kPage, head, qe.NKV, off, i + half, qe.D)] = yb;
+        }
+      } else if (slot >= 0) {
+        const int e0 = row0 - qe.H - qe.KVD, g = e0 / qe.D, j = e0 % qe.D;
+        const float *bv = qe.bias + qe.H + qe.KVD + e0;
+        qe.vpool[v_at(page, g, qe.NKV, off, j, qe.D)] = va + bv[0];
+        qe.vpool[v_at(page, g, qe.NKV, off, j + 1, qe.D)] = vb + bv[1];
+      }
+    }
+  } else if (kEpi == kEpiArgmax) {
     const int row = unit * 16 + prow;
     const bool valid = rvalid && row < w.rows;
     const float v = acc[0];
@@ -2094,12 +2140,8 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
     // projection 13.3 -> 11.6 us against chunks of 64; qkv and o 0.2 us
     // faster than one chunk of 32)
     const int groups = (units + 7) / 8;
-    if (kNM == 1)
-      launch_k((k_mv_q8s<kEpi, kNM, 1, kFmt>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
-               rows_b, n_tiles, o);
-    else
-      launch_k((k_mv_q8s<kEpi, kNM, 1, kFmt>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
-               rows_b, n_tiles, o);
+    launch_k((k_mv_q8s<kEpi, kNM, 1, kFmt>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
+             rows_b, n_tiles, o, QkvEpi{});
   }
 }
 
@@ -2161,6 +2203,17 @@ void launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActVi
       case kEpiArgmax: mv_f16<kEpiArgmax>(s, w, act, rows_b, o); break;
     }
   }
+}
+
+void launch_matvec_qkv(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
+                       const MatvecOut &o, const QkvEpi &q) {
+  const int n_tiles = (rows_b + 15) / 16, groups = (w.mtiles + 7) / 8;
+  if (w.dtype == 8)
+    launch_k((k_mv_q8s<kEpiQkv, 1, 1, 8>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act, rows_b,
+             n_tiles, o, q);
+  else
+    launch_k((k_mv_q8s<kEpiQkv, 1, 1, 2>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act, rows_b,
+             n_tiles, o, q);
 }
 
 void launch_argmax_reduce(hipStream_t s, int rows, const unsigned long long *part, int units,
