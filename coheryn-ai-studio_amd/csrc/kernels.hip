@@ -1223,10 +1223,11 @@ __global__ __launch_bounds__(256) void k_head_f16(MatrixView w, ActView act, int
 // v_mfma_f32_16x16x32_f16 order.  The reference sums these exact products in
 // f64 (cpu.rs:31-35); this regime differs from it by f32 rounding of the
 // partial sums and is held to a tolerance, while decode batches keep the
-// exact kernels.  A workgroup (4 waves) owns 128 features x 128 rows; wave
-// (wf, wr) computes features wf*64.. and rows wr*64.. as 4x4 MFMA tiles.  K is
-// staged through LDS in steps of 32, double-buffered, with the next step's
-// global loads in flight during the MFMAs.  For the SwiGLU epilogue the
+// exact kernels.  A workgroup (4 waves) owns 128 features x 32*kNB rows; wave
+// (wf, wr) computes features wf*64.. and rows wr*16*kNB.. as 4 x kNB MFMA
+// tiles.  K is staged through a ring of kStages LDS stages of 32 K-steps,
+// filled by direct-to-LDS loads with later steps in flight during the
+// MFMAs.  For the SwiGLU epilogue the
 // workgroup's feature tile is 64 gate rows and the 64 matching up rows; the
 // up waves hand their sums to the gate waves through LDS.
 // ---------------------------------------------------------------------------
