@@ -223,6 +223,41 @@ __global__ __launch_bounds__(256) void k_norm_act(const float *__restrict__ x,
   if (bad) atomicOr(&row_err[ib], kErrNonFinite);
 }
 
+// RMSNorm + Q8_0 operands for rows of at most 2048 elements: thread t owns
+// the 8-element group t (elements 8t .. 8t+7; groups past the row are the
+// zero padding of the last block pair).  It loads its x and weight values at
+// once, sums its squares in element order, and after the workgroup's f64 tree
+// normalizes and quantizes its group in registers: no LDS staging of the row
+// and one barrier pair fewer than k_norm_act.
+__global__ __launch_bounds__(256) void k_norm_q8(const float *__restrict__ x,
+                                                 const uint32_t *__restrict__ in_rows,
+                                                 const float *__restrict__ w, int H, float eps, int nbp,
+                                                 ActView act, uint32_t *row_err) {
+  __shared__ double red[4];
+  const int ob = blockIdx.x;
+  const int ib = in_rows ? (int)in_rows[ob] : ob;
+  const int kg = threadIdx.x;
+  const bool active = kg < nbp * 4, inrow = kg * 8 < H;  // H % 8 == 0
+  const int k0 = inrow ? kg * 8 : 0;
+  const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)ib * H + k0);
+  const float4 *wr = reinterpret_cast<const float4 *>(w + k0);
+  const float4 xa = xr[0], xb = xr[1], wa = wr[0], wb = wr[1];
+  const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+  const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+  double ss = -0.0;
+  if (inrow) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) ss += (double)(xv[i] * xv[i]);
+  }
+  const double total = block_sum_f64<256>(ss, red);
+  const float mean = (float)(total / (double)H);
+  const float scale = 1.0f / sqrtf(mean + eps);
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) v[i] = inrow ? xv[i] * scale * wv[i] : 0.0f;
+  if (quant_group_q8(v, active, ob, kg, nbp, act)) atomicOr(&row_err[ib], kErrNonFinite);
+}
+
 // Operand preparation of an f32 row (SwiGLU output before ffn_down).
 template <int kAct>
 __global__ __launch_bounds__(256) void k_quant_act(const float *__restrict__ src, int K, int nbp,
@@ -2083,7 +2118,9 @@ void launch_norm_act(hipStream_t s, int rows, const float *x, const uint32_t *in
                      const float *weight, int H, float eps, int act_dtype, int nbp, ActView act,
                      uint32_t *row_err) {
   const size_t lds = (size_t)H * sizeof(float);
-  if (act_dtype == 8)
+  if (act_dtype == 8 && nbp * 4 <= 256 && H % 8 == 0)  // one 8-element group per thread
+    launch_k(k_norm_q8, dim3(rows), dim3(256), 0, s, x, in_rows, weight, H, eps, nbp, act, row_err);
+  else if (act_dtype == 8)
     launch_k(k_norm_act<8>, dim3(rows), dim3(256), lds, s, x, in_rows, weight, H, eps,
                        nbp, act, row_err);
   else
