@@ -41,7 +41,7 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_decode128.json")
 CATEGORY_KERNEL = {"attn_scores": "k_attn_scores<64, 7>", "attn_softmax_stats": "k_attn_exp<7>",
                    "attn_pv": "k_attn_pv<64, 7>", "attn_combine_act": "k_attn_combine<8>",
                    "matvec_qkv": "k_mv_q8s<4, 1, 1, 8>", "matvec_o_residual": "k_mv_q8s<1, 1, 1, 8>",
-                   "matvec_gate_up_swiglu": "k_mv_q8w<2, 2, 8, 16>",
+                   "matvec_gate_up_swiglu": "k_mv_q8w<2, 2, 8, 16, 2>",
                    "matvec_down_residual": "k_mv_q8s<1, 1, 1, 8>",
                    "matvec_head_argmax": "k_mv_q8h<8, 14>"}
 PMC_CMD = ("COHX_GRAPHS=0 rocprofv3 --pmc {counter} --kernel-include-regex \"k_attn|k_mv\" --output-format csv "

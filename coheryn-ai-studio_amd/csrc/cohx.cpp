@@ -325,6 +325,8 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   if (!rc) rc = dalloc(ctx, &w.h, (size_t)R * F);
   if (!rc) rc = dalloc(ctx, &w.act_qs, rtiles * ctx->nbp_max * 512);
   if (!rc) rc = dalloc(ctx, &w.act_ds, rtiles * ctx->nbp_max * 16);
+  if (!rc && packed) rc = dalloc(ctx, &w.down_qs, rtiles * ctx->nbp_f * 512);
+  if (!rc && packed) rc = dalloc(ctx, &w.down_ds, rtiles * ctx->nbp_f * 16);
   if (!rc) rc = dalloc(ctx, &w.act_f16, (size_t)R * std::max(H, F));
   if (!rc) rc = dalloc(ctx, &w.scores, (size_t)R * NKV * d->max_context * 8);
   if (!rc) rc = dalloc(ctx, &w.chunk_max, (size_t)R * NH * ((d->max_context + 255) / 256));
@@ -1025,17 +1027,28 @@ int enqueue_device_step(cohx_ctx *ctx, const Prepared &p, int kv_grid, bool any_
     launch_norm_act(s, R, w.x, nullptr, ly.ffn_norm, H, d.norm_epsilon, act_dtype, ctx->nbp_h, act,
                     w.row_err);
     prof_end(ctx, e);
-    e = prof_begin(ctx, kCatMvGateUp, matrix_pass_bytes(ly.gu.view, R, F, false),
-                   2.0 * R * 2 * F * H);
-    launch_matvec(s, kEpiSwiglu, ly.gu.view, act, R,
-                  MatvecOut{w.h, F, nullptr, nullptr, w.row_err, nullptr});
-    prof_end(ctx, e);
-    e = prof_begin(ctx, kCatQuant, (double)R * F * 4 + (act_dtype == 8 ? (double)R * F / 32 * 34
-                                                                         : (double)R * F * 2), 0);
-    launch_quant_act(s, R, w.h, F, act_dtype, ctx->nbp_f, act, w.row_err);
-    prof_end(ctx, e);
+    // Q8_0/Q4_0 at K <= 1024: the SwiGLU quantizer runs in gate+up's
+    // epilogue into the down operand buffer; otherwise its own pass
+    const ActView down_act{w.down_qs, w.down_ds, nullptr};
+    const bool fused_quant = w.down_qs && ly.gu.view.nbp <= 32 && F % 64 == 0;
+    if (fused_quant) {
+      e = prof_begin(ctx, kCatMvGateUp,
+                     matrix_pass_bytes(ly.gu.view, R, 0, false) + (double)R * F / 32 * 34, 2.0 * R * 2 * F * H);
+      launch_matvec_swiglu_q8(s, ly.gu.view, act, R,
+                              MatvecOut{nullptr, 0, nullptr, nullptr, w.row_err, nullptr}, down_act);
+      prof_end(ctx, e);
+    } else {
+      e = prof_begin(ctx, kCatMvGateUp, matrix_pass_bytes(ly.gu.view, R, F, false), 2.0 * R * 2 * F * H);
+      launch_matvec(s, kEpiSwiglu, ly.gu.view, act, R,
+                    MatvecOut{w.h, F, nullptr, nullptr, w.row_err, nullptr});
+      prof_end(ctx, e);
+      e = prof_begin(ctx, kCatQuant, (double)R * F * 4 + (act_dtype == 8 ? (double)R * F / 32 * 34
+                                                                           : (double)R * F * 2), 0);
+      launch_quant_act(s, R, w.h, F, act_dtype, ctx->nbp_f, act, w.row_err);
+      prof_end(ctx, e);
+    }
     e = prof_begin(ctx, kCatMvDown, matrix_pass_bytes(ly.down.view, R, H, true), 2.0 * R * H * F);
-    launch_matvec(s, kEpiResidual, ly.down.view, act, R,
+    launch_matvec(s, kEpiResidual, ly.down.view, fused_quant ? down_act : act, R,
                   MatvecOut{w.x, H, nullptr, nullptr, w.row_err, nullptr});
     prof_end(ctx, e);
   }

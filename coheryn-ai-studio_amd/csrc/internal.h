@@ -39,6 +39,10 @@ struct Workspace {
   int32_t *row_slot = nullptr;
   float *x = nullptr, *qkv = nullptr, *q_rot = nullptr, *h = nullptr;
   int8_t *act_qs = nullptr;
+  // the down projection's Q8_0 operand when gate+up quantizes in its epilogue
+  // (it cannot overwrite act_qs while other workgroups still read gate+up's)
+  int8_t *down_qs = nullptr;
+  uint16_t *down_ds = nullptr;
   uint16_t *act_ds = nullptr, *act_f16 = nullptr;
   float *scores = nullptr;  // [rows][kv_heads][max_context][8]: scores, then weights
   float *chunk_max = nullptr, *logits = nullptr;

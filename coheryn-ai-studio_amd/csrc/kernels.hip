@@ -126,9 +126,12 @@ __global__ __launch_bounds__(256) void k_embed(MatrixView e, const uint32_t *__r
 // Q8_0 activation blocks (QuantizedInput::prepare, quant.rs:193-213):
 // d = max|x|/127 over the 32-element block, inv = 1/d (0 when d == 0), stored
 // scale f16(d), q = round-half-away(x*inv) as i8, in the B-operand tile layout.
-// One thread quantizes an 8-element group (a quarter of a block); the four groups of a block sit in four consecutive lanes (aligned),
-// combine their maxima with two shuffles, and each writes its 8 quantized
-// values as one 8-byte store into the B-operand tile layout.
+// One thread quantizes an 8-element group (a quarter of a block); the four
+// groups of a block sit in lanes kStride apart (kStride 1: four consecutive
+// aligned lanes; 16: lanes l, l+16, l+32, l+48), combine their maxima with
+// two shuffles, and each writes its 8 quantized values as one 8-byte store
+// into the B-operand tile layout.
+template <int kStride = 1>
 __device__ __forceinline__ bool quant_group_q8(const float (&v)[8], bool active, int row, int kg,
                                                int nbp, ActView act) {
   float m = 0.0f;
@@ -138,8 +141,8 @@ __device__ __forceinline__ bool quant_group_q8(const float (&v)[8], bool active,
     bad |= active && !finitef(v[i]);
     m = fmaxf(m, active ? fabsf(v[i]) : 0.0f);
   }
-  m = fmaxf(m, __shfl_xor(m, 1, kWave));
-  m = fmaxf(m, __shfl_xor(m, 2, kWave));
+  m = fmaxf(m, __shfl_xor(m, kStride, kWave));
+  m = fmaxf(m, __shfl_xor(m, 2 * kStride, kWave));
   const float d = m / 127.0f;
   const float inv = d == 0.0f ? 0.0f : 1.0f / d;
   const uint16_t hd = f2h(d);
@@ -771,22 +774,28 @@ __global__ __launch_bounds__(64 * kChainWaves) void k_mv_q8c(MatrixView w, ActVi
 // acc = fmaf((float)isum*dw, da, acc) for Q4_0.  K is limited to
 // 64 * kMaxPairs inputs (the B operand lives in registers).
 // ---------------------------------------------------------------------------
-template <int kEpi, int kNM, int kFmt, int kMaxPairs>
-__global__ __launch_bounds__(512) void k_mv_q8w(MatrixView w, ActView act, int rows_b, int n_tiles,
-                                                MatvecOut o) {
+template <int kEpi, int kNM, int kFmt, int kMaxPairs, int kU>
+__global__ __launch_bounds__(512 * kU) void k_mv_q8w(MatrixView w, ActView act, int rows_b, int n_tiles,
+                                                     MatvecOut o, ActView qout) {
+  static_assert(kU == 1 || (kU == 2 && kEpi == kEpiSwiglu), "two units per workgroup: the fused quantizer");
   constexpr int kPairBytes = kFmt == 8 ? 1024 : 512;  // weight bytes per tile per block pair
   constexpr int kCopy = 8;                            // 16-byte copy items per thread (<= 64 KB)
   extern __shared__ uint4 smem[];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const int nthreads = blockDim.x, unit = blockIdx.x;
-  const int tile0 = blockIdx.y * 8, nt = tile0 + wave;
-  const int nbt = min(8, n_tiles - tile0);
+  const int nthreads = blockDim.x;
+  // kU units per workgroup of kU * W waves (W = min(n_tiles, 8) for every
+  // workgroup): wave w takes unit kU * blockIdx.x + w / W and batch tile
+  // tile0 + w % W (past n_tiles in a last, partial row of tiles: not live)
+  const int tile0 = blockIdx.y * 8, nbt = min(8, n_tiles - tile0);
+  const int W = nthreads / (kWave * kU);
+  const int uw = wave / W, bt = wave % W;
+  const int unit = blockIdx.x * kU + uw, nt = tile0 + bt;
   const int npairs = w.nbp / 2, nbp = w.nbp;
-  const int nw = kNM * npairs * kPairBytes / 16;  // copy items: weights, weight scales, batch scales
-  const int ns = kNM * nbp * 32 / 16;
+  const int nw = kU * kNM * npairs * kPairBytes / 16;  // copy items: weights, weight scales, batch scales
+  const int ns = kU * kNM * nbp * 32 / 16;
   const int nd = nbt * nbp * 32 / 16;
-  const uint4 *gw = reinterpret_cast<const uint4 *>(w.qs + (size_t)unit * kNM * npairs * kPairBytes);
-  const uint4 *gs = reinterpret_cast<const uint4 *>(w.ds + (size_t)unit * kNM * nbp * 16);
+  const uint4 *gw = reinterpret_cast<const uint4 *>(w.qs + (size_t)blockIdx.x * kU * kNM * npairs * kPairBytes);
+  const uint4 *gs = reinterpret_cast<const uint4 *>(w.ds + (size_t)blockIdx.x * kU * kNM * nbp * 16);
   const uint4 *gd = reinterpret_cast<const uint4 *>(act.ds + (size_t)tile0 * nbp * 16);
   const bool live = nt < n_tiles;
   uint4 b[kMaxPairs];
@@ -812,10 +821,11 @@ __global__ __launch_bounds__(512) void k_mv_q8w(MatrixView w, ActView act, int r
   __shared__ uint64_t s_tab[32];  // expf's table for the SwiGLU epilogue
   if (kEpi == kEpiSwiglu && threadIdx.x < 32) s_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
   __syncthreads();
-  if (!live) return;
-  const uint8_t *sw = reinterpret_cast<const uint8_t *>(smem);
-  const uint16_t *ssc = reinterpret_cast<const uint16_t *>(smem + nw);  // [m][block][16 rows]
-  const uint16_t *sda = ssc + kNM * nbp * 16;                           // [wave][block][16 batch rows]
+  if (kU == 1 && !live) return;
+  // this wave's unit: its kNM tiles and their scales
+  const uint8_t *sw = reinterpret_cast<const uint8_t *>(smem) + (size_t)uw * kNM * npairs * kPairBytes;
+  const uint16_t *ssc = reinterpret_cast<const uint16_t *>(smem + nw) + uw * kNM * nbp * 16;  // [m][block][16]
+  const uint16_t *sda = reinterpret_cast<const uint16_t *>(smem + nw) + kU * kNM * nbp * 16;  // [tile][block][16]
   const int rsub = 4 * (lane / 16), col = lane % 16;
   const v4i zero = {0, 0, 0, 0};
   float acc[kNM][4];
@@ -825,7 +835,7 @@ __global__ __launch_bounds__(512) void k_mv_q8w(MatrixView w, ActView act, int r
     for (int i = 0; i < 4; i++) acc[m][i] = 0.0f;
 #pragma unroll
   for (int p = 0; p < kMaxPairs; p++) {
-    if (p < npairs) {
+    if (p < npairs && live) {
       uint4 a[kNM];
 #pragma unroll
       for (int m = 0; m < kNM; m++) {
@@ -840,7 +850,7 @@ __global__ __launch_bounds__(512) void k_mv_q8w(MatrixView w, ActView act, int r
       for (int h = 0; h < 2; h++) {
         const int blk = 2 * p + h;
         const long bop = h ? hi64(b[p]) : lo64(b[p]);
-        const uint32_t da = sda[(wave * nbp + blk) * 16 + col];
+        const uint32_t da = sda[(bt * nbp + blk) * 16 + col];
 #pragma unroll
         for (int m = 0; m < kNM; m++) {
           long aop;
@@ -870,7 +880,36 @@ __global__ __launch_bounds__(512) void k_mv_q8w(MatrixView w, ActView act, int r
   const bool rvalid = r < rows_b;
   const int er = (rvalid && o.err_rows) ? (int)o.err_rows[r] : r;
   bool bad = false;
-  if (kEpi == kEpiSwiglu) {
+  if constexpr (kU == 2) {
+    // Fused SwiGLU quantizer: the two units' 32 outputs are one Q8_0 block
+    // (block blockIdx.x) of each batch row.  Each wave parks its 16 x 16
+    // SwiGLU values in LDS; then the
+    // first unit's wave of each batch tile gives lane l the block's elements
+    // 8 (l / 16) .. + 7 of batch row l % 16 and runs k_quant_act's arithmetic.
+    // (over the weight tiles: every wave is past its MFMAs at the barrier;
+    // the launch allocates at least the 16 KB this needs)
+    float *s_h = reinterpret_cast<float *>(smem);  // [uw][bt][16 rows][16 batch rows]
+    __syncthreads();
+    if (live) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float g = acc[0][i], u = acc[kNM - 1][i];
+        bad |= rvalid && (!finitef(g) || !finitef(u));
+        s_h[((uw * 8 + bt) * 16 + rsub + i) * 16 + col] = (g / (1.0f + exp_f32_tab(-g, s_tab))) * u;
+      }
+    }
+    __syncthreads();
+    if (live && uw == 0) {
+      const int k = lane / 16;  // elements 8k .. 8k + 7 of the block
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const int el = 8 * k + e;
+        v[e] = s_h[(((el / 16) * 8 + bt) * 16 + el % 16) * 16 + col];
+      }
+      bad |= quant_group_q8<16>(v, rvalid, r, blockIdx.x * 4 + k, (w.rows / 64 + 1) & ~1, qout);
+    }
+  } else if (kEpi == kEpiSwiglu) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int row = unit * 16 + rsub + i;
@@ -2149,8 +2188,8 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
     const int nthreads = 64 * (n_tiles < 8 ? n_tiles : 8);
     const size_t lds = (size_t)kNM * (w.nbp / 2) * (kFmt == 8 ? 1024 : 512) + (size_t)kNM * w.nbp * 32 +
                        (size_t)8 * w.nbp * 32;
-    launch_k((k_mv_q8w<kEpi, kNM, kFmt, kWPairs>), dim3(units, by), dim3(nthreads), lds, s, w, act, rows_b,
-             n_tiles, o);
+    launch_k((k_mv_q8w<kEpi, kNM, kFmt, kWPairs, 1>), dim3(units, by), dim3(nthreads), lds, s, w, act, rows_b,
+             n_tiles, o, ActView{});
   } else if (kEpi == kEpiArgmax && kNM == 1 && n_tiles <= 8 && w.nbp <= 2 * kWPairs) {
     // LM head: persistent workgroups streaming weight tiles through LDS, two
     // per CU (4 waves per SIMD); always 8 waves, since the tile copy needs
@@ -2252,6 +2291,27 @@ void launch_matvec_qkv(hipStream_t s, const MatrixView &w, const ActView &act, i
   else
     launch_k((k_mv_q8s<kEpiQkv, 1, 1, 2>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act, rows_b,
              n_tiles, o, q);
+}
+
+bool launch_matvec_swiglu_q8(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
+                             const MatvecOut &o, const ActView &qout) {
+  constexpr int kWPairs = 16;
+  const int F = w.rows / 2, n_tiles = (rows_b + 15) / 16;
+  if ((w.dtype != 8 && w.dtype != 2) || w.nbp > 2 * kWPairs || F % 64 != 0) return false;
+  const int groups = w.mtiles / 4;  // pairs of (gate, up) tile units: one Q8_0 block each
+  const int by = (n_tiles + 7) / 8, nthreads = 2 * 64 * (n_tiles < 8 ? n_tiles : 8);
+  const size_t pair_bytes = w.dtype == 8 ? 1024 : 512;
+  // LDS: the two units' tiles and scales and the batch scales, and at least
+  // the epilogue's exchange of 2 units x 8 batch tiles x 16 x 16 floats
+  const size_t copy = 2 * 2 * (size_t)(w.nbp / 2) * pair_bytes + 2 * 2 * (size_t)w.nbp * 32 + 8 * (size_t)w.nbp * 32;
+  const size_t lds = copy > 2 * 8 * 256 * 4 ? copy : 2 * 8 * 256 * 4;
+  if (w.dtype == 8)
+    launch_k((k_mv_q8w<kEpiSwiglu, 2, 8, kWPairs, 2>), dim3(groups, by), dim3(nthreads), lds, s, w, act, rows_b,
+             n_tiles, o, qout);
+  else
+    launch_k((k_mv_q8w<kEpiSwiglu, 2, 2, kWPairs, 2>), dim3(groups, by), dim3(nthreads), lds, s, w, act, rows_b,
+             n_tiles, o, qout);
+  return true;
 }
 
 void launch_argmax_reduce(hipStream_t s, int rows, const unsigned long long *part, int units,
