@@ -15,6 +15,7 @@ without the built library raises, and nothing here falls back to the CPU.
 """
 import ctypes
 import os
+import weakref
 
 import numpy as np
 
@@ -132,6 +133,9 @@ EXPORTS = {
                                          ctypes.POINTER(ctypes.c_int32), ctypes.c_uint32]),
     "cohx_seq_read_kv": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                         ctypes.c_int, ctypes.POINTER(ctypes.c_float)]),
+    "cohx_seq_read_kv_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                             ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32,
+                                             ctypes.POINTER(ctypes.c_float)]),
     "cohx_seq_fill_synthetic": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                                ctypes.c_uint64, ctypes.c_uint32]),
     "cohx_step": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Batch), ctypes.POINTER(StepOut)]),
@@ -242,6 +246,9 @@ class Model:
 
     def close(self):
         if getattr(self, "h", None):
+            # generation states hold sequences of this context: release them first
+            for st in list(getattr(self, "_states", ())):
+                st.free()
             lib().cohx_destroy(self.h)
             self.h = None
 
@@ -282,6 +289,13 @@ class Model:
         out = np.zeros((self.seq_length(seq), c["kv_heads"] * c["head_dim"]), np.float32)
         self._check(lib().cohx_seq_read_kv(self.h, seq, layer, 1 if values else 0,
                                            out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+        return out
+
+    def seq_read_kv_rows(self, seq, layer, first, count, values=False):
+        c = self.config
+        out = np.zeros((count, c["kv_heads"] * c["head_dim"]), np.float32)
+        self._check(lib().cohx_seq_read_kv_rows(self.h, seq, layer, 1 if values else 0, first, count,
+                                                out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
         return out
 
     def seq_fill_synthetic(self, seq, rows, seed, stream):
@@ -385,7 +399,11 @@ class Model:
         rc = lib().cohx_gen_begin(self.h, _u32p(p), p.size, ctypes.byref(c),
                                   prior.h if prior is not None else None, ctypes.byref(h))
         self._check(rc)
-        return GenerationState(self, h)
+        st = GenerationState(self, h)
+        if not hasattr(self, "_states"):
+            self._states = weakref.WeakSet()
+        self._states.add(st)
+        return st
 
     def step_batch(self, states):
         arr = (ctypes.c_void_p * len(states))(*[s.h for s in states])
@@ -420,7 +438,8 @@ class GenerationState:
 
     def free(self):
         if getattr(self, "h", None):
-            lib().cohx_gen_free(self.h)
+            if getattr(self.model, "h", None):  # a closed context already released it
+                lib().cohx_gen_free(self.h)
             self.h = None
 
     def needs_forward(self):

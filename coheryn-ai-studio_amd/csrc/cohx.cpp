@@ -66,6 +66,19 @@ int halloc(cohx_ctx *ctx, T **p, size_t count) {
   return COHX_OK;
 }
 
+// Carves one workspace out of `base` (or only counts its bytes when base is
+// null): every buffer starts on a 256-byte boundary.
+struct Carver {
+  uint8_t *base;
+  size_t off = 0;
+  template <typename T>
+  void take(T *&p, size_t count) {
+    off = (off + 255) & ~(size_t)255;
+    p = base ? reinterpret_cast<T *>(base + off) : nullptr;
+    off += std::max<size_t>(count, 1) * sizeof(T);
+  }
+};
+
 // Matrix-core tile view of a Q8_0 matrix with `rows` rows of width K.
 int make_q8(cohx_ctx *ctx, DeviceMatrix &m, int rows, int K, int mtiles) {
   m.view.dtype = 8;
@@ -205,6 +218,60 @@ size_t row_bytes(uint32_t dtype, uint64_t width) {
 
 }  // namespace
 
+namespace cohx {
+size_t layout_workspace(const cohx_model_desc &d, int nbp_h, int nbp_f, uint32_t R, uint32_t NL,
+                        uint32_t kv_cap, bool logits, uint8_t *base, Workspace *out) {
+  const size_t H = d.hidden, F = d.intermediate, V = d.vocabulary, NH = d.heads, NKV = d.kv_heads,
+               D = d.head_dim, KVD = NKV * D;
+  const bool packed = d.weight_dtype != COHX_F16;
+  const size_t rtiles = (R + 15) / 16, nbp_max = (size_t)std::max(nbp_h, nbp_f);
+  const size_t nsc = (kv_cap + 255) / 256, chunks = (kv_cap + kChunk - 1) / kChunk;
+  Workspace tmp;
+  Workspace &w = out ? *out : tmp;
+  w = Workspace();
+  w.rows = R;
+  w.lanes = NL;
+  w.kv_cap = kv_cap;
+  w.max_chunks = (uint32_t)chunks;
+  w.max_tiles = (R + 15) / 16 + NL;
+  w.logits_room = logits;
+  Carver c{base};
+  c.take(w.lane_info, (size_t)NL * 4);
+  c.take(w.tokens, R);
+  c.take(w.cu, NL + 1);
+  c.take(w.row_pos, R);
+  c.take(w.row_slot, R);
+  c.take(w.row_lane, R);
+  c.take(w.row_token, R);
+  c.take(w.row_seq, R);
+  c.take(w.lane_last, NL);
+  c.take(w.row_err, R);
+  c.take(w.x, R * H);
+  c.take(w.qkv, R * (H + 2 * KVD));
+  c.take(w.q_rot, R * H);
+  c.take(w.h, R * F);
+  c.take(w.act_qs, rtiles * nbp_max * 512);
+  c.take(w.act_ds, rtiles * nbp_max * 16);
+  if (packed) {
+    c.take(w.down_qs, rtiles * nbp_f * 512);
+    c.take(w.down_ds, rtiles * nbp_f * 16);
+  }
+  c.take(w.act_f16, R * std::max(H, F));
+  c.take(w.scores, R * NKV * kv_cap * 8);
+  c.take(w.chunk_max, R * NH * nsc);
+  c.take(w.den_part, R * NH * nsc);
+  c.take(w.tiles, w.max_tiles);
+  c.take(w.row_skip, R);
+  c.take(w.row_map, R);
+  c.take(w.direct, R * H);
+  c.take(w.partial, R * NH * chunks * D);
+  if (logits) c.take(w.logits, (size_t)NL * V);
+  c.take(w.argmax, NL);
+  c.take(w.argmax_part, (size_t)NL * ((V + 15) / 16));
+  return (c.off + 255) & ~(size_t)255;
+}
+}  // namespace cohx
+
 extern "C" {
 
 const char *cohx_last_error(const cohx_ctx *ctx) { return ctx ? ctx->err.c_str() : "null context"; }
@@ -305,47 +372,24 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   for (int32_t p = (int32_t)pages - 1; p >= 0; p--) ctx->free_pages.push_back(p);
   ctx->seqs.resize(d->max_seqs);
   for (int32_t s = (int32_t)d->max_seqs - 1; s >= 0; s--) ctx->free_seqs.push_back((uint32_t)s);
-  // step workspaces
-  Workspace &w = ctx->ws;
-  const size_t rtiles = (size_t)(R + 15) / 16;
+  // step workspaces: one device block carved by layout_workspace, and pinned
+  // host staging
+  if (!rc) {
+    const size_t bytes = layout_workspace(*d, ctx->nbp_h, ctx->nbp_f, R, d->max_lanes, d->max_context,
+                                          true, nullptr, nullptr);
+    rc = dalloc(ctx, &ctx->ws_block, bytes);
+    if (!rc)
+      layout_workspace(*d, ctx->nbp_h, ctx->nbp_f, R, d->max_lanes, d->max_context, true, ctx->ws_block,
+                       &ctx->ws);
+  }
+  Staging &h = ctx->host;
   const uint32_t NL = d->max_lanes;
-  if (!rc) rc = dalloc(ctx, &w.lane_info, (size_t)NL * 4);
-  if (!rc) rc = dalloc(ctx, &w.tokens, R);
-  if (!rc) rc = dalloc(ctx, &w.cu, NL + 1);
-  if (!rc) rc = dalloc(ctx, &w.row_pos, R);
-  if (!rc) rc = dalloc(ctx, &w.row_slot, R);
-  if (!rc) rc = dalloc(ctx, &w.row_lane, R);
-  if (!rc) rc = dalloc(ctx, &w.row_token, R);
-  if (!rc) rc = dalloc(ctx, &w.row_seq, R);
-  if (!rc) rc = dalloc(ctx, &w.lane_last, NL);
-  if (!rc) rc = dalloc(ctx, &w.row_err, R);
-  if (!rc) rc = dalloc(ctx, &w.x, (size_t)R * H);
-  if (!rc) rc = dalloc(ctx, &w.qkv, (size_t)R * (H + 2 * KVD));
-  if (!rc) rc = dalloc(ctx, &w.q_rot, (size_t)R * H);
-  if (!rc) rc = dalloc(ctx, &w.h, (size_t)R * F);
-  if (!rc) rc = dalloc(ctx, &w.act_qs, rtiles * ctx->nbp_max * 512);
-  if (!rc) rc = dalloc(ctx, &w.act_ds, rtiles * ctx->nbp_max * 16);
-  if (!rc && packed) rc = dalloc(ctx, &w.down_qs, rtiles * ctx->nbp_f * 512);
-  if (!rc && packed) rc = dalloc(ctx, &w.down_ds, rtiles * ctx->nbp_f * 16);
-  if (!rc) rc = dalloc(ctx, &w.act_f16, (size_t)R * std::max(H, F));
-  if (!rc) rc = dalloc(ctx, &w.scores, (size_t)R * NKV * d->max_context * 8);
-  if (!rc) rc = dalloc(ctx, &w.chunk_max, (size_t)R * NH * ((d->max_context + 255) / 256));
-  if (!rc) rc = dalloc(ctx, &w.den_part, (size_t)R * NH * ((d->max_context + 255) / 256));
-  w.max_tiles = (R + 15) / 16 + (int)d->max_lanes;
-  if (!rc) rc = dalloc(ctx, &w.tiles, (size_t)w.max_tiles);
-  if (!rc) rc = dalloc(ctx, &w.row_skip, (size_t)R);
-  if (!rc) rc = dalloc(ctx, &w.row_map, (size_t)R);
-  if (!rc) rc = dalloc(ctx, &w.direct, (size_t)R * H);
-  if (!rc) rc = halloc(ctx, &w.h_tiles, (size_t)w.max_tiles);
-  if (!rc) rc = halloc(ctx, &w.h_row_skip, (size_t)R);
-  if (!rc) rc = halloc(ctx, &w.h_row_map, (size_t)R);
-  if (!rc) rc = dalloc(ctx, &w.partial, (size_t)R * NH * ctx->max_chunks * D);
-  if (!rc) rc = dalloc(ctx, &w.logits, (size_t)NL * V);
-  if (!rc) rc = dalloc(ctx, &w.argmax, NL);
-  if (!rc) rc = dalloc(ctx, &w.argmax_part, (size_t)NL * ((V + 15) / 16));
-  if (!rc) rc = halloc(ctx, &w.h_upload, (size_t)NL * 4 + R);
-  if (!rc) rc = halloc(ctx, &w.h_row_err, R);
-  if (!rc) rc = halloc(ctx, &w.h_argmax, NL);
+  if (!rc) rc = halloc(ctx, &h.h_tiles, (size_t)ctx->ws.max_tiles);
+  if (!rc) rc = halloc(ctx, &h.h_row_skip, (size_t)R);
+  if (!rc) rc = halloc(ctx, &h.h_row_map, (size_t)R);
+  if (!rc) rc = halloc(ctx, &h.h_upload, (size_t)NL * 4 + R);
+  if (!rc) rc = halloc(ctx, &h.h_row_err, R);
+  if (!rc) rc = halloc(ctx, &h.h_argmax, NL);
   if (rc) return bail(rc);
   *out = ctx;
   return COHX_OK;
@@ -357,12 +401,9 @@ void cohx_destroy(cohx_ctx *ctx) {
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   drop_graphs(ctx);
   for (void *p : ctx->allocations) (void)hipFree(p);
-  if (ctx->ws.h_upload) (void)hipHostFree(ctx->ws.h_upload);
-  if (ctx->ws.h_row_err) (void)hipHostFree(ctx->ws.h_row_err);
-  if (ctx->ws.h_argmax) (void)hipHostFree(ctx->ws.h_argmax);
-  if (ctx->ws.h_tiles) (void)hipHostFree(ctx->ws.h_tiles);
-  if (ctx->ws.h_row_skip) (void)hipHostFree(ctx->ws.h_row_skip);
-  if (ctx->ws.h_row_map) (void)hipHostFree(ctx->ws.h_row_map);
+  for (void *p : {(void *)ctx->host.h_upload, (void *)ctx->host.h_row_err, (void *)ctx->host.h_argmax,
+                  (void *)ctx->host.h_tiles, (void *)ctx->host.h_row_skip, (void *)ctx->host.h_row_map})
+    if (p) (void)hipHostFree(p);
   q35_free(ctx);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -630,6 +671,34 @@ uint32_t cohx_seq_pages(const cohx_ctx *ctx, uint32_t seq, int32_t *out, uint32_
   return n;
 }
 
+int cohx_seq_read_kv_rows(cohx_ctx *ctx, uint32_t seq, uint32_t layer, int values, uint32_t first,
+                          uint32_t count, float *out) {
+  if (ctx && ctx->q35) return fail(ctx, COHX_UNSUPPORTED, "row ranges are for paged Qwen2 contexts");
+  if (!ctx || !valid_seq(ctx, seq) || layer >= ctx->desc.layers || (!out && count))
+    return COHX_INVALID_REQUEST;
+  const Sequence &q = ctx->seqs[seq];
+  if ((uint64_t)first + count > q.length) return fail(ctx, COHX_INVALID_REQUEST, "rows beyond the length");
+  HIP_TRY(hipSetDevice(ctx->device));
+  const int NKV = ctx->desc.kv_heads, D = ctx->desc.head_dim;
+  const float *pool = (values ? ctx->vpool : ctx->kpool) + (size_t)layer * ctx->layer_stride;
+  std::vector<float> page((size_t)NKV * kPage * D);
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  const uint32_t end = first + count;
+  for (uint32_t i = first / kPage; i * kPage < end; i++) {
+    HIP_TRY(hipMemcpy(page.data(), pool + (size_t)q.pages[i] * page.size(),
+                      page.size() * sizeof(float), hipMemcpyDeviceToHost));
+    for (uint32_t o = 0; o < (uint32_t)kPage; o++) {
+      const uint32_t pos = i * kPage + o;
+      if (pos < first || pos >= end) continue;
+      for (int g = 0; g < NKV; g++)
+        for (int j = 0; j < D; j++)
+          out[((size_t)(pos - first) * NKV + g) * D + j] =
+              page[values ? v_at(0, g, NKV, (int)o, j, D) : k_at(0, i, g, NKV, (int)o, j, D)];
+    }
+  }
+  return COHX_OK;
+}
+
 int cohx_seq_read_kv(cohx_ctx *ctx, uint32_t seq, uint32_t layer, int values, float *out) {
   if (!ctx || !valid_seq(ctx, seq) || layer >= ctx->desc.layers || !out)
     return COHX_INVALID_REQUEST;
@@ -637,22 +706,7 @@ int cohx_seq_read_kv(cohx_ctx *ctx, uint32_t seq, uint32_t layer, int values, fl
     (void)hipSetDevice(ctx->device);
     return q35_read_state(ctx, seq, layer, values, out);
   }
-  HIP_TRY(hipSetDevice(ctx->device));
-  const Sequence &q = ctx->seqs[seq];
-  const int NKV = ctx->desc.kv_heads, D = ctx->desc.head_dim;
-  const float *pool = (values ? ctx->vpool : ctx->kpool) + (size_t)layer * ctx->layer_stride;
-  std::vector<float> page((size_t)NKV * kPage * D);
-  HIP_TRY(hipStreamSynchronize(ctx->stream));
-  for (size_t i = 0; i * kPage < q.length; i++) {
-    HIP_TRY(hipMemcpy(page.data(), pool + (size_t)q.pages[i] * page.size(),
-                      page.size() * sizeof(float), hipMemcpyDeviceToHost));
-    for (int o = 0; o < kPage && i * kPage + o < q.length; o++)
-      for (int g = 0; g < NKV; g++)
-        for (int j = 0; j < D; j++)
-          out[((i * kPage + o) * NKV + g) * D + j] =
-              page[values ? v_at(0, g, NKV, o, j, D) : k_at(0, (uint32_t)i, g, NKV, o, j, D)];
-  }
-  return COHX_OK;
+  return cohx_seq_read_kv_rows(ctx, seq, layer, values, 0, ctx->seqs[seq].length, out);
 }
 
 int cohx_seq_fill_synthetic(cohx_ctx *ctx, uint32_t seq, uint32_t rows, uint64_t seed,
@@ -704,14 +758,16 @@ struct Prepared {
   bool single_token = true;   // every lane carries one token (a pure decode step)
 };
 
-// Host validation (batch.rs:119-131) and upload of the device batch.
-int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, Prepared &p) {
+// Host validation (batch.rs:119-131) and upload of the device batch into w.
+int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, Prepared &p,
+                  Workspace &w) {
   const cohx_model_desc &d = ctx->desc;
   if (!batch || batch->n_lanes == 0 || batch->n_lanes > d.max_lanes || !batch->lanes)
     return fail(ctx, COHX_INVALID_REQUEST,
                 "batch width must be in 1..=" + std::to_string(d.max_lanes));
   if (!ctx->finalized) return fail(ctx, COHX_INVALID_REQUEST, "model tensors not finalized");
-  uint32_t *info = ctx->ws.h_upload;
+  Staging &hs = ctx->host;
+  uint32_t *info = hs.h_upload;
   uint32_t *toks = info + (size_t)d.max_lanes * 4;
   // duplicate sequences within one step are a shared failure
   for (uint32_t i = 0; i < batch->n_lanes; i++)
@@ -765,8 +821,7 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
   p.n_exact = p.rows;
   p.max_kv_exact = p.max_kv;
   if (regime) {
-    Workspace &w = ctx->ws;
-    std::memset(w.h_row_skip, 0, p.rows * sizeof(uint32_t));
+    std::memset(hs.h_row_skip, 0, p.rows * sizeof(uint32_t));
     for (size_t k = 0; k < n; k++) {
       const uint32_t nt = info[k * 4 + 0], start = info[k * 4 + 1], seq = info[k * 4 + 2],
                      row0 = info[k * 4 + 3];
@@ -776,10 +831,10 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
       }
       p.kv_chunk_lanes += start + nt;
       for (uint32_t t = 0; t < nt; t += 16) {
-        w.h_tiles[p.n_tiles++] = int4{(int)(row0 + t), (int)std::min(16u, nt - t), (int)seq,
-                                      (int)(start + t)};
+        hs.h_tiles[p.n_tiles++] = int4{(int)(row0 + t), (int)std::min(16u, nt - t), (int)seq,
+                                       (int)(start + t)};
         for (uint32_t j = t; j < std::min(nt, t + 16); j++) {
-          w.h_row_skip[row0 + j] = 1;
+          hs.h_row_skip[row0 + j] = 1;
           p.kv_rows_chunk += (uint64_t)start + j + 1;
         }
       }
@@ -787,37 +842,34 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
     if (!p.n_tiles) p.max_kv_exact = p.max_kv;
     if (p.n_tiles) {
       // longest KV first, so the short tiles fill in behind the long ones
-      std::stable_sort(w.h_tiles, w.h_tiles + p.n_tiles,
+      std::stable_sort(hs.h_tiles, hs.h_tiles + p.n_tiles,
                        [](const int4 &a, const int4 &b) { return a.w + a.y > b.w + b.y; });
       p.n_exact = 0;
       for (uint32_t r = 0; r < p.rows; r++)
-        if (!w.h_row_skip[r]) w.h_row_map[p.n_exact++] = r;
-      HIP_TRY(hipMemcpyAsync(w.tiles, w.h_tiles, p.n_tiles * sizeof(int4), hipMemcpyHostToDevice,
+        if (!hs.h_row_skip[r]) hs.h_row_map[p.n_exact++] = r;
+      HIP_TRY(hipMemcpyAsync(w.tiles, hs.h_tiles, p.n_tiles * sizeof(int4), hipMemcpyHostToDevice,
                              ctx->stream));
-      HIP_TRY(hipMemcpyAsync(w.row_skip, w.h_row_skip, p.rows * sizeof(uint32_t),
+      HIP_TRY(hipMemcpyAsync(w.row_skip, hs.h_row_skip, p.rows * sizeof(uint32_t),
                              hipMemcpyHostToDevice, ctx->stream));
       if (p.n_exact)
-        HIP_TRY(hipMemcpyAsync(w.row_map, w.h_row_map, p.n_exact * sizeof(uint32_t),
+        HIP_TRY(hipMemcpyAsync(w.row_map, hs.h_row_map, p.n_exact * sizeof(uint32_t),
                                hipMemcpyHostToDevice, ctx->stream));
     }
   }
-  HIP_TRY(hipMemcpyAsync(ctx->ws.lane_info, info, n * 4 * sizeof(uint32_t), hipMemcpyHostToDevice,
+  HIP_TRY(hipMemcpyAsync(w.lane_info, info, n * 4 * sizeof(uint32_t), hipMemcpyHostToDevice,
                          ctx->stream));
-  HIP_TRY(hipMemcpyAsync(ctx->ws.tokens, toks, p.rows * sizeof(uint32_t), hipMemcpyHostToDevice,
+  HIP_TRY(hipMemcpyAsync(w.tokens, toks, p.rows * sizeof(uint32_t), hipMemcpyHostToDevice,
                          ctx->stream));
   return COHX_OK;
 }
 
 // The device packer over the uploaded lanes (ragged rows, positions, slots).
-void enqueue_pack(cohx_ctx *ctx, int n_lanes) {
-  Workspace &w = ctx->ws;
+void enqueue_pack(cohx_ctx *ctx, const Workspace &w, int n_lanes) {
   launch_pack(ctx->stream, n_lanes, w.lane_info, w.tokens, ctx->page_table, ctx->max_pages, w.cu,
               w.row_pos, w.row_slot, w.row_lane, w.row_token, w.row_seq, w.lane_last, w.row_err);
 }
 
-ActView act_view(cohx_ctx *ctx) {
-  return ActView{ctx->ws.act_qs, ctx->ws.act_ds, ctx->ws.act_f16};
-}
+ActView act_view(const Workspace &w) { return ActView{w.act_qs, w.act_ds, w.act_f16}; }
 
 }  // namespace
 
@@ -828,14 +880,14 @@ extern "C" int cohx_pack(cohx_ctx *ctx, const cohx_batch *batch, uint32_t *cu, u
   HIP_TRY(hipSetDevice(ctx->device));
   Prepared p;
   std::vector<cohx_lane_out> outs(batch ? batch->n_lanes : 0);
-  int rc = prepare_batch(ctx, batch, outs.data(), p);
+  Workspace &w = ctx->ws;
+  int rc = prepare_batch(ctx, batch, outs.data(), p, w);
   if (rc) return rc;
   if (p.included.size() != batch->n_lanes)
     return fail(ctx, COHX_INVALID_REQUEST, "a lane failed validation");
-  enqueue_pack(ctx, (int)p.included.size());
+  enqueue_pack(ctx, w, (int)p.included.size());
   HIP_TRY(hipGetLastError());
   std::vector<int32_t> slot32(p.rows);
-  Workspace &w = ctx->ws;
   HIP_TRY(hipMemcpyAsync(cu, w.cu, (batch->n_lanes + 1) * 4, hipMemcpyDeviceToHost, ctx->stream));
   HIP_TRY(hipMemcpyAsync(positions, w.row_pos, p.rows * 4, hipMemcpyDeviceToHost, ctx->stream));
   HIP_TRY(hipMemcpyAsync(slot32.data(), w.row_slot, p.rows * 4, hipMemcpyDeviceToHost, ctx->stream));
@@ -928,11 +980,11 @@ extern "C" uint32_t cohx_profile_read(const cohx_ctx *ctx, cohx_kernel_stat *out
 // the layers, final norm, LM head and argmax.  Launch-only (no host waits), so
 // it can be captured into a graph.  kv_grid (>= the longest attended length)
 // sizes the attention grids; blocks past a row's length exit at once.
-int enqueue_device_step(cohx_ctx *ctx, const Prepared &p, int kv_grid, bool any_logits) {
+int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_grid, bool any_logits) {
   const cohx_model_desc &d = ctx->desc;
   set_prefill_mfma(ctx->prefill_mfma);
   const int pk = prof_begin(ctx, kCatPack, 0.0, 0.0);
-  enqueue_pack(ctx, (int)p.included.size());
+  enqueue_pack(ctx, w, (int)p.included.size());
   prof_end(ctx, pk);
   const int R = (int)p.rows, NL = (int)p.included.size();
   const int H = d.hidden, F = d.intermediate, NH = d.heads, NKV = d.kv_heads, D = d.head_dim,
@@ -940,15 +992,14 @@ int enqueue_device_step(cohx_ctx *ctx, const Prepared &p, int kv_grid, bool any_
   // packed weights (Q8_0, Q4_0) take Q8_0 activation blocks (quant.rs:181-183)
   const int act_dtype = d.weight_dtype == COHX_F16 ? 1 : 8;
   const double act_row = act_dtype == 8 ? (double)H / 32 * 34 : (double)H * 2;
-  Workspace &w = ctx->ws;
   hipStream_t s = ctx->stream;
   StepDims sd{H, F, (int)d.vocabulary, NH, NKV, D, KVD, NH / NKV, d.norm_epsilon,
-              1.0f / sqrtf((float)D), ctx->max_pages, (int)d.max_context, ctx->max_chunks,
+              1.0f / sqrtf((float)D), ctx->max_pages, (int)w.kv_cap, (int)w.max_chunks,
               p.n_tiles ? w.row_skip : nullptr, p.n_tiles ? w.direct : nullptr,
               p.n_tiles ? w.row_map : nullptr};
   const int RX = (int)p.n_exact;  // rows of the exact attention passes
   if (p.n_tiles) kv_grid = (int)((p.max_kv_exact + 255) / 256 * 256);
-  const ActView act = act_view(ctx);
+  const ActView act = act_view(w);
   // attended positions summed over the exact passes' rows and the tiles' rows
   const double kv_rows = (double)(p.kv_rows_read - p.kv_rows_chunk);
   const double kv_chunk = (double)p.kv_rows_chunk;
@@ -1030,14 +1081,17 @@ int enqueue_device_step(cohx_ctx *ctx, const Prepared &p, int kv_grid, bool any_
     // Q8_0/Q4_0 at K <= 1024: the SwiGLU quantizer runs in gate+up's
     // epilogue into the down operand buffer; otherwise its own pass
     const ActView down_act{w.down_qs, w.down_ds, nullptr};
-    const bool fused_quant = w.down_qs && ly.gu.view.nbp <= 32 && F % 64 == 0;
-    if (fused_quant) {
+    bool fused_quant = false;
+    if (w.down_qs) {
       e = prof_begin(ctx, kCatMvGateUp,
                      matrix_pass_bytes(ly.gu.view, R, 0, false) + (double)R * F / 32 * 34, 2.0 * R * 2 * F * H);
-      launch_matvec_swiglu_q8(s, ly.gu.view, act, R,
-                              MatvecOut{nullptr, 0, nullptr, nullptr, w.row_err, nullptr}, down_act);
+      // false (nothing launched) for shapes the fused quantizer does not cover
+      fused_quant = launch_matvec_swiglu_q8(s, ly.gu.view, act, R,
+                                            MatvecOut{nullptr, 0, nullptr, nullptr, w.row_err, nullptr},
+                                            down_act, ly.down.view.nbp);
       prof_end(ctx, e);
-    } else {
+    }
+    if (!fused_quant) {
       e = prof_begin(ctx, kCatMvGateUp, matrix_pass_bytes(ly.gu.view, R, F, false), 2.0 * R * 2 * F * H);
       launch_matvec(s, kEpiSwiglu, ly.gu.view, act, R,
                     MatvecOut{w.h, F, nullptr, nullptr, w.row_err, nullptr});
@@ -1070,14 +1124,16 @@ int enqueue_device_step(cohx_ctx *ctx, const Prepared &p, int kv_grid, bool any_
   return COHX_OK;
 }
 
-extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
-  if (ctx && ctx->q35) return q35_step(ctx, batch, out);
-  if (!ctx || !out || !out->lanes) return COHX_INVALID_REQUEST;
+namespace {
+
+// One ragged step over `batch` with its device scratch in w.  graphs: decode
+// steps may replay a captured graph (the buffers in w must then stay fixed).
+int run_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out, Workspace &w, bool graphs) {
   const auto t_start = std::chrono::steady_clock::now();
   HIP_TRY(hipSetDevice(ctx->device));
   const cohx_model_desc &d = ctx->desc;
   Prepared p;
-  int rc = prepare_batch(ctx, batch, out->lanes, p);
+  int rc = prepare_batch(ctx, batch, out->lanes, p, w);
   if (rc) {
     ctx->prof.pending.clear();
     ctx->prof.next = 0;
@@ -1095,15 +1151,16 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
   }
   const int R = (int)p.rows, NL = (int)p.included.size();
   const int KVD = d.kv_heads * d.head_dim;
-  Workspace &w = ctx->ws;
   hipStream_t s = ctx->stream;
+  const Staging &hs = ctx->host;
   bool any_logits = false;
   for (int k = 0; k < NL; k++)
     if (batch->lanes[p.included[k]].want_logits == 1u && out->lanes[p.included[k]].logits)
       any_logits = true;
+  if (any_logits && !w.logits) return fail(ctx, COHX_RESOURCE, "the workspace has no room for logits");
   const int kv_grid = (int)((p.max_kv + 255) / 256 * 256);
-  if (ctx->prof.on || !ctx->use_graphs || !p.single_token) {
-    rc = enqueue_device_step(ctx, p, kv_grid, any_logits);
+  if (ctx->prof.on || !graphs || !p.single_token) {
+    rc = enqueue_device_step(ctx, w, p, kv_grid, any_logits);
     if (rc) return rc;
   } else {
     const StepKey key{(uint32_t)R, (uint32_t)NL, (uint32_t)kv_grid, any_logits};
@@ -1112,7 +1169,7 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
       if (ctx->graphs.size() >= kMaxGraphs) drop_graphs(ctx);
       hipGraph_t g = nullptr;
       HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-      rc = enqueue_device_step(ctx, p, kv_grid, any_logits);
+      rc = enqueue_device_step(ctx, w, p, kv_grid, any_logits);
       const hipError_t ec = hipStreamEndCapture(s, &g);
       if (rc || ec != hipSuccess) {
         if (g) (void)hipGraphDestroy(g);
@@ -1126,9 +1183,9 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
     }
     HIP_TRY(hipGraphLaunch(it->second, s));
   }
-  HIP_TRY(hipMemcpyAsync(w.h_argmax, w.argmax, NL * sizeof(unsigned long long),
+  HIP_TRY(hipMemcpyAsync(hs.h_argmax, w.argmax, NL * sizeof(unsigned long long),
                          hipMemcpyDeviceToHost, s));
-  HIP_TRY(hipMemcpyAsync(w.h_row_err, w.row_err, R * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipMemcpyAsync(hs.h_row_err, w.row_err, R * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
   for (int k = 0; k < NL; k++) {
     const cohx_lane &ln = batch->lanes[p.included[k]];
     float *dst = out->lanes[p.included[k]].logits;
@@ -1144,10 +1201,10 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
     const int i = p.included[k];
     const cohx_lane &ln = batch->lanes[i];
     uint32_t bits = 0;
-    for (uint32_t j = 0; j < ln.n_tokens; j++) bits |= w.h_row_err[row + j];
+    for (uint32_t j = 0; j < ln.n_tokens; j++) bits |= hs.h_row_err[row + j];
     row += ln.n_tokens;
     cohx_lane_out &o = out->lanes[i];
-    o.argmax = 0xffffffffu - (uint32_t)(w.h_argmax[k] & 0xffffffffull);
+    o.argmax = 0xffffffffu - (uint32_t)(hs.h_argmax[k] & 0xffffffffull);
     if (bits & kErrPage)
       o.status = COHX_RESOURCE;
     else if (bits)
@@ -1165,4 +1222,12 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
                         std::chrono::steady_clock::now() - t_start)
                         .count();
   return COHX_OK;
+}
+
+}  // namespace
+
+extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
+  if (ctx && ctx->q35) return q35_step(ctx, batch, out);
+  if (!ctx || !out || !out->lanes) return COHX_INVALID_REQUEST;
+  return run_step(ctx, batch, out, ctx->ws, ctx->use_graphs);
 }

@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "expf.h"
+
 namespace cohx {
 
 constexpr int kWave = 64;
@@ -21,54 +23,9 @@ constexpr uint32_t kErrPage = 4u;       // Error::resource (slot outside the pag
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// ---------------------------------------------------------------------------
-// exp for binary32 with the same results as glibc's expf on x86-64, which is
-// what the engine's f32::exp calls on Linux.  Method: Szabolcs Nagy's exp2
-// table reduction (ARM optimized-routines, glibc >= 2.28 e_expf.c):
-// x*32/ln2 = k + r, 2^(k/32) from a 32-entry table, a cubic in r, all in
-// binary64, one final rounding.  Table entries are asuint64(2^(i/32)) - (i<<47)
-// with 2^(i/32) correctly rounded (derived independently in high precision);
-// the reduction uses fused multiply-adds, matching the FMA build that glibc
-// selects on CPUs with FMA.  Agreement with the host libm was checked on all
-// 2^32 inputs.
-// ---------------------------------------------------------------------------
-__constant__ static const uint64_t kExp2Tab[32] = {
-    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
-    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
-    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
-    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
-    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
-    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
-    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
-    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
-
-// expf with the 2^(i/32) table read from `tab`: kExp2Tab itself, or a copy
-// a kernel has staged in LDS (a per-lane indexed constant load is a memory
-// round trip per call; an LDS read is not).
-__device__ __forceinline__ float exp_f32_tab(float x, const uint64_t *tab) {
-  uint32_t ux = __float_as_uint(x);
-  uint32_t abstop = (ux >> 20) & 0x7ffu;
-  if (abstop >= 0x42bu) {  // |x| >= 88 or nan
-    if (ux == 0xff800000u) return 0.0f;
-    if (abstop >= 0x7f8u) return x + x;
-    if (x > 0x1.62e42ep6f) return __builtin_inff();
-    if (x < -0x1.9fe368p6f) return 0.0f;
-  }
-  const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
-  const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
-               c2 = 0x1.62e42ff0c52d6p-1 / 32;
-  double xd = (double)x;
-  double kd = __fma_rn(inv_ln2_n, xd, shift);
-  uint64_t ki = (uint64_t)__double_as_longlong(kd);
-  kd -= shift;
-  double r = __fma_rn(inv_ln2_n, xd, -kd);
-  uint64_t t = tab[ki % 32] + (ki << 47);
-  double s = __longlong_as_double((long long)t);
-  double z = __fma_rn(c0, r, c1), r2 = r * r, y = __fma_rn(c2, r, 1.0);
-  y = __fma_rn(z, r2, y);
-  y = y * s;
-  return (float)y;
-}
+// glibc-identical expf (expf.h); the table in constant memory for kernels
+// that do not stage it in LDS.
+__constant__ static const uint64_t kExp2Tab[32] = COHX_EXP2_TABLE;
 __device__ __forceinline__ float exp_f32(float x) { return exp_f32_tab(x, kExp2Tab); }
 
 // binary16 <-> binary32 (round to nearest even; the `half` crate contract).

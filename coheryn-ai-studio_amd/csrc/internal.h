@@ -32,6 +32,8 @@ struct Sequence {
   std::vector<int32_t> pages;  // logical page -> physical page
 };
 
+// Device scratch of one step, carved from one block of device memory by
+// layout_workspace (the context's own block, sized for its capacities).
 struct Workspace {
   uint32_t *lane_info = nullptr, *tokens = nullptr;
   uint32_t *cu = nullptr, *row_pos = nullptr, *row_lane = nullptr, *row_token = nullptr,
@@ -44,9 +46,9 @@ struct Workspace {
   int8_t *down_qs = nullptr;
   uint16_t *down_ds = nullptr;
   uint16_t *act_ds = nullptr, *act_f16 = nullptr;
-  float *scores = nullptr;  // [rows][kv_heads][max_context][8]: scores, then weights
+  float *scores = nullptr;  // [rows][kv_heads][kv_cap][8]: scores, then weights
   float *chunk_max = nullptr, *logits = nullptr;
-  double *partial = nullptr;
+  double *partial = nullptr;   // [rows][heads][max_chunks][head_dim]
   double *den_part = nullptr;  // [rows][heads][256-token chunks] softmax denominator partials
   // prefill chunks on the matrix cores: 16-row tiles, per-row flags, f32
   // output, and the list of rows left to the exact attention passes
@@ -54,17 +56,28 @@ struct Workspace {
   uint32_t *row_skip = nullptr;
   uint32_t *row_map = nullptr;
   float *direct = nullptr;
-  int max_tiles = 0;
   unsigned long long *argmax = nullptr;
-  unsigned long long *argmax_part = nullptr;  // [max_lanes][head m-tiles]
-  // pinned host staging
+  unsigned long long *argmax_part = nullptr;  // [lanes][head m-tiles]
+  // capacities the buffers were laid out for
+  uint32_t rows = 0, lanes = 0, kv_cap = 0, max_chunks = 0, max_tiles = 0;
+  bool logits_room = false;
+};
+
+// Pinned host staging of a context (uploads of the batch, read-back of results).
+struct Staging {
   uint32_t *h_upload = nullptr;  // lane_info then tokens
   uint32_t *h_row_err = nullptr;
-  int4 *h_tiles = nullptr;        // pinned staging for tiles, row flags and the row list
+  int4 *h_tiles = nullptr;        // tiles, row flags and the row list of the prefill regime
   uint32_t *h_row_skip = nullptr;
   uint32_t *h_row_map = nullptr;
   unsigned long long *h_argmax = nullptr;
 };
+
+// Bytes of a workspace for `rows` packed rows, `lanes` lanes and attention over
+// at most kv_cap positions (logits: room for every lane's logits); with a
+// non-null base, also fills `w` with buffers carved from it (256-byte aligned).
+size_t layout_workspace(const cohx_model_desc &d, int nbp_h, int nbp_f, uint32_t rows, uint32_t lanes,
+                        uint32_t kv_cap, bool logits, uint8_t *base, Workspace *w);
 
 enum ProfCat {
   kCatPack, kCatEmbed, kCatNorm, kCatMvQkv, kCatQkvPost, kCatAttnScores, kCatAttnSoftmax,
@@ -125,7 +138,9 @@ struct cohx_ctx {
   std::vector<std::string> uploaded;
   bool finalized = false;
   uint64_t matrix_bytes = 0;
-  cohx::Workspace ws;
+  cohx::Workspace ws;      // laid out for max_rows / max_lanes / max_context
+  uint8_t *ws_block = nullptr;
+  cohx::Staging host;
   cohx::Profiler prof;
   std::vector<void *> allocations;
   bool use_graphs = true;    // replay each step's launches as one captured graph

@@ -72,12 +72,14 @@ void set_launch_events(hipEvent_t start, hipEvent_t stop);
 void launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActView &act,
                    int rows_b, const MatvecOut &o);
 // Q8_0/Q4_0 gate+up with the SwiGLU quantizer in its epilogue: writes the
-// down projection's Q8_0 operand to qout (which must not alias act) instead
-// of the f32 SwiGLU rows; the same bits as launch_matvec (kEpiSwiglu) then
+// down projection's Q8_0 operand to qout (which must not alias act; laid out
+// with qout_nbp block pairs per row, the down projection's) instead of the
+// f32 SwiGLU rows; the same bits as launch_matvec (kEpiSwiglu) then
 // launch_quant_act.  Returns false (nothing launched) for shapes it does not
-// cover: K > 1024 or F not a multiple of 64.
+// cover: K > 1024, F not a multiple of 64, or qout_nbp not F/32 rounded up
+// to even.
 bool launch_matvec_swiglu_q8(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
-                             const MatvecOut &o, const ActView &qout);
+                             const MatvecOut &o, const ActView &qout, int qout_nbp);
 void launch_argmax_reduce(hipStream_t s, int rows, const unsigned long long *part, int units,
                           unsigned long long *out);
 // Q8_0/Q4_0 qkv projection with launch_qkv_post's work in its epilogue (bias,

@@ -776,7 +776,7 @@ __global__ __launch_bounds__(64 * kChainWaves) void k_mv_q8c(MatrixView w, ActVi
 // ---------------------------------------------------------------------------
 template <int kEpi, int kNM, int kFmt, int kMaxPairs, int kU>
 __global__ __launch_bounds__(512 * kU) void k_mv_q8w(MatrixView w, ActView act, int rows_b, int n_tiles,
-                                                     MatvecOut o, ActView qout) {
+                                                     MatvecOut o, ActView qout, int qout_nbp) {
   static_assert(kU == 1 || (kU == 2 && kEpi == kEpiSwiglu), "two units per workgroup: the fused quantizer");
   constexpr int kPairBytes = kFmt == 8 ? 1024 : 512;  // weight bytes per tile per block pair
   constexpr int kCopy = 8;                            // 16-byte copy items per thread (<= 64 KB)
@@ -907,7 +907,7 @@ __global__ __launch_bounds__(512 * kU) void k_mv_q8w(MatrixView w, ActView act, 
         const int el = 8 * k + e;
         v[e] = s_h[(((el / 16) * 8 + bt) * 16 + el % 16) * 16 + col];
       }
-      bad |= quant_group_q8<16>(v, rvalid, r, blockIdx.x * 4 + k, (w.rows / 64 + 1) & ~1, qout);
+      bad |= quant_group_q8<16>(v, rvalid, r, blockIdx.x * 4 + k, qout_nbp, qout);
     }
   } else if (kEpi == kEpiSwiglu) {
 #pragma unroll
@@ -2189,7 +2189,7 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
     const size_t lds = (size_t)kNM * (w.nbp / 2) * (kFmt == 8 ? 1024 : 512) + (size_t)kNM * w.nbp * 32 +
                        (size_t)8 * w.nbp * 32;
     launch_k((k_mv_q8w<kEpi, kNM, kFmt, kWPairs, 1>), dim3(units, by), dim3(nthreads), lds, s, w, act, rows_b,
-             n_tiles, o, ActView{});
+             n_tiles, o, ActView{}, 0);
   } else if (kEpi == kEpiArgmax && kNM == 1 && n_tiles <= 8 && w.nbp <= 2 * kWPairs) {
     // LM head: persistent workgroups streaming weight tiles through LDS, two
     // per CU (4 waves per SIMD); always 8 waves, since the tile copy needs
@@ -2294,10 +2294,12 @@ void launch_matvec_qkv(hipStream_t s, const MatrixView &w, const ActView &act, i
 }
 
 bool launch_matvec_swiglu_q8(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
-                             const MatvecOut &o, const ActView &qout) {
+                             const MatvecOut &o, const ActView &qout, int qout_nbp) {
   constexpr int kWPairs = 16;
   const int F = w.rows / 2, n_tiles = (rows_b + 15) / 16;
   if ((w.dtype != 8 && w.dtype != 2) || w.nbp > 2 * kWPairs || F % 64 != 0) return false;
+  // the epilogue writes whole block pairs of the down projection's operand
+  if (qout_nbp != ((F / 32 + 1) & ~1)) return false;
   const int groups = w.mtiles / 4;  // pairs of (gate, up) tile units: one Q8_0 block each
   const int by = (n_tiles + 7) / 8, nthreads = 2 * 64 * (n_tiles < 8 ? n_tiles : 8);
   const size_t pair_bytes = w.dtype == 8 ? 1024 : 512;
@@ -2307,10 +2309,10 @@ bool launch_matvec_swiglu_q8(hipStream_t s, const MatrixView &w, const ActView &
   const size_t lds = copy > 2 * 8 * 256 * 4 ? copy : 2 * 8 * 256 * 4;
   if (w.dtype == 8)
     launch_k((k_mv_q8w<kEpiSwiglu, 2, 8, kWPairs, 2>), dim3(groups, by), dim3(nthreads), lds, s, w, act, rows_b,
-             n_tiles, o, qout);
+             n_tiles, o, qout, qout_nbp);
   else
     launch_k((k_mv_q8w<kEpiSwiglu, 2, 2, kWPairs, 2>), dim3(groups, by), dim3(nthreads), lds, s, w, act, rows_b,
-             n_tiles, o, qout);
+             n_tiles, o, qout, qout_nbp);
   return true;
 }
 

@@ -94,6 +94,11 @@ uint32_t cohx_seq_pages(const cohx_ctx *ctx, uint32_t seq, int32_t *out, uint32_
 /* Copy one layer's K (values=0) or V (values=1) rows [0, length) to host,
  * kv_heads*head_dim floats per row. */
 int cohx_seq_read_kv(cohx_ctx *ctx, uint32_t seq, uint32_t layer, int values, float *out);
+/* The same for rows [first, first + count) only (first + count <= length);
+ * copies just the pages those rows occupy.  Test utility; the engine keeps
+ * its KV rows in host memory (inference.rs:1019-1043). */
+int cohx_seq_read_kv_rows(cohx_ctx *ctx, uint32_t seq, uint32_t layer, int values, uint32_t first,
+                          uint32_t count, float *out);
 /* Benchmark/test utility with no engine counterpart: fill rows [length, rows)
  * of every layer with seeded values hash(seed, stream, layer, K/V, pos, elem)
  * on the device and set the length to `rows` (rows >= length; on a fresh

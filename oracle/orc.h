@@ -114,11 +114,13 @@ int orc_session_truncate(orc_session *s, uint32_t rows);
 /* Copy one layer's K or V rows [0, position) out (kv_heads*head_dim floats per row). */
 int orc_session_kv(const orc_model *m, const orc_session *s, uint32_t layer, int values,
                    float *out);
-/* Seeded synthetic cache rows [0, rows) for every layer; sets position = rows.
- * Value = hash(seed, stream, layer, K/V, position, element) mapped onto
- * multiples of 2^-23 in [-1, 1). */
+/* Seeded synthetic cache value = hash(seed, stream, layer, K/V, position,
+ * element) mapped onto multiples of 2^-23 in [-1, 1). */
 float orc_synthetic_kv(uint64_t seed, uint32_t stream, uint32_t layer, uint32_t which,
                        uint32_t position, uint32_t element);
+/* Rows [position, rows) of every layer take orc_synthetic_kv values (the GPU
+ * library's cohx_seq_fill_synthetic contract: appending after a shared prefix
+ * keeps the prefix); the position becomes rows. */
 int orc_session_fill_synthetic(const orc_model *m, orc_session *s, uint32_t rows, uint64_t seed,
                                uint32_t stream);
 const float *orc_session_logits(const orc_session *s);

@@ -419,10 +419,10 @@ float orc_synthetic_kv(uint64_t seed, uint32_t stream, uint32_t layer, uint32_t 
 
 int orc_session_fill_synthetic(const orc_model *m, orc_session *s, uint32_t rows, uint64_t seed,
                                uint32_t stream) {
-  if (rows > s->context) return ORC_RESOURCE;
+  if (rows > s->context || rows < s->position) return ORC_RESOURCE;
   size_t kvd = (size_t)m->c.kv_heads * m->c.head_dim;
   for (uint32_t l = 0; l < m->c.layers; l++)
-    for (uint32_t p = 0; p < rows; p++)
+    for (uint32_t p = s->position; p < rows; p++)
       for (uint32_t e = 0; e < kvd; e++) {
         size_t at = ((size_t)l * s->context + p) * kvd + e;
         s->keys[at] = orc_synthetic_kv(seed, stream, l, 0, p, e);

@@ -293,3 +293,50 @@ def test_graph_replays_match_direct_launches():
         toks = ag
     for a, b in zip(sg, sd):
         assert np.array_equal(mg.seq_read_kv(a, 0, True), md.seq_read_kv(b, 0, True))
+
+
+# Shapes off the Qwen2.5-0.5B path: the intermediate width is an odd number of
+# 32-element blocks per 64 (F % 64 == 32: gate+up cannot quantize the down
+# operand in its epilogue), and a hidden width above 1024 (gate+up and the head
+# leave the short-K kernels).
+ODD_F = synth.config(layers=2, hidden=128, intermediate=224, heads=4, kv_heads=2, vocabulary=300,
+                     context=512)
+WIDE_H = synth.config(layers=2, hidden=1152, intermediate=256, heads=18, kv_heads=9,
+                      vocabulary=300, context=512)
+
+
+@pytest.mark.parametrize("shape", ["tiny", "odd_f", "wide_h"])
+@pytest.mark.parametrize("dtype", ["q8_0", "q4_0"])
+def test_tall_ragged_steps_match_oracle(dtype, shape):
+    """Packed steps of 197 rows (13 batch tiles: more than one row of the
+    8-tile gate+up workgroups, the second one partial), then a decode step,
+    bit for bit against the oracle: logits of every lane, greedy ids, the K/V
+    rows of every layer."""
+    cfg = {"tiny": TINY, "odd_f": ODD_F, "wide_h": WIDE_H}[shape]
+    print(f"case: tall ragged steps {dtype} {shape}", flush=True)
+    c, t, m, o = build(dtype, 12, cfg=cfg, max_lanes=4, max_rows=200, max_seqs=4, max_context=256)
+    rng = np.random.default_rng(13)
+    V = c["vocabulary"]
+    seqs = [m.seq_alloc() for _ in range(3)]
+    sess = [o.session(256) for _ in range(3)]
+    m.seq_fill_synthetic(seqs[2], 21, 6, 2)
+    sess[2].fill_synthetic(21, 6, 2)
+    mismatched = 0
+    for step, lens in enumerate(((90, 70, 37), (1, 1, 1))):
+        toks = [[int(v) for v in rng.integers(0, V, n)] for n in lens]
+        res = m.step([dict(seq=s, tokens=tk, logits=True) for s, tk in zip(seqs, toks)])
+        width = max(lens)
+        for j in range(width):
+            live = [i for i in range(3) if j < lens[i]]
+            errs = o.forward_batch([sess[i] for i in live], [toks[i][j] for i in live])
+            assert not errs.any()
+        for i, r in enumerate(res):
+            assert r["status"] == 0
+            want = sess[i].logits()
+            mismatched += compare_logits(r["logits"], want, dtype, f"{shape} step {step} lane {i}")
+            assert r["argmax"] == orc.Sampler().sample(want)[1]
+    for i in range(3):
+        for layer in range(c["layers"]):
+            for values in (False, True):
+                assert np.array_equal(m.seq_read_kv(seqs[i], layer, values), sess[i].kv(layer, values))
+    assert mismatched == 0

@@ -17,3 +17,16 @@ def test_log1pf_restatement_equals_glibc(tmp_path):
     print(out.stdout)
     assert out.returncode == 0, out.stdout
     assert "mismatches 0" in out.stdout
+
+
+def test_expf_restatement_equals_glibc(tmp_path):
+    """The GPU expf (csrc/expf.h: SwiGLU, softmax, the Qwen3.5 gates) against
+    glibc's expf, bit for bit."""
+    exe = tmp_path / "ef"
+    subprocess.run(["g++", "-O2", "-ffp-contract=off", "-fno-fast-math", "-I", CSRC,
+                    os.path.join(ROOT, "tests", "host_expf.cpp"), "-o", str(exe), "-lm"],
+                   check=True)
+    out = subprocess.run([str(exe), "7"], capture_output=True, text=True, timeout=300)
+    print(out.stdout)
+    assert out.returncode == 0, out.stdout
+    assert "mismatches 0" in out.stdout

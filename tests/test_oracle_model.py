@@ -221,3 +221,18 @@ def test_synthetic_kv_fill_is_seeded_and_bounded():
     s2 = m.session()
     s2.fill_synthetic(20, 1234, 4)
     assert not np.array_equal(s2.kv(1), k)
+
+
+def test_synthetic_kv_fill_appends_after_the_current_rows():
+    """A second fill keeps rows [0, position) and fills only the new rows with
+    its own stream (the GPU contract for a forked, shared prefix)."""
+    c, t = synth.in_memory(TINY, "q8_0", seed=8)
+    m = orc.Model(c, t, threads=1)
+    s = m.session()
+    assert s.fill_synthetic(10, 77, 1) == 0
+    assert s.fill_synthetic(25, 77, 2) == 0
+    assert s.position == 25
+    k = s.kv(0, True)
+    assert k[9, 3] == orc.synthetic_kv(77, 1, 0, 1, 9, 3)
+    assert k[10, 3] == orc.synthetic_kv(77, 2, 0, 1, 10, 3)
+    assert s.fill_synthetic(5, 77, 3) != 0  # never shrinks
