@@ -139,6 +139,7 @@ EXPORTS = {
     "cohx_seq_fill_synthetic": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
                                                ctypes.c_uint64, ctypes.c_uint32]),
     "cohx_step": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Batch), ctypes.POINTER(StepOut)]),
+    "cohx_step_noalloc": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Batch), ctypes.POINTER(StepOut)]),
     "cohx_pack": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Batch),
                                  ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32),
                                  ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_uint32)]),
@@ -315,9 +316,10 @@ class Model:
             arr[i].want_logits = 1 if ln.get("logits") else (SKIP_HEAD if ln.get("skip_head") else 0)
         return Batch(len(lanes), arr), keep
 
-    def step(self, lanes):
+    def step(self, lanes, noalloc=False):
         """lanes: [{"seq", "tokens", "start"?, "logits"?: bool, "skip_head"?: bool}] -> list
-        of dicts (status, argmax, logits)."""
+        of dicts (status, argmax, logits).  noalloc: through cohx_step_noalloc
+        (device scratch from the library's static array)."""
         batch, keep = self._batch(lanes)
         outs = (LaneOut * len(lanes))()
         bufs = []
@@ -331,7 +333,8 @@ class Model:
                 bufs.append(None)
         so = StepOut()
         so.lanes = outs
-        self._check(lib().cohx_step(self.h, ctypes.byref(batch), ctypes.byref(so)))
+        entry = lib().cohx_step_noalloc if noalloc else lib().cohx_step
+        self._check(entry(self.h, ctypes.byref(batch), ctypes.byref(so)))
         res = [dict(status=outs[i].status, argmax=outs[i].argmax, logits=bufs[i])
                for i in range(len(lanes))]
         self.last_step = dict(width=so.width, rows=so.rows, matrix_bytes=so.matrix_bytes,

@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "device.h"
@@ -272,6 +273,35 @@ size_t layout_workspace(const cohx_model_desc &d, int nbp_h, int nbp_f, uint32_t
 }
 }  // namespace cohx
 
+// ---- device scratch of the allocation-free step ------------------------------
+// cohx_step_noalloc carves its workspace from this array instead of the
+// context's block.  Each device that loads the library holds its own copy
+// until the process ends; host code uses only the address resolved per
+// device below, never the array's name (a host-side stand-in).
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<uint8_t *> g_scratch_ptr;  // per device, resolved once with that device current
+
+// Called by cohx_create with ctx->device current.
+int resolve_scratch(cohx_ctx *ctx) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if ((size_t)ctx->device >= g_scratch_ptr.size()) g_scratch_ptr.resize(ctx->device + 1, nullptr);
+  uint8_t *&p = g_scratch_ptr[ctx->device];
+  if (!p) {
+    void *addr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess)
+      return fail(ctx, COHX_DEVICE, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    p = static_cast<uint8_t *>(addr);
+  }
+  ctx->scratch = p;
+  return COHX_OK;
+}
+}  // namespace
+
 extern "C" {
 
 const char *cohx_last_error(const cohx_ctx *ctx) { return ctx ? ctx->err.c_str() : "null context"; }
@@ -306,6 +336,7 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   if (hipSetDevice(device) != hipSuccess) return bail(COHX_DEVICE);
   if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess)
     return bail(COHX_DEVICE);
+  if (int rc_s = resolve_scratch(ctx)) return bail(rc_s);
   const int H = d->hidden, F = d->intermediate, V = d->vocabulary, NH = d->heads,
             NKV = d->kv_heads, D = d->head_dim, KVD = NKV * D, L = d->layers;
   const int R = d->max_rows;
@@ -1230,4 +1261,49 @@ extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *
   if (ctx && ctx->q35) return q35_step(ctx, batch, out);
   if (!ctx || !out || !out->lanes) return COHX_INVALID_REQUEST;
   return run_step(ctx, batch, out, ctx->ws, ctx->use_graphs);
+}
+
+// The same step as cohx_step with every device buffer the step needs beyond
+// the context's weights, KV pool and page tables carved from the static
+// scratch array, sized for this batch; launches are issued directly (no
+// graph instantiation).  No device allocation of any kind.
+extern "C" int cohx_step_noalloc(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
+  if (!ctx || !out || !out->lanes) return COHX_INVALID_REQUEST;
+  if (ctx->q35) return fail(ctx, COHX_UNSUPPORTED, "cohx_step_noalloc serves Qwen2 contexts");
+  if (!batch || !batch->lanes || batch->n_lanes == 0 || batch->n_lanes > ctx->desc.max_lanes)
+    return fail(ctx, COHX_INVALID_REQUEST,
+                "batch width must be in 1..=" + std::to_string(ctx->desc.max_lanes));
+  if (!ctx->scratch) return fail(ctx, COHX_DEVICE, "the scratch array was not resolved");
+  // upper bounds of what the step packs: lanes that fail validation only shrink it
+  uint64_t rows = 0;
+  uint32_t kv = 1;
+  bool logits = false;
+  for (uint32_t i = 0; i < batch->n_lanes; i++) {
+    const cohx_lane &ln = batch->lanes[i];
+    rows += ln.n_tokens;
+    const bool live = valid_seq(ctx, ln.seq);
+    const uint64_t start = ln.start_position == COHX_AT_END ? (live ? ctx->seqs[ln.seq].length : 0)
+                                                            : ln.start_position;
+    kv = (uint32_t)std::max<uint64_t>(kv, std::min<uint64_t>(start + ln.n_tokens, ctx->desc.max_context));
+    logits |= ln.want_logits == 1u && out->lanes[i].logits;
+  }
+  rows = std::min<uint64_t>(std::max<uint64_t>(rows, 1), ctx->desc.max_rows);
+  const size_t need = layout_workspace(ctx->desc, ctx->nbp_h, ctx->nbp_f, (uint32_t)rows, batch->n_lanes,
+                                       kv, logits, nullptr, nullptr);
+  if (need > kScratchBytes)
+    return fail(ctx, COHX_RESOURCE,
+                "cohx_step_noalloc: this step needs " + std::to_string(need) + " bytes of scratch, more than its " +
+                    std::to_string(kScratchBytes) + " (fewer rows, lanes, logits or attended positions)");
+  Workspace w;
+  layout_workspace(ctx->desc, ctx->nbp_h, ctx->nbp_f, (uint32_t)rows, batch->n_lanes, kv, logits, ctx->scratch,
+                   &w);
+  // Every buffer of the step is written before it is read (the packer
+  // clears the row error bits), so nothing left by an earlier call, of this
+  // or another context on the device, needs clearing.  Calls that overlap on
+  // one device race on the array.
+  const bool prof = ctx->prof.on;  // the timing events would be created here
+  ctx->prof.on = false;
+  const int rc = run_step(ctx, batch, out, w, false);
+  ctx->prof.on = prof;
+  return rc;
 }

@@ -141,6 +141,7 @@ struct cohx_ctx {
   cohx::Workspace ws;      // laid out for max_rows / max_lanes / max_context
   uint8_t *ws_block = nullptr;
   cohx::Staging host;
+  uint8_t *scratch = nullptr;  // this device's static scratch array (cohx_step_noalloc)
   cohx::Profiler prof;
   std::vector<void *> allocations;
   bool use_graphs = true;    // replay each step's launches as one captured graph

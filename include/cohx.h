@@ -155,6 +155,19 @@ typedef struct {
  * success. */
 int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out);
 
+/* cohx_step without any device allocation, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference, whose step allocates nothing
+ * on a device.  Same inputs, outputs and bits as cohx_step; the step's
+ * device scratch (activations, attention partials, argmax keys, the staging
+ * of requested logits) comes from one static 64 MiB array per device instead
+ * of the context's workspace, and launches are issued directly (no graph).
+ * A batch whose scratch would exceed 64 MiB fails with COHX_RESOURCE.  Every
+ * call on a device shares that device's array: calls that overlap on one
+ * device (from several threads or contexts) race and must be serialized by
+ * the caller. */
+int cohx_step_noalloc(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out);
+
 /* Packing only (test hook for the bit-exact packer): runs the device packer for
  * `batch` and copies cu_seqlens[n+1], positions[R], slots[R] (page*16 + offset)
  * and lanes[R] back.  Sequences are not advanced. */
