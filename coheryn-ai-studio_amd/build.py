@@ -14,7 +14,8 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libcohx.so")
-SOURCES = ["csrc/kernels.hip", "csrc/cohx.cpp", "csrc/gen.cpp", "csrc/q35_kernels.hip", "csrc/q35.cpp"]
+SOURCES = ["csrc/kernels.hip", "csrc/cohx.cpp", "csrc/gen.cpp", "csrc/q35_kernels.hip", "csrc/q35.cpp",
+           "csrc/gguf.cpp"]
 HEADERS = ["csrc/device.h", "csrc/kernels.h", "csrc/internal.h", "../include/cohx.h"]
 ARCH = os.environ.get("COHX_ARCH", "gfx950")
 

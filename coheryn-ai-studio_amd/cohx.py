@@ -121,6 +121,10 @@ EXPORTS = {
                                           ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p,
                                           ctypes.c_size_t]),
     "cohx_finalize": (ctypes.c_int, [ctypes.c_void_p]),
+    "cohx_load_gguf": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(ModelDesc),
+                                      ctypes.POINTER(ctypes.c_void_p), ctypes.c_char_p, ctypes.c_size_t]),
+    "cohx_gguf_inspect": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ModelDesc), ctypes.c_char_p,
+                                         ctypes.c_size_t]),
     "cohx_seq_alloc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32,
                                       ctypes.POINTER(ctypes.c_uint32)]),
     "cohx_seq_fork": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
@@ -143,6 +147,11 @@ EXPORTS = {
     "cohx_pack": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Batch),
                                  ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32),
                                  ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_uint32)]),
+    "cohx_matvec": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                   ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32,
+                                   ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float),
+                                   ctypes.POINTER(ctypes.c_uint8), ctypes.POINTER(ctypes.c_float),
+                                   ctypes.POINTER(ctypes.c_int32)]),
     "cohx_profile": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "cohx_profile_read": (ctypes.c_uint32, [ctypes.c_void_p, ctypes.POINTER(KernelStat),
                                             ctypes.c_uint32]),
@@ -189,7 +198,19 @@ def _u32p(a):
     return a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
 
 
-DTYPE = {"f16": 1, "q8_0": 8, "q4_0": 2}
+def inspect_gguf(path):
+    """cohx_gguf_inspect: the library's parse and validation of a file; returns
+    (status, desc or None, message)."""
+    d = ModelDesc()
+    err = ctypes.create_string_buffer(512)
+    rc = lib().cohx_gguf_inspect(os.fsencode(path), ctypes.byref(d), err, 512)
+    return rc, (d if rc == 0 else None), err.value.decode()
+
+
+DTYPE = {"f16": 1, "q8_0": 8, "q4_0": 2, "q5_0": 6, "q4_k": 12, "q6_k": 14}
+MIXED = 0x100  # COHX_MIXED: each matrix takes the dtype of its tensor
+# bytes of one prepared operand block and the values it covers (Q8_0 / Q8_K / F16)
+ACT_BLOCK = {1: (2, 1), 2: (34, 32), 6: (34, 32), 8: (34, 32), 12: (292, 256), 14: (292, 256)}
 
 
 class Model:
@@ -200,7 +221,8 @@ class Model:
         self.config = dict(config)
         L = lib()
         mats = [t for n, t in tensors.items() if len(t.shape) == 2]
-        wdt = mats[0].dtype
+        # one dtype for every matrix, or COHX_MIXED (a Q4_K_M-style file)
+        wdt = mats[0].dtype if len({t.dtype for t in mats}) == 1 else MIXED
         d = ModelDesc()
         for k in ("layers", "hidden", "intermediate", "heads", "kv_heads", "head_dim",
                   "vocabulary", "context"):
@@ -241,6 +263,27 @@ class Model:
         meta, tensors = gguf.read(path)
         return cls(gguf.qwen2_config(meta), tensors, **kw)
 
+    @classmethod
+    def load(cls, path, max_lanes=16, max_rows=None, max_seqs=None, max_context=0, kv_pages=0,
+             device=0):
+        """Model::load through the library's own GGUF loader (cohx_load_gguf):
+        the file is parsed, validated and uploaded in C++."""
+        d = ModelDesc()
+        d.max_lanes, d.max_rows, d.max_seqs = max_lanes, max_rows or max_lanes, max_seqs or max_lanes
+        d.max_context, d.kv_pages = max_context, kv_pages
+        h = ctypes.c_void_p()
+        err = ctypes.create_string_buffer(512)
+        rc = lib().cohx_load_gguf(os.fsencode(path), device, ctypes.byref(d), ctypes.byref(h), err, 512)
+        if rc:
+            raise CohxError(rc, err.value.decode())
+        self = cls.__new__(cls)
+        self.config = {k: getattr(d, k) for k in ("layers", "hidden", "intermediate", "heads", "kv_heads",
+                                                   "head_dim", "vocabulary", "context")}
+        self.config.update(rope_base=d.rope_base, norm_epsilon=d.norm_epsilon)
+        self.desc, self.h = d, h
+        self.max_lanes, self.max_context = d.max_lanes, d.max_context
+        return self
+
     def _check(self, rc):
         if rc:
             raise CohxError(rc, lib().cohx_last_error(self.h).decode())
@@ -255,6 +298,25 @@ class Model:
 
     def __del__(self):
         self.close()
+
+    def matvec(self, dtype, rows, K, payload, inputs, decode=False):
+        """cohx_matvec: one matrix (GGUF payload) against f32 input rows through
+        the step's operand preparation and exact kernels.  Returns (out [n][rows],
+        prepared operand bytes [n][...], statuses [n], decoded rows or None)."""
+        x = np.ascontiguousarray(inputs, np.float32).reshape(-1, K)
+        n = x.shape[0]
+        w = np.ascontiguousarray(payload, np.uint8)
+        out = np.zeros((n, rows), np.float32)
+        bb, bv = ACT_BLOCK[dtype]
+        act = np.zeros((n, K // bv * bb), np.uint8)
+        st = np.zeros(n, np.int32)
+        dec = np.zeros((rows, K), np.float32) if decode else None
+        fp = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))  # noqa: E731
+        self._check(lib().cohx_matvec(
+            self.h, dtype, rows, K, w.ctypes.data, w.nbytes, n, fp(x), fp(out),
+            act.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), fp(dec) if decode else None,
+            st.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))))
+        return out, act, st, dec
 
     # ---- sequences ---------------------------------------------------------
     def seq_alloc(self, capacity=None):

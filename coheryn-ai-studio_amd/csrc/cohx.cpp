@@ -124,6 +124,58 @@ int make_f16(cohx_ctx *ctx, DeviceMatrix &m, int rows, int K) {
   return rc;
 }
 
+// K-quant tiles (device.h kq_*) of a matrix with `rows` rows of width K
+// (K % 256 == 0).
+int make_kq(cohx_ctx *ctx, DeviceMatrix &m, int rows, int K, int mtiles) {
+  m.view.dtype = kFmtKQ;
+  m.view.rows = rows;
+  m.view.K = K;
+  m.view.nb = K / 256;
+  m.view.nbp = 0;
+  m.view.mtiles = mtiles;
+  const size_t tb = (size_t)mtiles * m.view.nb;  // (tile, block) pairs
+  int rc = dalloc(ctx, &m.qs, tb * 4096);
+  if (!rc) rc = dalloc(ctx, &m.ksc, tb * 64);
+  if (!rc) rc = dalloc(ctx, &m.ds, tb * 16);
+  if (!rc) rc = dalloc(ctx, &m.kdm, tb * 16);
+  if (!rc) rc = dalloc(ctx, &m.kmin, tb * 128);
+  m.view.qs = m.qs;
+  m.view.ds = m.ds;
+  m.view.ksc = m.ksc;
+  m.view.kdm = m.kdm;
+  m.view.kmin = m.kmin;
+  return rc;
+}
+
+// Device format a GGUF matrix dtype is held in (0: unsupported).
+int device_format(uint32_t dtype) {
+  switch (dtype) {
+    case COHX_F16: return kFmtF16;
+    case COHX_Q8_0: case COHX_Q5_0: return kFmtQ8;
+    case COHX_Q4_0: return kFmtQ4;
+    case COHX_Q4_K: case COHX_Q6_K: return kFmtKQ;
+    default: return 0;
+  }
+}
+
+// Allocates m in the device format of `dtype` on its first part; later parts
+// must share that format.  For the tiled formats mtiles counts 16-row tiles.
+int ensure_matrix(cohx_ctx *ctx, DeviceMatrix &m, uint32_t dtype, int rows, int K, int mtiles) {
+  const int fmt = device_format(dtype);
+  if (m.view.dtype) {
+    if (m.view.dtype != fmt)
+      return fail(ctx, COHX_UNSUPPORTED,
+                  "the parts of a fused matrix must share one family (Q8_0/Q5_0, Q4_0, F16 or Q4_K/Q6_K)");
+    return COHX_OK;
+  }
+  switch (fmt) {
+    case kFmtQ8: return make_q8(ctx, m, rows, K, mtiles);
+    case kFmtQ4: return make_q4(ctx, m, rows, K, mtiles);
+    case kFmtKQ: return make_kq(ctx, m, rows, K, mtiles);
+    default: return make_f16(ctx, m, rows, K);
+  }
+}
+
 // Device row of source row r when the rows are query or key heads of
 // rope_d elements (0: identity): element i of a head lands on row 2i and
 // element i + rope_d/2 on row 2i + 1, so the two halves NeoX RoPE rotates
@@ -190,29 +242,146 @@ int upload_q4(cohx_ctx *ctx, DeviceMatrix &m, const uint8_t *src, int rows, int 
   return COHX_OK;
 }
 
+// GGUF Q5_0 rows (quant.rs:102-114: value j = low nibble of byte 6+j with
+// bit j of the high word, value j+16 = high nibble with bit j+16; minus 16)
+// as Q8_0 blocks with the same scale: the 5-bit values widen to int8 exactly,
+// and the Q5_0 chain fmaf(dw*da, isum, sum) (quant.rs:273-285) is the Q8_0
+// chain with its multiplicands swapped, so the same kernels give its bits.
+std::vector<uint8_t> q5_as_q8(const uint8_t *src, size_t blocks) {
+  std::vector<uint8_t> out(blocks * 34);
+  for (size_t i = 0; i < blocks; i++) {
+    const uint8_t *b = src + i * 22;
+    uint8_t *o = out.data() + i * 34;
+    o[0] = b[0];
+    o[1] = b[1];
+    const uint32_t high = (uint32_t)b[2] | ((uint32_t)b[3] << 8) | ((uint32_t)b[4] << 16) | ((uint32_t)b[5] << 24);
+    for (int j = 0; j < 16; j++) {
+      o[2 + j] = (uint8_t)(int8_t)((int)((b[6 + j] & 15) | (((high >> j) & 1) << 4)) - 16);
+      o[18 + j] = (uint8_t)(int8_t)((int)((b[6 + j] >> 4) | (((high >> (j + 16)) & 1) << 4)) - 16);
+    }
+  }
+  return out;
+}
+
+// quant.rs:44-55: the 6-bit (scale, min) pair of Q4_K group g.
+void k4_pair(const uint8_t *sc, int g, int &scale, int &minimum) {
+  if (g < 4) {
+    scale = sc[g] & 63;
+    minimum = sc[g + 4] & 63;
+  } else {
+    scale = (sc[g + 4] & 15) | ((sc[g - 4] >> 6) << 4);
+    minimum = (sc[g + 4] >> 4) | ((sc[g] >> 6) << 4);
+  }
+}
+
+// GGUF Q4_K (144-byte) / Q6_K (210-byte) rows -> K-quant tiles, tile i of the
+// source at tile_first + i*tile_step.  Per 256-element block: the values as
+// int8 (Q4_K nibble 0..15, quant.rs:116-133; Q6_K q6_value - 32, quant.rs:56-64),
+// the scale of each 16-element sub-group (Q4_K: its group's, Q6_K: the
+// int8 at byte 192 + s), d, and for Q4_K dmin and the group mins.
+int upload_kq(cohx_ctx *ctx, DeviceMatrix &m, uint32_t dtype, const uint8_t *src, int rows, int tile_first,
+              int tile_step) {
+  const int nb = m.view.nb, tiles = (rows + 15) / 16;
+  const size_t bb = dtype == COHX_Q4_K ? 144 : 210;
+  std::vector<int8_t> vals((size_t)tiles * nb * 4096, 0);
+  std::vector<uint32_t> sc((size_t)tiles * nb * 64, 0);
+  std::vector<uint16_t> dd((size_t)tiles * nb * 16, 0), dm((size_t)tiles * nb * 16, 0);
+  std::vector<uint8_t> mins((size_t)tiles * nb * 128, 0);
+  for (int r = 0; r < rows; r++) {
+    const int t = r / 16, rr = r % 16;
+    for (int b = 0; b < nb; b++) {
+      const uint8_t *blk = src + ((size_t)r * nb + b) * bb;
+      const size_t wr = kq_row(t, nb, b, rr);
+      int subscale[16];
+      if (dtype == COHX_Q4_K) {
+        dd[wr] = (uint16_t)(blk[0] | (blk[1] << 8));
+        dm[wr] = (uint16_t)(blk[2] | (blk[3] << 8));
+        for (int g = 0; g < 8; g++) {
+          int scale, minimum;
+          k4_pair(blk + 4, g, scale, minimum);
+          subscale[2 * g] = subscale[2 * g + 1] = scale;
+          mins[wr * 8 + g] = (uint8_t)minimum;
+        }
+      } else {
+        dd[wr] = (uint16_t)(blk[208] | (blk[209] << 8));
+        for (int s2 = 0; s2 < 16; s2++) subscale[s2] = (int8_t)blk[192 + s2];
+      }
+      for (int i = 0; i < 256; i++) {
+        int v;
+        if (dtype == COHX_Q4_K) {
+          const int g = i / 32;
+          const uint8_t packed = blk[16 + (g / 2) * 32 + i % 32];
+          v = g % 2 == 0 ? (packed & 15) : (packed >> 4);
+        } else {
+          const int half = i / 128, grp = (i % 128) / 32, ln = i % 32;
+          const uint8_t low = blk[half * 64 + (grp % 2) * 32 + ln];
+          const int lo4 = grp < 2 ? (low & 15) : (low >> 4);
+          const int hi2 = (blk[128 + half * 32 + ln] >> (2 * grp)) & 3;
+          v = (lo4 | (hi2 << 4)) - 32;
+        }
+        const int c = i % 8, mm = i / 8;
+        vals[kq_byte(t, nb, b, c, (mm / 8) * 16 + rr, mm % 8)] = (int8_t)v;
+      }
+      for (int kg = 0; kg < 4; kg++) {
+        uint32_t word = 0;
+        for (int j = 0; j < 4; j++) word |= (uint32_t)(uint8_t)(int8_t)subscale[4 * kg + j] << (8 * j);
+        sc[kq_row(t, nb, b, 0) * 4 + kg * 16 + rr] = word;
+      }
+    }
+  }
+  const size_t tv = (size_t)nb * 4096, ts = (size_t)nb * 64 * 4, th = (size_t)nb * 16 * 2,
+               tm = (size_t)nb * 128;
+  HIP_TRY(hipMemcpy2D(m.qs + (size_t)tile_first * tv, tv * tile_step, vals.data(), tv, tv, tiles,
+                      hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy2D((uint8_t *)m.ksc + (size_t)tile_first * ts, ts * tile_step, sc.data(), ts, ts, tiles,
+                      hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy2D((uint8_t *)m.ds + (size_t)tile_first * th, th * tile_step, dd.data(), th, th, tiles,
+                      hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy2D((uint8_t *)m.kdm + (size_t)tile_first * th, th * tile_step, dm.data(), th, th, tiles,
+                      hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy2D(m.kmin + (size_t)tile_first * tm, tm * tile_step, mins.data(), tm, tm, tiles,
+                      hipMemcpyHostToDevice));
+  if (dtype == COHX_Q4_K) m.view.has_min = 1;
+  return COHX_OK;
+}
+
 int upload_f16(cohx_ctx *ctx, DeviceMatrix &m, const void *src, int rows, int row_first) {
   HIP_TRY(hipMemcpy(m.f16 + (size_t)row_first * m.view.K, src, (size_t)rows * m.view.K * 2,
                     hipMemcpyHostToDevice));
   return COHX_OK;
 }
 
-// Q8_0/Q4_0: `first` and `step` count 16-row tiles and rope_d reorders the
-// rows (rope_row); F16: `first` counts rows and the order is the source's.
+// Tiled formats: `first` and `step` count 16-row tiles and rope_d reorders
+// the rows (rope_row; Q8/Q4 only); F16: `first` counts rows and the order is
+// the source's.  The matrix is already allocated (ensure_matrix).
 int upload_matrix(cohx_ctx *ctx, DeviceMatrix &m, uint32_t dtype, const void *data, int rows,
                   int first, int step, int rope_d = 0) {
-  if (dtype != (uint32_t)m.view.dtype)
-    return fail(ctx, COHX_UNSUPPORTED, "matrix dtype differs from the context's weight dtype");
-  if (dtype == 8) return upload_q8(ctx, m, (const uint8_t *)data, rows, first, step, rope_d);
-  if (dtype == 2) return upload_q4(ctx, m, (const uint8_t *)data, rows, first, step, rope_d);
-  return upload_f16(ctx, m, data, rows, first);
+  const uint8_t *src = (const uint8_t *)data;
+  switch (dtype) {
+    case COHX_Q8_0: return upload_q8(ctx, m, src, rows, first, step, rope_d);
+    case COHX_Q5_0: {
+      const std::vector<uint8_t> q8 = q5_as_q8(src, (size_t)rows * (m.view.K / 32));
+      return upload_q8(ctx, m, q8.data(), rows, first, step, rope_d);
+    }
+    case COHX_Q4_0: return upload_q4(ctx, m, src, rows, first, step, rope_d);
+    case COHX_Q4_K: case COHX_Q6_K: return upload_kq(ctx, m, dtype, src, rows, first, step);
+    default: return upload_f16(ctx, m, data, rows, first);
+  }
 }
 
+// quant.rs:13-35 row_bytes (0: unsupported dtype or width not block-aligned).
 size_t row_bytes(uint32_t dtype, uint64_t width) {
+  const uint64_t blk = dtype == COHX_Q4_K || dtype == COHX_Q6_K ? 256
+                       : (dtype == COHX_Q4_0 || dtype == COHX_Q5_0 || dtype == COHX_Q8_0) ? 32 : 1;
+  if (!width || width % blk) return 0;
   switch (dtype) {
-    case 0: return width * 4;
-    case 1: return width * 2;
-    case 2: return width / 32 * 18;
-    case 8: return width / 32 * 34;
+    case COHX_F32: return width * 4;
+    case COHX_F16: return width * 2;
+    case COHX_Q4_0: return width / 32 * 18;
+    case COHX_Q5_0: return width / 32 * 22;
+    case COHX_Q8_0: return width / 32 * 34;
+    case COHX_Q4_K: return width / 256 * 144;
+    case COHX_Q6_K: return width / 256 * 210;
     default: return 0;
   }
 }
@@ -225,6 +394,7 @@ size_t layout_workspace(const cohx_model_desc &d, int nbp_h, int nbp_f, uint32_t
   const size_t H = d.hidden, F = d.intermediate, V = d.vocabulary, NH = d.heads, NKV = d.kv_heads,
                D = d.head_dim, KVD = NKV * D;
   const bool packed = d.weight_dtype != COHX_F16;
+  const bool kquant = d.weight_dtype == COHX_Q4_K || d.weight_dtype == COHX_Q6_K || d.weight_dtype == COHX_MIXED;
   const size_t rtiles = (R + 15) / 16, nbp_max = (size_t)std::max(nbp_h, nbp_f);
   const size_t nsc = (kv_cap + 255) / 256, chunks = (kv_cap + kChunk - 1) / kChunk;
   Workspace tmp;
@@ -258,6 +428,12 @@ size_t layout_workspace(const cohx_model_desc &d, int nbp_h, int nbp_f, uint32_t
     c.take(w.down_ds, rtiles * nbp_f * 16);
   }
   c.take(w.act_f16, R * std::max(H, F));
+  if (kquant) {
+    const size_t nb256 = std::max(H, F) / 256;
+    c.take(w.act_kd, rtiles * 16 * nb256);
+    c.take(w.act_ksum, rtiles * 16 * nb256 * 16);
+    c.take(w.act_f32, R * H);
+  }
   c.take(w.scores, R * NKV * kv_cap * 8);
   c.take(w.chunk_max, R * NH * nsc);
   c.take(w.den_part, R * NH * nsc);
@@ -314,8 +490,7 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
       d->head_dim > 128 || d->heads / d->kv_heads > (uint32_t)kMaxGroup || d->hidden % 32 ||
       d->intermediate % 32 || !d->vocabulary)
     return COHX_INVALID_GGUF;
-  if (d->weight_dtype != COHX_Q8_0 && d->weight_dtype != COHX_Q4_0 && d->weight_dtype != COHX_F16)
-    return COHX_UNSUPPORTED;
+  if (d->weight_dtype != COHX_MIXED && !device_format(d->weight_dtype)) return COHX_UNSUPPORTED;
   if (!attention_shape_supported((int)d->head_dim, (int)(d->heads / d->kv_heads)))
     return COHX_UNSUPPORTED;
   if (d->kv_dtype != 0) return COHX_UNSUPPORTED;
@@ -348,35 +523,17 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   const uint32_t pages = d->kv_pages ? d->kv_pages : d->max_seqs * (uint32_t)ctx->max_pages;
   ctx->layer_stride = (size_t)pages * NKV * kPage * D;
   int rc = COHX_OK;
-  // weights
+  // vectors; each matrix is allocated in its device format by its first
+  // uploaded part (ensure_matrix)
   ctx->layers.resize(L);
-  const bool packed = d->weight_dtype == COHX_Q8_0 || d->weight_dtype == COHX_Q4_0;
-  auto make_packed = [&](DeviceMatrix &m, int rows, int K, int mtiles) {
-    return d->weight_dtype == COHX_Q8_0 ? make_q8(ctx, m, rows, K, mtiles)
-                                        : make_q4(ctx, m, rows, K, mtiles);
-  };
   for (int l = 0; l < L && !rc; l++) {
     Layer &ly = ctx->layers[l];
     rc = dalloc(ctx, &ly.attn_norm, H);
     if (!rc) rc = dalloc(ctx, &ly.ffn_norm, H);
     if (!rc) rc = dalloc(ctx, &ly.bqkv, H + 2 * KVD);
-    if (packed) {
-      if (!rc) rc = make_packed(ly.qkv, H + 2 * KVD, H, H / 16 + 2 * ((KVD + 15) / 16));
-      if (!rc) rc = make_packed(ly.o, H, H, (H + 15) / 16);
-      if (!rc) rc = make_packed(ly.gu, 2 * F, H, 2 * ((F + 15) / 16));
-      if (!rc) rc = make_packed(ly.down, H, F, (H + 15) / 16);
-    } else {
-      if (!rc) rc = make_f16(ctx, ly.qkv, H + 2 * KVD, H);
-      if (!rc) rc = make_f16(ctx, ly.o, H, H);
-      if (!rc) rc = make_f16(ctx, ly.gu, 2 * F, H);
-      if (!rc) rc = make_f16(ctx, ly.down, H, F);
-    }
   }
   if (H % 16 || KVD % 16) rc = rc ? rc : COHX_INVALID_GGUF;
   if (!rc) rc = dalloc(ctx, &ctx->output_norm, H);
-  if (!rc) rc = packed ? make_packed(ctx->embd, V, H, (V + 15) / 16) : make_f16(ctx, ctx->embd, V, H);
-  if (!rc && !d->tied)
-    rc = packed ? make_packed(ctx->output, V, H, (V + 15) / 16) : make_f16(ctx, ctx->output, V, H);
   // RoPE table: (cos, sin) of the engine's iterative angle (cpu.rs:59-73).
   if (!rc) {
     std::vector<float2> tab((size_t)d->max_context * (D / 2));
@@ -464,15 +621,28 @@ int cohx_upload_tensor(cohx_ctx *ctx, const char *name, uint32_t dtype, uint64_t
     HIP_TRY(hipMemcpy(dst + offset, data, len * 4, hipMemcpyHostToDevice));
     return COHX_OK;
   };
+  // a matrix: the context's dtype, or any supported one for COHX_MIXED
+  auto matrix_dtype_ok = [&]() -> int {
+    if (!device_format(dtype) || (d.weight_dtype != COHX_MIXED && dtype != d.weight_dtype))
+      return fail(ctx, COHX_UNSUPPORTED, "matrix dtype " + std::to_string(dtype) + " of " + n +
+                                             " is not the context's weight dtype");
+    return COHX_OK;
+  };
+  const int fmt = device_format(dtype);
+  const bool tiled = fmt == kFmtQ8 || fmt == kFmtQ4 || fmt == kFmtKQ;
   int rc = COHX_OK;
   if (n == "token_embd.weight") {
     if (!expect(H, V)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
-    rc = upload_matrix(ctx, ctx->embd, dtype, data, (int)V, 0, 1);
+    rc = matrix_dtype_ok();
+    if (!rc) rc = ensure_matrix(ctx, ctx->embd, dtype, (int)V, (int)H, (int)((V + 15) / 16));
+    if (!rc) rc = upload_matrix(ctx, ctx->embd, dtype, data, (int)V, 0, 1);
     ctx->embd.gguf_bytes = bytes;
   } else if (n == "output.weight") {
     if (d.tied) return fail(ctx, COHX_INVALID_REQUEST, "context was created with a tied head");
     if (!expect(H, V)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
-    rc = upload_matrix(ctx, ctx->output, dtype, data, (int)V, 0, 1);
+    rc = matrix_dtype_ok();
+    if (!rc) rc = ensure_matrix(ctx, ctx->output, dtype, (int)V, (int)H, (int)((V + 15) / 16));
+    if (!rc) rc = upload_matrix(ctx, ctx->output, dtype, data, (int)V, 0, 1);
     ctx->output.gguf_bytes = bytes;
   } else if (n == "output_norm.weight") {
     rc = vec_f32(ctx->output_norm, H, 0);
@@ -492,25 +662,36 @@ int cohx_upload_tensor(cohx_ctx *ctx, const char *name, uint32_t dtype, uint64_t
       const uint64_t rows = s == "attn_q.weight" ? H : KVD;
       const uint64_t first = s == "attn_q.weight" ? 0 : s == "attn_k.weight" ? H : H + KVD;
       if (!expect(H, rows)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
-      // Q8_0/Q4_0 query and key rows pair each head's RoPE halves (rope_row)
-      rc = upload_matrix(ctx, ly.qkv, dtype, data, (int)rows,
-                         (int)(dtype == 8 || dtype == 2 ? first / 16 : first), 1,
-                         s == "attn_v.weight" ? 0 : (int)d.head_dim);
+      rc = matrix_dtype_ok();
+      if (!rc)
+        rc = ensure_matrix(ctx, ly.qkv, dtype, (int)(H + 2 * KVD), (int)H, (int)(H / 16 + 2 * ((KVD + 15) / 16)));
+      // Q8/Q4 query and key rows pair each head's RoPE halves (rope_row) for
+      // the fused epilogue; K-quant and F16 rows keep the source order
+      if (!rc)
+        rc = upload_matrix(ctx, ly.qkv, dtype, data, (int)rows, (int)(tiled ? first / 16 : first), 1,
+                           s == "attn_v.weight" || fmt == kFmtKQ ? 0 : (int)d.head_dim);
       ly.qkv.gguf_bytes += bytes;
     } else if (s == "attn_output.weight") {
       if (!expect(H, H)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
-      rc = upload_matrix(ctx, ly.o, dtype, data, (int)H, 0, 1);
+      rc = matrix_dtype_ok();
+      if (!rc) rc = ensure_matrix(ctx, ly.o, dtype, (int)H, (int)H, (int)((H + 15) / 16));
+      if (!rc) rc = upload_matrix(ctx, ly.o, dtype, data, (int)H, 0, 1);
       ly.o.gguf_bytes = bytes;
     } else if (s == "ffn_gate.weight" || s == "ffn_up.weight") {
       if (!expect(H, F)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
       const bool up = s == "ffn_up.weight";
-      // Q8_0/Q4_0: gate tile i -> tile 2i, up tile i -> tile 2i+1; F16: gate rows then up rows.
-      rc = dtype == 8 || dtype == 2 ? upload_matrix(ctx, ly.gu, dtype, data, (int)F, up ? 1 : 0, 2)
-                      : upload_matrix(ctx, ly.gu, dtype, data, (int)F, up ? (int)F : 0, 1);
+      rc = matrix_dtype_ok();
+      if (!rc) rc = ensure_matrix(ctx, ly.gu, dtype, (int)(2 * F), (int)H, (int)(2 * ((F + 15) / 16)));
+      // tiled: gate tile i -> tile 2i, up tile i -> tile 2i+1; F16: gate rows then up rows.
+      if (!rc)
+        rc = tiled ? upload_matrix(ctx, ly.gu, dtype, data, (int)F, up ? 1 : 0, 2)
+                   : upload_matrix(ctx, ly.gu, dtype, data, (int)F, up ? (int)F : 0, 1);
       ly.gu.gguf_bytes += bytes;
     } else if (s == "ffn_down.weight") {
       if (!expect(F, H)) return fail(ctx, COHX_INVALID_GGUF, "incorrect shape for " + n);
-      rc = upload_matrix(ctx, ly.down, dtype, data, (int)H, 0, 1);
+      rc = matrix_dtype_ok();
+      if (!rc) rc = ensure_matrix(ctx, ly.down, dtype, (int)H, (int)F, (int)((H + 15) / 16));
+      if (!rc) rc = upload_matrix(ctx, ly.down, dtype, data, (int)H, 0, 1);
       ly.down.gguf_bytes = bytes;
     } else {
       return fail(ctx, COHX_UNSUPPORTED, "unexpected tensor in Qwen2 graph: " + n);
@@ -900,7 +1081,18 @@ void enqueue_pack(cohx_ctx *ctx, const Workspace &w, int n_lanes) {
               w.row_pos, w.row_slot, w.row_lane, w.row_token, w.row_seq, w.lane_last, w.row_err);
 }
 
-ActView act_view(const Workspace &w) { return ActView{w.act_qs, w.act_ds, w.act_f16}; }
+ActView act_view(const Workspace &w) {
+  return ActView{w.act_qs, w.act_ds, w.act_f16, w.act_kd, w.act_ksum, w.act_f32};
+}
+
+// Operand kind of a matrix's input and the block count its preparation takes
+// (Q8_0: 32-element block pairs; Q8_K: 256-element blocks).
+int act_of(const DeviceMatrix &m) { return act_kind(m.view.dtype); }
+int act_blocks(int kind, int K) { return kind == kActQ8K ? K / 256 : even(K / 32); }
+// Algorithmic bytes of one prepared operand row of width K.
+double act_row_bytes(int kind, int K) {
+  return kind == kActQ8 ? (double)K / 32 * 34 : kind == kActQ8K ? (double)K / 256 * 292 : (double)K * 2;
+}
 
 }  // namespace
 
@@ -926,6 +1118,116 @@ extern "C" int cohx_pack(cohx_ctx *ctx, const cohx_batch *batch, uint32_t *cu, u
   HIP_TRY(hipStreamSynchronize(ctx->stream));
   for (uint32_t r = 0; r < p.rows; r++) slots[r] = slot32[r];
   return COHX_OK;
+}
+
+// ---- one matrix on its own (test utility) -----------------------------------------
+
+extern "C" int cohx_matvec(cohx_ctx *ctx, uint32_t dtype, uint32_t rows, uint32_t K, const void *weights,
+                           size_t bytes, uint32_t n, const float *inputs, float *out, uint8_t *act_bytes,
+                           float *decoded, int32_t *status) {
+  if (ctx && ctx->q35) return fail(ctx, COHX_UNSUPPORTED, "cohx_matvec takes a Qwen2 context");
+  if (!ctx || !weights || !rows || !K || !n || !inputs || !out) return COHX_INVALID_REQUEST;
+  const int fmt = device_format(dtype);
+  const size_t rb = row_bytes(dtype, K);
+  if (!fmt || !rb) return fail(ctx, COHX_UNSUPPORTED, "unsupported matrix dtype or width");
+  if (fmt != kFmtF16 && K % 32) return fail(ctx, COHX_INVALID_GGUF, "width not block aligned");
+  if (rb * rows != bytes) return fail(ctx, COHX_INVALID_GGUF, "payload size mismatch");
+  HIP_TRY(hipSetDevice(ctx->device));
+  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  // everything allocated here is released before returning
+  const size_t keep = ctx->allocations.size();
+  auto release = [&](int rc) {
+    (void)hipStreamSynchronize(ctx->stream);
+    for (size_t i = keep; i < ctx->allocations.size(); i++) (void)hipFree(ctx->allocations[i]);
+    ctx->allocations.resize(keep);
+    return rc;
+  };
+  DeviceMatrix m;
+  int rc = ensure_matrix(ctx, m, dtype, (int)rows, (int)K, (int)((rows + 15) / 16));
+  if (!rc) rc = upload_matrix(ctx, m, dtype, weights, (int)rows, 0, 1);
+  if (rc) return release(rc);
+  const int kind = act_kind(fmt), blocks = act_blocks(kind, (int)K);
+  const size_t ntiles = (n + 15) / 16, npad = ntiles * 16;
+  float *d_in = nullptr, *d_out = nullptr, *d_dec = nullptr;
+  uint32_t *d_err = nullptr, *d_tok = nullptr;
+  ActView act{};
+  rc = dalloc(ctx, &d_in, (size_t)n * K);
+  if (!rc) rc = dalloc(ctx, &d_out, (size_t)n * rows);
+  if (!rc) rc = dalloc(ctx, &d_err, n);
+  if (!rc) rc = dalloc(ctx, &act.qs, npad * (size_t)std::max<int>(K, blocks * 32));
+  if (!rc) rc = dalloc(ctx, &act.ds, ntiles * (size_t)blocks * 16);
+  if (!rc) rc = dalloc(ctx, &act.f16, (size_t)n * K);
+  if (!rc) rc = dalloc(ctx, &act.kd, npad * (K / 256 + 1));
+  if (!rc) rc = dalloc(ctx, &act.ksum, npad * (K / 256 + 1) * 16);
+  if (decoded && !rc) rc = dalloc(ctx, &d_dec, (size_t)rows * K);
+  if (decoded && !rc) rc = dalloc(ctx, &d_tok, rows);
+  if (rc) return release(rc);
+  hipStream_t s = ctx->stream;
+  if (hipMemcpyAsync(d_in, inputs, (size_t)n * K * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+    return release(fail(ctx, COHX_DEVICE, "input upload"));
+  set_prefill_mfma(false);  // exact kernels only
+  launch_quant_act(s, (int)n, d_in, (int)K, kind, blocks, act, d_err);
+  launch_matvec(s, kEpiStore, m.view, act, (int)n, MatvecOut{d_out, (int)rows, nullptr, nullptr, d_err, nullptr});
+  if (decoded) {
+    std::vector<uint32_t> tok(rows);
+    for (uint32_t r = 0; r < rows; r++) tok[r] = r;
+    if (hipMemcpyAsync(d_tok, tok.data(), rows * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+      return release(fail(ctx, COHX_DEVICE, "token upload"));
+    uint32_t *d_derr = nullptr;
+    if ((rc = dalloc(ctx, &d_derr, rows))) return release(rc);
+    launch_embed(s, (int)rows, m.view, d_tok, d_dec, (int)K, d_derr);
+  }
+  if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess)
+    return release(fail(ctx, COHX_DEVICE, "matvec launch"));
+  std::vector<uint32_t> err(n);
+  if (hipMemcpy(out, d_out, (size_t)n * rows * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+      hipMemcpy(err.data(), d_err, n * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+      (decoded && hipMemcpy(decoded, d_dec, (size_t)rows * K * 4, hipMemcpyDeviceToHost) != hipSuccess))
+    return release(fail(ctx, COHX_DEVICE, "read back"));
+  if (status)
+    for (uint32_t i = 0; i < n; i++)
+      status[i] = err[i] & kErrPage ? COHX_RESOURCE : err[i] ? COHX_INVALID_GGUF : COHX_OK;
+  if (act_bytes) {  // each prepared input in the engine's byte form
+    const size_t qbytes = npad * (size_t)std::max<int>(K, blocks * 32);
+    std::vector<int8_t> qs(qbytes);
+    if (hipMemcpy(qs.data(), act.qs, qbytes, hipMemcpyDeviceToHost) != hipSuccess)
+      return release(fail(ctx, COHX_DEVICE, "read back"));
+    if (kind == kActQ8) {
+      std::vector<uint16_t> ds(ntiles * (size_t)blocks * 16);
+      if (hipMemcpy(ds.data(), act.ds, ds.size() * 2, hipMemcpyDeviceToHost) != hipSuccess)
+        return release(fail(ctx, COHX_DEVICE, "read back"));
+      for (uint32_t i = 0; i < n; i++)
+        for (uint32_t b = 0; b < K / 32; b++) {
+          uint8_t *o = act_bytes + ((size_t)i * (K / 32) + b) * 34;
+          const uint16_t d = ds[q8_scale(i / 16, blocks, (int)b, i % 16)];
+          o[0] = (uint8_t)d;
+          o[1] = (uint8_t)(d >> 8);
+          for (int e = 0; e < 32; e++) o[2 + e] = (uint8_t)qs[q8_byte(i / 16, blocks, (int)b, (e / 8) * 16 + i % 16, e % 8)];
+        }
+    } else if (kind == kActQ8K) {
+      std::vector<float> kd(npad * (K / 256 + 1));
+      std::vector<int16_t> ks(kd.size() * 16);
+      if (hipMemcpy(kd.data(), act.kd, kd.size() * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+          hipMemcpy(ks.data(), act.ksum, ks.size() * 2, hipMemcpyDeviceToHost) != hipSuccess)
+        return release(fail(ctx, COHX_DEVICE, "read back"));
+      for (uint32_t i = 0; i < n; i++)
+        for (int b = 0; b < blocks; b++) {
+          uint8_t *o = act_bytes + ((size_t)i * blocks + b) * 292;
+          const size_t ar = kq_row(i / 16, blocks, b, i % 16);
+          std::memcpy(o, &kd[ar], 4);
+          for (int e = 0; e < 256; e++)
+            o[4 + e] = (uint8_t)qs[kq_byte(i / 16, blocks, b, e % 8, ((e / 8) / 8) * 16 + i % 16, (e / 8) % 8)];
+          std::memcpy(o + 260, &ks[ar * 16], 32);
+        }
+    } else {
+      std::vector<uint16_t> h((size_t)n * K);
+      if (hipMemcpy(h.data(), act.f16, h.size() * 2, hipMemcpyDeviceToHost) != hipSuccess)
+        return release(fail(ctx, COHX_DEVICE, "read back"));
+      std::memcpy(act_bytes, h.data(), h.size() * 2);
+    }
+  }
+  return release(COHX_OK);
 }
 
 // ---- profiling -----------------------------------------------------------------
@@ -974,13 +1276,11 @@ void prof_collect(cohx_ctx *ctx) {
   p.next = 0;
 }
 
-// Algorithmic bytes of one Q8_0/F16 matrix pass over rows_b activation rows.
-double matrix_pass_bytes(const MatrixView &w, int rows_b, int out_rows, bool residual) {
-  const double wbytes = w.dtype == 8   ? (double)w.rows * w.K / 32 * 34
-                        : w.dtype == 2 ? (double)w.rows * w.K / 32 * 18
-                                       : (double)w.rows * w.K * 2;
-  const double abytes = w.dtype != 1 ? (double)rows_b * w.K / 32 * 34 : (double)rows_b * w.K * 2;
-  return wbytes + abytes + (double)rows_b * out_rows * 4 * (residual ? 2 : 1);
+// Algorithmic bytes of one matrix pass over rows_b activation rows: the GGUF
+// payload(s) it holds, the prepared operand rows and the f32 outputs.
+double matrix_pass_bytes(const DeviceMatrix &m, int rows_b, int out_rows, bool residual) {
+  const double abytes = rows_b * act_row_bytes(act_of(m), m.view.K);
+  return (double)m.gguf_bytes + abytes + (double)rows_b * out_rows * 4 * (residual ? 2 : 1);
 }
 
 }  // namespace
@@ -1020,9 +1320,11 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
   const int R = (int)p.rows, NL = (int)p.included.size();
   const int H = d.hidden, F = d.intermediate, NH = d.heads, NKV = d.kv_heads, D = d.head_dim,
             KVD = NKV * D;
-  // packed weights (Q8_0, Q4_0) take Q8_0 activation blocks (quant.rs:181-183)
-  const int act_dtype = d.weight_dtype == COHX_F16 ? 1 : 8;
-  const double act_row = act_dtype == 8 ? (double)H / 32 * 34 : (double)H * 2;
+  // each matrix's input is prepared in the form its dtype takes: Q8_0 blocks
+  // for Q4_0/Q5_0/Q8_0, Q8_K blocks for Q4_K/Q6_K (quant.rs:181-187),
+  // binary16 rounding for F16 (cpu.rs:37-48)
+  const int act_head = act_of(d.tied ? ctx->embd : ctx->output);
+  const double act_row = act_row_bytes(act_of(ctx->layers[0].qkv), H);
   hipStream_t s = ctx->stream;
   StepDims sd{H, F, (int)d.vocabulary, NH, NKV, D, KVD, NH / NKV, d.norm_epsilon,
               1.0f / sqrtf((float)D), ctx->max_pages, (int)w.kv_cap, (int)w.max_chunks,
@@ -1053,12 +1355,13 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
     Layer &ly = ctx->layers[l];
     float *kp = ctx->kpool + (size_t)l * ctx->layer_stride;
     float *vp = ctx->vpool + (size_t)l * ctx->layer_stride;
+    const int a_qkv = act_of(ly.qkv), a_o = act_of(ly.o), a_gu = act_of(ly.gu), a_down = act_of(ly.down);
     e = prof_begin(ctx, kCatNorm, b_norm, 0);
-    launch_norm_act(s, R, w.x, nullptr, ly.attn_norm, H, d.norm_epsilon, act_dtype, ctx->nbp_h, act,
+    launch_norm_act(s, R, w.x, nullptr, ly.attn_norm, H, d.norm_epsilon, a_qkv, act_blocks(a_qkv, H), act,
                     w.row_err);
     prof_end(ctx, e);
-    if (ly.qkv.view.dtype == 1) {
-      e = prof_begin(ctx, kCatMvQkv, matrix_pass_bytes(ly.qkv.view, R, H + 2 * KVD, false),
+    if (ly.qkv.view.dtype != kFmtQ8 && ly.qkv.view.dtype != kFmtQ4) {
+      e = prof_begin(ctx, kCatMvQkv, matrix_pass_bytes(ly.qkv, R, H + 2 * KVD, false),
                      2.0 * R * (H + 2 * KVD) * H);
       launch_matvec(s, kEpiStore, ly.qkv.view, act, R,
                     MatvecOut{w.qkv, H + 2 * KVD, nullptr, nullptr, w.row_err, nullptr});
@@ -1072,7 +1375,7 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
       // (rows uploaded in rope_row order); the bytes are the matrix pass plus
       // the post pass's writes
       e = prof_begin(ctx, kCatMvQkv,
-                     matrix_pass_bytes(ly.qkv.view, R, 0, false) + (double)R * (H + 2 * KVD) * 4 +
+                     matrix_pass_bytes(ly.qkv, R, 0, false) + (double)R * (H + 2 * KVD) * 4 +
                          (H + 2 * KVD) * 4,
                      2.0 * R * (H + 2 * KVD) * H);
       launch_matvec_qkv(s, ly.qkv.view, act, R,
@@ -1099,23 +1402,29 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
       prof_end(ctx, e);
     }
     e = prof_begin(ctx, kCatAttnCombine, b_combine, 0);
-    launch_attn_combine(s, R, sd, w.row_pos, w.partial, act_dtype, ctx->nbp_h, act, w.row_err);
+    if (a_o == kActQ8K) {  // f32 rows, then their Q8_K blocks
+      launch_attn_combine(s, R, sd, w.row_pos, w.partial, kActF32, 0, act, w.row_err);
+      launch_quant_act(s, R, w.act_f32, H, kActQ8K, act_blocks(kActQ8K, H), act, w.row_err);
+    } else {
+      launch_attn_combine(s, R, sd, w.row_pos, w.partial, a_o, act_blocks(a_o, H), act, w.row_err);
+    }
     prof_end(ctx, e);
-    e = prof_begin(ctx, kCatMvO, matrix_pass_bytes(ly.o.view, R, H, true), 2.0 * R * H * H);
+    e = prof_begin(ctx, kCatMvO, matrix_pass_bytes(ly.o, R, H, true), 2.0 * R * H * H);
     launch_matvec(s, kEpiResidual, ly.o.view, act, R,
                   MatvecOut{w.x, H, nullptr, nullptr, w.row_err, nullptr});
     prof_end(ctx, e);
     e = prof_begin(ctx, kCatNorm, b_norm, 0);
-    launch_norm_act(s, R, w.x, nullptr, ly.ffn_norm, H, d.norm_epsilon, act_dtype, ctx->nbp_h, act,
+    launch_norm_act(s, R, w.x, nullptr, ly.ffn_norm, H, d.norm_epsilon, a_gu, act_blocks(a_gu, H), act,
                     w.row_err);
     prof_end(ctx, e);
-    // Q8_0/Q4_0 at K <= 1024: the SwiGLU quantizer runs in gate+up's
-    // epilogue into the down operand buffer; otherwise its own pass
-    const ActView down_act{w.down_qs, w.down_ds, nullptr};
+    // Q8_0/Q4_0 gate+up at K <= 1024 feeding a Q8_0-operand down projection:
+    // the SwiGLU quantizer runs in gate+up's epilogue into the down operand
+    // buffer; otherwise its own pass
+    const ActView down_act{w.down_qs, w.down_ds, nullptr, nullptr, nullptr, nullptr};
     bool fused_quant = false;
-    if (w.down_qs) {
+    if (w.down_qs && a_down == kActQ8) {
       e = prof_begin(ctx, kCatMvGateUp,
-                     matrix_pass_bytes(ly.gu.view, R, 0, false) + (double)R * F / 32 * 34, 2.0 * R * 2 * F * H);
+                     matrix_pass_bytes(ly.gu, R, 0, false) + (double)R * F / 32 * 34, 2.0 * R * 2 * F * H);
       // false (nothing launched) for shapes the fused quantizer does not cover
       fused_quant = launch_matvec_swiglu_q8(s, ly.gu.view, act, R,
                                             MatvecOut{nullptr, 0, nullptr, nullptr, w.row_err, nullptr},
@@ -1123,28 +1432,27 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
       prof_end(ctx, e);
     }
     if (!fused_quant) {
-      e = prof_begin(ctx, kCatMvGateUp, matrix_pass_bytes(ly.gu.view, R, F, false), 2.0 * R * 2 * F * H);
+      e = prof_begin(ctx, kCatMvGateUp, matrix_pass_bytes(ly.gu, R, F, false), 2.0 * R * 2 * F * H);
       launch_matvec(s, kEpiSwiglu, ly.gu.view, act, R,
                     MatvecOut{w.h, F, nullptr, nullptr, w.row_err, nullptr});
       prof_end(ctx, e);
-      e = prof_begin(ctx, kCatQuant, (double)R * F * 4 + (act_dtype == 8 ? (double)R * F / 32 * 34
-                                                                           : (double)R * F * 2), 0);
-      launch_quant_act(s, R, w.h, F, act_dtype, ctx->nbp_f, act, w.row_err);
+      e = prof_begin(ctx, kCatQuant, (double)R * F * 4 + R * act_row_bytes(a_down, F), 0);
+      launch_quant_act(s, R, w.h, F, a_down, act_blocks(a_down, F), act, w.row_err);
       prof_end(ctx, e);
     }
-    e = prof_begin(ctx, kCatMvDown, matrix_pass_bytes(ly.down.view, R, H, true), 2.0 * R * H * F);
+    e = prof_begin(ctx, kCatMvDown, matrix_pass_bytes(ly.down, R, H, true), 2.0 * R * H * F);
     launch_matvec(s, kEpiResidual, ly.down.view, fused_quant ? down_act : act, R,
                   MatvecOut{w.x, H, nullptr, nullptr, w.row_err, nullptr});
     prof_end(ctx, e);
   }
   // final norm and head over the last row of every lane (batch.rs:250-266)
-  e = prof_begin(ctx, kCatNorm, (double)NL * H * 4 + H * 4 + NL * act_row, 0);
-  launch_norm_act(s, NL, w.x, w.lane_last, ctx->output_norm, H, d.norm_epsilon, act_dtype,
-                  ctx->nbp_h, act, w.row_err);
+  e = prof_begin(ctx, kCatNorm, (double)NL * H * 4 + H * 4 + NL * act_row_bytes(act_head, H), 0);
+  launch_norm_act(s, NL, w.x, w.lane_last, ctx->output_norm, H, d.norm_epsilon, act_head,
+                  act_blocks(act_head, H), act, w.row_err);
   prof_end(ctx, e);
   const DeviceMatrix &head = d.tied ? ctx->embd : ctx->output;
   e = prof_begin(ctx, kCatMvHead,
-                 matrix_pass_bytes(head.view, NL, 0, false) + (any_logits ? (double)NL * d.vocabulary * 4 : 0.0) + NL * 8.0,
+                 matrix_pass_bytes(head, NL, 0, false) + (any_logits ? (double)NL * d.vocabulary * 4 : 0.0) + NL * 8.0,
                  2.0 * NL * d.vocabulary * H);
   launch_matvec(s, kEpiArgmax, head.view, act, NL,
                 MatvecOut{nullptr, 0, w.argmax_part, any_logits ? w.logits : nullptr, w.row_err,

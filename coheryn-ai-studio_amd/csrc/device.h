@@ -165,6 +165,35 @@ __host__ __device__ __forceinline__ size_t q4_byte(size_t tile, int nbp, int b, 
          (size_t)(b % 2) * 4 + (size_t)(k % 4);
 }
 
+// ---------------------------------------------------------------------------
+// K-quant tiles (Q4_K / Q6_K weights as the A operand, Q8_K activations as
+// the B operand).  The engine's K-format dot keeps eight integer sums per
+// 256-element block, sum[i % 8] over element i (quant.rs:294-341).  So each
+// block is stored as 8 lane-classes: class c holds elements c, c+8, ...,
+// c+248, and its 32 values are exactly the K run of one
+// v_mfma_i32_16x16x32_i8.  For tile t, block b (nb blocks per row), class c
+// and lane l, the 8 bytes at ((t*nb + b)*8 + c)*512 + l*8 + j hold row
+// t*16 + l%16, element c + 8*(8*(l/16) + j), as one int8 value (Q4_K 0..15,
+// Q6_K -32..31; activations -128..127).
+// Weight side data per (tile, block):
+//  * scales: 64 dwords; lane l's dword at (t*nb + b)*64 + l holds in byte s
+//    the integer scale of the 16-element sub-group 4*(l/16) + s of row l%16
+//    (Q4_K: its 32-element group's 6-bit scale; Q6_K: the int8 scale), which
+//    are exactly the sub-groups of the lane's 8 operand values (value j is in
+//    sub-group 4*(l/16) + j/2);
+//  * d and dmin (binary16) at (t*nb + b)*16 + row%16 (Q6_K: dmin = 0);
+//  * mins: 8 bytes per row at ((t*nb + b)*16 + row%16)*8 (Q6_K: zeros).
+// Activation side data per (batch tile, block): d (f32) at (t*nb + b)*16 +
+// row%16 and the 16 sums of 16 consecutive values (int16) at
+// ((t*nb + b)*16 + row%16)*16, as QuantizedInput stores them.
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ size_t kq_byte(size_t tile, int nb, int b, int c, int lane, int j) {
+  return (((tile * (size_t)nb + (size_t)b) * 8 + (size_t)c) * 64 + (size_t)lane) * 8 + (size_t)j;
+}
+__host__ __device__ __forceinline__ size_t kq_row(size_t tile, int nb, int b, int row16) {
+  return (tile * (size_t)nb + (size_t)b) * 16 + (size_t)row16;
+}
+
 // One block's 4-byte word -> the 8 signed operand bytes (nibble - 8), as the
 // low 64 bits of an MFMA A/B operand.  Bytewise (n | 0x80) - 8 never borrows
 // across bytes; the final XOR removes the 0x80 bias.

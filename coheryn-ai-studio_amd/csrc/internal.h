@@ -13,11 +13,16 @@
 
 namespace cohx {
 
+// One (possibly fused) matrix; allocated in its device format by the first
+// part uploaded (view.dtype 0 until then).
 struct DeviceMatrix {
   MatrixView view{};
   int8_t *qs = nullptr;
   uint16_t *ds = nullptr;
   uint16_t *f16 = nullptr;
+  uint32_t *ksc = nullptr;  // K-quant side data (device.h kq_*)
+  uint16_t *kdm = nullptr;
+  uint8_t *kmin = nullptr;
   uint64_t gguf_bytes = 0;  // bytes of the GGUF payload(s) it holds
 };
 
@@ -46,6 +51,11 @@ struct Workspace {
   int8_t *down_qs = nullptr;
   uint16_t *down_ds = nullptr;
   uint16_t *act_ds = nullptr, *act_f16 = nullptr;
+  // Q8_K operands (K-quant weights): block scales and 16-value sums; f32 rows
+  // staged for their quantizer (attention output)
+  float *act_kd = nullptr;
+  int16_t *act_ksum = nullptr;
+  float *act_f32 = nullptr;
   float *scores = nullptr;  // [rows][kv_heads][kv_cap][8]: scores, then weights
   float *chunk_max = nullptr, *logits = nullptr;
   double *partial = nullptr;   // [rows][heads][max_chunks][head_dim]

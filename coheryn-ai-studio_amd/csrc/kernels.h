@@ -7,23 +7,44 @@ namespace cohx {
 
 // Device view of one matrix.  Q8_0: tiled int8 + f16 block scales (device.h
 // layout).  F16: row-major binary16 exactly as in the GGUF file.
+// Device formats (MatrixView::dtype): 1 = F16; 8 = Q8 tiles (GGUF Q8_0, and
+// Q5_0, whose 5-bit values widen to int8 losslessly and whose block chain is
+// Q8_0's); 2 = Q4_0 tiles; 12 = K-quant tiles (GGUF Q4_K and Q6_K).
+constexpr int kFmtF16 = 1, kFmtQ8 = 8, kFmtQ4 = 2, kFmtKQ = 12;
+// Activation operand kinds: binary16-rounded rows, Q8_0 blocks, Q8_K blocks.
+constexpr int kActF16 = 1, kActQ8 = 8, kActQ8K = 15;
+// Producer-only kind: f32 rows into ActView::f32, quantized by a following
+// launch_quant_act(kActQ8K).
+constexpr int kActF32 = 32;
+
 struct MatrixView {
-  int dtype;     // 1 = F16, 8 = Q8_0
+  int dtype;     // device format (kFmt*)
   int rows;      // logical output rows
   int K;         // input width
-  int nb, nbp;   // 32-element blocks, rounded up to even
+  int nb, nbp;   // 32-element blocks, rounded up to even (K-quants: nb = 256-element blocks)
   int mtiles;    // ceil(rows/16)
   const int8_t *qs;
-  const uint16_t *ds;
+  const uint16_t *ds;  // Q8/Q4 block scales; K-quants: d per (tile, block, row)
   const uint16_t *f16;
+  // K-quant side data (device.h kq_* layout)
+  const uint32_t *ksc;  // sub-group scales
+  const uint16_t *kdm;  // dmin
+  const uint8_t *kmin;  // group mins
+  int has_min;          // any Q4_K part (else the min chain is skipped: it stays +0)
 };
 
 // Activation operand buffers for the next matrix.
 struct ActView {
-  int8_t *qs;     // Q8 tiled (B operand)
+  int8_t *qs;     // Q8 tiled (B operand); K-quant tiled for Q8_K
   uint16_t *ds;   // Q8 block scales
   uint16_t *f16;  // binary16-rounded activations, row-major [rows][K]
+  float *kd;      // Q8_K block scales
+  int16_t *ksum;  // Q8_K 16-value sums
+  float *f32;     // f32 rows [rows][K] (kActF32 producers)
 };
+
+// Operand kind a matrix of device format `fmt` consumes.
+inline int act_kind(int fmt) { return fmt == kFmtF16 ? kActF16 : fmt == kFmtKQ ? kActQ8K : kActQ8; }
 
 struct StepDims {
   int H, F, V, NH, NKV, D, KVD, G;  // G = NH/NKV

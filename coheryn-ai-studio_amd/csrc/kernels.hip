@@ -113,6 +113,17 @@ __global__ __launch_bounds__(256) void k_embed(MatrixView e, const uint32_t *__r
       const float d = h2f(e.ds[q8_scale(mt, e.nbp, b, c)]);
       bad |= !finitef(d);
       v = d * (float)q;
+    } else if (e.dtype == kFmtKQ) {
+      // Q4_K: (d*scale)*q - dmin*min; Q6_K: (d*scale)*q, stored with dmin = +0
+      // and min = 0, so the same expression gives the same value (quant.rs:83-86,122-135)
+      const int mt = tok / 16, rr = tok % 16, b = k / 256, i = k % 256, m = i / 8;
+      const int q = e.qs[kq_byte(mt, e.nb, b, i % 8, (m / 8) * 16 + rr, m % 8)];
+      const int sub = i / 16;
+      const int sc = (int)(int8_t)(e.ksc[kq_row(mt, e.nb, b, 0) * 4 + (sub / 4) * 16 + rr] >> (8 * (sub % 4)));
+      const size_t wr = kq_row(mt, e.nb, b, rr);
+      const float dw = h2f(e.ds[wr]), dm = h2f(e.kdm[wr]);
+      bad |= !finitef(dw) || !finitef(dm);
+      v = (dw * (float)sc) * (float)q - dm * (float)e.kmin[wr * 8 + i / 32];
     } else {
       v = h2f(e.f16[(size_t)tok * H + k]);
       bad |= !finitef(v);
@@ -160,6 +171,74 @@ __device__ __forceinline__ bool quant_group_q8(const float (&v)[8], bool active,
     if (g == 0) act.ds[q8_scale(row / 16, nbp, b, row % 16)] = hd;
   }
   return bad;
+}
+
+// ---------------------------------------------------------------------------
+// Q8_K activation block (QuantizedInput::prepare for Q4_K/Q6_K weights,
+// quant.rs:214-233), one wave per 256-element block; lane l brings elements
+// 4l .. 4l+3 in v.  m = the first element of largest magnitude (signed);
+// all-zero blocks stay zero (d = 0, sums 0); else inv = -127/m, d = 1/inv
+// and q = min(round_ties_even(x*inv), 127) as i8, plus the sums of each 16
+// consecutive q.  Writes the K-quant B-operand tiles (device.h kq_*).
+// Returns the row's error bits (non-finite input; scale overflow).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t quant_block_q8k(const float (&v)[4], int row, int b, int nb, ActView act) {
+  const int lane = threadIdx.x % kWave;
+  bool bad = false;
+  // (|x|, lowest index) key; |x| of a finite float orders as its bits
+  unsigned long long key = 0;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    bad |= !finitef(v[e]);
+    const unsigned long long k = ((unsigned long long)__float_as_uint(fabsf(v[e])) << 32) |
+                                 (unsigned long long)(0xffffffffu - (uint32_t)(4 * lane + e));
+    key = k > key ? k : key;
+  }
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) {
+    const unsigned long long o = __shfl_xor(key, m, kWave);
+    key = o > key ? o : key;
+  }
+  const int idx = (int)(0xffffffffu - (uint32_t)key);
+  const float cand = v[idx & 3];
+  const float maximum = __shfl(cand, idx >> 2, kWave);
+  uint32_t err = bad ? kErrNonFinite : 0u;
+  uint32_t qw = 0;
+  float d = 0.0f;
+  if (maximum != 0.0f) {
+    const float inv = -127.0f / maximum;
+    d = 1.0f / inv;
+    if (!finitef(inv) || !finitef(d)) err |= kErrScale;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      qw |= (uint32_t)(uint8_t)sat_i8(fminf(rintf(v[e] * inv), 127.0f)) << (8 * e);
+  }
+  // 16-value sums: lanes 4s .. 4s+3 hold sub-group s
+  int sum = 0;
+#pragma unroll
+  for (int e = 0; e < 4; e++) sum += (int)(int8_t)(qw >> (8 * e));
+  sum += __shfl_xor(sum, 1, kWave);
+  sum += __shfl_xor(sum, 2, kWave);
+  const size_t tile = (size_t)(row / 16);
+  const size_t rb = kq_row(tile, nb, b, row % 16);
+  if (lane % 4 == 0) act.ksum[rb * 16 + lane / 4] = (int16_t)sum;
+  if (lane == 0) act.kd[rb] = d;
+  // lane T < 32 writes class c = T % 8, k-group kg = T / 8: values j = 0..7
+  // are elements c + 64 kg + 8 j, byte c % 4 of lane 16 kg + 2 j + c / 4
+  const int c = lane % 8, kg = (lane / 8) % 4;
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint32_t w = (uint32_t)__shfl((int)qw, 16 * kg + 2 * j + c / 4, kWave);
+    const uint32_t byte = (w >> (8 * (c % 4))) & 0xffu;
+    if (j < 4)
+      lo |= byte << (8 * j);
+    else
+      hi |= byte << (8 * (j - 4));
+  }
+  if (lane < 32)
+    *reinterpret_cast<uint2 *>(act.qs + kq_byte(tile, nb, b, c, kg * 16 + row % 16, 0)) = make_uint2(lo, hi);
+  return err;
 }
 
 // ---------------------------------------------------------------------------
@@ -216,6 +295,16 @@ __global__ __launch_bounds__(256) void k_norm_act(const float *__restrict__ x,
       for (int i = 0; i < 8; i++) v[i] = (active && kg * 8 + i < H) ? y[kg * 8 + i] : 0.0f;
       bad |= quant_group_q8(v, active, ob, kg, nbp, act);
     }
+  } else if (kAct == kActQ8K) {
+    // one wave per 256-element block (H % 256 == 0; nbp = H / 256)
+    uint32_t err = 0;
+    const int lane = threadIdx.x % kWave;
+    for (int b = threadIdx.x / kWave; b < nbp; b += 4) {
+      const float v[4] = {y[b * 256 + 4 * lane], y[b * 256 + 4 * lane + 1], y[b * 256 + 4 * lane + 2],
+                          y[b * 256 + 4 * lane + 3]};
+      err |= quant_block_q8k(v, ob, b, nbp, act);
+    }
+    if (err) atomicOr(&row_err[ib], err);
   } else {
     for (int k = threadIdx.x; k < H; k += 256) {
       const uint16_t h = f2h(y[k]);
@@ -284,6 +373,15 @@ __global__ __launch_bounds__(256) void k_quant_act(const float *__restrict__ src
       for (int i = 0; i < 8; i++) v[i] = (active && kg * 8 + i < K) ? s[kg * 8 + i] : 0.0f;
     }
     bad |= quant_group_q8(v, active, r, kg, nbp, act);
+  } else if (kAct == kActQ8K) {
+    // block y takes 256-element blocks [4 y, 4 y + 4): one per wave (nbp = K / 256)
+    const int b = blockIdx.y * 4 + (int)threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    if (b < nbp) {
+      const float4 a = reinterpret_cast<const float4 *>(s + (size_t)b * 256)[lane];
+      const float v[4] = {a.x, a.y, a.z, a.w};
+      const uint32_t err = quant_block_q8k(v, r, b, nbp, act);
+      if (err) atomicOr(&row_err[r], err);
+    }
   } else {
     for (int k = blockIdx.y * 256 + threadIdx.x; k < K; k += 256 * gridDim.y) {
       const uint16_t h = f2h(s[k]);
@@ -545,6 +643,168 @@ __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int r
         else
           *p = v;
       }
+    }
+  }
+  if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
+}
+
+// ---------------------------------------------------------------------------
+// K-quant matvec (Q4_K / Q6_K weights, Q8_K activations; quant.rs:294-341).
+// A workgroup of 8 waves owns kNM weight tiles x one batch tile, and wave c
+// owns lane-class c (device.h kq_*), i.e. the engine's integers[c] and
+// lanes[c].  Per block, in block order, the wave multiplies each weight value
+// by its sub-group scale (|w| <= 4096), splits it as 128*hi + lo with hi and
+// lo int8, and two int8 MFMAs give the exact class sum 128*(hi.a) + lo.a for
+// every (row, batch row) of the tile; then
+// lanes[c] = fmaf(dw*da, f32(integers[c]), lanes[c]).  Lanes 0-31 of each
+// wave also run the Q4_K min chain of one (row, batch row) pair:
+// sum = fmaf(-(dmin*da), f32(sum_g min_g * (s_2g + s_2g+1)), sum).  After the
+// last block the chains meet in LDS and sum + lanes[0] + ... + lanes[7] is
+// added in that order.  Q6_K has no min chain; its sum starts at +0 too.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void kq_split(uint2 q, uint32_t sc, long &hi, long &lo) {
+  uint32_t h[2] = {0u, 0u}, l[2] = {0u, 0u};
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint32_t word = j < 4 ? q.x : q.y;
+    const int v = (int)(int8_t)(word >> (8 * (j % 4)));
+    const int s = (int)(int8_t)(sc >> (8 * (j / 2)));
+    const int p = v * s;
+    h[j / 4] |= (uint32_t)((p >> 7) & 0xff) << (8 * (j % 4));
+    l[j / 4] |= (uint32_t)(p & 0x7f) << (8 * (j % 4));
+  }
+  hi = (long)(((unsigned long)h[1] << 32) | h[0]);
+  lo = (long)(((unsigned long)l[1] << 32) | l[0]);
+}
+
+template <int kEpi, int kNM>
+__global__ __launch_bounds__(512) void k_mv_kq(MatrixView w, ActView act, int rows_b, int n_tiles,
+                                               MatvecOut o) {
+  __shared__ float s_lane[8][kNM][256];
+  __shared__ float s_min[kNM][256];
+  __shared__ unsigned long long s_key[4][16];
+  const int lane = threadIdx.x % kWave, c = threadIdx.x / kWave;
+  const int units = w.mtiles / kNM;
+  const int group = blockIdx.x / (8 * n_tiles), rem = blockIdx.x % (8 * n_tiles);
+  const int nt = rem / 8, unit = group * 8 + rem % 8;
+  if (unit >= units) return;
+  const int nb = w.nb;
+  const v4i zero = {0, 0, 0, 0};
+  // the (row, batch row) pair of this lane's min chain: slot p of the MFMA
+  // output layout, row 4*((p%64)/16) + p/64, batch row p%16
+  const int p = c * 32 + (lane % 32);
+  const int mrow = 4 * ((p % 64) / 16) + p / 64, mcol = p % 16;
+  const bool mown = w.has_min && lane < 32;
+  float L[kNM][4], S[kNM];
+#pragma unroll
+  for (int m = 0; m < kNM; m++) {
+    S[m] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) L[m][i] = 0.0f;
+  }
+  for (int b = 0; b < nb; b++) {
+    const uint2 av = *reinterpret_cast<const uint2 *>(act.qs + kq_byte(nt, nb, b, c, lane, 0));
+    const long bop = (long)(((unsigned long)av.y << 32) | av.x);
+    const float da = act.kd[kq_row(nt, nb, b, lane % 16)];
+#pragma unroll
+    for (int m = 0; m < kNM; m++) {
+      const size_t tile = (size_t)unit * kNM + m;
+      const uint2 qv = *reinterpret_cast<const uint2 *>(w.qs + kq_byte(tile, nb, b, c, lane, 0));
+      const uint32_t sc = w.ksc[kq_row(tile, nb, b, 0) * 4 + lane];
+      const uint2 dw4 = *reinterpret_cast<const uint2 *>(w.ds + kq_row(tile, nb, b, 4 * (lane / 16)));
+      long hi, lo;
+      kq_split(qv, sc, hi, lo);
+      v4i ih = __builtin_amdgcn_mfma_i32_16x16x32_i8(hi, bop, zero, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) ih[i] *= 128;
+      const v4i is = __builtin_amdgcn_mfma_i32_16x16x32_i8(lo, bop, ih, 0, 0, 0);
+      const uint16_t dws[4] = {(uint16_t)dw4.x, (uint16_t)(dw4.x >> 16), (uint16_t)dw4.y,
+                               (uint16_t)(dw4.y >> 16)};
+#pragma unroll
+      for (int i = 0; i < 4; i++) L[m][i] = fmaf(h2f(dws[i]) * da, (float)is[i], L[m][i]);
+    }
+    if (mown) {
+      const size_t ar = kq_row(nt, nb, b, mcol);
+      const float dam = act.kd[ar];
+      const uint4 g0 = *reinterpret_cast<const uint4 *>(act.ksum + ar * 16);
+      const uint4 g1 = *reinterpret_cast<const uint4 *>(act.ksum + ar * 16 + 8);
+      const uint32_t gw[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+      for (int m = 0; m < kNM; m++) {
+        const size_t wr = kq_row((size_t)unit * kNM + m, nb, b, mrow);
+        const uint2 mn = *reinterpret_cast<const uint2 *>(w.kmin + wr * 8);
+        int ms = 0;
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+          const int mg = (int)(((g < 4 ? mn.x : mn.y) >> (8 * (g % 4))) & 0xffu);
+          const int gsum = (int)(int16_t)(gw[g] & 0xffffu) + (int)(int16_t)(gw[g] >> 16);
+          ms += mg * gsum;
+        }
+        S[m] = fmaf(-(h2f(w.kdm[wr]) * dam), (float)ms, S[m]);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < kNM; m++) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) s_lane[c][m][i * 64 + lane] = L[m][i];
+    if (lane < 32) s_min[m][p] = S[m];
+  }
+  __syncthreads();
+  // ---- the chains meet; then the epilogue (as k_mv_q8s)
+  const int t = threadIdx.x, prow = 4 * ((t % 64) / 16) + t / 64, pcol = t % 16;
+  float acc[kNM];
+#pragma unroll
+  for (int m = 0; m < kNM; m++) {
+    acc[m] = 0.0f;
+    if (t < 256) {
+      float v = s_min[m][t];
+#pragma unroll
+      for (int cc = 0; cc < 8; cc++) v = v + s_lane[cc][m][t];
+      acc[m] = v;
+    }
+  }
+  const int r = nt * 16 + pcol;
+  const bool rvalid = t < 256 && r < rows_b;
+  const int er = (rvalid && o.err_rows) ? (int)o.err_rows[r] : r;
+  bool bad = false;
+  if constexpr (kEpi == kEpiArgmax) {
+    const int row = unit * 16 + prow;
+    const bool valid = rvalid && row < w.rows;
+    const float v = acc[0];
+    if (valid) {
+      bad = !finitef(v);
+      if (o.logits) o.logits[(size_t)r * w.rows + row] = v;
+    }
+    unsigned long long key = valid ? argmax_key(v, row) : 0ull;
+    unsigned long long x = __shfl_xor(key, 16, kWave);
+    key = x > key ? x : key;
+    x = __shfl_xor(key, 32, kWave);
+    key = x > key ? x : key;
+    if (t < 256 && lane < 16) s_key[c][lane] = key;
+    __syncthreads();
+    if (t < 16) {
+      unsigned long long best = s_key[0][t];
+#pragma unroll
+      for (int i = 1; i < 4; i++) best = s_key[i][t] > best ? s_key[i][t] : best;
+      if (nt * 16 + t < rows_b) o.argmax[(size_t)(nt * 16 + t) * units + unit] = best;
+    }
+  } else if (rvalid) {
+    const int row = unit * 16 + prow;
+    if (kEpi == kEpiSwiglu) {
+      if (row < w.rows / 2) {
+        const float g = acc[0], u = acc[kNM - 1];
+        bad = !finitef(g) || !finitef(u);
+        o.out[(size_t)r * o.ld + row] = (g / (1.0f + exp_f32(-g))) * u;
+      }
+    } else if (row < w.rows) {
+      const float v = acc[0];
+      bad = !finitef(v);
+      float *q = o.out + (size_t)r * o.ld + row;
+      if (kEpi == kEpiResidual)
+        *q = *q + v;
+      else
+        *q = v;
     }
   }
   if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
@@ -2122,6 +2382,8 @@ __global__ __launch_bounds__(128) void k_attn_combine(StepDims d,
 #pragma unroll
     for (int i = 0; i < 8; i++) v[i] = j < ng ? o_s[j * 8 + i] : 0.0f;
     if (j < ((ng + 3) & ~3)) bad |= quant_group_q8(v, j < ng, r, h * ng + j, nbp, act);
+  } else if (kAct == kActF32) {  // f32 rows for a following Q8_K quantizer
+    if (active) act.f32[(size_t)r * d.H + h * d.D + j] = o;
   } else if (active) {
     const uint16_t hv = f2h(o);
     bad |= !finitef(h2f(hv));
@@ -2206,6 +2468,9 @@ void launch_norm_act(hipStream_t s, int rows, const float *x, const uint32_t *in
   const size_t lds = (size_t)H * sizeof(float);
   if (act_dtype == 8 && nbp * 4 <= 256 && H % 8 == 0)  // one 8-element group per thread
     launch_k(k_norm_q8, dim3(rows), dim3(256), 0, s, x, in_rows, weight, H, eps, nbp, act, row_err);
+  else if (act_dtype == kActQ8K)  // nbp = H / 256 blocks
+    launch_k(k_norm_act<kActQ8K>, dim3(rows), dim3(256), lds, s, x, in_rows, weight, H, eps,
+                       nbp, act, row_err);
   else if (act_dtype == 8)
     launch_k(k_norm_act<8>, dim3(rows), dim3(256), lds, s, x, in_rows, weight, H, eps,
                        nbp, act, row_err);
@@ -2216,6 +2481,10 @@ void launch_norm_act(hipStream_t s, int rows, const float *x, const uint32_t *in
 
 void launch_quant_act(hipStream_t s, int rows, const float *src, int K, int act_dtype, int nbp,
                       ActView act, uint32_t *row_err) {
+  if (act_dtype == kActQ8K) {  // nbp = K / 256 blocks, four per workgroup
+    launch_k(k_quant_act<kActQ8K>, dim3(rows, (nbp + 3) / 4), dim3(256), 0, s, src, K, nbp, act, row_err);
+    return;
+  }
   const int splits = (nbp * 4 + 255) / 256;  // 256 groups of 8 values per workgroup
   if (act_dtype == 8)
     launch_k(k_quant_act<8>, dim3(rows, splits), dim3(256), 0, s, src, K, nbp, act, row_err);
@@ -2303,9 +2572,23 @@ static void mv_f16(hipStream_t s, const MatrixView &w, const ActView &act, int r
   launch_k(k_mv_f16<kEpi>, dim3((out_rows + 3) / 4), dim3(256), 0, s, w, act, rows_b, o);
 }
 
+template <int kEpi, int kNM>
+static void mv_kq(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b, const MatvecOut &o) {
+  const int units = w.mtiles / kNM, n_tiles = (rows_b + 15) / 16;
+  launch_k((k_mv_kq<kEpi, kNM>), dim3((units + 7) / 8 * 8 * n_tiles), dim3(512), 0, s, w, act, rows_b,
+           n_tiles, o);
+}
+
 void launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActView &act,
                    int rows_b, const MatvecOut &o) {
-  if (w.dtype == 8) {
+  if (w.dtype == kFmtKQ) {
+    switch (epi) {
+      case kEpiStore: mv_kq<kEpiStore, 1>(s, w, act, rows_b, o); break;
+      case kEpiResidual: mv_kq<kEpiResidual, 1>(s, w, act, rows_b, o); break;
+      case kEpiSwiglu: mv_kq<kEpiSwiglu, 2>(s, w, act, rows_b, o); break;
+      case kEpiArgmax: mv_kq<kEpiArgmax, 1>(s, w, act, rows_b, o); break;
+    }
+  } else if (w.dtype == 8) {
     switch (epi) {
       case kEpiStore: mv_q8<kEpiStore, 1, 8>(s, w, act, rows_b, o); break;
       case kEpiResidual: mv_q8<kEpiResidual, 1, 8>(s, w, act, rows_b, o); break;
@@ -2481,8 +2764,11 @@ void launch_attn_combine(hipStream_t s, int rows, const StepDims &d, const uint3
                          const double *partial, int act_dtype, int nbp, ActView act,
                          uint32_t *row_err) {
   const int threads = ((d.D + kWave - 1) / kWave) * kWave;
-  if (act_dtype == 8)
-    launch_k(k_attn_combine<8>, dim3(rows, d.NH), dim3(threads), 0, s, d, row_pos,
+  if (act_dtype == kActQ8)
+    launch_k(k_attn_combine<kActQ8>, dim3(rows, d.NH), dim3(threads), 0, s, d, row_pos,
+                       partial, nbp, act, row_err);
+  else if (act_dtype == kActF32)
+    launch_k(k_attn_combine<kActF32>, dim3(rows, d.NH), dim3(threads), 0, s, d, row_pos,
                        partial, nbp, act, row_err);
   else
     launch_k(k_attn_combine<1>, dim3(rows, d.NH), dim3(threads), 0, s, d, row_pos,

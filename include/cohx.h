@@ -40,8 +40,17 @@ enum {
   COHX_DEVICE = 7           /* HIP runtime failure */
 };
 
-/* GGML dtypes accepted for matrices (gguf.rs:104-128; BF16 for Qwen3.5). */
-enum { COHX_F32 = 0, COHX_F16 = 1, COHX_Q4_0 = 2, COHX_Q8_0 = 8, COHX_BF16 = 30 };
+/* GGML dtypes (gguf.rs:104-128; quant.rs:7-12; BF16 for Qwen3.5).  Qwen2
+ * matrices may be F16, Q4_0, Q5_0, Q8_0, Q4_K or Q6_K; vectors are F32. */
+enum { COHX_F32 = 0, COHX_F16 = 1, COHX_Q4_0 = 2, COHX_Q5_0 = 6, COHX_Q8_0 = 8, COHX_Q4_K = 12,
+       COHX_Q6_K = 14, COHX_BF16 = 30 };
+/* cohx_model_desc.weight_dtype for files whose matrices differ in dtype (the
+ * engine binds mixed-type files through one graph, docs/QUANTIZATION.md;
+ * e.g. a Q4_K_M file holds Q5_0, Q8_0, Q4_K and Q6_K matrices): each matrix
+ * takes the dtype of its uploaded tensor.  The parts of a fused matrix
+ * (q/k/v, gate/up) must then agree in family: Q8_0 with Q5_0, Q4_K with
+ * Q6_K, Q4_0 alone, F16 alone. */
+#define COHX_MIXED 0x100u
 
 typedef struct cohx_ctx cohx_ctx;
 
@@ -50,7 +59,8 @@ typedef struct cohx_ctx cohx_ctx;
 typedef struct {
   uint32_t layers, hidden, intermediate, heads, kv_heads, head_dim, vocabulary, context;
   float rope_base, norm_epsilon;
-  uint32_t weight_dtype; /* dtype of every 2-D matrix: COHX_F16, COHX_Q8_0 or COHX_Q4_0 */
+  uint32_t weight_dtype; /* dtype of every 2-D matrix (COHX_F16, COHX_Q4_0, COHX_Q5_0,
+                          * COHX_Q8_0, COHX_Q4_K, COHX_Q6_K), or COHX_MIXED */
   uint32_t tied;         /* 1: logits use token_embd.weight (batch.rs:261-265) */
   uint32_t kv_dtype;     /* 0: f32 KV cache (the engine's, README.md:78) */
   uint32_t max_lanes;    /* lanes per step */
@@ -70,6 +80,24 @@ int cohx_create(const cohx_model_desc *desc, int device, cohx_ctx **out);
 void cohx_destroy(cohx_ctx *ctx);
 /* Human-readable text of the last failure on this context. */
 const char *cohx_last_error(const cohx_ctx *ctx);
+
+/* Model::load from a GGUF file (inference.rs:238-297): the engine's bounded
+ * v3 header parser (gguf.rs:304-496), its Qwen2 configuration and graph
+ * checks (compat.rs:54-221) and end-of-generation ids (eos, eot and
+ * "<|endoftext|>", tokenizer.rs:224-236,304-306), then cohx_create,
+ * cohx_upload_tensor of every tensor from a read-only mapping of the file, and
+ * cohx_finalize.  desc: in, the capacities (max_lanes, max_rows, max_seqs,
+ * max_context, kv_pages; 0 takes 16 lanes, rows = lanes, seqs = lanes,
+ * max_context = min(context, 4096)); out, the file's configuration,
+ * weight_dtype (one dtype or COHX_MIXED), tied flag and EOG ids.  err (may be
+ * NULL) receives the failure's text.  Malformed files fail with
+ * COHX_INVALID_GGUF, unsupported ones with COHX_UNSUPPORTED, as the engine
+ * classifies them. */
+int cohx_load_gguf(const char *path, int device, cohx_model_desc *desc, cohx_ctx **out, char *err,
+                   size_t err_cap);
+/* The parsing and validation of cohx_load_gguf alone (no device work):
+ * fills desc as cohx_load_gguf would. */
+int cohx_gguf_inspect(const char *path, cohx_model_desc *desc, char *err, size_t err_cap);
 
 /* Upload one GGUF tensor by name, payload in the file's block layout
  * (gguf.rs:96-103 Tensor; the library repacks into its HBM layout).
@@ -173,6 +201,21 @@ int cohx_step_noalloc(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out
  * and lanes[R] back.  Sequences are not advanced. */
 int cohx_pack(cohx_ctx *ctx, const cohx_batch *batch, uint32_t *cu_seqlens, uint32_t *positions,
               int64_t *slots, uint32_t *lanes);
+
+/* One matrix on its own (test utility with no engine counterpart, like
+ * cohx_pack): `rows` GGUF rows of width K in `dtype` (F16, Q4_0, Q5_0, Q8_0,
+ * Q4_K, Q6_K) against n f32 input vectors, through the step's own operand
+ * preparation (QuantizedInput::prepare, quant.rs:175-240; binary16 rounding
+ * for F16, cpu.rs:37-48) and exact matvec kernels (quant.rs:245-349 dot):
+ * out[i*rows + r] = dot(row r, input i).  Optional outputs: act_bytes gets
+ * each prepared input in the engine's byte form (Q8_0 34 B per 32 values,
+ * Q8_K 292 B per 256, F16 2 B per value), decoded gets the rows as the
+ * embedding lookup decodes them (rows*K floats, quant.rs:67-137), status[i]
+ * the input's status (COHX_INVALID_GGUF for a non-finite input, scale or
+ * result).  Device memory is allocated for the call and released. */
+int cohx_matvec(cohx_ctx *ctx, uint32_t dtype, uint32_t rows, uint32_t K, const void *weights, size_t bytes,
+                uint32_t n, const float *inputs, float *out, uint8_t *act_bytes, float *decoded,
+                int32_t *status);
 
 /* Opt-in per-kernel timing of cohx_step (no engine counterpart; the engine
  * reports only BatchStep byte counts, batch.rs:3-9).  enable=1 clears the

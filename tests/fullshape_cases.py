@@ -25,6 +25,7 @@ SEED_Q4 = 32      # C4: Q4_0
 SEED_F16_C1 = 33  # C1: F16
 SEED_F16_C3 = 34  # C3: F16
 SEED_Q35 = 35     # C5: Qwen3.5-0.8B bf16
+SEED_Q4KM = 36    # Q4_K_M-style mixed dtypes (the reference's published decode format)
 
 
 def digest(a):
@@ -58,6 +59,18 @@ def c2(lanes):
     kv = [int(v) for v in rng.integers(64, 2049, lanes)]
     tokens = [int(v) for v in rng.integers(0, V_QWEN2, lanes)]
     return {"model_seed": SEED_Q8, "dtype": "q8_0", "fill_seed": 7000 + lanes, "kv": kv,
+            "tokens": tokens, "steps": 2, "context": 2048 + 8, "kv_check_layers": [0, 11, 23]}
+
+
+def q4km(lanes=32):
+    """The Qwen2.5-0.5B shape in the dtype pattern of the publisher's Q4_K_M
+    file (synth.q4_k_m_dtype: Q5_0 q/k/o/gate/up and embedding, Q8_0 or Q5_0
+    v, Q6_K or Q4_K down, untied Q8_0 head), as configs[1]: decode-only
+    lanes over seeded KV of U[64, 2048] tokens, two greedy steps."""
+    rng = np.random.default_rng(1100 + lanes)
+    kv = [int(v) for v in rng.integers(64, 2049, lanes)]
+    tokens = [int(v) for v in rng.integers(0, V_QWEN2, lanes)]
+    return {"model_seed": SEED_Q4KM, "dtype": "q4_k_m", "fill_seed": 7200 + lanes, "kv": kv,
             "tokens": tokens, "steps": 2, "context": 2048 + 8, "kv_check_layers": [0, 11, 23]}
 
 

@@ -8,7 +8,7 @@ the float32 logits, the greedy id, the top-2 values and the SHA-256 of the
 K/V rows each step appends.  tests/test_gpu_baseline_shapes.py runs the same
 inputs through the HIP library and compares.
 
-    python tests/golden/make_fullshape.py [case ...]   # c2_32 c2_128 c4 c1 c3 c5
+    python tests/golden/make_fullshape.py [case ...]   # c2_32 c2_128 c4 c1 c3 c5 q4km_32
 
 The oracle runs on this machine's cores (minutes per case; C5 the longest).
 """
@@ -53,8 +53,8 @@ def decode_steps(o, sess, tokens, steps):
     return out
 
 
-def run_c2(lanes):
-    spec = fc.c2(lanes)
+def run_c2(lanes, spec=None):
+    spec = spec or fc.c2(lanes)
     c, t = synth.in_memory(synth.config(), spec["dtype"], seed=spec["model_seed"])
     o = orc.Model(c, t, threads=THREADS)
     sess = []
@@ -186,7 +186,7 @@ def run_c5():
 
 
 CASES = {"c2_32": lambda: run_c2(32), "c2_128": lambda: run_c2(128), "c4": run_c4, "c1": run_c1,
-         "c3": run_c3, "c5": run_c5}
+         "c3": run_c3, "c5": run_c5, "q4km_32": lambda: run_c2(32, fc.q4km(32))}
 
 
 def main():

@@ -101,6 +101,24 @@ def test_c2_q8_0_ragged_decode_matches_oracle(q8_model, lanes):
     m.close()
 
 
+def test_q4_k_m_full_shape_decode_matches_oracle():
+    """The Qwen2.5-0.5B shape with the publisher Q4_K_M file's dtypes (Q5_0,
+    Q8_0, Q4_K, Q6_K; untied Q8_0 head): 32 decode lanes over KV U[64, 2048]."""
+    spec = fc.q4km(32)
+    fx = fixture("q4km_32", spec)
+    print("building the Q4_K_M-style Qwen2.5-0.5B-shape model", flush=True)
+    c, t = synth.in_memory(synth.config(), spec["dtype"], seed=spec["model_seed"])
+    lanes = len(spec["kv"])
+    m = cohx.Model(c, t, max_lanes=lanes, max_rows=lanes, max_seqs=lanes, max_context=spec["context"])
+    seqs = []
+    for i, n in enumerate(spec["kv"]):
+        s = m.seq_alloc()
+        m.seq_fill_synthetic(s, n, spec["fill_seed"], i)
+        seqs.append(s)
+    run_decode(m, seqs, spec["kv"], spec, fx, "q4km_32")
+    m.close()
+
+
 def test_c4_q4_0_shared_prefix_groups_match_oracle():
     """8 groups of 16 lanes forked from 256-token prefixes
     (shared pages, copy on write), contexts up to 4096."""
