@@ -1078,7 +1078,8 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
 // The device packer over the uploaded lanes (ragged rows, positions, slots).
 void enqueue_pack(cohx_ctx *ctx, const Workspace &w, int n_lanes) {
   launch_pack(ctx->stream, n_lanes, w.lane_info, w.tokens, ctx->page_table, ctx->max_pages, w.cu,
-              w.row_pos, w.row_slot, w.row_lane, w.row_token, w.row_seq, w.lane_last, w.row_err);
+              w.row_pos, w.row_slot, w.row_lane, w.row_token, w.row_seq, w.lane_last, w.row_err, w.argmax,
+              n_lanes);
 }
 
 ActView act_view(const Workspace &w) {
@@ -1401,14 +1402,16 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
                      w.den_part, w.partial);
       prof_end(ctx, e);
     }
+    // Q8_K operands: the combine writes f32 rows, then their blocks
+    const int a_comb = a_o == kActQ8K ? kActF32 : a_o;
     e = prof_begin(ctx, kCatAttnCombine, b_combine, 0);
-    if (a_o == kActQ8K) {  // f32 rows, then their Q8_K blocks
-      launch_attn_combine(s, R, sd, w.row_pos, w.partial, kActF32, 0, act, w.row_err);
-      launch_quant_act(s, R, w.act_f32, H, kActQ8K, act_blocks(kActQ8K, H), act, w.row_err);
-    } else {
-      launch_attn_combine(s, R, sd, w.row_pos, w.partial, a_o, act_blocks(a_o, H), act, w.row_err);
-    }
+    launch_attn_combine(s, R, sd, w.row_pos, w.partial, a_comb, act_blocks(a_comb, H), act, w.row_err);
     prof_end(ctx, e);
+    if (a_o == kActQ8K) {
+      e = prof_begin(ctx, kCatQuant, (double)R * H * 4 + R * act_row_bytes(kActQ8K, H), 0);
+      launch_quant_act(s, R, w.act_f32, H, kActQ8K, act_blocks(kActQ8K, H), act, w.row_err);
+      prof_end(ctx, e);
+    }
     e = prof_begin(ctx, kCatMvO, matrix_pass_bytes(ly.o, R, H, true), 2.0 * R * H * H);
     launch_matvec(s, kEpiResidual, ly.o.view, act, R,
                   MatvecOut{w.x, H, nullptr, nullptr, w.row_err, nullptr});
@@ -1454,10 +1457,12 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
   e = prof_begin(ctx, kCatMvHead,
                  matrix_pass_bytes(head, NL, 0, false) + (any_logits ? (double)NL * d.vocabulary * 4 : 0.0) + NL * 8.0,
                  2.0 * NL * d.vocabulary * H);
-  launch_matvec(s, kEpiArgmax, head.view, act, NL,
-                MatvecOut{nullptr, 0, w.argmax_part, any_logits ? w.logits : nullptr, w.row_err,
-                          w.lane_last});
-  launch_argmax_reduce(s, NL, w.argmax_part, head.view.mtiles, w.argmax);
+  // the final keys start at zero (the packer clears them); a head kernel that
+  // raises them itself needs no reduce over per-tile partials
+  if (!launch_matvec(s, kEpiArgmax, head.view, act, NL,
+                     MatvecOut{nullptr, 0, w.argmax_part, any_logits ? w.logits : nullptr, w.row_err,
+                               w.lane_last, w.argmax}))
+    launch_argmax_reduce(s, NL, w.argmax_part, head.view.mtiles, w.argmax);
   prof_end(ctx, e);
   HIP_TRY(hipGetLastError());
   return COHX_OK;

@@ -66,7 +66,7 @@ struct Workspace {
   uint32_t *row_skip = nullptr;
   uint32_t *row_map = nullptr;
   float *direct = nullptr;
-  unsigned long long *argmax = nullptr;
+  unsigned long long *argmax = nullptr;  // final keys per lane, zeroed by the packer
   unsigned long long *argmax_part = nullptr;  // [lanes][head m-tiles]
   // capacities the buffers were laid out for
   uint32_t rows = 0, lanes = 0, kv_cap = 0, max_chunks = 0, max_tiles = 0;

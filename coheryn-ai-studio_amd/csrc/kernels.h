@@ -70,12 +70,16 @@ struct MatvecOut {
   float *logits;               // kEpiArgmax: optional [rows_b][V] (nullptr: none)
   uint32_t *row_err;           // per batch row error bits
   const uint32_t *err_rows;    // batch row -> packed row index for error bits (nullptr: same)
+  // kEpiArgmax: the final key of each batch row (zero before the launch), which
+  // kernels that see many tiles per workgroup raise with one atomic max per
+  // row instead of writing partials; launch_matvec then returns true
+  unsigned long long *argmax_final;
 };
 
 void launch_pack(hipStream_t s, int n_lanes, const uint32_t *lane_info, const uint32_t *tokens,
                  const int32_t *page_table, int max_pages, uint32_t *cu, uint32_t *row_pos,
                  int32_t *row_slot, uint32_t *row_lane, uint32_t *row_token, uint32_t *row_seq,
-                 uint32_t *lane_last, uint32_t *row_err);
+                 uint32_t *lane_last, uint32_t *row_err, unsigned long long *keys, int n_keys);
 void launch_embed(hipStream_t s, int rows, const MatrixView &emb, const uint32_t *row_token,
                   float *x, int H, uint32_t *row_err);
 // in_rows: optional map from output batch row to input row of x (final norm over logit rows).
@@ -90,7 +94,8 @@ void set_prefill_mfma(bool on);
 // Timing events for the next launches (see the launch helper); both null ends it.
 void set_launch_events(hipEvent_t start, hipEvent_t stop);
 
-void launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActView &act,
+// Returns true when a kEpiArgmax launch wrote o.argmax_final (no reduce needed).
+bool launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActView &act,
                    int rows_b, const MatvecOut &o);
 // Q8_0/Q4_0 gate+up with the SwiGLU quantizer in its epilogue: writes the
 // down projection's Q8_0 operand to qout (which must not alias act; laid out

@@ -58,9 +58,12 @@ __global__ __launch_bounds__(1024) void k_pack(int n, const uint32_t *__restrict
                                                uint32_t *cu, uint32_t *row_pos, int32_t *row_slot,
                                                uint32_t *row_lane, uint32_t *row_token,
                                                uint32_t *row_seq, uint32_t *lane_last,
-                                               uint32_t *row_err) {
+                                               uint32_t *row_err, unsigned long long *keys,
+                                               int n_keys) {
   __shared__ uint32_t scan[1024];
   const int i = threadIdx.x;
+  // the step's final argmax keys start at zero (the head raises them)
+  for (int k = i; k < n_keys; k += 1024) keys[k] = 0ull;
   const uint32_t nt = i < n ? info[i * 4] : 0u;
   scan[i] = nt;
   __syncthreads();
@@ -1251,6 +1254,7 @@ __global__ __launch_bounds__(512, 4) void k_mv_q8h(MatrixView w, ActView act, in
   const bool rvalid = live && r < rows_b;
   const int er = (rvalid && o.err_rows) ? (int)o.err_rows[r] : r;
   bool bad = false;
+  unsigned long long run = 0ull;  // the row's best key over this workgroup's tiles
   for (int it = 0; unit < units; it++, unit += gridDim.x) {
     const int next = unit + gridDim.x;
     // the next tile's share of this thread (kCopy == 4 items), requested now;
@@ -1323,7 +1327,7 @@ __global__ __launch_bounds__(512, 4) void k_mv_q8h(MatrixView w, ActView act, in
       key = x > key ? x : key;
       x = __shfl_xor(key, 32, kWave);
       key = x > key ? x : key;
-      if (lane < 16 && rvalid) o.argmax[(size_t)r * units + unit] = key;
+      run = key > run ? key : run;
     }
     if (next < units) {
       uint4 *dst = smem + ((it + 1) & 1) * tile_items;
@@ -1335,6 +1339,7 @@ __global__ __launch_bounds__(512, 4) void k_mv_q8h(MatrixView w, ActView act, in
     }
     __syncthreads();
   }
+  if (lane < 16 && rvalid && run) atomicMax(o.argmax_final + r, run);
   if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
 }
 
@@ -2451,10 +2456,10 @@ __global__ void k_fill_u32(uint32_t *p, size_t n, uint32_t v) {
 void launch_pack(hipStream_t s, int n_lanes, const uint32_t *lane_info, const uint32_t *tokens,
                  const int32_t *page_table, int max_pages, uint32_t *cu, uint32_t *row_pos,
                  int32_t *row_slot, uint32_t *row_lane, uint32_t *row_token, uint32_t *row_seq,
-                 uint32_t *lane_last, uint32_t *row_err) {
+                 uint32_t *lane_last, uint32_t *row_err, unsigned long long *keys, int n_keys) {
   launch_k(k_pack, dim3(1), dim3(1024), 0, s, n_lanes, lane_info, tokens, page_table,
                      max_pages, cu, row_pos, row_slot, row_lane, row_token, row_seq, lane_last,
-                     row_err);
+                     row_err, keys, n_keys);
 }
 
 void launch_embed(hipStream_t s, int rows, const MatrixView &emb, const uint32_t *row_token,
@@ -2493,7 +2498,7 @@ void launch_quant_act(hipStream_t s, int rows, const float *src, int K, int act_
 }
 
 template <int kEpi, int kNM, int kFmt>
-static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
+static bool mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
                   const MatvecOut &o) {
   const int units = w.mtiles / kNM;
   const int n_tiles = (rows_b + 15) / 16;
@@ -2506,7 +2511,7 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
                        (size_t)8 * w.nbp * 32;
     launch_k((k_mv_q8w<kEpi, kNM, kFmt, kWPairs, 1>), dim3(units, by), dim3(nthreads), lds, s, w, act, rows_b,
              n_tiles, o, ActView{}, 0);
-  } else if (kEpi == kEpiArgmax && kNM == 1 && n_tiles <= 8 && w.nbp <= 2 * kWPairs) {
+  } else if (kEpi == kEpiArgmax && kNM == 1 && n_tiles <= 8 && w.nbp <= 2 * kWPairs && o.argmax_final) {
     // LM head: persistent workgroups streaming weight tiles through LDS, two
     // per CU (4 waves per SIMD); always 8 waves, since the tile copy needs
     // them all (waves past the last batch tile only copy)
@@ -2518,6 +2523,7 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
       launch_k((k_mv_q8h<kFmt, 14>), dim3(blocks), dim3(nthreads), lds, s, w, act, rows_b, n_tiles, o);
     else
       launch_k((k_mv_q8h<kFmt, kWPairs>), dim3(blocks), dim3(nthreads), lds, s, w, act, rows_b, n_tiles, o);
+    return true;
   } else if ((kEpi == kEpiArgmax || kEpi == kEpiSwiglu) && w.nbp <= 64) {
     // short K, many weight tiles (the LM head, gate+up beyond k_mv_q8w's K):
     // register chains, 4 waves per workgroup; the head takes 4 batch tiles
@@ -2536,6 +2542,7 @@ static void mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
     launch_k((k_mv_q8s<kEpi, kNM, 1, kFmt>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
              rows_b, n_tiles, o, QkvEpi{});
   }
+  return false;
 }
 
 // Packed batches at least this tall take the matrix-core F16 linear.
@@ -2579,7 +2586,7 @@ static void mv_kq(hipStream_t s, const MatrixView &w, const ActView &act, int ro
            n_tiles, o);
 }
 
-void launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActView &act,
+bool launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActView &act,
                    int rows_b, const MatvecOut &o) {
   if (w.dtype == kFmtKQ) {
     switch (epi) {
@@ -2593,14 +2600,14 @@ void launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActVi
       case kEpiStore: mv_q8<kEpiStore, 1, 8>(s, w, act, rows_b, o); break;
       case kEpiResidual: mv_q8<kEpiResidual, 1, 8>(s, w, act, rows_b, o); break;
       case kEpiSwiglu: mv_q8<kEpiSwiglu, 2, 8>(s, w, act, rows_b, o); break;
-      case kEpiArgmax: mv_q8<kEpiArgmax, 1, 8>(s, w, act, rows_b, o); break;
+      case kEpiArgmax: return mv_q8<kEpiArgmax, 1, 8>(s, w, act, rows_b, o);
     }
   } else if (w.dtype == 2) {
     switch (epi) {
       case kEpiStore: mv_q8<kEpiStore, 1, 2>(s, w, act, rows_b, o); break;
       case kEpiResidual: mv_q8<kEpiResidual, 1, 2>(s, w, act, rows_b, o); break;
       case kEpiSwiglu: mv_q8<kEpiSwiglu, 2, 2>(s, w, act, rows_b, o); break;
-      case kEpiArgmax: mv_q8<kEpiArgmax, 1, 2>(s, w, act, rows_b, o); break;
+      case kEpiArgmax: return mv_q8<kEpiArgmax, 1, 2>(s, w, act, rows_b, o);
     }
   } else {
     switch (epi) {
@@ -2610,6 +2617,7 @@ void launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActVi
       case kEpiArgmax: mv_f16<kEpiArgmax>(s, w, act, rows_b, o); break;
     }
   }
+  return false;
 }
 
 void launch_matvec_qkv(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
