@@ -57,6 +57,22 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def host_info():
+    """The host the CPU baselines run on: logical CPUs, the ones this process
+    may use, and the CPU model."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"nproc": os.cpu_count(), "usable_cpus": usable, "cpu_model": model}
+
+
 def model_file(seed, dtype="q8_0"):
     path = f"/tmp/cohx_qwen25_05b_{dtype}_seed{seed}.gguf"
     if not os.path.exists(path):
@@ -174,9 +190,12 @@ def run_c4(seed, steps, warmup):
         model.seq_free(base)
     seq_arr = np.asarray(seqs, np.uint32)
     tokens = rng.integers(0, cfg["vocabulary"], lanes).astype(np.uint32)
+    init_tokens, first_out = tokens.tolist(), None
     for _ in range(warmup):
         st, tokens = model.step_decode(seq_arr, tokens)
         assert not st.any()
+        if first_out is None:
+            first_out = tokens.tolist()
     kv0 = [model.seq_length(s) for s in seqs]
     start = tokens.copy()
     trace = []
@@ -195,11 +214,13 @@ def run_c4(seed, steps, warmup):
         same &= bool(np.array_equal(tokens, trace[i]))
     stats = model.profile_read()
     model.profile(False)
+    matrix_bytes = model.matrix_bytes
+    del model
     L, kvd = cfg["layers"], cfg["kv_heads"] * cfg["head_dim"]
     per_tok = L * kvd * 4 * 2
     mean_private = sum(n - C4_PREFIX + 1 + (steps - 1) / 2.0 for n in kv0)
     unique_kv = (C4_GROUPS * C4_PREFIX + mean_private) * per_tok + lanes * per_tok
-    sb = model.matrix_bytes + unique_kv + lanes * cfg["hidden"] // 32 * 18
+    sb = matrix_bytes + unique_kv + lanes * cfg["hidden"] // 32 * 18
     ms = elapsed * 1e3 / steps
     top = max(stats, key=lambda x: x["total_ms"])
     log(f"[bench] c4: {lanes * steps / elapsed:.0f} tok/s, {ms:.3f} ms/step, replay same tokens: {same}")
@@ -212,7 +233,40 @@ def run_c4(seed, steps, warmup):
                               "unit": "GB/s", "frac": sb / (ms / 1e3) / HBM_PEAK},
             "dominant_kernel": {"kernel": top["name"],
                                 "avg_launch_us": top["total_ms"] * 1e3 / top["launches"]},
-            "replay_same_tokens": same}
+            "replay_same_tokens": same,
+            "_cpu": dict(cfg=cfg, tensors=tensors, init=init_tokens, first=first_out, seed=seed,
+                         suffix=suffix)}
+
+
+def c4_cpu_baseline(c, steps, threads):
+    """The oracle on the first 16-lane group of the C4 workload (a 16-lane
+    unit, batch.rs:65): the same Q4_0 weights, the group's shared 256-token
+    prefix and private suffixes and the same first tokens as the GPU run;
+    `steps` decode steps.  Also checks the first step's greedy ids against
+    the GPU's first (warm-up) step."""
+    import orc
+    m = orc.Model(c["cfg"], c["tensors"], threads=threads)
+    sess = []
+    for i in range(C4_GROUP):
+        s = m.session(C4_CONTEXT)
+        s.fill_synthetic(C4_PREFIX, c["seed"], 1000)
+        s.fill_synthetic(C4_PREFIX + c["suffix"][i], c["seed"], i)
+        sess.append(s)
+    toks = c["init"][:C4_GROUP]
+    first = None
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        errs = m.forward_batch(sess, toks)
+        assert not errs.any()
+        toks = [int(orc.Sampler().sample(s.logits())[1]) for s in sess]
+        if first is None:
+            first = list(toks)
+    el = time.perf_counter() - t0
+    return {"value": C4_GROUP * steps / el, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"oracle, the first group's {C4_GROUP} lanes (one unit), {steps} decode steps "
+                      f"from the GPU run's initial state; {el:.1f}s",
+            "greedy_equal_first_step": int(sum(a == b for a, b in zip(first, c["first"][:C4_GROUP]))),
+            "host": host_info()}
 
 
 C3_CHUNKS, C3_DECODE, C3_CONTEXT = 8, 56, 4608
@@ -272,6 +326,7 @@ def run_c3(seed, steps, warmup):
         same &= toks == trace[i]
     stats = model.profile_read()
     model.profile(False)
+    del model
     lin = [x for x in stats if x["name"] in ("matvec_qkv", "matvec_o_residual", "matvec_gate_up_swiglu",
                                             "matvec_down_residual")]
     lin_flops = sum(x["flops"] for x in lin)
@@ -287,8 +342,53 @@ def run_c3(seed, steps, warmup):
             "roofline": {"bound": "mfma", "kernel": "linears (k_gemm_f16)",
                          "achieved": tflops, "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
                          "frac": tflops * 1e12 / MFMA_F16_PEAK},
+            "attention_chunk": chunk_roofline(stats, steps),
             "kernels": {x["name"]: {"ms_per_step": x["total_ms"] / steps} for x in stats if x["launches"]},
-            "replay_same_tokens": same}
+            "replay_same_tokens": same,
+            "_cpu": dict(cfg=cfg, tensors=tensors, chunks=chunks[warmup], kv=kv, seed=seed)}
+
+
+def chunk_roofline(stats, steps):
+    """The prefill chunks' attention on the matrix cores: QK^T and PV flops of
+    the chunk rows (4 * heads * head_dim per attended position) over its time."""
+    x = next((x for x in stats if x["name"] == "attn_chunk_mfma" and x["launches"]), None)
+    if not x:
+        return None
+    tf = x["flops"] / (x["total_ms"] / 1e3) / 1e12
+    return {"bound": "mfma", "kernel": "k_attn_chunk", "achieved": tf, "peak": MFMA_F16_PEAK / 1e12,
+            "unit": "TFLOP/s", "frac": tf * 1e12 / MFMA_F16_PEAK, "ms_per_step": x["total_ms"] / steps,
+            "note": "three bf16 products per f32 product (hi/lo split); the peak is one product's"}
+
+
+C3_CPU_TOKENS = 24
+
+
+def c3_cpu_baseline(c, threads):
+    """The oracle on a sample of one C3 step: the 8 chunk lanes' first
+    C3_CPU_TOKENS prompt tokens (the engine forwards prompts one token per
+    lane per step, docs/BATCHING.md:23, in 16-lane units) and one step of the
+    56 decode lanes over their seeded KV (4 units), on the same F16 weights."""
+    import orc
+    m = orc.Model(c["cfg"], c["tensors"], threads=threads)
+    pre = [m.session(C3_CONTEXT) for _ in range(C3_CHUNKS)]
+    dec = []
+    for i, k in enumerate(c["kv"]):
+        s = m.session(C3_CONTEXT)
+        s.fill_synthetic(k, c["seed"], 500 + i)
+        dec.append(s)
+    toks = [int(v) for v in np.random.default_rng(7).integers(0, c["cfg"]["vocabulary"], C3_DECODE)]
+    t0 = time.perf_counter()
+    for j in range(C3_CPU_TOKENS):
+        errs = m.forward_batch(pre, [ch[j] for ch in c["chunks"]])
+        assert not errs.any()
+    for u in range(0, C3_DECODE, 16):
+        errs = m.forward_batch(dec[u:u + 16], toks[u:u + 16])
+        assert not errs.any()
+    el = time.perf_counter() - t0
+    rows = C3_CHUNKS * C3_CPU_TOKENS + C3_DECODE
+    return {"value": rows / el, "unit": "packed rows/s", "cores": threads, "kind": "port",
+            "sample": f"oracle, the first {C3_CPU_TOKENS} tokens of the 8 prompt chunks and one step of "
+                      f"the 56 decode lanes ({rows} rows); {el:.1f}s", "host": host_info()}
 
 
 def measured_traffic(category, lanes):
@@ -457,6 +557,81 @@ def summarize_c5_trace(trace_csv, bench_json):
           f"Summary: `python bench.py --summarize-c5-trace <dir>/<name>_kernel_trace.csv <bench stdout>`")
 
 
+LEG_TRACE_CMD = ("COHX_GRAPHS=0 rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o <name> -- "
+                 "python3 bench.py --only {leg}")
+LEG_PMC_CMD = ("COHX_GRAPHS=0 rocprofv3 --pmc {counters} --kernel-include-regex \"{regex}\" --output-format csv "
+               "-d <dir> -o <name> -- python3 bench.py --only {leg}")
+MFMA_COUNTERS = "SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_MOPS_BF16 GRBM_GUI_ACTIVE"
+MI355X_CUS = 256
+
+
+def summarize_leg(leg, trace_csv, bench_json, fetch_csv=None, write_csv=None, mfma_csv=None,
+                  copy_fetch_csv=None, copy_write_csv=None):
+    """Markdown summary of the rocprofv3 runs of one workload (`bench.py
+    --only <leg>`): per kernel instance and grid the dispatch count and mean
+    duration (kernel trace); HBM bytes per dispatch from FETCH_SIZE /
+    WRITE_SIZE scaled by the same counters over a 1 GiB copy; for the matrix-
+    core kernels the MFMA counters (SQ_INSTS_VALU_MFMA_MOPS_* count units of
+    512 flops; busy share = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x
+    256 CUs))."""
+    import csv
+    groups = {}
+    with open(trace_csv) as f:
+        for row in csv.DictReader(f):
+            k = (kernel_instance(row["Kernel_Name"]),
+                 f'{row["Grid_Size_X"]}x{row["Grid_Size_Y"]}x{row["Grid_Size_Z"]}')
+            groups.setdefault(k, []).append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+    with open(bench_json) as f:
+        line = json.loads(f.read().strip().splitlines()[-1])
+    print(f"# {leg.upper()}: kernel trace and counters\n")
+    print(f"Workload: {line['workload']}.\n")
+    print(f"Plain run (`python3 bench.py --only {leg}`): {line['value']:.0f} {line['unit']}, "
+          f"{line['ms_per_step']:.3f} ms/step.\n")
+    print(f"Kernel trace: `{LEG_TRACE_CMD.format(leg=leg)}`\n")
+    print("| kernel | grid (threads) | dispatches | mean us | min us | max us | total ms |")
+    print("|---|---:|---:|---:|---:|---:|---:|")
+    for (name, gx), d in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:25]:
+        print(f"| {name} | {gx} | {len(d)} | {sum(d) / len(d):.2f} | {min(d):.2f} | {max(d):.2f} | "
+              f"{sum(d) / 1e3:.2f} |")
+    if fetch_csv and write_csv and copy_fetch_csv and copy_write_csv:
+        cf = counter_means(copy_fetch_csv)["__amd_rocclr_copyBuffer"][0] * 1024
+        cw = counter_means(copy_write_csv)["__amd_rocclr_copyBuffer"][0] * 1024
+        ff, fw = float(1 << 30) / cf, float(1 << 30) / cw
+        fetch, write = counter_means(fetch_csv), counter_means(write_csv)
+        print(f"\nHBM traffic: `{LEG_PMC_CMD.format(counters='FETCH_SIZE', regex='k_', leg=leg)}`, then "
+              f"`WRITE_SIZE`; scaled by the same counters over a 1 GiB copy (`{COPY_CMD.format(counter='FETCH_SIZE')}`: "
+              f"factors {ff:.4f} fetch, {fw:.4f} write).\n")
+        print("| kernel | dispatches | FETCH KiB | WRITE KiB | HBM bytes per launch |")
+        print("|---|---:|---:|---:|---:|")
+        for k, (fk, n) in sorted(fetch.items(), key=lambda kv: -kv[1][0]):
+            wk = write.get(k, (0.0, 0))[0]
+            print(f"| {k} | {n} | {fk:.0f} | {wk:.0f} | {(fk * ff + wk * fw) * 1024 / 1e6:.2f} MB |")
+    if mfma_csv:
+        acc = {}
+        with open(mfma_csv) as f:
+            for row in csv.DictReader(f):
+                k = kernel_instance(row["Kernel_Name"])
+                a = acc.setdefault(k, {"_d": set(), "_ns": 0.0})
+                a[row["Counter_Name"]] = a.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+                if row["Dispatch_Id"] not in a["_d"]:
+                    a["_d"].add(row["Dispatch_Id"])
+                    a["_ns"] += int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+        print(f"\nMatrix cores: `{LEG_PMC_CMD.format(counters=MFMA_COUNTERS, regex='k_gemm_f16|k_attn_chunk', leg=leg)}`\n")
+        print("| kernel | dispatches | MFMA busy share | MOPS f16 (x512 flop) | MOPS bf16 (x512 flop) | "
+              "counted TFLOP/s |")
+        print("|---|---:|---:|---:|---:|---:|")
+        for k, a in sorted(acc.items()):
+            busy = a.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / max(a.get("GRBM_GUI_ACTIVE", 1.0) * MI355X_CUS, 1.0)
+            mops = a.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0) + a.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0)
+            tf = mops * 512 / (a["_ns"] * 1e-9) / 1e12 if a["_ns"] else 0.0
+            print(f"| {k} | {len(a['_d'])} | {busy:.3f} | {a.get('SQ_INSTS_VALU_MFMA_MOPS_F16', 0.0):.3g} | "
+                  f"{a.get('SQ_INSTS_VALU_MFMA_MOPS_BF16', 0.0):.3g} | {tf:.0f} |")
+        print("\nThe counted rate covers every MFMA issued, including the chunk attention's three bf16 "
+              "products per f32 product; the bench's TFLOP/s count the algorithmic flops once.")
+    print(f"\nSummary: `python3 bench.py --summarize-leg {leg} <trace.csv> <bench stdout> [<fetch.csv> "
+          f"<write.csv> <mfma.csv or -> <copy_fetch.csv> <copy_write.csv>]`")
+
+
 def copy_probe():
     """A plain device copy of known size, for scaling the FETCH_SIZE and
     WRITE_SIZE counters to bytes (the tensors are plumbing, not the product)."""
@@ -557,6 +732,17 @@ def run_c5(seed, cpu_steps, threads, with_cpu=True):
                                 "ms_per_step": es["elapsed"] * 1e3 / es["steps"],
                                 "elapsed_s": es["elapsed"]},
             "same_tokens_both_schedules": same, "seed": seed + 5}
+    # one-token schedule: each step reads every weight once and each
+    # sequence's recurrent state (conv ring and delta memory, read and written)
+    lin = sum(1 for f in cfg["full"] if not f)
+    state = lin * (cfg["linear_value_heads"] * cfg["linear_key_dim"] * cfg["linear_value_dim"] * 4 * 2)
+    sb = model.matrix_bytes + C5_SEQS * state
+    es_s = es["elapsed"] / es["steps"]
+    line["engine_schedule"]["step_roofline"] = {
+        "bound": "hbm", "bytes_per_step": sb, "achieved": sb / es_s / 1e9, "peak": HBM_PEAK / 1e9,
+        "unit": "GB/s", "frac": sb / es_s / HBM_PEAK,
+        "note": "weights once plus each sequence's delta memory read and written; the exact step is "
+                "bound by one wave's issue rate on its f64 chains, not by HBM"}
     del model
     if with_cpu:
         import orc
@@ -571,7 +757,7 @@ def run_c5(seed, cpu_steps, threads, with_cpu=True):
             "value": C5_SEQS * cpu_steps / el, "unit": "rows/s", "cores": threads, "kind": "port",
             "sample": f"oracle, the first {cpu_steps} prompt tokens of all {C5_SEQS} sequences, "
                       f"one token per sequence per step, no head (prompt rows); {el:.1f}s",
-            "gpu_engine_schedule_rows_per_s": es["rows"] / es["elapsed"]}
+            "gpu_engine_schedule_rows_per_s": es["rows"] / es["elapsed"], "host": host_info()}
     return line
 
 
@@ -590,6 +776,8 @@ def main():
     ap.add_argument("--no-c5", action="store_true", help="skip the Qwen3.5 hybrid workload")
     ap.add_argument("--c5-only", action="store_true",
                     help="run only the Qwen3.5 hybrid workload and print its JSON")
+    ap.add_argument("--only", choices=["c3", "c4", "c5"],
+                    help="run only this workload and print its JSON (profiling runs)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 1 GiB device-to-device 4 times (counter calibration)")
     ap.add_argument("--summarize-counters", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
@@ -598,6 +786,9 @@ def main():
                     help="print a markdown summary of a rocprofv3 --kernel-trace run of --c5-only")
     ap.add_argument("--summarize-trace", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_JSON"),
                     help="print a markdown summary of a rocprofv3 --kernel-trace run (no GPU)")
+    ap.add_argument("--summarize-leg", nargs="+", metavar="ARG",
+                    help="LEG TRACE_CSV BENCH_JSON [FETCH WRITE MFMA COPY_FETCH COPY_WRITE]: markdown "
+                         "summary of the rocprofv3 runs of `--only LEG` (no GPU)")
     args = ap.parse_args()
     if args.copy_probe:
         copy_probe()
@@ -611,14 +802,29 @@ def main():
     if args.summarize_trace:
         summarize_trace(*args.summarize_trace)
         return
+    if args.summarize_leg:
+        a = [None if x == "-" else x for x in args.summarize_leg] + [None] * (8 - len(args.summarize_leg))
+        summarize_leg(a[0], a[1], a[2], fetch_csv=a[3], write_csv=a[4], mfma_csv=a[5], copy_fetch_csv=a[6],
+                      copy_write_csv=a[7])
+        return
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
               "(the step shards by sequence with no collectives; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
-    threads = min(16, os.cpu_count() or 1)
-    if args.c5_only:
+    threads = min(16, host_info()["usable_cpus"] or 1)
+    if args.c5_only or args.only == "c5":
         print(json.dumps(run_c5(args.seed, args.cpu_steps // 2, threads,
                                 with_cpu=not args.no_cpu_baseline)), flush=True)
+        return
+    if args.only == "c4":
+        r = run_c4(args.seed, 128, args.warmup)
+        r.pop("_cpu")
+        print(json.dumps(r), flush=True)
+        return
+    if args.only == "c3":
+        r = run_c3(args.seed, 8, 2)
+        r.pop("_cpu")
+        print(json.dumps(r), flush=True)
         return
     path = model_file(args.seed)
     meta, tensors = gguf.read(path)
@@ -666,8 +872,18 @@ def main():
     if not args.no_c4:
         del model
         line["c4"] = run_c4(args.seed, 128, args.warmup)
+        c4c = line["c4"].pop("_cpu")
+        if not args.no_cpu_baseline:
+            log(f"[bench] c4 cpu baseline: oracle, {C4_GROUP} lanes x 8 steps, {threads} threads")
+            line["c4"]["cpu_baseline"] = c4_cpu_baseline(c4c, 8, threads)
+        del c4c
     if not args.no_c3:
         line["c3"] = run_c3(args.seed, 8, 2)
+        c3c = line["c3"].pop("_cpu")
+        if not args.no_cpu_baseline:
+            log(f"[bench] c3 cpu baseline: oracle, {threads} threads")
+            line["c3"]["cpu_baseline"] = c3_cpu_baseline(c3c, threads)
+        del c3c
     if not args.no_c5:
         line["c5"] = run_c5(args.seed, args.cpu_steps // 2, threads, with_cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
@@ -675,10 +891,16 @@ def main():
         log(f"[bench] cpu baseline: oracle, {n_cpu} lanes x {args.cpu_steps} steps, {threads} threads")
         first, tps, el = cpu_baseline(cfg, tensors, main_r["kv"], main_r["start_tokens"], args.seed,
                                       n_cpu, args.cpu_steps, threads)
+        log(f"[bench] cpu baseline: oracle, {n_cpu} lanes x 2 steps, 1 thread")
+        _, tps1, el1 = cpu_baseline(cfg, tensors, main_r["kv"], main_r["start_tokens"], args.seed,
+                                    n_cpu, 2, 1)
         line["cpu_baseline"] = {
             "value": tps, "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"first {n_cpu} of the {args.lanes} lanes (one 16-lane unit, batch.rs:65), "
-                      f"{args.cpu_steps} decode steps, same weights/KV/tokens; {el:.1f}s"}
+                      f"{args.cpu_steps} decode steps, same weights/KV/tokens; {el:.1f}s",
+            "threads_1": {"value": tps1, "unit": "tok/s", "cores": 1,
+                          "sample": f"the same lanes, 2 decode steps on one thread; {el1:.1f}s"},
+            "host": host_info()}
         gpu_first = main_r["first_argmax"][:n_cpu]
         line["parity"] = {"lanes": n_cpu, "greedy_equal": int(sum(a == b for a, b in zip(first, gpu_first))),
                           "check": "first-step greedy token, GPU vs CPU oracle, same inputs"}

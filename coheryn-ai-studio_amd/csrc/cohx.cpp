@@ -1340,9 +1340,13 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
   int e;
   // per-launch algorithmic bytes
   const double b_norm = (double)R * H * 4 + H * 4 + R * act_row;
-  const double b_scores = kv_rows * KVD * 4 + (double)RX * H * 4 + kv_rows * NH * 4;
-  const double b_softmax = kv_rows * NH * 4 * 2;
-  const double b_pv = kv_rows * KVD * 4 + kv_rows * NH * 4 + (double)RX * H * 4;
+  // algorithmic bytes of the exact attention passes: the K rows attended
+  // (and the queries) for the scores, the V rows for the values; the score,
+  // exponent and partial-sum buffers between the passes are intermediates
+  // and count nothing, nor does the exponent pass
+  const double b_scores = kv_rows * KVD * 4 + (double)RX * H * 4;
+  const double b_softmax = 0.0;
+  const double b_pv = kv_rows * KVD * 4;
   const double f_attn = kv_rows * NH * D * 2;
   // chunk tiles: each lane's K and V once, Q in and O out; QK^T and PV flops
   const double b_chunk = (double)p.kv_chunk_lanes * KVD * 4 * 2 + (R - RX) * (double)H * 4 * 2;
