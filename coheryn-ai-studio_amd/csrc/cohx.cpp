@@ -1458,6 +1458,9 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
                   act_blocks(act_head, H), act, w.row_err);
   prof_end(ctx, e);
   const DeviceMatrix &head = d.tied ? ctx->embd : ctx->output;
+  // a step in the packed-prefill regime (its linears on the matrix cores)
+  // takes the F16 head there too; otherwise the head stays exact
+  set_head_mfma(p.n_tiles > 0 || (ctx->prefill_mfma && head.view.dtype == kFmtF16 && R >= 128));
   e = prof_begin(ctx, kCatMvHead,
                  matrix_pass_bytes(head, NL, 0, false) + (any_logits ? (double)NL * d.vocabulary * 4 : 0.0) + NL * 8.0,
                  2.0 * NL * d.vocabulary * H);
@@ -1467,6 +1470,7 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
                      MatvecOut{nullptr, 0, w.argmax_part, any_logits ? w.logits : nullptr, w.row_err,
                                w.lane_last, w.argmax}))
     launch_argmax_reduce(s, NL, w.argmax_part, head.view.mtiles, w.argmax);
+  set_head_mfma(false);
   prof_end(ctx, e);
   HIP_TRY(hipGetLastError());
   return COHX_OK;

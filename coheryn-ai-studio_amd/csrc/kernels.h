@@ -91,6 +91,9 @@ void launch_quant_act(hipStream_t s, int rows, const float *src, int K, int act_
 // Packed F16 batches of 128+ rows on the matrix cores (f32 sums, within tolerance
 // of the reference's f64 sums) or always on the exact kernels.
 void set_prefill_mfma(bool on);
+// The F16 LM head of the next launches on the matrix cores too (f32 sums; a
+// step in the packed-prefill regime, at 16 or more logit rows).
+void set_head_mfma(bool on);
 // Timing events for the next launches (see the launch helper); both null ends it.
 void set_launch_events(hipEvent_t start, hipEvent_t stop);
 

@@ -28,6 +28,7 @@ namespace cohx {
 namespace {
 thread_local hipEvent_t t_ev_start = nullptr, t_ev_stop = nullptr;
 thread_local bool g_prefill_mfma = true;  // set per step from the context
+thread_local bool g_head_mfma = false;    // this step's F16 head on the matrix cores
 
 template <typename F, typename... Args>
 void launch_k(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args... args) {
@@ -41,6 +42,7 @@ void launch_k(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args
 }  // namespace
 
 void set_prefill_mfma(bool on) { g_prefill_mfma = on; }
+void set_head_mfma(bool on) { g_head_mfma = on; }
 
 void set_launch_events(hipEvent_t start, hipEvent_t stop) {
   t_ev_start = start;
@@ -1671,6 +1673,38 @@ __global__ __launch_bounds__(256) void k_gemm_f16(MatrixView w, const uint16_t *
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
   // ---- epilogue: lane holds features (tile row) 4*(lane/16)+i of rows (tile col) lane%16
+  if constexpr (kEpi == kEpiArgmax) {
+    // per (batch row, 16-feature tile) partial keys, as the exact head
+    // kernels write them for k_argmax_reduce; logits on request
+#pragma unroll
+    for (int b = 0; b < kNB; b++) {
+      const int r = r0 + wr * 16 * kNB + b * 16 + lr;
+      const bool rvalid = r < rows_b;
+      bool bad = false;
+#pragma unroll
+      for (int a = 0; a < 4; a++) {
+        const int ft = f0 + wf * 64 + a * 16, fb = ft + 4 * (lane / 16);
+        unsigned long long key = 0ull;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float v = acc[a][b][i];
+          if (rvalid && fb + i < w.rows) {
+            bad |= !finitef(v);
+            if (o.logits) o.logits[(size_t)r * w.rows + fb + i] = v;
+            const unsigned long long k = argmax_key(v, fb + i);
+            key = k > key ? k : key;
+          }
+        }
+        unsigned long long x2 = __shfl_xor(key, 16, kWave);
+        key = x2 > key ? x2 : key;
+        x2 = __shfl_xor(key, 32, kWave);
+        key = x2 > key ? x2 : key;
+        if (lane < 16 && rvalid && ft < w.rows) o.argmax[(size_t)r * w.mtiles + ft / 16] = key;
+      }
+      if (bad) atomicOr(&o.row_err[o.err_rows ? (int)o.err_rows[r] : r], kErrNonFinite);
+    }
+    return;
+  }
   if (kEpi == kEpiSwiglu) {
     float *s_up = reinterpret_cast<float *>(s_mem);  // 2 x 4 kNB x 4 x 64 floats
     if (wf == 1) {
@@ -2553,6 +2587,13 @@ static void mv_f16(hipStream_t s, const MatrixView &w, const ActView &act, int r
                    const MatvecOut &o) {
   const int out_rows = kEpi == kEpiSwiglu ? w.rows / 2 : w.rows;
   // tall packed batches: matrix cores (f32 sums); the head always stays exact
+  // the head of a step in the packed-prefill regime: the same matrix-core
+  // GEMM, 64 rows per workgroup, partial keys per 16-row tile
+  if (kEpi == kEpiArgmax && g_head_mfma && rows_b >= 16 && w.K % kGemmBK == 0) {
+    launch_k(k_gemm_f16<kEpi, 2, kGemmStages2>, dim3((w.rows + kGemmBM - 1) / kGemmBM, (rows_b + 63) / 64),
+             dim3(256), kGemmStages2 * (128 + 64) * 64, s, w, (const uint16_t *)act.f16, rows_b, o);
+    return;
+  }
   if (kEpi != kEpiArgmax && g_prefill_mfma && rows_b >= kPrefillRows && w.K % kGemmBK == 0 &&
       (kEpi != kEpiSwiglu || out_rows % (kGemmBM / 2) == 0)) {
     const int ftile = kEpi == kEpiSwiglu ? kGemmBM / 2 : kGemmBM;

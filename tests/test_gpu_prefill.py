@@ -138,3 +138,45 @@ def test_chunk_attention_matches_oracle_within_tolerance():
         o.forward_batch([sa], [tok])
     assert res[0]["status"] == 0
     close(res[0]["logits"], sa.logits(), "chunk-only step")
+
+
+def test_regime_head_on_matrix_cores_matches_oracle():
+    """A packed-prefill step with 18 logit rows: the F16 head runs on the
+    matrix cores too (f32 sums), every lane within tolerance of the oracle,
+    greedy ids equal where the margin allows; with the regime off the same
+    step is bit-exact."""
+    print("case: regime step with 18 lanes (head on the matrix cores)", flush=True)
+    cfg = synth.config(layers=2, hidden=128, intermediate=256, heads=4, kv_heads=2,
+                       vocabulary=700, context=512)
+    c, t = synth.in_memory(cfg, "f16", seed=35)
+    kw = dict(max_lanes=20, max_rows=256, max_seqs=20, max_context=256)
+    mm, me = make(c, t, True, **kw), make(c, t, False, **kw)
+    o = orc.Model(c, t, threads=8)
+    rng = np.random.default_rng(11)
+    chunk = [int(v) for v in rng.integers(0, c["vocabulary"], 140)]
+    toks = [int(v) for v in rng.integers(0, c["vocabulary"], 17)]
+    res = {}
+    for name, m in (("mfma", mm), ("exact", me)):
+        a = m.seq_alloc()
+        dec = [m.seq_alloc() for _ in toks]
+        for i, s in enumerate(dec):
+            m.seq_fill_synthetic(s, 20 + 3 * i, 13, i)
+        res[name] = m.step([dict(seq=a, tokens=chunk, logits=True)] +
+                           [dict(seq=s, tokens=[tk], logits=True) for s, tk in zip(dec, toks)])
+    sa = o.session(256)
+    for tok in chunk:
+        o.forward_batch([sa], [tok])
+    sess = []
+    for i in range(len(toks)):
+        s = o.session(256)
+        s.fill_synthetic(20 + 3 * i, 13, i)
+        sess.append(s)
+    o.forward_batch(sess, toks)
+    want = [sa.logits()] + [s.logits() for s in sess]
+    for i, w in enumerate(want):
+        assert res["mfma"][i]["status"] == 0 and res["exact"][i]["status"] == 0
+        assert np.array_equal(res["exact"][i]["logits"], w), i
+        close(res["mfma"][i]["logits"], w, f"lane {i}")
+        if res["mfma"][i]["argmax"] != res["exact"][i]["argmax"]:
+            order = np.sort(w)
+            assert order[-1] - order[-2] <= 2 * float(np.abs(res["mfma"][i]["logits"] - w).max()), i
