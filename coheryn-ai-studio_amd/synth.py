@@ -192,10 +192,13 @@ def config(**overrides):
     return c
 
 
-def build(cfg, dtype="q8_0", seed=0, eos_token_id=None, tied=None, std=0.02):
+def build(cfg, dtype="q8_0", seed=0, eos_token_id=None, tied=None, std=0.02, spread=None):
     """Returns (metadata, [(name, shape, dtype, payload)]) for a seeded model.
     dtype "q4_k_m" gives each matrix the dtype q4_k_m_dtype picks (and an
-    untied head, as the publisher's file has); tied defaults to True otherwise."""
+    untied head, as the publisher's file has); tied defaults to True otherwise.
+    spread=(lo, hi) multiplies every matrix row, norm weight and bias element
+    by 2^U[lo, hi] (integer exponents): activations, K/V rows and products
+    then span many binades (tests of the reduction orders)."""
     mixed = dtype == "q4_k_m"
     wdt = None if mixed else (DTYPES[dtype] if isinstance(dtype, str) else dtype)
     tied = (not mixed) if tied is None else tied
@@ -204,28 +207,36 @@ def build(cfg, dtype="q8_0", seed=0, eos_token_id=None, tied=None, std=0.02):
     kvd = cfg["kv_heads"] * cfg["head_dim"]
     eos = V - 1 if eos_token_id is None else eos_token_id
 
+    def scale(shape):
+        if spread is None:
+            return np.float32(1.0)
+        return np.exp2(rng.integers(spread[0], spread[1] + 1, shape)).astype(np.float32)
+
     def normal(rows, width):
-        return rng.standard_normal((rows, width), dtype=np.float32) * np.float32(std)
+        return rng.standard_normal((rows, width), dtype=np.float32) * np.float32(std) * scale((rows, 1))
+
+    def ones(n):
+        return np.ones((1, n), np.float32) * scale((1, n))
 
     def mat(name, rows, width, layer=None):
         t = q4_k_m_dtype(name, width, layer, L) if mixed else wdt
         return t, encode(normal(rows, width), t)
 
     tensors = [("token_embd.weight", (H, V), *mat("token_embd.weight", V, H)),
-               ("output_norm.weight", (H,), 0, encode(np.ones((1, H), np.float32), 0))]
+               ("output_norm.weight", (H,), 0, encode(ones(H), 0))]
     if not tied:
         tensors.append(("output.weight", (H, V), *mat("output.weight", V, H)))
     for i in range(L):
         p = f"blk.{i}."
         tensors += [
-            (p + "attn_norm.weight", (H,), 0, encode(np.ones((1, H), np.float32), 0)),
-            (p + "ffn_norm.weight", (H,), 0, encode(np.ones((1, H), np.float32), 0)),
+            (p + "attn_norm.weight", (H,), 0, encode(ones(H), 0)),
+            (p + "ffn_norm.weight", (H,), 0, encode(ones(H), 0)),
             (p + "attn_q.weight", (H, H), *mat("attn_q.weight", H, H, i)),
             (p + "attn_k.weight", (H, kvd), *mat("attn_k.weight", kvd, H, i)),
             (p + "attn_v.weight", (H, kvd), *mat("attn_v.weight", kvd, H, i)),
-            (p + "attn_q.bias", (H,), 0, encode(normal(1, H), 0)),
-            (p + "attn_k.bias", (kvd,), 0, encode(normal(1, kvd), 0)),
-            (p + "attn_v.bias", (kvd,), 0, encode(normal(1, kvd), 0)),
+            (p + "attn_q.bias", (H,), 0, encode(normal(1, H) * scale((1, H)), 0)),
+            (p + "attn_k.bias", (kvd,), 0, encode(normal(1, kvd) * scale((1, kvd)), 0)),
+            (p + "attn_v.bias", (kvd,), 0, encode(normal(1, kvd) * scale((1, kvd)), 0)),
             (p + "attn_output.weight", (H, H), *mat("attn_output.weight", H, H, i)),
             (p + "ffn_gate.weight", (H, F), *mat("ffn_gate.weight", F, H, i)),
             (p + "ffn_up.weight", (H, F), *mat("ffn_up.weight", F, H, i)),
