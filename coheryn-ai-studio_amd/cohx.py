@@ -99,6 +99,14 @@ class GenOptions(ctypes.Structure):
                 ("stop_tokens", ctypes.POINTER(ctypes.c_uint32)), ("context", ctypes.c_uint32)]
 
 
+YIELD_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)
+
+
+class StepHooks(ctypes.Structure):
+    _fields_ = [("yield_", YIELD_FN), ("user", ctypes.c_void_p),
+                ("cancel", ctypes.POINTER(ctypes.c_uint32))]
+
+
 class KernelStat(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("launches", ctypes.c_uint64),
                 ("total_ms", ctypes.c_double), ("bytes", ctypes.c_double),
@@ -144,6 +152,11 @@ EXPORTS = {
                                                ctypes.c_uint64, ctypes.c_uint32]),
     "cohx_step": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Batch), ctypes.POINTER(StepOut)]),
     "cohx_step_noalloc": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Batch), ctypes.POINTER(StepOut)]),
+    "cohx_step_hooked": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Batch), ctypes.POINTER(StepOut),
+                                        ctypes.POINTER(StepHooks)]),
+    "cohx_step_batch_hooked": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint32,
+                                              ctypes.c_void_p, YIELD_FN, ctypes.c_void_p]),
+    "cohx_gen_compatible": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "cohx_pack": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Batch),
                                  ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32),
                                  ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_uint32)]),
@@ -378,10 +391,13 @@ class Model:
             arr[i].want_logits = 1 if ln.get("logits") else (SKIP_HEAD if ln.get("skip_head") else 0)
         return Batch(len(lanes), arr), keep
 
-    def step(self, lanes, noalloc=False):
+    def step(self, lanes, noalloc=False, yield_fn=None, cancel=None):
         """lanes: [{"seq", "tokens", "start"?, "logits"?: bool, "skip_head"?: bool}] -> list
         of dicts (status, argmax, logits).  noalloc: through cohx_step_noalloc
-        (device scratch from the library's static array)."""
+        (device scratch from the library's static array).  yield_fn (called
+        while the device computes; a true return asks to stop) and cancel (a
+        uint32 array of per-lane flags, read before the launch and after the
+        device finishes) go through cohx_step_hooked."""
         batch, keep = self._batch(lanes)
         outs = (LaneOut * len(lanes))()
         bufs = []
@@ -395,6 +411,16 @@ class Model:
                 bufs.append(None)
         so = StepOut()
         so.lanes = outs
+        if yield_fn is not None or cancel is not None:
+            cb = YIELD_FN((lambda _u: int(bool(yield_fn()))) if yield_fn else 0)
+            hk = StepHooks(cb, None, cancel.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
+                           if cancel is not None else None)
+            rc = lib().cohx_step_hooked(self.h, ctypes.byref(batch), ctypes.byref(so), ctypes.byref(hk))
+            res = [dict(status=outs[i].status, argmax=outs[i].argmax, logits=bufs[i])
+                   for i in range(len(lanes))]
+            if rc:
+                raise CohxError(rc, lib().cohx_last_error(self.h).decode())
+            return res
         entry = lib().cohx_step_noalloc if noalloc else lib().cohx_step
         self._check(entry(self.h, ctypes.byref(batch), ctypes.byref(so)))
         res = [dict(status=outs[i].status, argmax=outs[i].argmax, logits=bufs[i])
@@ -470,10 +496,15 @@ class Model:
         self._states.add(st)
         return st
 
-    def step_batch(self, states):
+    def step_batch(self, states, yield_fn=None):
+        """Model::step_batch; yield_fn: the WorkYield hook (cohx_step_batch_hooked)."""
         arr = (ctypes.c_void_p * len(states))(*[s.h for s in states])
         st = BatchStepC()
-        self._check(lib().cohx_step_batch(self.h, arr, len(states), ctypes.byref(st)))
+        if yield_fn is None:
+            self._check(lib().cohx_step_batch(self.h, arr, len(states), ctypes.byref(st)))
+        else:
+            cb = YIELD_FN(lambda _u: int(bool(yield_fn())))
+            self._check(lib().cohx_step_batch_hooked(self.h, arr, len(states), ctypes.byref(st), cb, None))
         return dict(width=st.width, completed_tokens=st.completed_tokens,
                     matrix_tiles=st.matrix_tiles, matrix_bytes=st.matrix_bytes)
 
@@ -534,6 +565,9 @@ class GenerationState:
 
     def cancel(self):
         lib().cohx_gen_cancel(self.h)
+
+    def compatible(self, other):
+        return bool(lib().cohx_gen_compatible(self.h, other.h))
 
 
 def generate(model, prompt, options):

@@ -593,6 +593,7 @@ void cohx_destroy(cohx_ctx *ctx) {
                   (void *)ctx->host.h_tiles, (void *)ctx->host.h_row_skip, (void *)ctx->host.h_row_map})
     if (p) (void)hipHostFree(p);
   q35_free(ctx);
+  if (ctx->done) (void)hipEventDestroy(ctx->done);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -972,7 +973,7 @@ struct Prepared {
 
 // Host validation (batch.rs:119-131) and upload of the device batch into w.
 int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, Prepared &p,
-                  Workspace &w) {
+                  Workspace &w, const volatile uint32_t *cancel = nullptr) {
   const cohx_model_desc &d = ctx->desc;
   if (!batch || batch->n_lanes == 0 || batch->n_lanes > d.max_lanes || !batch->lanes)
     return fail(ctx, COHX_INVALID_REQUEST,
@@ -992,7 +993,9 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
     const bool live = valid_seq(ctx, ln.seq);
     const uint32_t start =
         (live && ln.start_position == COHX_AT_END) ? ctx->seqs[ln.seq].length : ln.start_position;
-    if (!live || ln.n_tokens == 0 || !ln.tokens || start != ctx->seqs[ln.seq].length) {
+    if (cancel && cancel[i]) {
+      status = COHX_CANCELLED;  // Cancellation::check before the forward
+    } else if (!live || ln.n_tokens == 0 || !ln.tokens || start != ctx->seqs[ln.seq].length) {
       status = COHX_INVALID_REQUEST;
     } else {
       for (uint32_t j = 0; j < ln.n_tokens; j++)
@@ -1480,12 +1483,13 @@ namespace {
 
 // One ragged step over `batch` with its device scratch in w.  graphs: decode
 // steps may replay a captured graph (the buffers in w must then stay fixed).
-int run_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out, Workspace &w, bool graphs) {
+int run_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out, Workspace &w, bool graphs,
+             const cohx_step_hooks *hooks = nullptr) {
   const auto t_start = std::chrono::steady_clock::now();
   HIP_TRY(hipSetDevice(ctx->device));
   const cohx_model_desc &d = ctx->desc;
   Prepared p;
-  int rc = prepare_batch(ctx, batch, out->lanes, p, w);
+  int rc = prepare_batch(ctx, batch, out->lanes, p, w, hooks ? hooks->cancel : nullptr);
   if (rc) {
     ctx->prof.pending.clear();
     ctx->prof.next = 0;
@@ -1545,9 +1549,11 @@ int run_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out, Workspa
       HIP_TRY(hipMemcpyAsync(dst, w.logits + (size_t)k * d.vocabulary, d.vocabulary * sizeof(float),
                              hipMemcpyDeviceToHost, s));
   }
-  HIP_TRY(hipStreamSynchronize(s));
+  const int wrc = wait_step(ctx, s, hooks);
+  if (wrc && wrc != COHX_CANCELLED) return wrc;
   prof_collect(ctx);
-  // lane statuses from row error bits; advance healthy sequences
+  // lane statuses from row error bits; advance healthy sequences (none when
+  // the yield hook asked to stop: a shared failure)
   uint32_t row = 0;
   for (int k = 0; k < NL; k++) {
     const int i = p.included[k];
@@ -1557,12 +1563,18 @@ int run_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out, Workspa
     row += ln.n_tokens;
     cohx_lane_out &o = out->lanes[i];
     o.argmax = 0xffffffffu - (uint32_t)(hs.h_argmax[k] & 0xffffffffull);
-    if (bits & kErrPage)
+    if (wrc || (hooks && hooks->cancel && hooks->cancel[i]))
+      o.status = COHX_CANCELLED;
+    else if (bits & kErrPage)
       o.status = COHX_RESOURCE;
     else if (bits)
       o.status = COHX_INVALID_GGUF;
     else
       ctx->seqs[ln.seq].length += ln.n_tokens;
+  }
+  if (wrc) {
+    out->width = 0;
+    return fail(ctx, COHX_CANCELLED, "shared batch compute cancelled");
   }
   uint32_t width = 0;
   for (uint32_t i = 0; i < batch->n_lanes; i++) width += out->lanes[i].status == COHX_OK;
@@ -1579,10 +1591,40 @@ int run_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out, Workspa
 }  // namespace
 
 extern "C" int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
-  if (ctx && ctx->q35) return q35_step(ctx, batch, out);
+  if (ctx && ctx->q35) return q35_step(ctx, batch, out, nullptr);
   if (!ctx || !out || !out->lanes) return COHX_INVALID_REQUEST;
   return run_step(ctx, batch, out, ctx->ws, ctx->use_graphs);
 }
+
+extern "C" int cohx_step_hooked(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out,
+                                const cohx_step_hooks *hooks) {
+  if (ctx && ctx->q35) return q35_step(ctx, batch, out, hooks);
+  if (!ctx || !out || !out->lanes) return COHX_INVALID_REQUEST;
+  return run_step(ctx, batch, out, ctx->ws, ctx->use_graphs, hooks);
+}
+
+namespace cohx {
+int wait_step(cohx_ctx *ctx, hipStream_t s, const cohx_step_hooks *hooks) {
+  if (!hooks || !hooks->yield) {
+    HIP_TRY(hipStreamSynchronize(s));
+    return COHX_OK;
+  }
+  if (!ctx->done) HIP_TRY(hipEventCreateWithFlags(&ctx->done, hipEventDisableTiming));
+  HIP_TRY(hipEventRecord(ctx->done, s));
+  int stop = 0;
+  for (;;) {
+    const hipError_t q = hipEventQuery(ctx->done);
+    if (q == hipSuccess) break;
+    if (q != hipErrorNotReady) return fail(ctx, COHX_DEVICE, std::string("step: ") + hipGetErrorString(q));
+    if (stop) {  // nothing more to offer the caller: wait for the device
+      HIP_TRY(hipEventSynchronize(ctx->done));
+      break;
+    }
+    stop = hooks->yield(hooks->user);
+  }
+  return stop ? COHX_CANCELLED : COHX_OK;
+}
+}  // namespace cohx
 
 // The same step as cohx_step with every device buffer the step needs beyond
 // the context's weights, KV pool and page tables carved from the static

@@ -7,6 +7,7 @@
 // and never copy logits; any other sampling setting copies the last row's
 // logits and runs the seeded host sampler.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstring>
 #include <vector>
@@ -164,14 +165,21 @@ struct cohx_gen {
   std::vector<uint32_t> ids;
   std::vector<uint32_t> stop_tokens;
   uint32_t max_tokens = 0;
-  bool done = false, cancelled = false;
+  bool done = false;
+  // Cancellation token (set from any thread); the state machine observes it
+  // on the owning thread
+  std::atomic<bool> cancel{false};
   uint32_t reason = COHX_FINISH_LENGTH;
   int32_t error = COHX_OK;
   std::vector<float> logits;  // last forward's logits (only when the sampler needs them)
   uint32_t argmax = 0;
 
   bool prefilling() const { return cursor < prompt.size(); }
-  bool needs_forward() const { return !done && (prefilling() || pending >= 0); }
+  bool cancelled() const { return cancel.load(std::memory_order_acquire); }
+  // generate_impl (inference.rs:655-664): a decode-phase cancellation
+  // finishes the generation with reason Cancelled
+  bool finished() const { return done || (cancelled() && !prefilling()); }
+  bool needs_forward() const { return !finished() && (prefilling() || pending >= 0); }
 };
 
 namespace {
@@ -189,7 +197,7 @@ int next_token(cohx_gen *g, uint32_t *token) {
     g->error = COHX_OK;
     return e;
   }
-  if (g->cancelled) return COHX_CANCELLED;
+  if (g->cancelled()) return COHX_CANCELLED;
   if (g->done) return COHX_INVALID_REQUEST;
   if (g->cursor < g->prompt.size()) {
     *token = g->prompt[g->cursor];
@@ -243,13 +251,13 @@ int cohx_gen_begin(cohx_ctx *ctx, const uint32_t *prompt, uint32_t n_prompt,
   // A hybrid (Qwen3.5) context's recurrent state cannot be rewound, so there
   // the prior sequence is taken over only when all of it is such a prefix.
   size_t common = 0;
-  if (prior && prior->ctx == ctx && prior->has_seq && prior->done) {
+  if (prior && prior->ctx == ctx && prior->has_seq && prior->finished()) {
     while (common < prior->kv_tokens.size() && common < g->prompt.size() &&
            prior->kv_tokens[common] == g->prompt[common])
       common++;
     common = std::min(common, g->prompt.size() - 1);
   }
-  if (prior && prior->ctx == ctx && prior->has_seq && prior->done &&
+  if (prior && prior->ctx == ctx && prior->has_seq && prior->finished() &&
       ctx->seqs[prior->seq].capacity >= context &&
       (!ctx->q35 || common == prior->kv_tokens.size())) {
     g->seq = prior->seq;
@@ -272,6 +280,11 @@ int cohx_gen_begin(cohx_ctx *ctx, const uint32_t *prompt, uint32_t n_prompt,
 
 // Model::step_batch (batch.rs:64-116)
 int cohx_step_batch(cohx_ctx *ctx, cohx_gen *const *states, uint32_t n, cohx_batch_step *stats) {
+  return cohx_step_batch_hooked(ctx, states, n, stats, nullptr, nullptr);
+}
+
+int cohx_step_batch_hooked(cohx_ctx *ctx, cohx_gen *const *states, uint32_t n, cohx_batch_step *stats,
+                           int (*yield)(void *user), void *user) {
   if (!ctx || !states) return COHX_INVALID_REQUEST;
   if (n == 0 || n > ctx->desc.max_lanes)
     return fail(ctx, COHX_INVALID_REQUEST,
@@ -321,7 +334,10 @@ int cohx_step_batch(cohx_ctx *ctx, cohx_gen *const *states, uint32_t n, cohx_bat
   cohx_batch batch{(uint32_t)lanes.size(), lanes.data()};
   cohx_step_out so{};
   so.lanes = outs.data();
-  const int rc = cohx_step(ctx, &batch, &so);
+  std::vector<uint32_t> before(lanes.size());
+  for (size_t k = 0; k < lanes.size(); k++) before[k] = lanes[k].start_position;
+  const cohx_step_hooks hooks{yield, user, nullptr};
+  const int rc = cohx_step_hooked(ctx, &batch, &so, yield ? &hooks : nullptr);
   if (rc) {  // shared failure: every participant observes it (batch.rs:98-105)
     for (uint32_t i : lane_of)
       if (!states[i]->error) states[i]->error = rc;
@@ -330,6 +346,14 @@ int cohx_step_batch(cohx_ctx *ctx, cohx_gen *const *states, uint32_t n, cohx_bat
   uint32_t completed = 0;
   for (size_t k = 0; k < lanes.size(); k++) {
     cohx_gen *g = states[lane_of[k]];
+    // cancelled while the device computed: on a Qwen2 context the forward is
+    // dropped (the sequence keeps its length), as the engine's check between
+    // layers would have stopped it; a Qwen3.5 step stands (its recurrent
+    // state cannot be rewound) and the next step observes the token
+    if (!outs[k].status && !ctx->q35 && g->cancelled()) {
+      cohx_seq_truncate(ctx, g->seq, before[k]);
+      outs[k].status = COHX_CANCELLED;
+    }
     if (outs[k].status) {
       g->error = outs[k].status;
       continue;
@@ -374,7 +398,13 @@ int cohx_gen_sample(cohx_gen *g, int64_t *token) {
     g->error = COHX_OK;
     return e;
   }
-  if (g->cancelled) return COHX_CANCELLED;
+  if (g->cancelled()) {
+    if (!g->prefilling() && !g->done) {
+      g->done = true;
+      g->reason = COHX_FINISH_CANCELLED;
+    }
+    return COHX_CANCELLED;
+  }
   if (g->done || g->needs_forward()) return COHX_OK;
   if (g->ids.size() == g->max_tokens) {
     g->done = true;
@@ -402,12 +432,14 @@ int cohx_gen_sample(cohx_gen *g, int64_t *token) {
 }
 
 int cohx_gen_needs_forward(const cohx_gen *g) { return g && g->needs_forward(); }
-int cohx_gen_is_finished(const cohx_gen *g) { return g && g->done; }
+int cohx_gen_is_finished(const cohx_gen *g) { return g && g->finished(); }
 int cohx_gen_is_prefilling(const cohx_gen *g) { return g && g->prefilling(); }
 uint32_t cohx_gen_finish_reason(const cohx_gen *g) {
-  if (!g || !g->done) return COHX_FINISH_NONE;
-  return g->reason;
+  if (!g || !g->finished()) return COHX_FINISH_NONE;
+  return g->done ? g->reason : (uint32_t)COHX_FINISH_CANCELLED;
 }
+
+int cohx_gen_compatible(const cohx_gen *a, const cohx_gen *b) { return a && b && a->ctx == b->ctx; }
 
 uint32_t cohx_gen_tokens(const cohx_gen *g, uint32_t *out, uint32_t cap) {
   if (!g) return 0;
@@ -417,14 +449,7 @@ uint32_t cohx_gen_tokens(const cohx_gen *g, uint32_t *out, uint32_t cap) {
 }
 
 void cohx_gen_cancel(cohx_gen *g) {
-  if (!g) return;
-  g->cancelled = true;
-  // generate_impl (inference.rs:655-664): a decode-phase cancellation finishes
-  // the generation with reason Cancelled.
-  if (!g->prefilling()) {
-    g->done = true;
-    g->reason = COHX_FINISH_CANCELLED;
-  }
+  if (g) g->cancel.store(true, std::memory_order_release);
 }
 
 void cohx_gen_free(cohx_gen *g) {

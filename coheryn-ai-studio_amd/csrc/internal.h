@@ -158,6 +158,7 @@ struct cohx_ctx {
   bool prefill_mfma = true;  // F16 batches of 128+ rows on the matrix cores
   std::map<cohx::StepKey, hipGraphExec_t> graphs;
   cohx::Q35Model *q35 = nullptr;  // set for Qwen3.5 contexts (cohx_create_qwen35)
+  hipEvent_t done = nullptr;      // completion event of a hooked step (created on first use)
 };
 
 namespace cohx {
@@ -171,5 +172,9 @@ int q35_finalize(cohx_ctx *ctx);
 int q35_seq_reset(cohx_ctx *ctx, uint32_t seq);
 int q35_seq_copy(cohx_ctx *ctx, uint32_t src, uint32_t dst, uint32_t rows);
 int q35_read_state(cohx_ctx *ctx, uint32_t seq, uint32_t layer, int which, float *out);
-int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out);
+int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out, const cohx_step_hooks *hooks);
+// Waits for everything enqueued on `s`; with a yield hook, calls it between
+// polls of a completion event instead of blocking.  Returns COHX_CANCELLED
+// (after the device has finished) when the hook asked to stop.
+int wait_step(cohx_ctx *ctx, hipStream_t s, const cohx_step_hooks *hooks);
 }

@@ -479,7 +479,7 @@ int q35_read_state(cohx_ctx *ctx, uint32_t seq, uint32_t layer, int which, float
 // carry several consecutive tokens (a prompt chunk); the linears run over all
 // packed rows, and the recurrences walk each lane's tokens in order, so the
 // result equals stepping the tokens one at a time.
-int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
+int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out, const cohx_step_hooks *hooks) {
   const auto t_start = std::chrono::steady_clock::now();
   Q35Model *q = ctx->q35;
   const cohx_model_desc &d = ctx->desc;
@@ -504,7 +504,9 @@ int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
     const bool live = ln.seq < ctx->seqs.size() && ctx->seqs[ln.seq].live;
     const uint32_t len = live ? ctx->seqs[ln.seq].length : 0;
     const uint32_t start = (live && ln.start_position == COHX_AT_END) ? len : ln.start_position;
-    if (!live || ln.n_tokens == 0 || !ln.tokens || start != len) {
+    if (hooks && hooks->cancel && hooks->cancel[i]) {
+      st = COHX_CANCELLED;  // Cancellation::check before the forward
+    } else if (!live || ln.n_tokens == 0 || !ln.tokens || start != len) {
       st = COHX_INVALID_REQUEST;
     } else {
       for (uint32_t j = 0; j < ln.n_tokens; j++)
@@ -620,7 +622,11 @@ int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out) {
       Q35_TRY(hipMemcpyAsync(dst, q->logits + (size_t)head_of[k] * q->V, q->V * 4,
                              hipMemcpyDeviceToHost, s));
   }
-  Q35_TRY(hipStreamSynchronize(s));
+  // the recurrent state was updated in place and cannot be rewound, so the
+  // completed step stands; a stop request from the yield hook (or a lane's
+  // cancellation) takes effect at the next step
+  const int wrc = wait_step(ctx, s, hooks);
+  if (wrc && wrc != COHX_CANCELLED) return wrc;
   uint32_t width = 0;
   uint64_t kv_rows = 0;
   for (int k = 0; k < NL; k++) {

@@ -183,6 +183,34 @@ typedef struct {
  * success. */
 int cohx_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out);
 
+/* Cooperation with the caller's scheduler during a step (no counterpart
+ * needed on a GPU otherwise, since the host only waits while the device
+ * computes):
+ *  - yield: the engine's WorkYield (multimodal.rs:6; the Qwen3.5 step calls
+ *    it between layers, qwen35/execution.rs:306-309, and the scheduler uses it
+ *    to release and re-acquire its compute permit, scheduler/batching.rs:
+ *    229-239).  Here it is called while the device computes the step, between
+ *    polls of the step's completion, so the caller can hand its permit to
+ *    other work; it may block.  A non-zero return is the Err of WorkYield
+ *    (shared cancellation, shutdown): the call waits for the device, then
+ *    fails with COHX_CANCELLED and no lane advances.
+ *  - cancel: n_lanes flags (may be NULL), the lanes' Cancellation tokens
+ *    (inference.rs:32-68, checked between layers and row tiles,
+ *    tensor.rs:361-367).  A lane whose flag is set before the launch is left
+ *    out with COHX_CANCELLED (its peers are not perturbed); a Qwen2 lane whose
+ *    flag is set by the time the device finishes also reports COHX_CANCELLED
+ *    and its sequence does not advance.  A Qwen3.5 step that completed stands
+ *    (its recurrent state cannot be rewound); the flag is seen by the next
+ *    step. */
+typedef struct {
+  int (*yield)(void *user);
+  void *user;
+  const volatile uint32_t *cancel;
+} cohx_step_hooks;
+/* cohx_step with hooks (NULL: exactly cohx_step). */
+int cohx_step_hooked(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out,
+                     const cohx_step_hooks *hooks);
+
 /* cohx_step without any device allocation, for callers that cannot allocate
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  No counterpart in the reference, whose step allocates nothing
@@ -303,6 +331,11 @@ int cohx_gen_begin(cohx_ctx *ctx, const uint32_t *prompt, uint32_t n_prompt,
                    const cohx_gen_options *options, cohx_gen *prior, cohx_gen **out);
 /* Model::step_batch (batch.rs:64-116): one token per lane, 1..=max_lanes lanes. */
 int cohx_step_batch(cohx_ctx *ctx, cohx_gen *const *states, uint32_t n, cohx_batch_step *out);
+/* cohx_step_batch with the WorkYield hook (see cohx_step_hooks); the states'
+ * own cancellation (cohx_gen_cancel, which may be called from any thread while
+ * a step runs) is checked before the launch and after the device finishes. */
+int cohx_step_batch_hooked(cohx_ctx *ctx, cohx_gen *const *states, uint32_t n, cohx_batch_step *out,
+                           int (*yield)(void *user), void *user);
 /* Model::step_generation (generation.rs:244-257): the single-lane path. */
 int cohx_step_generation(cohx_ctx *ctx, cohx_gen *state);
 /* GenerationState::sample (generation.rs:319-394): *token = id or -1 for none. */
@@ -313,7 +346,13 @@ int cohx_gen_is_prefilling(const cohx_gen *state);
 uint32_t cohx_gen_finish_reason(const cohx_gen *state);
 /* Generated ids so far; returns the count (copies at most cap). */
 uint32_t cohx_gen_tokens(const cohx_gen *state, uint32_t *out, uint32_t cap);
+/* Cancellation::cancel for this generation; thread-safe (an atomic flag):
+ * the owning thread observes it at its next step, sample or state query. */
 void cohx_gen_cancel(cohx_gen *state);
+/* GenerationState::compatible (generation.rs:271-275): both states belong to
+ * the same context (the engine also requires equal execution settings, which
+ * are the context's here). */
+int cohx_gen_compatible(const cohx_gen *a, const cohx_gen *b);
 void cohx_gen_free(cohx_gen *state);
 
 #ifdef __cplusplus
