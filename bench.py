@@ -735,7 +735,8 @@ def run_c5(seed, cpu_steps, threads, with_cpu=True):
     # one-token schedule: each step reads every weight once and each
     # sequence's recurrent state (conv ring and delta memory, read and written)
     lin = sum(1 for f in cfg["full"] if not f)
-    state = lin * (cfg["linear_value_heads"] * cfg["linear_key_dim"] * cfg["linear_value_dim"] * 4 * 2)
+    conv_ch = 2 * cfg["key_heads"] * cfg["key_dim"] + cfg["value_heads"] * cfg["value_dim"]
+    state = lin * (cfg["value_heads"] * cfg["key_dim"] * cfg["value_dim"] + conv_ch * cfg["conv_kernel"]) * 4 * 2
     sb = model.matrix_bytes + C5_SEQS * state
     es_s = es["elapsed"] / es["steps"]
     line["engine_schedule"]["step_roofline"] = {

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libcohx.so")
 SOURCES = ["csrc/kernels.hip", "csrc/cohx.cpp", "csrc/gen.cpp", "csrc/q35_kernels.hip", "csrc/q35.cpp",
-           "csrc/gguf.cpp"]
+           "csrc/gguf.cpp", "csrc/blas.cpp"]
 HEADERS = ["csrc/device.h", "csrc/kernels.h", "csrc/internal.h", "../include/cohx.h"]
 ARCH = os.environ.get("COHX_ARCH", "gfx950")
 
@@ -57,7 +57,8 @@ def build(verbose=False):
         objs = list(ex.map(compile_one, SOURCES))
     tmp = LIB + ".tmp"
     # -z defs: an undefined symbol (say, a kernel stub the host pass dropped) fails the build
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", tmp, *objs]
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", tmp, *objs,
+           "-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)

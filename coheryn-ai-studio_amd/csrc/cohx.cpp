@@ -404,7 +404,8 @@ size_t layout_workspace(const cohx_model_desc &d, int nbp_h, int nbp_f, uint32_t
   w.lanes = NL;
   w.kv_cap = kv_cap;
   w.max_chunks = (uint32_t)chunks;
-  w.max_tiles = (R + 15) / 16 + NL;
+  // prefill-chunk attention work items: 16-row tiles x key segments
+  w.max_tiles = ((R + 15) / 16 + NL) * ((kv_cap + kChunkSegKeys - 1) / kChunkSegKeys);
   w.logits_room = logits;
   Carver c{base};
   c.take(w.lane_info, (size_t)NL * 4);
@@ -504,6 +505,7 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   if (const char *g = std::getenv("COHX_GRAPHS")) ctx->use_graphs = std::strcmp(g, "0") != 0;
   // COHX_PREFILL_MFMA=0 keeps tall F16 batches on the exact (f64-sum) kernels
   if (const char *g = std::getenv("COHX_PREFILL_MFMA")) ctx->prefill_mfma = std::strcmp(g, "0") != 0;
+  if (const char *g = std::getenv("COHX_GEMM_LIB")) ctx->use_gemm_lib = std::strcmp(g, "0") != 0;
   auto bail = [&](int rc) {
     cohx_destroy(ctx);
     return rc;
@@ -588,6 +590,7 @@ void cohx_destroy(cohx_ctx *ctx) {
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   drop_graphs(ctx);
+  gemm_lib_destroy(ctx->gemm_lib);
   for (void *p : ctx->allocations) (void)hipFree(p);
   for (void *p : {(void *)ctx->host.h_upload, (void *)ctx->host.h_row_err, (void *)ctx->host.h_argmax,
                   (void *)ctx->host.h_tiles, (void *)ctx->host.h_row_skip, (void *)ctx->host.h_row_map})
@@ -1046,8 +1049,9 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
       }
       p.kv_chunk_lanes += start + nt;
       for (uint32_t t = 0; t < nt; t += 16) {
-        hs.h_tiles[p.n_tiles++] = int4{(int)(row0 + t), (int)std::min(16u, nt - t), (int)seq,
-                                       (int)(start + t)};
+        const uint32_t rows_t = std::min(16u, nt - t), kv_end = start + t + rows_t;
+        for (uint32_t sg = 0; sg * kChunkSegKeys < kv_end; sg++)
+          hs.h_tiles[p.n_tiles++] = int4{(int)(row0 + t), (int)(rows_t | (sg << 8)), (int)seq, (int)(start + t)};
         for (uint32_t j = t; j < std::min(nt, t + 16); j++) {
           hs.h_row_skip[row0 + j] = 1;
           p.kv_rows_chunk += (uint64_t)start + j + 1;
@@ -1057,8 +1061,13 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
     if (!p.n_tiles) p.max_kv_exact = p.max_kv;
     if (p.n_tiles) {
       // longest KV first, so the short tiles fill in behind the long ones
+      // (a work item's keys: to the end of its segment or of its rows)
+      auto keys = [](const int4 &a) {
+        const int seg = a.y >> 8, end = a.w + (a.y & 0xff);
+        return std::min(end, (seg + 1) * kChunkSegKeys) - seg * kChunkSegKeys;
+      };
       std::stable_sort(hs.h_tiles, hs.h_tiles + p.n_tiles,
-                       [](const int4 &a, const int4 &b) { return a.w + a.y > b.w + b.y; });
+                       [&](const int4 &a, const int4 &b) { return keys(a) > keys(b); });
       p.n_exact = 0;
       for (uint32_t r = 0; r < p.rows; r++)
         if (!hs.h_row_skip[r]) hs.h_row_map[p.n_exact++] = r;
@@ -1274,6 +1283,11 @@ void prof_collect(cohx_ctx *ctx) {
       p.ms[l.cat] += ms;
       p.bytes[l.cat] += l.bytes;
       p.flops[l.cat] += l.flops;
+    } else {
+      // an interval whose launcher launched nothing (a fused path that
+      // declined the shape): its events were never recorded; clear the error
+      // so the step's next status check does not report it
+      (void)hipGetLastError();
     }
   }
   p.pending.clear();
@@ -1318,6 +1332,31 @@ extern "C" uint32_t cohx_profile_read(const cohx_ctx *ctx, cohx_kernel_stat *out
 int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_grid, bool any_logits) {
   const cohx_model_desc &d = ctx->desc;
   set_prefill_mfma(ctx->prefill_mfma);
+  set_gemm_lib(nullptr, nullptr, 0);
+  {
+    // the regime's F16 linears through the library: steps that carry prompt
+    // rows (never captured into a graph, so a step's arithmetic does not
+    // depend on the graph setting), on the context's own workspace (not the
+    // allocation-free call, which keeps the matrix-core kernel); gate+up's
+    // sums go to the attention score buffer, which is dead by then
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const bool eager = hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone;
+    if (eager && !p.single_token && &w == &ctx->ws && ctx->use_gemm_lib && ctx->prefill_mfma &&
+        d.weight_dtype == COHX_F16 && p.rows >= 128 && !ctx->gemm_lib_failed) {
+      if (!ctx->gemm_lib) {
+        constexpr size_t kGemmWorkspace = 32u << 20;
+        void *gws = nullptr;
+        if (dalloc(ctx, reinterpret_cast<uint8_t **>(&gws), kGemmWorkspace) == COHX_OK)
+          ctx->gemm_lib = gemm_lib_create(gws, kGemmWorkspace);
+        if (!ctx->gemm_lib) {
+          ctx->gemm_lib_failed = true;
+          (void)hipGetLastError();
+        }
+      }
+      if (ctx->gemm_lib)
+        set_gemm_lib(ctx->gemm_lib, w.scores, (size_t)w.rows * d.kv_heads * w.kv_cap * 8);
+    }
+  }
   const int pk = prof_begin(ctx, kCatPack, 0.0, 0.0);
   enqueue_pack(ctx, w, (int)p.included.size());
   prof_end(ctx, pk);
@@ -1393,7 +1432,7 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
     }
     if (p.n_tiles) {
       e = prof_begin(ctx, kCatAttnChunk, b_chunk, f_chunk);
-      launch_attn_chunk(s, p.n_tiles, sd, w.tiles, w.q_rot, kp, vp, ctx->page_table, w.direct);
+      launch_attn_chunk(s, p.n_tiles, sd, w.tiles, w.q_rot, kp, vp, ctx->page_table, w.partial);
       prof_end(ctx, e);
     }
     if (RX) {
@@ -1441,6 +1480,22 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
                                             down_act, ly.down.view.nbp);
       prof_end(ctx, e);
     }
+    if (!fused_quant && a_down == kActF16) {
+      // F16 in the packed-prefill regime: library GEMM, then SwiGLU into
+      // the down operand (false: nothing launched)
+      e = prof_begin(ctx, kCatMvGateUp, matrix_pass_bytes(ly.gu, R, 0, false) + (double)R * F * 2,
+                     2.0 * R * 2 * F * H);
+      fused_quant = launch_matvec_swiglu_f16(s, ly.gu.view, act, R,
+                                             MatvecOut{nullptr, 0, nullptr, nullptr, w.row_err, nullptr},
+                                             w.act_f16);
+      prof_end(ctx, e);
+      if (fused_quant) {
+        e = prof_begin(ctx, kCatMvDown, matrix_pass_bytes(ly.down, R, H, true), 2.0 * R * H * F);
+        launch_matvec(s, kEpiResidual, ly.down.view, act, R, MatvecOut{w.x, H, nullptr, nullptr, w.row_err, nullptr});
+        prof_end(ctx, e);
+        continue;
+      }
+    }
     if (!fused_quant) {
       e = prof_begin(ctx, kCatMvGateUp, matrix_pass_bytes(ly.gu, R, F, false), 2.0 * R * 2 * F * H);
       launch_matvec(s, kEpiSwiglu, ly.gu.view, act, R,
@@ -1474,6 +1529,7 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
                                w.lane_last, w.argmax}))
     launch_argmax_reduce(s, NL, w.argmax_part, head.view.mtiles, w.argmax);
   set_head_mfma(false);
+  set_gemm_lib(nullptr, nullptr, 0);
   prof_end(ctx, e);
   HIP_TRY(hipGetLastError());
   return COHX_OK;

@@ -97,6 +97,19 @@ void set_head_mfma(bool on);
 // Timing events for the next launches (see the launch helper); both null ends it.
 void set_launch_events(hipEvent_t start, hipEvent_t stop);
 
+// Library GEMMs (hipBLASLt, blas.cpp) for the packed-prefill regime's F16
+// linears: Y[M][N] (+)= X[M][K] . W[N][K]^T, binary16 operands, f32 sums.
+struct GemmLib;
+GemmLib *gemm_lib_create(void *workspace, size_t workspace_bytes);
+void gemm_lib_destroy(GemmLib *lib);
+// false: nothing launched (no algorithm for the shape)
+bool gemm_lib_f16(GemmLib *lib, hipStream_t s, const uint16_t *w, int N, int K, const uint16_t *x, int M,
+                  float *out, int ldo, bool accumulate);
+// The next launches' F16 linears in the regime go through `lib` (nullptr:
+// the matrix-core kernel); gate+up writes its [rows][2F] f32 sums to
+// `scratch` (at least scratch_floats) before the SwiGLU pass.
+void set_gemm_lib(GemmLib *lib, float *scratch, size_t scratch_floats);
+
 // Returns true when a kEpiArgmax launch wrote o.argmax_final (no reduce needed).
 bool launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActView &act,
                    int rows_b, const MatvecOut &o);
@@ -109,6 +122,14 @@ bool launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActVi
 // to even.
 bool launch_matvec_swiglu_q8(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
                              const MatvecOut &o, const ActView &qout, int qout_nbp);
+// F16 gate+up of a step in the packed-prefill regime through the library GEMM
+// (set_gemm_lib), its SwiGLU pass writing the down projection's binary16
+// operand rows out_f16[rows_b][F] directly: the bits of launch_matvec
+// (kEpiSwiglu) then launch_quant_act(kActF16) over the same sums.  Returns
+// false (nothing launched) when no library GEMM is set or the shape is not
+// covered (F % 8, scratch room).
+bool launch_matvec_swiglu_f16(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
+                              const MatvecOut &o, uint16_t *out_f16);
 void launch_argmax_reduce(hipStream_t s, int rows, const unsigned long long *part, int units,
                           unsigned long long *out);
 // Q8_0/Q4_0 qkv projection with launch_qkv_post's work in its epilogue (bias,
@@ -145,11 +166,17 @@ void launch_attn_pv(hipStream_t s, int rows, int max_kv, const StepDims &d, cons
                     const uint32_t *row_pos, const uint32_t *row_seq, const int32_t *page_table,
                     const float *escores, const double *den_part, double *partial);
 // Matrix-core attention for prefill chunks (tolerance regime): tiles[i] =
-// {first packed row, rows (<= 16), sequence, position of the first row}.
+// {first packed row, rows (<= 16) | key segment << 8, sequence, position of
+// the first row}; a workgroup attends to keys [seg * kChunkSegKeys, + kChunkSegKeys)
+// and writes the segment's row max, row sum and unnormalized output as f32
+// (chunk_seg_at) into the rows' partial-sum space, which the combine pass
+// merges in segment order.
+constexpr int kChunkSegKeys = 512;
+constexpr int kChunkSegFloats = 2 + 64;  // m, l, o[64] (head_dim 64)
 bool attention_chunk_supported(int D, int G);
 void launch_attn_chunk(hipStream_t s, int n_tiles, const StepDims &d, const int4 *tiles,
                        const float *q_rot, const float *kpool, const float *vpool,
-                       const int32_t *page_table, float *direct);
+                       const int32_t *page_table, double *partial);
 void launch_attn_combine(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
                          const double *partial, int act_dtype, int nbp, ActView act,
                          uint32_t *row_err);

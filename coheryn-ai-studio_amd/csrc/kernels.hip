@@ -29,6 +29,9 @@ namespace {
 thread_local hipEvent_t t_ev_start = nullptr, t_ev_stop = nullptr;
 thread_local bool g_prefill_mfma = true;  // set per step from the context
 thread_local bool g_head_mfma = false;    // this step's F16 head on the matrix cores
+thread_local GemmLib *g_lib = nullptr;     // library GEMMs for the regime's F16 linears
+thread_local float *g_lib_scratch = nullptr;
+thread_local size_t g_lib_scratch_floats = 0;
 
 template <typename F, typename... Args>
 void launch_k(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args... args) {
@@ -43,6 +46,23 @@ void launch_k(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args
 
 void set_prefill_mfma(bool on) { g_prefill_mfma = on; }
 void set_head_mfma(bool on) { g_head_mfma = on; }
+// Library GEMMs take no timing events of their own: while they are set, the
+// interval's start and stop are plain markers around the library call.
+static void lib_mark_begin(hipStream_t s) {
+  if (t_ev_start) {
+    (void)hipEventRecord(t_ev_start, s);
+    t_ev_start = nullptr;
+  }
+}
+static void lib_mark_end(hipStream_t s) {
+  if (t_ev_stop) (void)hipEventRecord(t_ev_stop, s);
+}
+
+void set_gemm_lib(GemmLib *lib, float *scratch, size_t scratch_floats) {
+  g_lib = lib;
+  g_lib_scratch = scratch;
+  g_lib_scratch_floats = scratch_floats;
+}
 
 void set_launch_events(hipEvent_t start, hipEvent_t stop) {
   t_ev_start = start;
@@ -477,10 +497,11 @@ __device__ __forceinline__ long hi64(uint4 v) {
 // launch_matvec never selects it.
 constexpr int kEpiQkv = 4;
 
-template <int kEpi, int kNM, int kP, int kFmt>
+template <int kEpi, int kNM, int kD, int kFmt>
 __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int rows_b,
                                                 int n_tiles, MatvecOut o, QkvEpi qe) {
-  constexpr int kW = 8, kCB = 2 * kW * kP;  // blocks per chunk: kP pairs per wave
+  static_assert(kD >= 2, "at least the next chunk in flight");
+  constexpr int kW = 8, kCB = 2 * kW;  // blocks per chunk: one pair per wave
   __shared__ float s_isum[kCB][kNM * 256];
   __shared__ float s_dw[kCB][kNM * 16];
   __shared__ float s_da[kCB][16];
@@ -500,65 +521,65 @@ __global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int r
   float acc[kNM];
 #pragma unroll
   for (int m = 0; m < kNM; m++) acc[m] = 0.0f;
-  Q8Regs<kNM> cur[kP], nxt[kP];
+  // kD - 1 chunks in flight ahead of the one consumed (a ring of registers)
+  Q8Regs<kNM> ring[kD];
 #pragma unroll
-  for (int pp = 0; pp < kP; pp++)
-    q8_load<kNM, kFmt>(cur[pp], w, act, unit, nt, min(pp * kW + wave, npairs - 1), lane);
-  for (int c = 0; c < nchunks; c++) {
-    // the last chunk prefetches a clamped (valid, unused) pair rather than branch
+  for (int i = 0; i < kD - 1; i++)
+    q8_load<kNM, kFmt>(ring[i], w, act, unit, nt, min(i * kW + wave, npairs - 1), lane);
+  for (int c0 = 0; c0 < nchunks; c0 += kD) {
 #pragma unroll
-    for (int pp = 0; pp < kP; pp++)
-      q8_load<kNM, kFmt>(nxt[pp], w, act, unit, nt, min((c + 1) * kW * kP + pp * kW + wave, npairs - 1),
-                         lane);
+    for (int u = 0; u < kD; u++) {
+      const int c = c0 + u;
+      if (c < nchunks) {
+        // chunks past the last prefetch a clamped (valid, unused) pair rather than branch
+        q8_load<kNM, kFmt>(ring[(u + kD - 1) % kD], w, act, unit, nt,
+                           min((c + kD - 1) * kW + wave, npairs - 1), lane);
+        const Q8Regs<kNM> &cur = ring[u];
+        if (c * kW + wave < npairs) {
 #pragma unroll
-    for (int pp = 0; pp < kP; pp++) {
-      const int cp = pp * kW + wave;  // pair index within the chunk
-      if (c * kW * kP + cp < npairs) {
+          for (int h = 0; h < 2; h++) {
+            const int blk = 2 * wave + h;
+            const long bop = h ? hi64(cur.b) : lo64(cur.b);
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-          const int blk = 2 * cp + h;
-          const long bop = h ? hi64(cur[pp].b) : lo64(cur[pp].b);
+            for (int m = 0; m < kNM; m++) {
+              long aop;
+              if constexpr (kFmt == 8)
+                aop = h ? hi64(cur.a[m]) : lo64(cur.a[m]);
+              else
+                aop = q4_operand(h ? cur.a[m].y : cur.a[m].x);
+              const v4i s4 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, zero, 0, 0, 0);
 #pragma unroll
-          for (int m = 0; m < kNM; m++) {
-            long aop;
-            if constexpr (kFmt == 8)
-              aop = h ? hi64(cur[pp].a[m]) : lo64(cur[pp].a[m]);
-            else
-              aop = q4_operand(h ? cur[pp].a[m].y : cur[pp].a[m].x);
-            const v4i s4 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, zero, 0, 0, 0);
+              for (int i = 0; i < 4; i++)
+                s_isum[blk][m * 256 + i * 64 + lane] = (float)s4[i];
+            }
+          }
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-              s_isum[blk][m * 256 + i * 64 + lane] = (float)s4[i];
+          for (int v = 0; v < Q8Regs<kNM>::kSV; v++) {
+            const int sl = v * 64 + lane, blk = 2 * wave + (sl % 32) / 16;
+            if (sl < kNM * 32)
+              s_dw[blk][(sl / 32) * 16 + sl % 16] = h2f(cur.sc[v]);
+            else if (sl < kNM * 32 + 32)
+              s_da[blk][sl % 16] = h2f(cur.sc[v]);
           }
         }
-#pragma unroll
-        for (int v = 0; v < Q8Regs<kNM>::kSV; v++) {
-          const int sl = v * 64 + lane, blk = 2 * cp + (sl % 32) / 16;
-          if (sl < kNM * 32)
-            s_dw[blk][(sl / 32) * 16 + sl % 16] = h2f(cur[pp].sc[v]);
-          else if (sl < kNM * 32 + 32)
-            s_da[blk][sl % 16] = h2f(cur[pp].sc[v]);
-        }
-      }
-    }
-    __syncthreads();
-    if (t < 256) {
-      const int nblk = min(kCB, nbp - c * kCB);
+        __syncthreads();
+        if (t < 256) {
+          const int nblk = min(kCB, nbp - c * kCB);
 #pragma unroll 8
-      for (int blk = 0; blk < nblk; blk++) {
-        const float da = s_da[blk][pcol];
+          for (int blk = 0; blk < nblk; blk++) {
+            const float da = s_da[blk][pcol];
 #pragma unroll
-        for (int m = 0; m < kNM; m++) {
-          if constexpr (kFmt == 8)
-            acc[m] = fmaf(s_isum[blk][m * 256 + t], s_dw[blk][m * 16 + prow] * da, acc[m]);
-          else
-            acc[m] = fmaf(s_isum[blk][m * 256 + t] * s_dw[blk][m * 16 + prow], da, acc[m]);
+            for (int m = 0; m < kNM; m++) {
+              if constexpr (kFmt == 8)
+                acc[m] = fmaf(s_isum[blk][m * 256 + t], s_dw[blk][m * 16 + prow] * da, acc[m]);
+              else
+                acc[m] = fmaf(s_isum[blk][m * 256 + t] * s_dw[blk][m * 16 + prow], da, acc[m]);
+            }
+          }
         }
+        __syncthreads();
       }
     }
-    __syncthreads();
-#pragma unroll
-    for (int pp = 0; pp < kP; pp++) cur[pp] = nxt[pp];
   }
   // ---- epilogue
   const int r = nt * 16 + pcol;
@@ -877,7 +898,7 @@ __global__ __launch_bounds__(64 * kChainWaves) void k_mv_q8c(MatrixView w, ActVi
                                                             int n_tiles, MatvecOut o) {
   constexpr uint32_t kPairBytes = kFmt == 8 ? 1024 : 512;  // weight bytes per tile per block pair
   const int lane = threadIdx.x % kWave;
-  const int ng = blockIdx.y * kChainWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int ng = blockIdx.y * (int)(blockDim.x / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int unit = blockIdx.x;
   if (ng * kNN >= n_tiles) return;
   const int npairs = w.nbp / 2, nbp = w.nbp, rsub = 4 * (lane / 16), col = lane % 16;
@@ -1200,6 +1221,148 @@ __global__ __launch_bounds__(512 * kU) void k_mv_q8w(MatrixView w, ActView act, 
       }
   }
   if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
+}
+
+// ---------------------------------------------------------------------------
+// Gate+up projection with SwiGLU and the down projection's Q8_0 quantizer in
+// the epilogue (Q8_0/Q4_0 weights, K <= 64 * kMaxPairs).  A workgroup owns one
+// Q8_0 block of the SwiGLU output (two 16-row units: gate and up tiles
+// 4q .. 4q+3) for kNB batch tiles; wave w multiplies weight tile 4q + w % 4
+// with batch tile w / 4, the whole K in block order, so each (row, batch row)
+// chain is the reference's (quant.rs:265-292) as in k_mv_q8w.  The wave's
+// weight tile goes straight to registers; the batch tiles' B operand and all
+// block scales are copied to LDS once per workgroup, in the same memory round
+// trip.  Workgroups of one block q sit on one XCD (blockIdx % 8), so the
+// weight tiles shared by its batch groups are fetched into that L2 once.
+// ---------------------------------------------------------------------------
+template <int kFmt, int kNB, int kNN, int kMaxPairs>
+__global__ __launch_bounds__(256 * kNB) void k_mv_gu(MatrixView w, ActView act, int rows_b, int n_tiles,
+                                                     uint32_t *row_err, const uint32_t *err_rows,
+                                                     ActView qout, int qout_nbp) {
+  constexpr int kPairBytes = kFmt == 8 ? 1024 : 512;
+  constexpr int kBT = kNB * kNN;  // batch tiles per workgroup
+  extern __shared__ uint4 smem[];
+  __shared__ uint64_t s_tab[32];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int nq = w.mtiles / 4, nbg = (n_tiles + kBT - 1) / kBT;
+  const int g8 = blockIdx.x / (8 * nbg), rem = blockIdx.x % (8 * nbg);
+  const int bg = rem / 8, q = g8 * 8 + rem % 8;
+  if (q >= nq) return;  // whole workgroup, before any barrier
+  const int npairs = w.nbp / 2, nbp = w.nbp;
+  const int tw = wave % 4, tile = 4 * q + tw;
+  const int tile0 = bg * kBT, nbt = min(kBT, n_tiles - tile0);
+  // LDS: [kBT][npairs][64] uint4 B operand, then [4][nbp][16] weight scales,
+  // then [kBT][nbp][16] batch scales (u16)
+  const int nb_items = nbt * npairs * 64, nw_items = 4 * nbp * 2, nd_items = nbt * nbp * 2;
+  const uint4 *gb = reinterpret_cast<const uint4 *>(act.qs) + (size_t)tile0 * npairs * 64;
+  const uint4 *gw = reinterpret_cast<const uint4 *>(w.ds + (size_t)4 * q * nbp * 16);
+  const uint4 *gd = reinterpret_cast<const uint4 *>(act.ds + (size_t)tile0 * nbp * 16);
+  const int total = nb_items + nw_items + nd_items;
+  // the wave's weight tile into registers (branch-free: pairs past K reload the last)
+  uint4 a[kMaxPairs];
+#pragma unroll
+  for (int p = 0; p < kMaxPairs; p++) {
+    const int pp = min(p, npairs - 1);
+    if constexpr (kFmt == 8) {
+      a[p] = *reinterpret_cast<const uint4 *>(w.qs + q8_byte(tile, nbp, 2 * pp, lane, 0));
+    } else {
+      const uint2 v = *reinterpret_cast<const uint2 *>(w.qs + q4_byte(tile, nbp, 2 * pp, lane, 0));
+      a[p] = make_uint4(v.x, v.y, 0u, 0u);
+    }
+  }
+  constexpr int kCopy = 8;
+  for (int base = 0; base < total; base += kCopy * 256 * kNB) {
+    uint4 cp[kCopy];
+#pragma unroll
+    for (int k = 0; k < kCopy; k++) {
+      const int i = min(base + (int)threadIdx.x + k * 256 * kNB, total - 1);
+      cp[k] = i < nb_items ? gb[i] : i < nb_items + nw_items ? gw[i - nb_items] : gd[i - nb_items - nw_items];
+    }
+#pragma unroll
+    for (int k = 0; k < kCopy; k++) {
+      const int i = base + (int)threadIdx.x + k * 256 * kNB;
+      if (i < total) smem[i] = cp[k];
+    }
+  }
+  if (threadIdx.x < 32) s_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
+  __syncthreads();
+  // wave w: weight tile 4q + w % 4 against batch tiles (w / 4) * kNN + n
+  const int bt0 = (wave / 4) * kNN;
+  const uint16_t *sdw = reinterpret_cast<const uint16_t *>(smem + nb_items) + (size_t)tw * nbp * 16;
+  const uint16_t *sda = reinterpret_cast<const uint16_t *>(smem + nb_items + nw_items);
+  const int rsub = 4 * (lane / 16), col = lane % 16;
+  const v4i zero = {0, 0, 0, 0};
+  float acc[kNN][4];
+#pragma unroll
+  for (int n = 0; n < kNN; n++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
+#pragma unroll
+  for (int p = 0; p < kMaxPairs; p++) {
+    if (p < npairs) {
+#pragma unroll
+      for (int n = 0; n < kNN; n++) {
+        const int bt = bt0 + n;
+        if (bt < nbt) {
+          const uint4 b = smem[(bt * npairs + p) * 64 + lane];
+#pragma unroll
+          for (int h = 0; h < 2; h++) {
+            const int blk = 2 * p + h;
+            long aop;
+            if constexpr (kFmt == 8)
+              aop = h ? hi64(a[p]) : lo64(a[p]);
+            else
+              aop = q4_operand(h ? a[p].y : a[p].x);
+            const v4i sum = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, h ? hi64(b) : lo64(b), zero, 0, 0, 0);
+            const uint2 s2 = *reinterpret_cast<const uint2 *>(sdw + blk * 16 + rsub);
+            const uint32_t da = sda[(bt * nbp + blk) * 16 + col];
+            if constexpr (kFmt == 8) {
+              const float sc[4] = {scale_mul<0, 0>(s2.x, da), scale_mul<1, 0>(s2.x, da),
+                                   scale_mul<0, 0>(s2.y, da), scale_mul<1, 0>(s2.y, da)};
+#pragma unroll
+              for (int i = 0; i < 4; i++) acc[n][i] = fmaf((float)sum[i], sc[i], acc[n][i]);
+            } else {
+              const float t[4] = {mul_half<0>((float)sum[0], s2.x), mul_half<1>((float)sum[1], s2.x),
+                                  mul_half<0>((float)sum[2], s2.y), mul_half<1>((float)sum[3], s2.y)};
+#pragma unroll
+              for (int i = 0; i < 4; i++) acc[n][i] = fma_half(t[i], da, acc[n][i]);
+            }
+          }
+        }
+      }
+    }
+  }
+  // ---- epilogue: the block's 4 x 16 x 16 chains per batch tile meet in LDS
+  // (the B operand's space: every wave is past its last LDS read at the barrier)
+  __syncthreads();
+  float *s_o = reinterpret_cast<float *>(smem);  // [kBT][tw][16 rows][16 batch rows]
+#pragma unroll
+  for (int n = 0; n < kNN; n++) {
+    const int bt = bt0 + n;
+    if (bt < nbt) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) s_o[((bt * 4 + tw) * 16 + rsub + i) * 16 + col] = acc[n][i];
+    }
+  }
+  __syncthreads();
+  // wave w quantizes batch tiles w, w + 4 kNB, ...: lane l takes elements
+  // 8 (l / 16) .. + 7 of the block for batch row l % 16
+  for (int bt = wave; bt < nbt; bt += 4 * kNB) {
+    const int k = lane / 16, r = (tile0 + bt) * 16 + col;
+    const bool rvalid = r < rows_b;
+    bool bad = false;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const int el = 8 * k + e, u = el / 16, row = el % 16;
+      const float g = s_o[((bt * 4 + 2 * u) * 16 + row) * 16 + col];
+      const float up = s_o[((bt * 4 + 2 * u + 1) * 16 + row) * 16 + col];
+      bad |= rvalid && (!finitef(g) || !finitef(up));
+      v[e] = (g / (1.0f + exp_f32_tab(-g, s_tab))) * up;
+    }
+    bad |= quant_group_q8<16>(v, rvalid, r, q * 4 + k, qout_nbp, qout);
+    if (bad) atomicOr(&row_err[err_rows ? (int)err_rows[r] : r], kErrNonFinite);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -2188,6 +2351,13 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
+// Segment record of a chunk row: in the row's own partial-sum space (the
+// exact passes skip chunk rows), kChunkSegFloats floats per key segment.
+__device__ __forceinline__ float *chunk_seg_at(double *partial, const StepDims &d, int row, int head, int seg) {
+  return reinterpret_cast<float *>(partial + ((size_t)row * d.NH + head) * d.max_chunks * d.D) +
+         seg * kChunkSegFloats;
+}
+
 namespace chunk {
 constexpr int kD = 64, kKT = 64, kS = 72;  // head dim, keys per tile, LDS row stride (bf16)
 constexpr int kItems = kKT / 2 * kD / 4;   // staging items: (token pair, 4 dims)
@@ -2211,7 +2381,7 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
                                                         const float *__restrict__ kpool,
                                                         const float *__restrict__ vpool,
                                                         const int32_t *__restrict__ pt,
-                                                        float *__restrict__ direct) {
+                                                        double *__restrict__ partial) {
   using namespace chunk;
   constexpr int kThreads = 64 * kG, kPer = (kItems + kThreads - 1) / kThreads;
   __shared__ __align__(16) __bf16 s_kh[kKT * kS];
@@ -2221,7 +2391,8 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
   const int4 tile = tiles[blockIdx.x / d.NKV];  // first row, rows, sequence, position of first row
   const int g = blockIdx.x % d.NKV, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int h = g * kG + wave, grp = lane / 16, c = lane % 16;
-  const int nr = tile.y, pos0 = tile.w, kv_end = pos0 + nr;
+  const int nr = tile.y & 0xff, seg = tile.y >> 8, pos0 = tile.w, kv_end = pos0 + nr;
+  const int t_begin = seg * kChunkSegKeys, t_end = min(t_begin + kChunkSegKeys, kv_end);
   const int prow = pos0 + min(c, nr - 1);  // rows past the tile repeat its last row
   const int32_t *ptr = pt + (size_t)tile.z * d.max_pages;
   // B operand of S^T: Q[row c][dims 32ks + 8grp .. +7] in log2 units, split
@@ -2260,7 +2431,7 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
         rk[u][e] = make_float4(0.f, 0.f, 0.f, 0.f);
         rv[u][e] = rk[u][e];
         const int t = t0 + 2 * (i / 16) + e;
-        if (i < kItems && t < kv_end) {
+        if (i < kItems && t < t_end) {
           const int32_t phys = ptr[t / kPage];
           rk[u][e] = *reinterpret_cast<const float4 *>(kpool + k_at(phys, t / kPage, g, d.NKV, t % kPage, 4 * (i % 16), kD));
           rv[u][e] = *reinterpret_cast<const float4 *>(vpool + v_at(phys, g, d.NKV, t % kPage, 4 * (i % 16), kD));
@@ -2306,7 +2477,7 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
       }
     }
   };
-  for (int t0 = 0; t0 < kv_end; t0 += kKT) {
+  for (int t0 = t_begin; t0 < t_end; t0 += kKT) {
     fetch(t0);
     __syncthreads();  // every wave is done with the previous tile
     stash();
@@ -2326,12 +2497,14 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
         s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[ks], s[n], 0, 0, 0);
       }
     }
-    if (t0 + kKT - 1 > pos0) {  // the tile reaches the chunk: causal mask key <= row
+    if (t0 + kKT - 1 > pos0 || t0 + kKT > t_end) {  // causal mask key <= row; keys past the segment
 #pragma unroll
       for (int n = 0; n < 4; n++)
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-          if (t0 + 16 * n + 4 * grp + i > prow) s[n][i] = -__builtin_inff();
+        for (int i = 0; i < 4; i++) {
+          const int t = t0 + 16 * n + 4 * grp + i;
+          if (t > prow || t >= t_end) s[n][i] = -__builtin_inff();
+        }
     }
     float mx = m;
 #pragma unroll
@@ -2340,7 +2513,10 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
       for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[n][i]);
     mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
     mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float alpha = __builtin_amdgcn_exp2f(m - mx);  // 0 on the first tile
+    // a row whose keys so far are all masked (a segment past its position)
+    // keeps m = -inf and p = 0
+    const float mref = mx == -__builtin_inff() ? 0.0f : mx;
+    const float alpha = __builtin_amdgcn_exp2f(m - mref);  // 0 on the first live tile
     m = mx;
     // B operand of O^T: P[row c][k-slot j of step ks], split into hi/lo
     bf16x8 ph[2], pl[2];
@@ -2349,7 +2525,7 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
     for (int ks = 0; ks < 2; ks++)
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        const float p = __builtin_amdgcn_exp2f(s[2 * ks + j / 4][j % 4] - mx);
+        const float p = __builtin_amdgcn_exp2f(s[2 * ks + j / 4][j % 4] - mref);
         sum += p;
         __bf16 hi, lo;
         split(p, hi, lo);
@@ -2375,12 +2551,15 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
   l += __shfl_xor(l, 16, kWave);
   l += __shfl_xor(l, 32, kWave);
   if (c >= nr) return;
-  const float inv = 1.0f / l;
-  float *out = direct + (size_t)(tile.x + c) * d.H + h * kD + 4 * grp;
+  // the segment's (m, l, o) of row c, head h (log2 units, o unnormalized)
+  float *out = chunk_seg_at(partial, d, tile.x + c, h, seg);
+  if (grp == 0) {
+    out[0] = m;
+    out[1] = l;
+  }
 #pragma unroll
   for (int n = 0; n < 4; n++)
-    *reinterpret_cast<float4 *>(out + 16 * n) =
-        make_float4(o[n][0] * inv, o[n][1] * inv, o[n][2] * inv, o[n][3] * inv);
+    *reinterpret_cast<float4 *>(out + 2 + 16 * n + 4 * grp) = make_float4(o[n][0], o[n][1], o[n][2], o[n][3]);
 }
 
 // Pass 4: chunks combined in order, rounded to f32, and prepared as the
@@ -2410,7 +2589,43 @@ __global__ __launch_bounds__(128) void k_attn_combine(StepDims d,
         if (c0 + i < nch) acc = (c0 + i == 0) ? v[i] : acc + v[i];
     }
   }
-  const float o = direct ? (active ? d.direct[(size_t)r * d.H + h * d.D + j] : 0.0f) : (float)acc;
+  float o = (float)acc;
+  if (direct && active) {
+    // the chunk kernel's key segments merged in order: M = max m_s,
+    // o = sum 2^(m_s - M) o_s / sum 2^(m_s - M) l_s (log2 units)
+    // (batches of 8 segments requested at once, clamped into range)
+    const float *sg = chunk_seg_at(const_cast<double *>(partial), d, r, h, 0);
+    const int nseg = (kv + kChunkSegKeys - 1) / kChunkSegKeys;
+    constexpr int kB = 8;
+    float M = -__builtin_inff(), L = 0.0f, O = 0.0f;
+    for (int s0 = 0; s0 < nseg; s0 += kB) {
+      float mv[kB], lv[kB], ov[kB];
+#pragma unroll
+      for (int i = 0; i < kB; i++) {
+        const float *rec = sg + min(s0 + i, nseg - 1) * kChunkSegFloats;
+        mv[i] = rec[0];
+        lv[i] = rec[1];
+        ov[i] = rec[2 + j];
+      }
+      float Mb = M;
+#pragma unroll
+      for (int i = 0; i < kB; i++)
+        if (s0 + i < nseg) Mb = fmaxf(Mb, mv[i]);
+      const float rescale = M == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(M - Mb);
+      L *= rescale;
+      O *= rescale;
+#pragma unroll
+      for (int i = 0; i < kB; i++) {
+        if (s0 + i < nseg) {
+          const float a = mv[i] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mv[i] - Mb);
+          L += a * lv[i];
+          O += a * ov[i];
+        }
+      }
+      M = Mb;
+    }
+    o = O / L;
+  }
   bool bad = active && !finitef(o);
   if (kAct == 8) {
     if (active) o_s[j] = o;
@@ -2573,14 +2788,83 @@ static bool mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
     // projection 13.3 -> 11.6 us against chunks of 64; qkv and o 0.2 us
     // faster than one chunk of 32)
     const int groups = (units + 7) / 8;
-    launch_k((k_mv_q8s<kEpi, kNM, 1, kFmt>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
-             rows_b, n_tiles, o, QkvEpi{});
+    launch_k((k_mv_q8s<kEpi, kNM, 2, kFmt>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
+               rows_b, n_tiles, o, QkvEpi{});
   }
   return false;
 }
 
 // Packed batches at least this tall take the matrix-core F16 linear.
 constexpr int kPrefillRows = 128;
+
+// SwiGLU over a library GEMM's gate+up sums gu[row][0 .. 2F) (gate, then up):
+// h = (g / (1 + exp(-g))) * u into out[row][i], the same arithmetic and
+// non-finite check as k_gemm_f16's SwiGLU epilogue.  Thread = 4 outputs.
+__global__ __launch_bounds__(256) void k_swiglu_rows(const float *__restrict__ gu, int rows, int F,
+                                                     float *__restrict__ out, int ld, uint32_t *row_err,
+                                                     const uint32_t *err_rows) {
+  const int r = blockIdx.y, i = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (r >= rows || i >= F) return;
+  const float *g = gu + (size_t)r * 2 * F + i;
+  bool bad = false;
+  float v[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    if (i + k < F) {
+      const float a = g[k], u = g[F + k];
+      bad |= !finitef(a) || !finitef(u);
+      v[k] = (a / (1.0f + exp_f32(-a))) * u;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+    if (i + k < F) out[(size_t)r * ld + i + k] = v[k];
+  if (bad) atomicOr(&row_err[err_rows ? (int)err_rows[r] : r], kErrNonFinite);
+}
+
+// The same over 8 outputs per thread, rounding h to binary16 into the down
+// projection's operand (k_quant_act's rounding and check): F % 8 == 0.
+__global__ __launch_bounds__(256) void k_swiglu_f16_rows(const float *__restrict__ gu, int rows, int F,
+                                                         uint16_t *__restrict__ out, uint32_t *row_err,
+                                                         const uint32_t *err_rows) {
+  const int r = blockIdx.y, i = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (r >= rows || i >= F) return;
+  const float4 *g4 = reinterpret_cast<const float4 *>(gu + (size_t)r * 2 * F + i);
+  const float4 *u4 = reinterpret_cast<const float4 *>(gu + (size_t)r * 2 * F + F + i);
+  const float4 ga = g4[0], gb = g4[1], ua = u4[0], ub = u4[1];
+  const float g[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+  const float u[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
+  bool bad = false;
+  uint32_t packed[4];
+#pragma unroll
+  for (int k = 0; k < 8; k += 2) {
+    uint16_t hv[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const float a = g[k + j], b = u[k + j];
+      bad |= !finitef(a) || !finitef(b);
+      hv[j] = f2h((a / (1.0f + exp_f32(-a))) * b);
+      bad |= !finitef(h2f(hv[j]));
+    }
+    packed[k / 2] = (uint32_t)hv[0] | ((uint32_t)hv[1] << 16);
+  }
+  *reinterpret_cast<uint4 *>(out + (size_t)r * F + i) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  if (bad) atomicOr(&row_err[err_rows ? (int)err_rows[r] : r], kErrNonFinite);
+}
+
+bool launch_matvec_swiglu_f16(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
+                              const MatvecOut &o, uint16_t *out_f16) {
+  const int F = w.rows / 2;
+  if (!g_lib || !g_prefill_mfma || rows_b < kPrefillRows || w.dtype != kFmtF16 || F % 8 ||
+      (size_t)rows_b * w.rows > g_lib_scratch_floats)
+    return false;
+  lib_mark_begin(s);
+  if (!gemm_lib_f16(g_lib, s, w.f16, w.rows, w.K, (const uint16_t *)act.f16, rows_b, g_lib_scratch, w.rows, false))
+    return false;
+  launch_k(k_swiglu_f16_rows, dim3((F + 2047) / 2048, rows_b), dim3(256), 0, s, (const float *)g_lib_scratch,
+           rows_b, F, out_f16, o.row_err, o.err_rows);
+  return true;
+}
 
 template <int kEpi>
 static void mv_f16(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
@@ -2593,6 +2877,26 @@ static void mv_f16(hipStream_t s, const MatrixView &w, const ActView &act, int r
     launch_k(k_gemm_f16<kEpi, 2, kGemmStages2>, dim3((w.rows + kGemmBM - 1) / kGemmBM, (rows_b + 63) / 64),
              dim3(256), kGemmStages2 * (128 + 64) * 64, s, w, (const uint16_t *)act.f16, rows_b, o);
     return;
+  }
+  if (kEpi != kEpiArgmax && g_prefill_mfma && g_lib && rows_b >= kPrefillRows) {
+    // library GEMM; non-finite outputs of the plain and residual forms are
+    // flagged by the row's next consumer (norm, attention) as the same error
+    if (kEpi == kEpiStore || kEpi == kEpiResidual) {
+      lib_mark_begin(s);
+      if (gemm_lib_f16(g_lib, s, w.f16, w.rows, w.K, (const uint16_t *)act.f16, rows_b, o.out, o.ld,
+                       kEpi == kEpiResidual)) {
+        lib_mark_end(s);
+        return;
+      }
+    } else if (kEpi == kEpiSwiglu && (size_t)rows_b * w.rows <= g_lib_scratch_floats) {
+      lib_mark_begin(s);
+      if (gemm_lib_f16(g_lib, s, w.f16, w.rows, w.K, (const uint16_t *)act.f16, rows_b, g_lib_scratch, w.rows,
+                       false)) {
+        launch_k(k_swiglu_rows, dim3((out_rows + 1023) / 1024, rows_b), dim3(256), 0, s,
+                 (const float *)g_lib_scratch, rows_b, out_rows, o.out, o.ld, o.row_err, o.err_rows);
+        return;
+      }
+    }
   }
   if (kEpi != kEpiArgmax && g_prefill_mfma && rows_b >= kPrefillRows && w.K % kGemmBK == 0 &&
       (kEpi != kEpiSwiglu || out_rows % (kGemmBM / 2) == 0)) {
@@ -2665,10 +2969,10 @@ void launch_matvec_qkv(hipStream_t s, const MatrixView &w, const ActView &act, i
                        const MatvecOut &o, const QkvEpi &q) {
   const int n_tiles = (rows_b + 15) / 16, groups = (w.mtiles + 7) / 8;
   if (w.dtype == 8)
-    launch_k((k_mv_q8s<kEpiQkv, 1, 1, 8>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act, rows_b,
+    launch_k((k_mv_q8s<kEpiQkv, 1, 2, 8>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act, rows_b,
              n_tiles, o, q);
   else
-    launch_k((k_mv_q8s<kEpiQkv, 1, 1, 2>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act, rows_b,
+    launch_k((k_mv_q8s<kEpiQkv, 1, 2, 2>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act, rows_b,
              n_tiles, o, q);
 }
 
@@ -2679,6 +2983,21 @@ bool launch_matvec_swiglu_q8(hipStream_t s, const MatrixView &w, const ActView &
   if ((w.dtype != 8 && w.dtype != 2) || w.nbp > 2 * kWPairs || F % 64 != 0) return false;
   // the epilogue writes whole block pairs of the down projection's operand
   if (qout_nbp != ((F / 32 + 1) & ~1)) return false;
+  if (n_tiles < 8) {
+    // few batch tiles: one wave per (weight tile, batch tile), every CU busy
+    const int nq = w.mtiles / 4, npairs = w.nbp / 2;
+    const size_t items = (size_t)npairs * 64 + 4 * (size_t)w.nbp * 2 + (size_t)w.nbp * 2;
+    const size_t lds = items * 16 > 4096 ? items * 16 : 4096;
+    const dim3 grid((nq + 7) / 8 * 8 * n_tiles);
+    if (w.dtype == 8)
+      launch_k((k_mv_gu<8, 1, 1, kWPairs>), grid, dim3(256), lds, s, w, act, rows_b, n_tiles, o.row_err, o.err_rows,
+               qout, qout_nbp);
+    else
+      launch_k((k_mv_gu<2, 1, 1, kWPairs>), grid, dim3(256), lds, s, w, act, rows_b, n_tiles, o.row_err, o.err_rows,
+               qout, qout_nbp);
+    return true;
+  }
+  // eight batch tiles and more: the unit pair's weights shared through LDS
   const int groups = w.mtiles / 4;  // pairs of (gate, up) tile units: one Q8_0 block each
   const int by = (n_tiles + 7) / 8, nthreads = 2 * 64 * (n_tiles < 8 ? n_tiles : 8);
   const size_t pair_bytes = w.dtype == 8 ? 1024 : 512;
@@ -2794,14 +3113,14 @@ bool attention_chunk_supported(int D, int G) {
 
 void launch_attn_chunk(hipStream_t s, int n_tiles, const StepDims &d, const int4 *tiles,
                        const float *q_rot, const float *kpool, const float *vpool,
-                       const int32_t *page_table, float *direct) {
+                       const int32_t *page_table, double *partial) {
   if (n_tiles <= 0) return;
   const dim3 grid(n_tiles * d.NKV);  // tile-major: the longest tiles of every KV head first
   switch (d.G) {
 #define L(GG)                                                                                 \
   case GG:                                                                                    \
     launch_k(k_attn_chunk<GG>, grid, dim3(64 * GG), 0, s, d, tiles, q_rot, kpool, vpool,      \
-             page_table, direct);                                                             \
+             page_table, partial);                                                            \
     break;
     L(1) L(2) L(4) L(6) L(7) L(8)
 #undef L

@@ -2,7 +2,13 @@
 allocation) against cohx_step on the same context: two calls in a row, the
 second with a smaller batch, each equal bit for bit (logits of every lane,
 greedy ids, appended K/V rows); a batch whose scratch exceeds the array is
-refused with COHX_RESOURCE and leaves its sequences untouched."""
+refused with COHX_RESOURCE and leaves its sequences untouched.
+
+F16 in the packed-prefill regime: cohx_step runs the linears of a step with
+prompt rows as library GEMMs, while the allocation-free call keeps them on the
+in-house matrix-core kernel; both are f32 sums held to the regime's tolerance
+(logits max-abs 1e-2, K/V rows 1e-3), so that step is compared within it, and
+bit for bit with the library switched off (COHX_GEMM_LIB=0)."""
 import numpy as np
 import pytest
 
@@ -23,9 +29,11 @@ def snapshot(m, seqs, starts, res):
             for r in res], kv
 
 
-@pytest.mark.parametrize("dtype", ["q8_0", "f16"])
-def test_noalloc_step_equals_step(dtype):
-    print(f"case: noalloc vs step {dtype}", flush=True)
+@pytest.mark.parametrize("dtype,lib", [("q8_0", True), ("f16", False), ("f16", True)])
+def test_noalloc_step_equals_step(dtype, lib, monkeypatch):
+    print(f"case: noalloc vs step {dtype} (library GEMMs {'on' if lib else 'off'})", flush=True)
+    if not lib:
+        monkeypatch.setenv("COHX_GEMM_LIB", "0")
     c, t = synth.in_memory(TINY, dtype, seed=41)
     m = cohx.Model(c, t, max_lanes=8, max_rows=160, max_seqs=8, max_context=1024)
     seqs = [m.seq_alloc() for _ in range(5)]
@@ -46,13 +54,27 @@ def test_noalloc_step_equals_step(dtype):
         for s, n in zip(used, starts):
             m.seq_truncate(s, n)
         got = snapshot(m, used, starts, m.step(lanes, noalloc=True))
+        exact = not (dtype == "f16" and lib and k == 0)
         for (ws, wa, wl), (gs, ga, gl) in zip(want[0], got[0]):
-            assert ws == gs == 0 and wa == ga
+            assert ws == gs == 0
             assert (wl is None) == (gl is None)
-            if wl is not None:
-                assert np.array_equal(wl, gl), f"call {k}: logits differ"
+            if exact:
+                assert wa == ga
+                if wl is not None:
+                    assert np.array_equal(wl, gl), f"call {k}: logits differ"
+            elif wl is not None:
+                a, b = wl.view(np.float32), gl.view(np.float32)
+                diff = float(np.abs(a - b).max())
+                print(f"call {k}: logits max-abs {diff:.3g}", flush=True)
+                assert diff <= 1e-2
+                top = np.sort(a)[-2:]
+                if top[1] - top[0] > 2e-2:
+                    assert wa == ga
         for (wk, wv), (gk, gv) in zip(want[1], got[1]):
-            assert np.array_equal(wk, gk) and np.array_equal(wv, gv), f"call {k}: K/V rows differ"
+            if exact:
+                assert np.array_equal(wk, gk) and np.array_equal(wv, gv), f"call {k}: K/V rows differ"
+            else:
+                assert float(np.abs(wk - gk).max()) <= 1e-3 and float(np.abs(wv - gv).max()) <= 1e-3
     m.close()
 
 
