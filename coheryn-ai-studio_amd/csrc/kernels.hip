@@ -2384,17 +2384,26 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
                                                         double *__restrict__ partial) {
   using namespace chunk;
   constexpr int kThreads = 64 * kG, kPer = (kItems + kThreads - 1) / kThreads;
+  constexpr int kRawSlots = kKT * kD / 4;  // 16-byte slots of one raw f32 tile: [token][dim quad]
   __shared__ __align__(16) __bf16 s_kh[kKT * kS];
   __shared__ __align__(16) __bf16 s_kl[kKT * kS];
   __shared__ __align__(16) __bf16 s_vh[kD * kS];
   __shared__ __align__(16) __bf16 s_vl[kD * kS];
-  const int4 tile = tiles[blockIdx.x / d.NKV];  // first row, rows, sequence, position of first row
+  __shared__ __align__(16) float4 s_rk[kRawSlots];  // the next tile's raw K and V, straight from memory
+  __shared__ __align__(16) float4 s_rv[kRawSlots];
+  __shared__ int32_t s_pages[kChunkSegKeys / kPage];
+  const int4 tile = tiles[blockIdx.x / d.NKV];  // first row, rows | segment << 8, sequence, position of first row
   const int g = blockIdx.x % d.NKV, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int h = g * kG + wave, grp = lane / 16, c = lane % 16;
   const int nr = tile.y & 0xff, seg = tile.y >> 8, pos0 = tile.w, kv_end = pos0 + nr;
   const int t_begin = seg * kChunkSegKeys, t_end = min(t_begin + kChunkSegKeys, kv_end);
   const int prow = pos0 + min(c, nr - 1);  // rows past the tile repeat its last row
-  const int32_t *ptr = pt + (size_t)tile.z * d.max_pages;
+  {
+    // the segment's page-table entries (pages past the segment's keys unused)
+    const int32_t *ptr = pt + (size_t)tile.z * d.max_pages;
+    const int np = (t_end - t_begin + kPage - 1) / kPage;
+    for (int i = threadIdx.x; i < np; i += kThreads) s_pages[i] = ptr[t_begin / kPage + i];
+  }
   // B operand of S^T: Q[row c][dims 32ks + 8grp .. +7] in log2 units, split
   bf16x8 qh[2], ql[2];
   {
@@ -2418,36 +2427,35 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
 #pragma unroll
   for (int n = 0; n < 4; n++) o[n] = float4v{0.f, 0.f, 0.f, 0.f};
   float m = -__builtin_inff(), l = 0.0f;
-  // staging: item i = (token pair i / 16, dims 4 * (i % 16)); every load of
-  // a tile is issued before the first conversion (two resident workgroups
-  // per CU overlap one's staging with the other's matrix work)
-  float4 rk[kPer][2], rv[kPer][2];
+  // raw staging: slot sl = token * 16 + dim quad of the tile; wave w issues
+  // slots 64u + lane for u = w, w + kG, ...: 16 bytes per lane straight into
+  // LDS (tokens past the segment read its last token; the split zeroes them)
   auto fetch = [&](int t0) {
-#pragma unroll
-    for (int u = 0; u < kPer; u++) {
-      const int i = threadIdx.x + u * kThreads;
-#pragma unroll
-      for (int e = 0; e < 2; e++) {
-        rk[u][e] = make_float4(0.f, 0.f, 0.f, 0.f);
-        rv[u][e] = rk[u][e];
-        const int t = t0 + 2 * (i / 16) + e;
-        if (i < kItems && t < t_end) {
-          const int32_t phys = ptr[t / kPage];
-          rk[u][e] = *reinterpret_cast<const float4 *>(kpool + k_at(phys, t / kPage, g, d.NKV, t % kPage, 4 * (i % 16), kD));
-          rv[u][e] = *reinterpret_cast<const float4 *>(vpool + v_at(phys, g, d.NKV, t % kPage, 4 * (i % 16), kD));
-        }
-      }
+    for (int u = wave; u < kRawSlots / kWave; u += kG) {
+      const int sl = u * kWave + lane, t = min(t0 + sl / 16, t_end - 1), qd = sl % 16;
+      const int32_t phys = s_pages[(t - t_begin) / kPage];
+      lds_load16(kpool + k_at(phys, t / kPage, g, d.NKV, t % kPage, 4 * qd, kD), s_rk + u * kWave);
+      lds_load16(vpool + v_at(phys, g, d.NKV, t % kPage, 4 * qd, kD), s_rv + u * kWave);
     }
   };
-  auto stash = [&]() {
+  // split: item i = (token pair i / 16, dims 4 * (i % 16)) from the raw tile
+  // into bf16 hi/lo K rows and V^T rows (zeros past the segment)
+  auto stash = [&](int t0) {
 #pragma unroll
     for (int u = 0; u < kPer; u++) {
       const int i = threadIdx.x + u * kThreads;
       if (i >= kItems) continue;
       const int k = 2 * (i / 16), d4 = 4 * (i % 16), vp = vperm(k);
+      float4 rk[2], rv[2];
 #pragma unroll
       for (int e = 0; e < 2; e++) {
-        const float kx[4] = {rk[u][e].x, rk[u][e].y, rk[u][e].z, rk[u][e].w};
+        const bool live = t0 + k + e < t_end;
+        rk[e] = live ? s_rk[(k + e) * 16 + i % 16] : make_float4(0.f, 0.f, 0.f, 0.f);
+        rv[e] = live ? s_rv[(k + e) * 16 + i % 16] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const float kx[4] = {rk[e].x, rk[e].y, rk[e].z, rk[e].w};
         bf16x4 hi, lo;
 #pragma unroll
         for (int x = 0; x < 4; x++) {
@@ -2460,8 +2468,8 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
         *reinterpret_cast<bf16x4 *>(s_kl + (k + e) * kS + d4) = lo;
       }
       // keys k and k+1 sit side by side in the V^T order (vperm keeps pairs)
-      const float v0[4] = {rv[u][0].x, rv[u][0].y, rv[u][0].z, rv[u][0].w};
-      const float v1[4] = {rv[u][1].x, rv[u][1].y, rv[u][1].z, rv[u][1].w};
+      const float v0[4] = {rv[0].x, rv[0].y, rv[0].z, rv[0].w};
+      const float v1[4] = {rv[1].x, rv[1].y, rv[1].z, rv[1].w};
 #pragma unroll
       for (int x = 0; x < 4; x++) {
         bf16x2 hi, lo;
@@ -2477,12 +2485,15 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
       }
     }
   };
+  __syncthreads();  // page entries
+  fetch(t_begin);
   for (int t0 = t_begin; t0 < t_end; t0 += kKT) {
-    fetch(t0);
-    __syncthreads();  // every wave is done with the previous tile
-    stash();
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's raw slots have landed
+    __syncthreads();                     // every wave's slots; every wave is done with the previous tile
+    stash(t0);
     __syncthreads();
-    // S^T tile: s[n][i] = S[row c][key t0 + 16n + 4grp + i]
+    if (t0 + kKT < t_end) fetch(t0 + kKT);  // the next raw tile lands while this one is multiplied
+  // S^T tile: s[n][i] = S[row c][key t0 + 16n + 4grp + i]
     float4v s[4];
 #pragma unroll
     for (int n = 0; n < 4; n++) {
