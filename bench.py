@@ -40,9 +40,9 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_decode128.json")
 # grid, so counters cannot tell them apart)
 CATEGORY_KERNEL = {"attn_scores": "k_attn_scores<64, 7>", "attn_softmax_stats": "k_attn_exp<7>",
                    "attn_pv": "k_attn_pv<64, 7>", "attn_combine_act": "k_attn_combine<8>",
-                   "matvec_qkv": "k_mv_q8s<4, 1, 1, 8>", "matvec_o_residual": "k_mv_q8s<1, 1, 1, 8>",
+                   "matvec_qkv": "k_mv_q8s<4, 1, 2, 8>", "matvec_o_residual": "k_mv_q8s<1, 1, 2, 8>",
                    "matvec_gate_up_swiglu": "k_mv_q8w<2, 2, 8, 16, 2>",
-                   "matvec_down_residual": "k_mv_q8s<1, 1, 1, 8>",
+                   "matvec_down_residual": "k_mv_q8s<1, 1, 2, 8>",
                    "matvec_head_argmax": "k_mv_q8h<8, 14>"}
 PMC_CMD = ("COHX_GRAPHS=0 rocprofv3 --pmc {counter} --kernel-include-regex \"k_attn|k_mv\" --output-format csv "
            "-d <dir> -o <name> -- python3 bench.py --steps 2 --warmup 1 --secondary-lanes 0 "
@@ -50,7 +50,7 @@ PMC_CMD = ("COHX_GRAPHS=0 rocprofv3 --pmc {counter} --kernel-include-regex \"k_a
 COPY_CMD = ("rocprofv3 --pmc {counter} --output-format csv -d <dir> -o <name> -- "
             "python3 bench.py --copy-probe")
 TRACE_CMD = ("COHX_GRAPHS=0 rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o <name> -- "
-             "python3 bench.py")
+             "python3 bench.py --no-cpu-baseline --no-c3 --no-c4 --no-c5")
 
 
 def log(*a):
@@ -440,7 +440,11 @@ def cpu_baseline(cfg, tensors, kv, start_tokens, seed, lanes, steps, threads):
 def kernel_instance(name):
     import re
     m = re.search(r"\b(k_\w+)(<[^>]*>)?\(", name)
-    return m.group(1) + (m.group(2) or "") if m else name
+    if m:
+        return m.group(1) + (m.group(2) or "")
+    if name.startswith("Cijk_"):  # hipBLASLt (Tensile) GEMM kernels
+        return "hipblaslt " + name[:48] + "..."
+    return name
 
 
 def counter_means(path):
@@ -598,7 +602,7 @@ def summarize_leg(leg, trace_csv, bench_json, fetch_csv=None, write_csv=None, mf
         cw = counter_means(copy_write_csv)["__amd_rocclr_copyBuffer"][0] * 1024
         ff, fw = float(1 << 30) / cf, float(1 << 30) / cw
         fetch, write = counter_means(fetch_csv), counter_means(write_csv)
-        print(f"\nHBM traffic: `{LEG_PMC_CMD.format(counters='FETCH_SIZE', regex='k_', leg=leg)}`, then "
+        print(f"\nHBM traffic: `{LEG_PMC_CMD.format(counters='FETCH_SIZE', regex='k_|Cijk', leg=leg)}`, then "
               f"`WRITE_SIZE`; scaled by the same counters over a 1 GiB copy (`{COPY_CMD.format(counter='FETCH_SIZE')}`: "
               f"factors {ff:.4f} fetch, {fw:.4f} write).\n")
         print("| kernel | dispatches | FETCH KiB | WRITE KiB | HBM bytes per launch |")
@@ -616,7 +620,7 @@ def summarize_leg(leg, trace_csv, bench_json, fetch_csv=None, write_csv=None, mf
                 if row["Dispatch_Id"] not in a["_d"]:
                     a["_d"].add(row["Dispatch_Id"])
                     a["_ns"] += int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
-        print(f"\nMatrix cores: `{LEG_PMC_CMD.format(counters=MFMA_COUNTERS, regex='k_gemm_f16|k_attn_chunk', leg=leg)}`\n")
+        print(f"\nMatrix cores: `{LEG_PMC_CMD.format(counters=MFMA_COUNTERS, regex='k_gemm_f16|k_attn_chunk|Cijk', leg=leg)}`\n")
         print("| kernel | dispatches | MFMA busy share | MOPS f16 (x512 flop) | MOPS bf16 (x512 flop) | "
               "counted TFLOP/s |")
         print("|---|---:|---:|---:|---:|---:|")
