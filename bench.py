@@ -651,6 +651,45 @@ def copy_probe():
           flush=True)
 
 
+def launch_floor(n=200, reps=20):
+    """The GPU's cost per kernel boundary: a HIP graph of n one-element
+    kernels (torch's add_, plumbing) replayed back to back, timed with
+    events on the stream that replays it, next to the same kernel timed one
+    launch at a time with dispatch events."""
+    import torch
+    x = torch.zeros(1, device="cuda")
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            x.add_(1.0)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        for _ in range(n):
+            x.add_(1.0)
+    with torch.cuda.stream(s):
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            g.replay()
+        b.record()
+    torch.cuda.synchronize()
+    graph_us = a.elapsed_time(b) * 1e3 / (n * reps)
+    single = []
+    with torch.cuda.stream(s):
+        for _ in range(n):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            x.add_(1.0)
+            b.record()
+            b.synchronize()
+            single.append(a.elapsed_time(b) * 1e3)
+    print(json.dumps({"graph_us_per_kernel": graph_us, "kernels_per_graph": n,
+                      "event_bracketed_us_per_kernel": sum(single) / len(single)}), flush=True)
+
+
 C5_SEQS, C5_PROMPT, C5_GEN, C5_CHUNK = 16, (64, 1024), 64, 256
 
 
@@ -785,6 +824,8 @@ def main():
                     help="run only this workload and print its JSON (profiling runs)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 1 GiB device-to-device 4 times (counter calibration)")
+    ap.add_argument("--launch-floor", action="store_true",
+                    help="only time a graph of one-element kernels (the cost of a kernel boundary)")
     ap.add_argument("--summarize-counters", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
                     help="write the traffic summary from rocprofv3 --pmc csv files (no GPU)")
     ap.add_argument("--summarize-c5-trace", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_JSON"),
@@ -797,6 +838,9 @@ def main():
     args = ap.parse_args()
     if args.copy_probe:
         copy_probe()
+        return
+    if args.launch_floor:
+        launch_floor()
         return
     if args.summarize_counters:
         summarize_counters(*args.summarize_counters, lanes=args.lanes)
