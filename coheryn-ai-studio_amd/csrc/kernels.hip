@@ -497,11 +497,11 @@ __device__ __forceinline__ long hi64(uint4 v) {
 // launch_matvec never selects it.
 constexpr int kEpiQkv = 4;
 
-template <int kEpi, int kNM, int kD, int kFmt>
-__global__ __launch_bounds__(512) void k_mv_q8s(MatrixView w, ActView act, int rows_b,
-                                                int n_tiles, MatvecOut o, QkvEpi qe) {
+template <int kEpi, int kNM, int kD, int kFmt, int kW = 8>
+__global__ __launch_bounds__(64 * kW) void k_mv_q8s(MatrixView w, ActView act, int rows_b,
+                                                    int n_tiles, MatvecOut o, QkvEpi qe) {
   static_assert(kD >= 2, "at least the next chunk in flight");
-  constexpr int kW = 8, kCB = 2 * kW;  // blocks per chunk: one pair per wave
+  constexpr int kCB = 2 * kW;  // blocks per chunk: one pair per wave
   __shared__ float s_isum[kCB][kNM * 256];
   __shared__ float s_dw[kCB][kNM * 16];
   __shared__ float s_da[kCB][16];
@@ -1072,8 +1072,8 @@ __global__ __launch_bounds__(512 * kU) void k_mv_q8w(MatrixView w, ActView act, 
   // kU units per workgroup of kU * W waves (W = min(n_tiles, 8) for every
   // workgroup): wave w takes unit kU * blockIdx.x + w / W and batch tile
   // tile0 + w % W (past n_tiles in a last, partial row of tiles: not live)
-  const int tile0 = blockIdx.y * 8, nbt = min(8, n_tiles - tile0);
   const int W = nthreads / (kWave * kU);
+  const int tile0 = blockIdx.y * W, nbt = min(W, n_tiles - tile0);
   const int uw = wave / W, bt = wave % W;
   const int unit = blockIdx.x * kU + uw, nt = tile0 + bt;
   const int npairs = w.nbp / 2, nbp = w.nbp;
@@ -1239,7 +1239,6 @@ template <int kFmt, int kNB, int kNN, int kMaxPairs>
 __global__ __launch_bounds__(256 * kNB) void k_mv_gu(MatrixView w, ActView act, int rows_b, int n_tiles,
                                                      uint32_t *row_err, const uint32_t *err_rows,
                                                      ActView qout, int qout_nbp) {
-  constexpr int kPairBytes = kFmt == 8 ? 1024 : 512;
   constexpr int kBT = kNB * kNN;  // batch tiles per workgroup
   extern __shared__ uint4 smem[];
   __shared__ uint64_t s_tab[32];
@@ -2056,8 +2055,13 @@ __device__ __forceinline__ void qk_finish(const float (&sc)[kH], bool valid, int
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   if (valid) {
     float *dst = scores + (((size_t)r * d.NKV + g) * d.kv_cap + t) * 8 + h0;
-    if (kH == 4 && h0 % 4 == 0) {
-      *reinterpret_cast<float4 *>(dst) = make_float4(sc[0], sc[1], sc[2], sc[3]);
+    if constexpr (kH == 4) {
+      if (h0 % 4 == 0) {
+        *reinterpret_cast<float4 *>(dst) = make_float4(sc[0], sc[1], sc[2], sc[3]);
+      } else {
+#pragma unroll
+        for (int h = 0; h < kH; h++) dst[h] = sc[h];
+      }
     } else {
 #pragma unroll
       for (int h = 0; h < kH; h++) dst[h] = sc[h];
@@ -2799,7 +2803,13 @@ static bool mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
     // projection 13.3 -> 11.6 us against chunks of 64; qkv and o 0.2 us
     // faster than one chunk of 32)
     const int groups = (units + 7) / 8;
-    launch_k((k_mv_q8s<kEpi, kNM, 2, kFmt>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
+    // few batch tiles: 16 waves, chunks of 32 blocks (half the chunk
+    // barriers on the long-K down projection; the grid is small anyway)
+    if (kNM == 1 && n_tiles <= 4)
+      launch_k((k_mv_q8s<kEpi, kNM, 2, kFmt, 16>), dim3(groups * 8 * n_tiles), dim3(1024), 0, s, w, act,
+               rows_b, n_tiles, o, QkvEpi{});
+    else
+      launch_k((k_mv_q8s<kEpi, kNM, 2, kFmt>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act,
                rows_b, n_tiles, o, QkvEpi{});
   }
   return false;
@@ -2979,7 +2989,10 @@ bool launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActVi
 void launch_matvec_qkv(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
                        const MatvecOut &o, const QkvEpi &q) {
   const int n_tiles = (rows_b + 15) / 16, groups = (w.mtiles + 7) / 8;
-  if (w.dtype == 8)
+  if (n_tiles <= 2 && w.dtype == 8)  // as for the residual projections, below 3 batch tiles
+    launch_k((k_mv_q8s<kEpiQkv, 1, 2, 8, 16>), dim3(groups * 8 * n_tiles), dim3(1024), 0, s, w, act, rows_b,
+             n_tiles, o, q);
+  else if (w.dtype == 8)
     launch_k((k_mv_q8s<kEpiQkv, 1, 2, 8>), dim3(groups * 8 * n_tiles), dim3(512), 0, s, w, act, rows_b,
              n_tiles, o, q);
   else
