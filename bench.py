@@ -690,6 +690,28 @@ def launch_floor(n=200, reps=20):
                       "event_bracketed_us_per_kernel": sum(single) / len(single)}), flush=True)
 
 
+def valu_probe():
+    """The exact attention pass's instruction pattern without memory traffic
+    (libcohx_probe.so, csrc/probe.hip): per thread, C independent f64 chains
+    fed by f32 products and widenings, E elements per group, timed at 1280,
+    2560 and 5120 workgroups of 256 threads (about 1.25, 2.5 and 5 waves per
+    SIMD on 1024 SIMDs).  Reports ns per wave triple per SIMD."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "coheryn-ai-studio_amd", "libcohx_probe.so"))
+    lib.cohx_probe_triples.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_float)]
+    steps, out = 64, []
+    for blocks in (1280, 2560, 5120):
+        for c, e in ((7, 4), (4, 4), (3, 2), (14, 2), (7, 8)):
+            ms = ctypes.c_float()
+            rc = lib.cohx_probe_triples(c, e, blocks, steps, ctypes.byref(ms))
+            if rc:
+                raise RuntimeError(f"probe failed ({rc})")
+            wave_triples_per_simd = blocks * 256 * steps * e * c / 64 / 1024
+            out.append({"chains": c, "elements": e, "workgroups": blocks, "us": ms.value * 1e3,
+                        "ns_per_wave_triple_per_simd": ms.value * 1e6 / wave_triples_per_simd})
+    print(json.dumps({"valu_probe": out}), flush=True)
+
+
 C5_SEQS, C5_PROMPT, C5_GEN, C5_CHUNK = 16, (64, 1024), 64, 256
 
 
@@ -826,6 +848,8 @@ def main():
                     help="only copy 1 GiB device-to-device 4 times (counter calibration)")
     ap.add_argument("--launch-floor", action="store_true",
                     help="only time a graph of one-element kernels (the cost of a kernel boundary)")
+    ap.add_argument("--valu-probe", action="store_true",
+                    help="only time the attention pass's f32-product / f64-chain pattern without memory")
     ap.add_argument("--summarize-counters", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
                     help="write the traffic summary from rocprofv3 --pmc csv files (no GPU)")
     ap.add_argument("--summarize-c5-trace", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_JSON"),
@@ -841,6 +865,9 @@ def main():
         return
     if args.launch_floor:
         launch_floor()
+        return
+    if args.valu_probe:
+        valu_probe()
         return
     if args.summarize_counters:
         summarize_counters(*args.summarize_counters, lanes=args.lanes)

@@ -17,6 +17,8 @@ LIB = os.path.join(HERE, "libcohx.so")
 SOURCES = ["csrc/kernels.hip", "csrc/cohx.cpp", "csrc/gen.cpp", "csrc/q35_kernels.hip", "csrc/q35.cpp",
            "csrc/gguf.cpp", "csrc/blas.cpp"]
 HEADERS = ["csrc/device.h", "csrc/kernels.h", "csrc/internal.h", "../include/cohx.h"]
+PROBE_SOURCE = "csrc/probe.hip"
+PROBE_LIB = os.path.join(HERE, "libcohx_probe.so")
 ARCH = os.environ.get("COHX_ARCH", "gfx950")
 
 FLAGS = [
@@ -53,8 +55,9 @@ def build(verbose=False):
             raise RuntimeError(f"hipcc failed on {src}")
         return obj
 
-    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        objs = list(ex.map(compile_one, SOURCES))
+    with ThreadPoolExecutor(max_workers=len(SOURCES) + 1) as ex:
+        objs = list(ex.map(compile_one, SOURCES + [PROBE_SOURCE]))
+    probe_obj = objs.pop()
     tmp = LIB + ".tmp"
     # -z defs: an undefined symbol (say, a kernel stub the host pass dropped) fails the build
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", tmp, *objs,
@@ -64,6 +67,14 @@ def build(verbose=False):
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError("link failed")
     os.replace(tmp, LIB)
+    # the instruction-rate probes of bench.py --valu-probe, a library of their own
+    tmp = PROBE_LIB + ".tmp"
+    r = subprocess.run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", tmp, probe_obj],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("probe link failed")
+    os.replace(tmp, PROBE_LIB)
     return LIB
 
 
