@@ -441,7 +441,6 @@ size_t layout_workspace(const cohx_model_desc &d, int nbp_h, int nbp_f, uint32_t
   c.take(w.tiles, w.max_tiles);
   c.take(w.row_skip, R);
   c.take(w.row_map, R);
-  c.take(w.direct, R * H);
   c.take(w.partial, R * NH * chunks * D);
   if (logits) c.take(w.logits, (size_t)NL * V);
   c.take(w.argmax, NL);
@@ -1371,8 +1370,7 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
   hipStream_t s = ctx->stream;
   StepDims sd{H, F, (int)d.vocabulary, NH, NKV, D, KVD, NH / NKV, d.norm_epsilon,
               1.0f / sqrtf((float)D), ctx->max_pages, (int)w.kv_cap, (int)w.max_chunks,
-              p.n_tiles ? w.row_skip : nullptr, p.n_tiles ? w.direct : nullptr,
-              p.n_tiles ? w.row_map : nullptr};
+              p.n_tiles ? w.row_skip : nullptr, p.n_tiles ? w.row_map : nullptr};
   const int RX = (int)p.n_exact;  // rows of the exact attention passes
   if (p.n_tiles) kv_grid = (int)((p.max_kv_exact + 255) / 256 * 256);
   const ActView act = act_view(w);

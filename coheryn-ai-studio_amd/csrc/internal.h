@@ -58,14 +58,14 @@ struct Workspace {
   float *act_f32 = nullptr;
   float *scores = nullptr;  // [rows][kv_heads][kv_cap][8]: scores, then weights
   float *chunk_max = nullptr, *logits = nullptr;
-  double *partial = nullptr;   // [rows][heads][max_chunks][head_dim]
+  double *partial = nullptr;   // [rows][heads][max_chunks][head_dim] (chunk rows: f32 segment records)
   double *den_part = nullptr;  // [rows][heads][256-token chunks] softmax denominator partials
-  // prefill chunks on the matrix cores: 16-row tiles, per-row flags, f32
-  // output, and the list of rows left to the exact attention passes
+  // prefill chunks on the matrix cores: (16-row tile, key segment) work
+  // items, per-row flags, and the list of rows left to the exact attention
+  // passes (chunk rows' segment records live in `partial`)
   int4 *tiles = nullptr;
   uint32_t *row_skip = nullptr;
   uint32_t *row_map = nullptr;
-  float *direct = nullptr;
   unsigned long long *argmax = nullptr;  // final keys per lane, zeroed by the packer
   unsigned long long *argmax_part = nullptr;  // [lanes][head m-tiles]
   // capacities the buffers were laid out for

@@ -53,10 +53,10 @@ struct StepDims {
   int kv_cap;                        // score row stride (>= max kv length this step)
   int max_chunks;                    // partial-sum stride
   // rows whose attention the matrix-core chunk kernel computes (nullptr: none);
-  // the combine pass reads their f32 output, and the exact passes run over
-  // row_map[0 .. n) only: block x takes row row_map[x] (nullptr: row x)
+  // the combine pass merges their key segments (chunk_seg_at), and the exact
+  // passes run over row_map[0 .. n) only: block x takes row row_map[x]
+  // (nullptr: row x)
   const uint32_t *row_skip;
-  const float *direct;               // [rows][H]
   const uint32_t *row_map;
 };
 
