@@ -171,7 +171,7 @@ void launch_attn_pv(hipStream_t s, int rows, int max_kv, const StepDims &d, cons
 // and writes the segment's row max, row sum and unnormalized output as f32
 // (chunk_seg_at) into the rows' partial-sum space, which the combine pass
 // merges in segment order.
-constexpr int kChunkSegKeys = 512;
+constexpr int kChunkSegKeys = 1024;
 constexpr int kChunkSegFloats = 2 + 64;  // m, l, o[64] (head_dim 64)
 bool attention_chunk_supported(int D, int G);
 void launch_attn_chunk(hipStream_t s, int n_tiles, const StepDims &d, const int4 *tiles,
