@@ -524,9 +524,12 @@ def summarize_trace(trace_csv, bench_json):
 
 C5_TRACE_CMD = ("rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o <name> -- "
                 "python3 bench.py --c5-only --no-cpu-baseline")
+C5_PMC_CMD = ("rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_MOPS_BF16 "
+              "GRBM_GUI_ACTIVE --kernel-include-regex \"Cijk\" --output-format csv -d <dir> -o <name> -- "
+              "python3 bench.py --c5-only --no-cpu-baseline")
 
 
-def summarize_c5_trace(trace_csv, bench_json):
+def summarize_c5_trace(trace_csv, bench_json, mfma_csv=None):
     """Markdown summary of a rocprofv3 --kernel-trace run of the C5 workload:
     per kernel and grid shape (the grid's y extent counts row groups, so the
     one-token schedule's 16-row steps separate from the prompt chunks) the
@@ -544,21 +547,28 @@ def summarize_c5_trace(trace_csv, bench_json):
         line = json.loads(f.read().strip().splitlines()[-1])
     es = line["engine_schedule"]
     print(f"Command: `{C5_TRACE_CMD}`\n")
-    print(f"Plain run of the same command: prompts in chunks of {line['prompt_chunk']}: "
-          f"{line['value']:.0f} generated tok/s ({line['rows_per_s']:.0f} rows/s); one token per "
-          f"sequence per step: {es['ms_per_step']:.3f} ms/step ({es['rows_per_s']:.0f} rows/s); "
-          f"same tokens: {line['same_tokens_both_schedules']}.\n")
+    ex = line["chunked_exact"]
+    print(f"Plain run of the same command: prompts in chunks of {line['prompt_chunk']} (packed-prefill "
+          f"regime): {line['value']:.0f} generated tok/s ({line['rows_per_s']:.0f} rows/s); the same "
+          f"schedule exact: {ex['value']:.0f} generated tok/s; one token per sequence per step: "
+          f"{es['ms_per_step']:.3f} ms/step ({es['rows_per_s']:.0f} rows/s); same tokens in the exact "
+          f"schedules: {line['same_tokens_both_exact_schedules']}, regime against exact: "
+          f"{line['regime_same_tokens_as_exact']}.\n")
     print("| kernel | grid (threads) | dispatches | mean us | min us | max us | total ms |")
     print("|---|---:|---:|---:|---:|---:|---:|")
     for (name, gx), d in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:30]:
         print(f"| {name} | {gx} | {len(d)} | {sum(d) / len(d):.2f} | {min(d):.2f} | {max(d):.2f} | "
               f"{sum(d) / 1e3:.2f} |")
-    print("\nThe 30 largest (kernel, grid) groups by total time, over both schedules.  Grid y of the\n"
+    print("\nThe 30 largest (kernel, grid) groups by total time, over the three runs.  Grid y of the\n"
           "matvec kernels counts row groups: `k_q35_mvpc` 20480x4 and `k_q35_mvd` 131584x1 / 114688x1\n"
           "are the 16-row steps of the one-token schedule (o/out/down projections; mix and gate+up),\n"
           "`k_q35_mvd<2, ...>` is the LM head with its argmax, and `k_q35_mv` with grid y in the hundreds\n"
-          "are the 256-token prompt chunks (up to 4096 rows).\n\n"
-          f"Summary: `python bench.py --summarize-c5-trace <dir>/<name>_kernel_trace.csv <bench stdout>`")
+          "are the 256-token prompt chunks (up to 4096 rows) of the exact run; `Cijk_` kernels are\n"
+          "the regime's library GEMMs, `k_q35_split` and `k_q35_finite` their operand split and check.\n\n"
+          f"Summary: `python bench.py --summarize-c5-trace <dir>/<name>_kernel_trace.csv <bench stdout> "
+          f"[<mfma counter_collection.csv>]`")
+    if mfma_csv:
+        print_mfma_table(mfma_csv, C5_PMC_CMD)
 
 
 LEG_TRACE_CMD = ("COHX_GRAPHS=0 rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o <name> -- "
@@ -567,6 +577,36 @@ LEG_PMC_CMD = ("COHX_GRAPHS=0 rocprofv3 --pmc {counters} --kernel-include-regex 
                "-d <dir> -o <name> -- python3 bench.py --only {leg}")
 MFMA_COUNTERS = "SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_MOPS_BF16 GRBM_GUI_ACTIVE"
 MI355X_CUS = 256
+
+
+def print_mfma_table(mfma_csv, cmd):
+    """Per matrix-core kernel instance: dispatches, MFMA busy share
+    (SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 256 CUs)), the MOPS
+    counters (units of 512 flops) and the counted TFLOP/s over the dispatches'
+    own durations."""
+    import csv
+    acc = {}
+    with open(mfma_csv) as f:
+        for row in csv.DictReader(f):
+            k = kernel_instance(row["Kernel_Name"])
+            a = acc.setdefault(k, {"_d": set(), "_ns": 0.0})
+            a[row["Counter_Name"]] = a.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+            if row["Dispatch_Id"] not in a["_d"]:
+                a["_d"].add(row["Dispatch_Id"])
+                a["_ns"] += int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+    print(f"\nMatrix cores: `{cmd}`\n")
+    print("| kernel | dispatches | MFMA busy share | MOPS f16 (x512 flop) | MOPS bf16 (x512 flop) | "
+          "counted TFLOP/s |")
+    print("|---|---:|---:|---:|---:|---:|")
+    for k, a in sorted(acc.items()):
+        busy = a.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / max(a.get("GRBM_GUI_ACTIVE", 1.0) * MI355X_CUS, 1.0)
+        mops = a.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0) + a.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0)
+        tf = mops * 512 / (a["_ns"] * 1e-9) / 1e12 if a["_ns"] else 0.0
+        print(f"| {k} | {len(a['_d'])} | {busy:.3f} | {a.get('SQ_INSTS_VALU_MFMA_MOPS_F16', 0.0):.3g} | "
+              f"{a.get('SQ_INSTS_VALU_MFMA_MOPS_BF16', 0.0):.3g} | {tf:.0f} |")
+    print("\nThe counted rate covers every MFMA issued (the chunk attention's three bf16 products per "
+          "f32 product, the Qwen3.5 regime's hi and lo GEMMs); the bench's TFLOP/s count the "
+          "algorithmic flops once.")
 
 
 def summarize_leg(leg, trace_csv, bench_json, fetch_csv=None, write_csv=None, mfma_csv=None,
@@ -611,27 +651,8 @@ def summarize_leg(leg, trace_csv, bench_json, fetch_csv=None, write_csv=None, mf
             wk = write.get(k, (0.0, 0))[0]
             print(f"| {k} | {n} | {fk:.0f} | {wk:.0f} | {(fk * ff + wk * fw) * 1024 / 1e6:.2f} MB |")
     if mfma_csv:
-        acc = {}
-        with open(mfma_csv) as f:
-            for row in csv.DictReader(f):
-                k = kernel_instance(row["Kernel_Name"])
-                a = acc.setdefault(k, {"_d": set(), "_ns": 0.0})
-                a[row["Counter_Name"]] = a.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
-                if row["Dispatch_Id"] not in a["_d"]:
-                    a["_d"].add(row["Dispatch_Id"])
-                    a["_ns"] += int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
-        print(f"\nMatrix cores: `{LEG_PMC_CMD.format(counters=MFMA_COUNTERS, regex='k_gemm_f16|k_attn_chunk|Cijk', leg=leg)}`\n")
-        print("| kernel | dispatches | MFMA busy share | MOPS f16 (x512 flop) | MOPS bf16 (x512 flop) | "
-              "counted TFLOP/s |")
-        print("|---|---:|---:|---:|---:|---:|")
-        for k, a in sorted(acc.items()):
-            busy = a.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / max(a.get("GRBM_GUI_ACTIVE", 1.0) * MI355X_CUS, 1.0)
-            mops = a.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0) + a.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0)
-            tf = mops * 512 / (a["_ns"] * 1e-9) / 1e12 if a["_ns"] else 0.0
-            print(f"| {k} | {len(a['_d'])} | {busy:.3f} | {a.get('SQ_INSTS_VALU_MFMA_MOPS_F16', 0.0):.3g} | "
-                  f"{a.get('SQ_INSTS_VALU_MFMA_MOPS_BF16', 0.0):.3g} | {tf:.0f} |")
-        print("\nThe counted rate covers every MFMA issued, including the chunk attention's three bf16 "
-              "products per f32 product; the bench's TFLOP/s count the algorithmic flops once.")
+        print_mfma_table(mfma_csv, LEG_PMC_CMD.format(counters=MFMA_COUNTERS, regex='k_gemm_f16|k_attn_chunk|Cijk',
+                                                      leg=leg))
     print(f"\nSummary: `python3 bench.py --summarize-leg {leg} <trace.csv> <bench stdout> [<fetch.csv> "
           f"<write.csv> <mfma.csv or -> <copy_fetch.csv> <copy_write.csv>]`")
 
@@ -760,10 +781,13 @@ def c5_generate(model, prompts, chunk, head_every_row=False):
 def run_c5(seed, cpu_steps, threads, with_cpu=True):
     """the Qwen3.5-0.8B hybrid shape (bf16 N(0,0.02)
     weights), 16 sequences with prompts U[64,1024] of random ids, 64 greedy
-    tokens each, exact arithmetic (bit-exact against the oracle).  Timed twice
-    from fresh sequences: with prompts in chunks of C5_CHUNK rows per lane per
-    step, and in the engine's one-token-per-step schedule; both must generate
-    the same tokens.  The CPU baseline steps the oracle over the first
+    tokens each.  Timed from fresh sequences: with prompts in chunks of
+    C5_CHUNK rows per lane per step (steps of 128+ rows in the packed-prefill
+    regime, the default: linears as library BF16 GEMMs with f32 sums, within
+    the stated tolerance), the same schedule with the regime off (exact, bit
+    for bit against the oracle), and the engine's one-token-per-step schedule
+    (exact).  The two exact runs must generate the same tokens; the regime's
+    agreement is reported.  The CPU baseline steps the oracle over the first
     prompt tokens of all 16 sequences (one token per sequence per step)."""
     import synth35
     t0 = time.perf_counter()
@@ -773,43 +797,64 @@ def run_c5(seed, cpu_steps, threads, with_cpu=True):
     plen = [int(v) for v in rng.integers(C5_PROMPT[0], C5_PROMPT[1] + 1, C5_SEQS)]
     prompts = [[int(v) for v in rng.integers(0, cfg["vocabulary"], n)] for n in plen]
     ctx = C5_PROMPT[1] + C5_GEN + 8
-    model = cohx.Qwen35(cfg, tensors, max_lanes=C5_SEQS, max_rows=C5_SEQS * C5_CHUNK,
-                        max_seqs=C5_SEQS, max_context=ctx)
-    c5_generate(model, [p[:C5_CHUNK + 3] for p in prompts[:4]], C5_CHUNK)  # warm-up
+
+    def make(regime):
+        old = os.environ.get("COHX_PREFILL_MFMA")
+        os.environ["COHX_PREFILL_MFMA"] = "1" if regime else "0"
+        try:
+            return cohx.Qwen35(cfg, tensors, max_lanes=C5_SEQS, max_rows=C5_SEQS * C5_CHUNK,
+                               max_seqs=C5_SEQS, max_context=ctx)
+        finally:
+            if old is None:
+                os.environ.pop("COHX_PREFILL_MFMA", None)
+            else:
+                os.environ["COHX_PREFILL_MFMA"] = old
+
     res = {}
-    for name, chunk in (("chunked", C5_CHUNK), ("engine_schedule", 1)):
-        t0 = time.perf_counter()
-        toks, steps, rows = c5_generate(model, prompts, chunk)
-        el = time.perf_counter() - t0
-        res[name] = dict(tokens=toks, steps=steps, rows=rows, elapsed=el)
-        log(f"[bench] c5 {name}: {C5_SEQS * C5_GEN / el:.0f} generated tok/s, {rows / el:.0f} rows/s, "
-            f"{steps} steps, {el:.2f}s")
-    ch, es = res["chunked"], res["engine_schedule"]
-    same = ch["tokens"] == es["tokens"]
+    for regime, runs in ((True, (("chunked", C5_CHUNK),)),
+                         (False, (("chunked_exact", C5_CHUNK), ("engine_schedule", 1)))):
+        model = make(regime)
+        c5_generate(model, [p[:C5_CHUNK + 3] for p in prompts[:4]], C5_CHUNK)  # warm-up
+        for name, chunk in runs:
+            t0 = time.perf_counter()
+            toks, steps, rows = c5_generate(model, prompts, chunk)
+            el = time.perf_counter() - t0
+            res[name] = dict(tokens=toks, steps=steps, rows=rows, elapsed=el)
+            log(f"[bench] c5 {name}: {C5_SEQS * C5_GEN / el:.0f} generated tok/s, {rows / el:.0f} rows/s, "
+                f"{steps} steps, {el:.2f}s")
+        matrix_bytes = model.matrix_bytes
+        del model
+    ch, ex, es = res["chunked"], res["chunked_exact"], res["engine_schedule"]
     line = {"workload": f"Qwen3.5-0.8B-shape hybrid (bf16 weights, f32 state), {C5_SEQS} sequences, "
-                        f"prompts U[{C5_PROMPT[0]},{C5_PROMPT[1]}], {C5_GEN} greedy tokens each; exact",
+                        f"prompts U[{C5_PROMPT[0]},{C5_PROMPT[1]}], {C5_GEN} greedy tokens each; prompt "
+                        f"steps of 128+ rows in the packed-prefill regime (library BF16 GEMMs, f32 sums)",
             "value": C5_SEQS * C5_GEN / ch["elapsed"], "unit": "generated tok/s (whole job)",
             "rows_per_s": ch["rows"] / ch["elapsed"], "elapsed_s": ch["elapsed"],
             "steps": ch["steps"], "prompt_chunk": C5_CHUNK, "prompt_rows": sum(plen),
-            "matrix_bytes": model.matrix_bytes,
+            "matrix_bytes": matrix_bytes,
+            "chunked_exact": {"value": C5_SEQS * C5_GEN / ex["elapsed"], "rows_per_s": ex["rows"] / ex["elapsed"],
+                              "elapsed_s": ex["elapsed"], "steps": ex["steps"]},
             "engine_schedule": {"value": C5_SEQS * C5_GEN / es["elapsed"],
                                 "rows_per_s": es["rows"] / es["elapsed"], "steps": es["steps"],
                                 "ms_per_step": es["elapsed"] * 1e3 / es["steps"],
                                 "elapsed_s": es["elapsed"]},
-            "same_tokens_both_schedules": same, "seed": seed + 5}
+            "same_tokens_both_exact_schedules": ex["tokens"] == es["tokens"],
+            "regime_same_tokens_as_exact": ch["tokens"] == ex["tokens"],
+            "regime_tokens_differing": sum(a != b for x, y in zip(ch["tokens"], ex["tokens"])
+                                           for a, b in zip(x, y)),
+            "seed": seed + 5}
     # one-token schedule: each step reads every weight once and each
     # sequence's recurrent state (conv ring and delta memory, read and written)
     lin = sum(1 for f in cfg["full"] if not f)
     conv_ch = 2 * cfg["key_heads"] * cfg["key_dim"] + cfg["value_heads"] * cfg["value_dim"]
     state = lin * (cfg["value_heads"] * cfg["key_dim"] * cfg["value_dim"] + conv_ch * cfg["conv_kernel"]) * 4 * 2
-    sb = model.matrix_bytes + C5_SEQS * state
+    sb = matrix_bytes + C5_SEQS * state
     es_s = es["elapsed"] / es["steps"]
     line["engine_schedule"]["step_roofline"] = {
         "bound": "hbm", "bytes_per_step": sb, "achieved": sb / es_s / 1e9, "peak": HBM_PEAK / 1e9,
         "unit": "GB/s", "frac": sb / es_s / HBM_PEAK,
         "note": "weights once plus each sequence's delta memory read and written; the exact step is "
                 "bound by one wave's issue rate on its f64 chains, not by HBM"}
-    del model
     if with_cpu:
         import orc
         m = orc.Qwen35Model(cfg, tensors, threads=threads)
@@ -852,8 +897,9 @@ def main():
                     help="only time the attention pass's f32-product / f64-chain pattern without memory")
     ap.add_argument("--summarize-counters", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
                     help="write the traffic summary from rocprofv3 --pmc csv files (no GPU)")
-    ap.add_argument("--summarize-c5-trace", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_JSON"),
-                    help="print a markdown summary of a rocprofv3 --kernel-trace run of --c5-only")
+    ap.add_argument("--summarize-c5-trace", nargs="+", metavar="ARG",
+                    help="KERNEL_TRACE_CSV BENCH_JSON [MFMA_CSV]: markdown summary of the rocprofv3 runs "
+                         "of --c5-only")
     ap.add_argument("--summarize-trace", nargs=2, metavar=("KERNEL_TRACE_CSV", "BENCH_JSON"),
                     help="print a markdown summary of a rocprofv3 --kernel-trace run (no GPU)")
     ap.add_argument("--summarize-leg", nargs="+", metavar="ARG",

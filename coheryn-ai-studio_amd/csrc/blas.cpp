@@ -1,9 +1,11 @@
-// Library GEMMs (hipBLASLt) for the F16 linears of a step in the
-// packed-prefill regime: Y[M][N] (+)= X[M][K] . W[N][K]^T with binary16
-// operands, exact products and f32 sums, the same contract as the regime's own
-// matrix-core kernel (k_gemm_f16) and held to the same tolerance against the
-// reference's sequential f64 dot (cpu.rs:31-48).  Only eager steps use it
-// (never under graph capture, never from the allocation-free entry point).
+// Library GEMMs (hipBLASLt) for the linears of a step in the packed-prefill
+// regime: Y[M][N] (+)= X[M][K] . W[N][K]^T with binary16 (Qwen2 F16) or
+// bfloat16 (Qwen3.5, whose f32 activations enter as a hi + lo pair of
+// bfloat16 GEMMs) operands, exact products and f32 sums, the same contract as
+// the regime's own matrix-core kernel (k_gemm_f16) and held to the same
+// tolerance against the reference's sequential f64 dot (cpu.rs:31-48).  Only
+// eager steps use it (never under graph capture, never from the
+// allocation-free entry point).
 #include <hipblaslt/hipblaslt.h>
 
 #include <map>
@@ -14,8 +16,9 @@
 namespace cohx {
 
 struct GemmLib {
-  // per (N, K, ldo, accumulate, M rounded up to 256): the matmul descriptor
-  // and the heuristic's algorithm; per exact M: the operand layouts
+  // per (operand type, N, K, ldo, accumulate, M rounded up to 256): the
+  // matmul descriptor and the heuristic's algorithm; per exact M: the
+  // operand layouts
   struct Plan {
     hipblasLtMatmulDesc_t op = nullptr;
     hipblasLtMatmulAlgo_t algo{};
@@ -28,8 +31,8 @@ struct GemmLib {
   hipblasLtHandle_t h = nullptr;
   void *ws = nullptr;
   size_t ws_bytes = 0;
-  std::map<std::tuple<int, int, int, bool, int>, Plan> plans;
-  std::map<std::tuple<int, int, int, int>, Shape> shapes;  // (N, K, M, ldo)
+  std::map<std::tuple<int, int, int, int, bool, int>, Plan> plans;
+  std::map<std::tuple<int, int, int, int, int>, Shape> shapes;  // (type, N, K, M, ldo)
 };
 
 namespace {
@@ -46,21 +49,20 @@ void release(GemmLib::Shape &l) {
 }
 
 // Column-major view: C (N x M, ld ldo) = op_T(W as K x N) . (X as K x M).
-bool make_shape(GemmLib::Shape &l, int N, int K, int M, int ldo) {
-  l.ok = !hipblasLtMatrixLayoutCreate(&l.a, HIP_R_16F, K, N, K) &&
-         !hipblasLtMatrixLayoutCreate(&l.b, HIP_R_16F, K, M, K) &&
+bool make_shape(GemmLib::Shape &l, hipDataType t, int N, int K, int M, int ldo) {
+  l.ok = !hipblasLtMatrixLayoutCreate(&l.a, t, K, N, K) && !hipblasLtMatrixLayoutCreate(&l.b, t, K, M, K) &&
          !hipblasLtMatrixLayoutCreate(&l.c, HIP_R_32F, N, M, ldo);
   return l.ok;
 }
 
-bool make_plan(GemmLib &lib, GemmLib::Plan &p, int N, int K, int Mb, int ldo) {
+bool make_plan(GemmLib &lib, GemmLib::Plan &p, hipDataType t, int N, int K, int Mb, int ldo) {
   if (hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) return false;
   const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
   if (hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) ||
       hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)))
     return false;
   GemmLib::Shape l;
-  if (!make_shape(l, N, K, Mb, ldo)) {
+  if (!make_shape(l, t, N, K, Mb, ldo)) {
     release(l);
     return false;
   }
@@ -101,26 +103,30 @@ void gemm_lib_destroy(GemmLib *lib) {
   delete lib;
 }
 
-bool gemm_lib_f16(GemmLib *lib, hipStream_t s, const uint16_t *w, int N, int K, const uint16_t *x, int M,
-                  float *out, int ldo, bool accumulate) {
+namespace {
+
+bool gemm_lib_run(GemmLib *lib, hipStream_t s, hipDataType t, const uint16_t *w, int N, int K, const uint16_t *x,
+                  int M, float *out, int ldo, bool accumulate) {
   if (!lib || M <= 0) return false;
   const int Mb = (M + 255) / 256 * 256;
-  auto pit = lib->plans.find(std::make_tuple(N, K, ldo, accumulate, Mb));
+  const auto pkey = std::make_tuple((int)t, N, K, ldo, accumulate, Mb);
+  auto pit = lib->plans.find(pkey);
   if (pit == lib->plans.end()) {
     GemmLib::Plan p;
-    if (!make_plan(*lib, p, N, K, Mb, ldo)) release(p);
-    pit = lib->plans.emplace(std::make_tuple(N, K, ldo, accumulate, Mb), p).first;
+    if (!make_plan(*lib, p, t, N, K, Mb, ldo)) release(p);
+    pit = lib->plans.emplace(pkey, p).first;
   }
   if (!pit->second.ok) return false;
-  auto sit = lib->shapes.find(std::make_tuple(N, K, M, ldo));
+  const auto skey = std::make_tuple((int)t, N, K, M, ldo);
+  auto sit = lib->shapes.find(skey);
   if (sit == lib->shapes.end()) {
     if (lib->shapes.size() >= 1024) {  // packed row counts vary step to step
       for (auto &kv : lib->shapes) release(kv.second);
       lib->shapes.clear();
     }
     GemmLib::Shape l;
-    if (!make_shape(l, N, K, M, ldo)) release(l);
-    sit = lib->shapes.emplace(std::make_tuple(N, K, M, ldo), l).first;
+    if (!make_shape(l, t, N, K, M, ldo)) release(l);
+    sit = lib->shapes.emplace(skey, l).first;
   }
   const GemmLib::Shape &l = sit->second;
   if (!l.ok) return false;
@@ -128,6 +134,18 @@ bool gemm_lib_f16(GemmLib *lib, hipStream_t s, const uint16_t *w, int N, int K, 
   const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
   return hipblasLtMatmul(lib->h, p.op, &alpha, w, l.a, x, l.b, &beta, out, l.c, out, l.c, &p.algo, lib->ws,
                          lib->ws_bytes, s) == HIPBLAS_STATUS_SUCCESS;
+}
+
+}  // namespace
+
+bool gemm_lib_f16(GemmLib *lib, hipStream_t s, const uint16_t *w, int N, int K, const uint16_t *x, int M,
+                  float *out, int ldo, bool accumulate) {
+  return gemm_lib_run(lib, s, HIP_R_16F, w, N, K, x, M, out, ldo, accumulate);
+}
+
+bool gemm_lib_bf16(GemmLib *lib, hipStream_t s, const uint16_t *w, int N, int K, const uint16_t *x, int M,
+                   float *out, int ldo, bool accumulate) {
+  return gemm_lib_run(lib, s, HIP_R_16BF, w, N, K, x, M, out, ldo, accumulate);
 }
 
 }  // namespace cohx

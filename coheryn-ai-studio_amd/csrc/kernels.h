@@ -97,14 +97,17 @@ void set_head_mfma(bool on);
 // Timing events for the next launches (see the launch helper); both null ends it.
 void set_launch_events(hipEvent_t start, hipEvent_t stop);
 
-// Library GEMMs (hipBLASLt, blas.cpp) for the packed-prefill regime's F16
-// linears: Y[M][N] (+)= X[M][K] . W[N][K]^T, binary16 operands, f32 sums.
+// Library GEMMs (hipBLASLt, blas.cpp) for the packed-prefill regime's
+// linears: Y[M][N] (+)= X[M][K] . W[N][K]^T (W and X row-major), binary16
+// or bfloat16 operands, f32 sums.
 struct GemmLib;
 GemmLib *gemm_lib_create(void *workspace, size_t workspace_bytes);
 void gemm_lib_destroy(GemmLib *lib);
 // false: nothing launched (no algorithm for the shape)
 bool gemm_lib_f16(GemmLib *lib, hipStream_t s, const uint16_t *w, int N, int K, const uint16_t *x, int M,
                   float *out, int ldo, bool accumulate);
+bool gemm_lib_bf16(GemmLib *lib, hipStream_t s, const uint16_t *w, int N, int K, const uint16_t *x, int M,
+                   float *out, int ldo, bool accumulate);
 // The next launches' F16 linears in the regime go through `lib` (nullptr:
 // the matrix-core kernel); gate+up writes its [rows][2F] f32 sums to
 // `scratch` (at least scratch_floats) before the SwiGLU pass.

@@ -53,6 +53,13 @@ void q35_matvec(hipStream_t s, int epi, const uint16_t *w, int rows_w, int valid
                 const float *x, int ldx, int R, float *out, int ldo, unsigned long long *part,
                 uint32_t *row_err, const uint32_t *err_row);
 int q35_matvec_blocks(int rows_w);
+// Packed-prefill regime: rows x[rows][K] (stride ldx; K and ldx multiples of
+// 4) as bfloat16 pairs hi = bf16(x), lo = bf16(x - hi) into hi/lo[rows][K],
+// the operands of the library GEMMs that replace q35_matvec there.
+void q35_split_bf16(hipStream_t s, int rows, int K, const float *x, int ldx, uint16_t *hi, uint16_t *lo);
+// row_err[r] |= the matvecs' non-finite bit for rows of out[rows][N] (stride
+// ldo, N % 4 == 0) holding a non-finite value.
+void q35_check_finite(hipStream_t s, int rows, int N, const float *out, int ldo, uint32_t *row_err);
 void q35_swiglu(hipStream_t s, int rows, const float *gu, int ldgu, int F, int up_off, float *h,
                 int ldh);
 void q35_conv(hipStream_t s, int lanes, Q35Lanes L, const float *mix, int ldm, const float *w,

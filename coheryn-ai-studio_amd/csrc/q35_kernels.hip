@@ -1067,6 +1067,47 @@ __global__ __launch_bounds__(576) void k_q35_attn(Q35Rows Rw, const float *__res
   }
 }
 
+// ---------------------------------------------------------------------------
+// Packed-prefill regime (steps of 128+ rows): the linears run as library
+// GEMMs over a row-major BF16 copy of each matrix.  An f32 activation x enters
+// as hi = bf16(x) and lo = bf16(x - hi) (round to nearest even), so hi + lo
+// is x to a relative 2^-17 or better, every product of two bfloat16 values is
+// exact in f32, and the f32 sums of hi . w + lo . w are what differ from the
+// reference's f64 dot (cpu.rs:31-48).  Thread = 4 consecutive inputs.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_q35_split(const float *__restrict__ x, int ldx, int K,
+                                                   uint16_t *__restrict__ hi, uint16_t *__restrict__ lo) {
+  const int r = blockIdx.y, k = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (k >= K) return;
+  const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)r * ldx + k);
+  const float f[4] = {v.x, v.y, v.z, v.w};
+  uint16_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const __bf16 bh = (__bf16)f[i];
+    const __bf16 bl = (__bf16)(f[i] - (float)bh);
+    h[i] = __builtin_bit_cast(uint16_t, bh);
+    l[i] = __builtin_bit_cast(uint16_t, bl);
+  }
+  *reinterpret_cast<uint2 *>(hi + (size_t)r * K + k) =
+      make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16);
+  *reinterpret_cast<uint2 *>(lo + (size_t)r * K + k) =
+      make_uint2(l[0] | (uint32_t)l[1] << 16, l[2] | (uint32_t)l[3] << 16);
+}
+
+// The matvecs' non-finite output check for the library GEMM's rows: block =
+// one row of out[.][N] (N % 4 == 0).
+__global__ __launch_bounds__(256) void k_q35_finite(const float *__restrict__ out, int ldo, int N,
+                                                    uint32_t *row_err) {
+  const int r = blockIdx.x;
+  bool bad = false;
+  for (int k = threadIdx.x * 4; k < N; k += 1024) {
+    const float4 v = *reinterpret_cast<const float4 *>(out + (size_t)r * ldo + k);
+    bad |= !finitef(v.x) || !finitef(v.y) || !finitef(v.z) || !finitef(v.w);
+  }
+  if (__syncthreads_or(bad) && threadIdx.x == 0) atomicOr(&row_err[r], kErrNonFinite);
+}
+
 }  // namespace
 
 // ---- launchers ---------------------------------------------------------------
@@ -1130,6 +1171,14 @@ void q35_matvec(hipStream_t s, int epi, const uint16_t *w, int rows_w, int valid
   else
     hipLaunchKernelGGL(k_q35_mv<kQ35Argmax>, grid, dim3(256), 0, s, w, rows_w, valid_rows, K, x,
                        ldx, R, out, ldo, part, row_err, err_row);
+}
+
+void q35_split_bf16(hipStream_t s, int rows, int K, const float *x, int ldx, uint16_t *hi, uint16_t *lo) {
+  hipLaunchKernelGGL(k_q35_split, dim3((K / 4 + 255) / 256, rows), dim3(256), 0, s, x, ldx, K, hi, lo);
+}
+
+void q35_check_finite(hipStream_t s, int rows, int N, const float *out, int ldo, uint32_t *row_err) {
+  hipLaunchKernelGGL(k_q35_finite, dim3(rows), dim3(256), 0, s, out, ldo, N, row_err);
 }
 
 void q35_swiglu(hipStream_t s, int rows, const float *gu, int ldgu, int F, int up_off, float *h,

@@ -287,18 +287,82 @@ def test_c3_f16_mixed_prefill_step_matches_oracle():
     m.close()
 
 
+def test_c5_qwen35_prefill_regime_greedy_ids_and_top_logits():
+    """configs[4] with the packed-prefill regime on (the default): the prompt
+    steps' linears run as library BF16 GEMMs.  Greedy ids must equal the
+    oracle's; every sampled lane's top-1 and top-2 logits (the fixture keeps
+    those values) within 1e-2 of the oracle's."""
+    import synth35
+    spec = fc.c5()
+    fx = fixture("c5", spec)
+    print("building the Qwen3.5-0.8B-shape model", flush=True)
+    cfg, t = synth35.in_memory(synth35.config(), seed=spec["model_seed"])
+    old = os.environ.get("COHX_PREFILL_MFMA")
+    os.environ["COHX_PREFILL_MFMA"] = "1"
+    try:
+        m = cohx.Qwen35(cfg, t, max_lanes=16, max_rows=16 * 256, max_seqs=16, max_context=spec["context"])
+    finally:
+        if old is None:
+            os.environ.pop("COHX_PREFILL_MFMA", None)
+        else:
+            os.environ["COHX_PREFILL_MFMA"] = old
+    prompts = spec["prompts"]
+    seqs = [m.seq_alloc() for _ in prompts]
+    cursor = [0] * len(prompts)
+    got = [[] for _ in prompts]
+    worst, gap = 0.0, float("inf")
+    while any(len(g) < spec["generate"] + 1 for g in got):
+        lanes, idx = [], []
+        for i, p in enumerate(prompts):
+            if len(got[i]) >= spec["generate"] + 1:
+                continue
+            if cursor[i] < len(p):
+                toks = p[cursor[i]:cursor[i] + 256]
+                ends = cursor[i] + len(toks) == len(p)
+                lanes.append(dict(seq=seqs[i], tokens=toks, logits=ends, skip_head=not ends))
+                idx.append((i, len(toks), ends))
+            else:
+                lanes.append(dict(seq=seqs[i], tokens=[got[i][-1]], logits=True))
+                idx.append((i, 1, True))
+        res = m.step(lanes)
+        for (i, n, sampled), r in zip(idx, res):
+            assert r["status"] == 0
+            cursor[i] += n
+            if sampled:
+                k = len(got[i])
+                want = fx["samples"][i][k]
+                sm = fc.summary(r["logits"])
+                worst = max(worst, abs(sm["top1"] - want["top1"]), abs(sm["top2"] - want["top2"]))
+                gap = min(gap, want["top1"] - want["top2"])
+                got[i].append(int(r["argmax"]))
+    print(f"case c5 regime: worst top-1/top-2 logit deviation {worst:.3g}, "
+          f"smallest oracle top-1/top-2 gap {gap:.3g}", flush=True)
+    assert got == [[x["argmax"] for x in s] for s in fx["samples"]]
+    assert worst <= 1e-2
+    m.close()
+
+
 def test_c5_qwen35_sixteen_prompts_match_oracle():
     """Qwen3.5-0.8B shape, 16 prompts of U[64, 1024] ids in chunks
     of 256 rows (rows before a prompt's end skip the head), then 4 greedy
     tokens: every sampled lane's logits, the ids, and the last linear layer's
-    conv ring and delta memory and the last full layer's K/V tail, bit for bit."""
+    conv ring and delta memory and the last full layer's K/V tail, bit for bit
+    (the packed-prefill regime off: every step on the exact matvecs)."""
     import synth35
     spec = fc.c5()
     fx = fixture("c5", spec)
     print("building the Qwen3.5-0.8B-shape model", flush=True)
     cfg, t = synth35.in_memory(synth35.config(), seed=spec["model_seed"])
     prompts = spec["prompts"]
-    m = cohx.Qwen35(cfg, t, max_lanes=16, max_rows=16 * 256, max_seqs=16, max_context=spec["context"])
+    old = os.environ.get("COHX_PREFILL_MFMA")
+    os.environ["COHX_PREFILL_MFMA"] = "0"
+    try:
+        m = cohx.Qwen35(cfg, t, max_lanes=16, max_rows=16 * 256, max_seqs=16, max_context=spec["context"])
+    finally:
+        if old is None:
+            os.environ.pop("COHX_PREFILL_MFMA", None)
+        else:
+            os.environ["COHX_PREFILL_MFMA"] = old
     seqs = [m.seq_alloc() for _ in prompts]
     cursor = [0] * len(prompts)
     got = [[] for _ in prompts]

@@ -23,15 +23,40 @@ def tiny(**kw):
     return synth35.config(**c)
 
 
+# The packed-prefill regime's stated tolerance: logits max-abs (the fp16
+# bound the engine's tolerance names) and the recurrent state it leaves
+# (K/V rows, conv ring, delta memory).  Greedy ids stay exact.
+REGIME_LOGITS_TOL = 1e-2
+REGIME_STATE_TOL = 1e-3
+
+
+def make_q35(cfg, t, regime, **kw):
+    """A GPU context; regime False keeps every step on the exact matvecs
+    (COHX_PREFILL_MFMA=0), True lets steps of 128+ rows take the library GEMMs."""
+    old = os.environ.get("COHX_PREFILL_MFMA")
+    os.environ["COHX_PREFILL_MFMA"] = "1" if regime else "0"
+    try:
+        return cohx.Qwen35(cfg, t, **kw)
+    finally:
+        if old is None:
+            del os.environ["COHX_PREFILL_MFMA"]
+        else:
+            os.environ["COHX_PREFILL_MFMA"] = old
+
+
 class Pair:
     """A GPU context and an oracle model over the same tensors, with one oracle
-    session per GPU sequence."""
+    session per GPU sequence.  With `tol` (the regime tests) logits and state
+    are held to REGIME_*_TOL instead of bit equality; greedy ids stay exact."""
 
-    def __init__(self, cfg, t, threads=8, **kw):
+    def __init__(self, cfg, t, threads=8, tol=False, **kw):
         self.cfg = cfg
-        self.gpu = cohx.Qwen35(cfg, t, **kw)
+        self.tol = tol
+        self.gpu = make_q35(cfg, t, tol, **kw)
         self.orc = orc.Qwen35Model(cfg, t, threads=threads)
         self.sessions = {}
+        self.worst_logit = 0.0
+        self.worst_state = 0.0
 
     def alloc(self):
         s = self.gpu.seq_alloc()
@@ -60,7 +85,11 @@ class Pair:
                 continue
             want = self.sessions[s].logits()
             got = r["logits"]
-            if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
+            if self.tol:
+                err = float(np.abs(got.astype(np.float64) - want).max())
+                self.worst_logit = max(self.worst_logit, err)
+                assert err <= REGIME_LOGITS_TOL, (s, err)
+            elif not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
                 bad = np.nonzero(got.view(np.uint32) != want.view(np.uint32))[0]
                 raise AssertionError(f"seq {s}: {bad.size} logits differ, first {bad[:4]}, "
                                      f"max-abs {np.abs(got - want).max():.3g}")
@@ -76,7 +105,12 @@ class Pair:
                 got = self.gpu.read_state(seq, layer, which)
                 want = ses.state(layer, which).reshape(-1)
                 assert got.size == want.size, (layer, which)
-                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (seq, layer, which)
+                if self.tol:
+                    err = float(np.abs(got.astype(np.float64) - want).max()) if got.size else 0.0
+                    self.worst_state = max(self.worst_state, err)
+                    assert err <= REGIME_STATE_TOL, (seq, layer, which, err)
+                else:
+                    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (seq, layer, which)
 
 
 def test_tiny_prefill_decode_and_state_bit_exact():
@@ -108,11 +142,9 @@ def test_tiny_ragged_chunks_across_steps():
     p.check_state(b)
 
 
-def test_tiny_large_packed_step_bit_exact():
-    print("case: tiny Qwen3.5, 141 packed rows (chunks of 100 and 40 plus a decode row): the "
-          "many-rows matvec form", flush=True)
+def _large_packed_tiny(regime):
     cfg, t = synth35.in_memory(tiny(), seed=12)
-    p = Pair(cfg, t, max_lanes=4, max_rows=160, max_context=160)
+    p = Pair(cfg, t, tol=regime, max_lanes=4, max_rows=160, max_context=160)
     a, b, c = p.alloc(), p.alloc(), p.alloc()
     rng = np.random.default_rng(13)
     pa = [int(v) for v in rng.integers(0, cfg["vocabulary"], 100)]
@@ -122,20 +154,47 @@ def test_tiny_large_packed_step_bit_exact():
     p.step([(a, [ta]), (b, [tb]), (c, [tc])])
     for s_ in (a, b, c):
         p.check_state(s_)
+    return p
+
+
+def test_tiny_large_packed_step_bit_exact():
+    print("case: tiny Qwen3.5, 141 packed rows (chunks of 100 and 40 plus a decode row): the "
+          "many-rows matvec form, regime off", flush=True)
+    _large_packed_tiny(False)
+
+
+def test_tiny_large_packed_step_prefill_regime_within_tolerance():
+    print("case: tiny Qwen3.5, 141 packed rows through the packed-prefill regime (library "
+          "BF16 GEMMs on hi/lo activations)", flush=True)
+    p = _large_packed_tiny(True)
+    print(f"case: worst logit max-abs {p.worst_logit:.3g}, worst state {p.worst_state:.3g}", flush=True)
+
+
+def _full_shape_packed(regime, n_prompt):
+    cfg, t = synth35.in_memory(synth35.config(), seed=14)
+    p = Pair(cfg, t, threads=16, tol=regime, max_lanes=2, max_rows=128, max_context=160)
+    a, b = p.alloc(), p.alloc()
+    rng = np.random.default_rng(15)
+    pa = [int(v) for v in rng.integers(0, cfg["vocabulary"], n_prompt)]
+    (tb,) = p.step([(b, [11])])
+    ta, tb = p.step([(a, pa), (b, [tb])])
+    p.step([(a, [ta]), (b, [tb])])
+    p.check_state(a)
+    p.check_state(b)
+    return p
 
 
 def test_full_shape_large_packed_step_bit_exact():
     print("case: Qwen3.5-0.8B shape, one step of 96 + 1 packed rows (many-rows matvec form)",
           flush=True)
-    cfg, t = synth35.in_memory(synth35.config(), seed=14)
-    p = Pair(cfg, t, threads=16, max_lanes=2, max_rows=128, max_context=128)
-    a, b = p.alloc(), p.alloc()
-    rng = np.random.default_rng(15)
-    pa = [int(v) for v in rng.integers(0, cfg["vocabulary"], 96)]
-    (tb,) = p.step([(b, [11])])
-    p.step([(a, pa), (b, [tb])])
-    p.check_state(a)
-    p.check_state(b)
+    _full_shape_packed(False, 96)
+
+
+def test_full_shape_prefill_regime_within_tolerance():
+    print("case: Qwen3.5-0.8B shape, one step of 127 + 1 packed rows through the packed-prefill "
+          "regime, then a decode step", flush=True)
+    p = _full_shape_packed(True, 127)
+    print(f"case: worst logit max-abs {p.worst_logit:.3g}, worst state {p.worst_state:.3g}", flush=True)
 
 
 def test_tiny_fused_mixer_matches_oracle_and_split_kernels():
