@@ -1060,7 +1060,7 @@ __global__ __launch_bounds__(64 * kChainWaves) void k_mv_q8c(MatrixView w, ActVi
 // acc = fmaf((float)isum*dw, da, acc) for Q4_0.  K is limited to
 // 64 * kMaxPairs inputs (the B operand lives in registers).
 // ---------------------------------------------------------------------------
-template <int kEpi, int kNM, int kFmt, int kMaxPairs, int kU>
+template <int kEpi, int kNM, int kFmt, int kMaxPairs, int kU, bool kExact = false>
 __global__ __launch_bounds__(512 * kU) void k_mv_q8w(MatrixView w, ActView act, int rows_b, int n_tiles,
                                                      MatvecOut o, ActView qout, int qout_nbp) {
   static_assert(kU == 1 || (kU == 2 && kEpi == kEpiSwiglu), "two units per workgroup: the fused quantizer");
@@ -1076,7 +1076,10 @@ __global__ __launch_bounds__(512 * kU) void k_mv_q8w(MatrixView w, ActView act, 
   const int tile0 = blockIdx.y * W, nbt = min(W, n_tiles - tile0);
   const int uw = wave / W, bt = wave % W;
   const int unit = blockIdx.x * kU + uw, nt = tile0 + bt;
-  const int npairs = w.nbp / 2, nbp = w.nbp;
+  // kExact: K is exactly kMaxPairs block pairs (checked by the launch), so
+  // the block loop below is straight-line code the compiler can schedule
+  // across pairs (MFMAs of later pairs issued under earlier chains)
+  const int npairs = kExact ? kMaxPairs : w.nbp / 2, nbp = kExact ? 2 * kMaxPairs : w.nbp;
   const int nw = kU * kNM * npairs * kPairBytes / 16;  // copy items: weights, weight scales, batch scales
   const int ns = kU * kNM * nbp * 32 / 16;
   const int nd = nbt * nbp * 32 / 16;
@@ -1119,47 +1122,56 @@ __global__ __launch_bounds__(512 * kU) void k_mv_q8w(MatrixView w, ActView act, 
   for (int m = 0; m < kNM; m++)
 #pragma unroll
     for (int i = 0; i < 4; i++) acc[m][i] = 0.0f;
+  // one block pair of the chain: the unit's tiles from LDS, an MFMA per
+  // (block, tile), then acc = fmaf(isum, scale product, acc) in block order
+  auto pair = [&](int p) __attribute__((always_inline)) {
+    uint4 a[kNM];
 #pragma unroll
-  for (int p = 0; p < kMaxPairs; p++) {
-    if (p < npairs && live) {
-      uint4 a[kNM];
+    for (int m = 0; m < kNM; m++) {
+      if constexpr (kFmt == 8) {
+        a[m] = *reinterpret_cast<const uint4 *>(sw + (m * npairs + p) * kPairBytes + lane * 16);
+      } else {
+        const uint2 v = *reinterpret_cast<const uint2 *>(sw + (m * npairs + p) * kPairBytes + lane * 8);
+        a[m] = make_uint4(v.x, v.y, 0u, 0u);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int blk = 2 * p + h;
+      const long bop = h ? hi64(b[p]) : lo64(b[p]);
+      const uint32_t da = sda[(bt * nbp + blk) * 16 + col];
 #pragma unroll
       for (int m = 0; m < kNM; m++) {
+        long aop;
+        if constexpr (kFmt == 8)
+          aop = h ? hi64(a[m]) : lo64(a[m]);
+        else
+          aop = q4_operand(h ? a[m].y : a[m].x);
+        const v4i sum = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, zero, 0, 0, 0);
+        const uint2 s2 = *reinterpret_cast<const uint2 *>(ssc + (m * nbp + blk) * 16 + rsub);
         if constexpr (kFmt == 8) {
-          a[m] = *reinterpret_cast<const uint4 *>(sw + (m * npairs + p) * kPairBytes + lane * 16);
+          const float sc[4] = {scale_mul<0, 0>(s2.x, da), scale_mul<1, 0>(s2.x, da), scale_mul<0, 0>(s2.y, da),
+                               scale_mul<1, 0>(s2.y, da)};
+#pragma unroll
+          for (int i = 0; i < 4; i++) acc[m][i] = fmaf((float)sum[i], sc[i], acc[m][i]);
         } else {
-          const uint2 v = *reinterpret_cast<const uint2 *>(sw + (m * npairs + p) * kPairBytes + lane * 8);
-          a[m] = make_uint4(v.x, v.y, 0u, 0u);
-        }
-      }
+          const float t[4] = {mul_half<0>((float)sum[0], s2.x), mul_half<1>((float)sum[1], s2.x),
+                              mul_half<0>((float)sum[2], s2.y), mul_half<1>((float)sum[3], s2.y)};
 #pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const int blk = 2 * p + h;
-        const long bop = h ? hi64(b[p]) : lo64(b[p]);
-        const uint32_t da = sda[(bt * nbp + blk) * 16 + col];
-#pragma unroll
-        for (int m = 0; m < kNM; m++) {
-          long aop;
-          if constexpr (kFmt == 8)
-            aop = h ? hi64(a[m]) : lo64(a[m]);
-          else
-            aop = q4_operand(h ? a[m].y : a[m].x);
-          const v4i sum = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, zero, 0, 0, 0);
-          const uint2 s2 = *reinterpret_cast<const uint2 *>(ssc + (m * nbp + blk) * 16 + rsub);
-          if constexpr (kFmt == 8) {
-            const float sc[4] = {scale_mul<0, 0>(s2.x, da), scale_mul<1, 0>(s2.x, da), scale_mul<0, 0>(s2.y, da),
-                                 scale_mul<1, 0>(s2.y, da)};
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[m][i] = fmaf((float)sum[i], sc[i], acc[m][i]);
-          } else {
-            const float t[4] = {mul_half<0>((float)sum[0], s2.x), mul_half<1>((float)sum[1], s2.x),
-                                mul_half<0>((float)sum[2], s2.y), mul_half<1>((float)sum[3], s2.y)};
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[m][i] = fma_half(t[i], da, acc[m][i]);
-          }
+          for (int i = 0; i < 4; i++) acc[m][i] = fma_half(t[i], da, acc[m][i]);
         }
       }
     }
+  };
+  if constexpr (kExact) {
+    if (live) {
+#pragma unroll
+      for (int p = 0; p < kMaxPairs; p++) pair(p);
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < kMaxPairs; p++)
+      if (p < npairs && live) pair(p);
   }
   // ---- epilogue: lane holds rows (unit*kNM + m)*16 + rsub + i of batch row nt*16 + col
   const int r = nt * 16 + col;
@@ -1235,7 +1247,7 @@ __global__ __launch_bounds__(512 * kU) void k_mv_q8w(MatrixView w, ActView act, 
 // trip.  Workgroups of one block q sit on one XCD (blockIdx % 8), so the
 // weight tiles shared by its batch groups are fetched into that L2 once.
 // ---------------------------------------------------------------------------
-template <int kFmt, int kNB, int kNN, int kMaxPairs>
+template <int kFmt, int kNB, int kNN, int kMaxPairs, bool kExact = false>
 __global__ __launch_bounds__(256 * kNB) void k_mv_gu(MatrixView w, ActView act, int rows_b, int n_tiles,
                                                      uint32_t *row_err, const uint32_t *err_rows,
                                                      ActView qout, int qout_nbp) {
@@ -1247,7 +1259,9 @@ __global__ __launch_bounds__(256 * kNB) void k_mv_gu(MatrixView w, ActView act, 
   const int g8 = blockIdx.x / (8 * nbg), rem = blockIdx.x % (8 * nbg);
   const int bg = rem / 8, q = g8 * 8 + rem % 8;
   if (q >= nq) return;  // whole workgroup, before any barrier
-  const int npairs = w.nbp / 2, nbp = w.nbp;
+  // kExact: K is exactly kMaxPairs block pairs (checked by the launch): the
+  // block loop is straight-line code, scheduled across pairs
+  const int npairs = kExact ? kMaxPairs : w.nbp / 2, nbp = kExact ? 2 * kMaxPairs : w.nbp;
   const int tw = wave % 4, tile = 4 * q + tw;
   const int tile0 = bg * kBT, nbt = min(kBT, n_tiles - tile0);
   // LDS: [kBT][npairs][64] uint4 B operand, then [4][nbp][16] weight scales,
@@ -1296,38 +1310,47 @@ __global__ __launch_bounds__(256 * kNB) void k_mv_gu(MatrixView w, ActView act, 
   for (int n = 0; n < kNN; n++)
 #pragma unroll
     for (int i = 0; i < 4; i++) acc[n][i] = 0.0f;
+  // one block pair against batch tile bt0 + n: an MFMA per block, then
+  // acc = fmaf(isum, scale product, acc) in block order
+  auto pair = [&](int p, int n) __attribute__((always_inline)) {
+    const int bt = bt0 + n;
+    const uint4 b = smem[(bt * npairs + p) * 64 + lane];
 #pragma unroll
-  for (int p = 0; p < kMaxPairs; p++) {
-    if (p < npairs) {
+    for (int h = 0; h < 2; h++) {
+      const int blk = 2 * p + h;
+      long aop;
+      if constexpr (kFmt == 8)
+        aop = h ? hi64(a[p]) : lo64(a[p]);
+      else
+        aop = q4_operand(h ? a[p].y : a[p].x);
+      const v4i sum = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, h ? hi64(b) : lo64(b), zero, 0, 0, 0);
+      const uint2 s2 = *reinterpret_cast<const uint2 *>(sdw + blk * 16 + rsub);
+      const uint32_t da = sda[(bt * nbp + blk) * 16 + col];
+      if constexpr (kFmt == 8) {
+        const float sc[4] = {scale_mul<0, 0>(s2.x, da), scale_mul<1, 0>(s2.x, da),
+                             scale_mul<0, 0>(s2.y, da), scale_mul<1, 0>(s2.y, da)};
 #pragma unroll
-      for (int n = 0; n < kNN; n++) {
-        const int bt = bt0 + n;
-        if (bt < nbt) {
-          const uint4 b = smem[(bt * npairs + p) * 64 + lane];
+        for (int i = 0; i < 4; i++) acc[n][i] = fmaf((float)sum[i], sc[i], acc[n][i]);
+      } else {
+        const float t[4] = {mul_half<0>((float)sum[0], s2.x), mul_half<1>((float)sum[1], s2.x),
+                            mul_half<0>((float)sum[2], s2.y), mul_half<1>((float)sum[3], s2.y)};
 #pragma unroll
-          for (int h = 0; h < 2; h++) {
-            const int blk = 2 * p + h;
-            long aop;
-            if constexpr (kFmt == 8)
-              aop = h ? hi64(a[p]) : lo64(a[p]);
-            else
-              aop = q4_operand(h ? a[p].y : a[p].x);
-            const v4i sum = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, h ? hi64(b) : lo64(b), zero, 0, 0, 0);
-            const uint2 s2 = *reinterpret_cast<const uint2 *>(sdw + blk * 16 + rsub);
-            const uint32_t da = sda[(bt * nbp + blk) * 16 + col];
-            if constexpr (kFmt == 8) {
-              const float sc[4] = {scale_mul<0, 0>(s2.x, da), scale_mul<1, 0>(s2.x, da),
-                                   scale_mul<0, 0>(s2.y, da), scale_mul<1, 0>(s2.y, da)};
+        for (int i = 0; i < 4; i++) acc[n][i] = fma_half(t[i], da, acc[n][i]);
+      }
+    }
+  };
+  if (kExact && bt0 + kNN <= nbt) {  // every batch tile of the wave present
 #pragma unroll
-              for (int i = 0; i < 4; i++) acc[n][i] = fmaf((float)sum[i], sc[i], acc[n][i]);
-            } else {
-              const float t[4] = {mul_half<0>((float)sum[0], s2.x), mul_half<1>((float)sum[1], s2.x),
-                                  mul_half<0>((float)sum[2], s2.y), mul_half<1>((float)sum[3], s2.y)};
+    for (int p = 0; p < kMaxPairs; p++)
 #pragma unroll
-              for (int i = 0; i < 4; i++) acc[n][i] = fma_half(t[i], da, acc[n][i]);
-            }
-          }
-        }
+      for (int n = 0; n < kNN; n++) pair(p, n);
+  } else {
+#pragma unroll
+    for (int p = 0; p < kMaxPairs; p++) {
+      if (p < npairs) {
+#pragma unroll
+        for (int n = 0; n < kNN; n++)
+          if (bt0 + n < nbt) pair(p, n);
       }
     }
   }
@@ -3003,6 +3026,9 @@ void launch_matvec_qkv(hipStream_t s, const MatrixView &w, const ActView &act, i
 bool launch_matvec_swiglu_q8(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
                              const MatvecOut &o, const ActView &qout, int qout_nbp) {
   constexpr int kWPairs = 16;
+  // K = 896 (Qwen2.5-0.5B's hidden size) gets kernels built for exactly its
+  // 14 block pairs (straight-line block loops)
+  constexpr int kExactPairs = 14;
   const int F = w.rows / 2, n_tiles = (rows_b + 15) / 16;
   if ((w.dtype != 8 && w.dtype != 2) || w.nbp > 2 * kWPairs || F % 64 != 0) return false;
   // the epilogue writes whole block pairs of the down projection's operand
@@ -3013,7 +3039,10 @@ bool launch_matvec_swiglu_q8(hipStream_t s, const MatrixView &w, const ActView &
     const size_t items = (size_t)npairs * 64 + 4 * (size_t)w.nbp * 2 + (size_t)w.nbp * 2;
     const size_t lds = items * 16 > 4096 ? items * 16 : 4096;
     const dim3 grid((nq + 7) / 8 * 8 * n_tiles);
-    if (w.dtype == 8)
+    if (w.dtype == 8 && npairs == kExactPairs)
+      launch_k((k_mv_gu<8, 1, 1, kExactPairs, true>), grid, dim3(256), lds, s, w, act, rows_b, n_tiles, o.row_err,
+               o.err_rows, qout, qout_nbp);
+    else if (w.dtype == 8)
       launch_k((k_mv_gu<8, 1, 1, kWPairs>), grid, dim3(256), lds, s, w, act, rows_b, n_tiles, o.row_err, o.err_rows,
                qout, qout_nbp);
     else
@@ -3029,7 +3058,10 @@ bool launch_matvec_swiglu_q8(hipStream_t s, const MatrixView &w, const ActView &
   // the epilogue's exchange of 2 units x 8 batch tiles x 16 x 16 floats
   const size_t copy = 2 * 2 * (size_t)(w.nbp / 2) * pair_bytes + 2 * 2 * (size_t)w.nbp * 32 + 8 * (size_t)w.nbp * 32;
   const size_t lds = copy > 2 * 8 * 256 * 4 ? copy : 2 * 8 * 256 * 4;
-  if (w.dtype == 8)
+  if (w.dtype == 8 && w.nbp == 2 * kExactPairs)
+    launch_k((k_mv_q8w<kEpiSwiglu, 2, 8, kExactPairs, 2, true>), dim3(groups, by), dim3(nthreads), lds, s, w, act,
+             rows_b, n_tiles, o, qout, qout_nbp);
+  else if (w.dtype == 8)
     launch_k((k_mv_q8w<kEpiSwiglu, 2, 8, kWPairs, 2>), dim3(groups, by), dim3(nthreads), lds, s, w, act, rows_b,
              n_tiles, o, qout, qout_nbp);
   else
