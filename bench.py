@@ -38,11 +38,11 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_decode128.json")
 # profiler category -> the kernel instance it times at the Qwen2.5-0.5B shape
 # (qkv, o and down are split-K instances; o and down share one instance and
 # grid, so counters cannot tell them apart)
-CATEGORY_KERNEL = {"attn_scores": "k_attn_scores<64, 7>", "attn_softmax_stats": "k_attn_exp<7>",
+CATEGORY_KERNEL = {"attn_scores": "k_attn_scores<64, 7, 2>", "attn_softmax_stats": "k_attn_exp<7>",
                    "attn_pv": "k_attn_pv<64, 7>", "attn_combine_act": "k_attn_combine<8>",
-                   "matvec_qkv": "k_mv_q8s<4, 1, 2, 8>", "matvec_o_residual": "k_mv_q8s<1, 1, 2, 8>",
-                   "matvec_gate_up_swiglu": "k_mv_q8w<2, 2, 8, 16, 2>",
-                   "matvec_down_residual": "k_mv_q8s<1, 1, 2, 8>",
+                   "matvec_qkv": "k_mv_q8s<4, 1, 2, 8, 8>", "matvec_o_residual": "k_mv_q8s<1, 1, 2, 8, 8>",
+                   "matvec_gate_up_swiglu": "k_mv_q8w<2, 2, 8, 14, 2, true>",
+                   "matvec_down_residual": "k_mv_q8s<1, 1, 2, 8, 8>",
                    "matvec_head_argmax": "k_mv_q8h<8, 14>"}
 PMC_CMD = ("COHX_GRAPHS=0 rocprofv3 --pmc {counter} --kernel-include-regex \"k_attn|k_mv\" --output-format csv "
            "-d <dir> -o <name> -- python3 bench.py --steps 2 --warmup 1 --secondary-lanes 0 "
