@@ -2124,7 +2124,9 @@ __global__ __launch_bounds__(256) void k_attn_scores(StepDims d, const float *__
   constexpr int kHL = kG - (kS - 1) * kH > 0 ? kG - (kS - 1) * kH : 1;  // heads of the last part
   constexpr int kE = kD == 64 ? (kH > 4 ? 4 : 2) : 1;                  // elements per group (VGPR budget)
   const int r = d.row_map ? (int)d.row_map[blockIdx.x] : (int)blockIdx.x;
-  const int g = blockIdx.y, part = blockIdx.z % kS, c = blockIdx.z / kS;
+  // chunks in reverse launch order: the high chunks only the longest rows
+  // have are dispatched first, the dense low chunks fill in behind them
+  const int g = blockIdx.y, part = blockIdx.z % kS, c = (int)(gridDim.z / kS) - 1 - (int)(blockIdx.z / kS);
   const int kv = (int)row_pos[r] + 1;
   const int t0 = c * kT;
   if (t0 >= kv) return;
@@ -2248,7 +2250,7 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
   static_assert(kChunk * 2 == 256, "one float4 of weights per thread");
   static_assert(kG <= 8, "a wave sums the denominators of at most two heads");
   const int r = d.row_map ? (int)d.row_map[blockIdx.x] : (int)blockIdx.x;
-  const int g = blockIdx.y, c = blockIdx.z;
+  const int g = blockIdx.y, c = (int)gridDim.z - 1 - (int)blockIdx.z;  // high chunks first, as in the scores pass
   const int kv = (int)row_pos[r] + 1, t0 = c * kChunk;
   if (t0 >= kv) return;
   __shared__ double red[3][kG][kD];
