@@ -733,6 +733,25 @@ def valu_probe():
     print(json.dumps({"valu_probe": out}), flush=True)
 
 
+def read_probe():
+    """The HBM read rate this device reaches with a plain streaming kernel
+    (libcohx_probe.so): 1 GiB and 4 GiB buffers (past the 256 MB last-level
+    cache) read with float4 loads by grids of 1024 to 8192 workgroups."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "coheryn-ai-studio_amd", "libcohx_probe.so"))
+    lib.cohx_probe_read.argtypes = [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_float)]
+    out = []
+    for mib in (1024, 4096):
+        for blocks in (1024, 2048, 4096, 8192):
+            ms = ctypes.c_float()
+            rc = lib.cohx_probe_read(mib, blocks, 10, ctypes.byref(ms))
+            if rc:
+                raise RuntimeError(f"probe failed ({rc})")
+            out.append({"mib": mib, "workgroups": blocks, "ms": ms.value,
+                        "read_TBps": (mib << 20) / (ms.value * 1e-3) / 1e12})
+    print(json.dumps({"read_probe": out, "best_read_TBps": max(o["read_TBps"] for o in out)}), flush=True)
+
+
 C5_SEQS, C5_PROMPT, C5_GEN, C5_CHUNK = 16, (64, 1024), 64, 256
 
 
@@ -895,6 +914,8 @@ def main():
                     help="only time a graph of one-element kernels (the cost of a kernel boundary)")
     ap.add_argument("--valu-probe", action="store_true",
                     help="only time the attention pass's f32-product / f64-chain pattern without memory")
+    ap.add_argument("--read-probe", action="store_true",
+                    help="only time a plain streaming read of 1 and 4 GiB (the reachable HBM read rate)")
     ap.add_argument("--summarize-counters", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
                     help="write the traffic summary from rocprofv3 --pmc csv files (no GPU)")
     ap.add_argument("--summarize-c5-trace", nargs="+", metavar="ARG",
@@ -914,6 +935,9 @@ def main():
         return
     if args.valu_probe:
         valu_probe()
+        return
+    if args.read_probe:
+        read_probe()
         return
     if args.summarize_counters:
         summarize_counters(*args.summarize_counters, lanes=args.lanes)

@@ -1,8 +1,8 @@
-// Instruction-rate probes for bench.py --valu-probe (built as libcohx_probe.so,
-// not part of the step library): the exact attention pass's instruction
-// pattern without memory traffic, to separate its VALU cost from its K/V
-// stream.  Every launch here is in bounds by construction: each thread reads
-// a fixed 256-float table and writes one double of its own.
+// Probes for bench.py --valu-probe and --read-probe (built as
+// libcohx_probe.so, not part of the step library): the exact attention
+// pass's instruction pattern without memory traffic, to separate its VALU
+// cost from its K/V stream, and a plain streaming read, for the HBM rate this
+// device reaches.  Every launch here is in bounds by construction.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -66,7 +66,51 @@ int time_triples(int blocks, int steps, float *ms_out) {
   return hipGetLastError() != hipSuccess;
 }
 
+// Streaming read: thread t of the grid sums float4s i = t, t + stride, ...
+// below n and writes its sum (so no load is dead); every index is in bounds.
+__global__ __launch_bounds__(256) void k_probe_read(const float4 *__restrict__ src, size_t n,
+                                                    float *__restrict__ out) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  float acc = 0.0f;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+    const float4 v = src[i];
+    acc += (v.x + v.y) + (v.z + v.w);
+  }
+  out[(size_t)blockIdx.x * 256 + threadIdx.x] = acc;
+}
+
 }  // namespace
+
+// Read bandwidth: `mib` MiB streamed `reps` times by a grid of `blocks`
+// workgroups (after one untimed pass); returns 0 and the mean ms per pass.
+extern "C" int cohx_probe_read(int mib, int blocks, int reps, float *ms) {
+  if (!ms || mib <= 0 || mib > 8192 || blocks <= 0 || blocks > 65536 || reps <= 0 || reps > 1000) return 2;
+  const size_t bytes = (size_t)mib << 20, n = bytes / 16;
+  float4 *src = nullptr;
+  float *out = nullptr;
+  if (hipMalloc(&src, bytes) != hipSuccess) return 1;
+  if (hipMalloc(&out, (size_t)blocks * 256 * sizeof(float)) != hipSuccess) {
+    (void)hipFree(src);
+    return 1;
+  }
+  (void)hipMemset(src, 0, bytes);
+  hipEvent_t a, b;
+  (void)hipEventCreate(&a);
+  (void)hipEventCreate(&b);
+  hipLaunchKernelGGL(k_probe_read, dim3(blocks), dim3(256), 0, 0, src, n, out);
+  (void)hipEventRecord(a, 0);
+  for (int r = 0; r < reps; r++) hipLaunchKernelGGL(k_probe_read, dim3(blocks), dim3(256), 0, 0, src, n, out);
+  (void)hipEventRecord(b, 0);
+  (void)hipEventSynchronize(b);
+  float total = 0.0f;
+  (void)hipEventElapsedTime(&total, a, b);
+  *ms = total / reps;
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  (void)hipFree(src);
+  (void)hipFree(out);
+  return hipGetLastError() != hipSuccess;
+}
 
 // Time `blocks` workgroups of 256 threads, each thread running `steps`
 // steps of E elements x C chains; returns 0 and the kernel time in ms.
