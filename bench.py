@@ -752,6 +752,30 @@ def read_probe():
     print(json.dumps({"read_probe": out, "best_read_TBps": max(o["read_TBps"] for o in out)}), flush=True)
 
 
+def kstream_probe():
+    """The scores pass's K-row access pattern without its arithmetic
+    (libcohx_probe.so, k_probe_kstream): 128 rows, KV U[64,2048], pages
+    scattered over an owned pool, 24 layer pools read in turn (past the 256 MB
+    last-level cache, as in a step).  Mode 0 launches one workgroup per (row,
+    head, 256-token chunk) as the pass does, mode 1 loads every chunk twice
+    (the pass's two head parts), mode 3 loads it twice within one 512-thread
+    workgroup, mode 2 walks the items with a fixed number of persistent
+    workgroups."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "coheryn-ai-studio_amd", "libcohx_probe.so"))
+    lib.cohx_probe_kstream.argtypes = [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_float),
+                                                            ctypes.POINTER(ctypes.c_double)]
+    out = []
+    for mode, blocks in ((0, 1), (1, 1), (3, 1), (2, 512), (2, 1024)):
+        ms, nbytes = ctypes.c_float(), ctypes.c_double()
+        rc = lib.cohx_probe_kstream(mode, blocks, 48, ctypes.byref(ms), ctypes.byref(nbytes))
+        if rc:
+            raise RuntimeError(f"probe failed ({rc})")
+        out.append({"mode": mode, "workgroups": blocks if mode == 2 else None, "us": ms.value * 1e3,
+                    "k_bytes": nbytes.value, "TBps": nbytes.value / (ms.value * 1e-3) / 1e12})
+    print(json.dumps({"kstream_probe": out}), flush=True)
+
+
 C5_SEQS, C5_PROMPT, C5_GEN, C5_CHUNK = 16, (64, 1024), 64, 256
 
 
@@ -914,6 +938,8 @@ def main():
                     help="only time a graph of one-element kernels (the cost of a kernel boundary)")
     ap.add_argument("--valu-probe", action="store_true",
                     help="only time the attention pass's f32-product / f64-chain pattern without memory")
+    ap.add_argument("--kstream-probe", action="store_true",
+                    help="only time the scores pass's K access pattern without arithmetic")
     ap.add_argument("--read-probe", action="store_true",
                     help="only time a plain streaming read of 1 and 4 GiB (the reachable HBM read rate)")
     ap.add_argument("--summarize-counters", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
@@ -938,6 +964,9 @@ def main():
         return
     if args.read_probe:
         read_probe()
+        return
+    if args.kstream_probe:
+        kstream_probe()
         return
     if args.summarize_counters:
         summarize_counters(*args.summarize_counters, lanes=args.lanes)
