@@ -339,7 +339,7 @@ def run_c3(seed, steps, warmup):
                         "rows over KV U[256,4096]; linears on the matrix cores (f32 sums)",
             "value": rows / elapsed, "unit": "packed rows/s", "ms_per_step": ms, "steps": steps,
             "mean_rows_per_step": rows / steps,
-            "roofline": {"bound": "mfma", "kernel": "linears (k_gemm_f16)",
+            "roofline": {"bound": "mfma", "kernel": "linears (hipBLASLt GEMMs in steps with prompt rows)",
                          "achieved": tflops, "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
                          "frac": tflops * 1e12 / MFMA_F16_PEAK},
             "attention_chunk": chunk_roofline(stats, steps),
@@ -752,6 +752,42 @@ def read_probe():
     print(json.dumps({"read_probe": out, "best_read_TBps": max(o["read_TBps"] for o in out)}), flush=True)
 
 
+def mfma_probe():
+    """The f16 matrix-core rate (libcohx_probe.so, k_probe_mfma): workgroups of
+    4 waves, each wave 8 independent 16x16x32 MFMA chains on registers."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "coheryn-ai-studio_amd", "libcohx_probe.so"))
+    lib.cohx_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_float)]
+    out = []
+    for blocks in (1024, 2048, 4096):
+        ms = ctypes.c_float()
+        if lib.cohx_probe_mfma(blocks, 256, ctypes.byref(ms)):
+            raise RuntimeError("probe failed")
+        flops = blocks * 4 * 8 * 256 * 16384
+        out.append({"workgroups": blocks, "ms": ms.value, "TFLOPs": flops / (ms.value * 1e-3) / 1e12})
+    print(json.dumps({"mfma_probe": out}), flush=True)
+
+
+def measured_peaks():
+    """The rates this device reaches, measured in the same run (libcohx_probe.so):
+    a plain streaming read of 1 GiB (`--read-probe`) and back-to-back f16
+    MFMAs (`--mfma-probe`); None when the probe library is absent."""
+    import ctypes
+    try:
+        lib = ctypes.CDLL(os.path.join(ROOT, "coheryn-ai-studio_amd", "libcohx_probe.so"))
+    except OSError:
+        return None
+    lib.cohx_probe_read.argtypes = [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_float)]
+    lib.cohx_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_float)]
+    rd, mf = ctypes.c_float(), ctypes.c_float()
+    if lib.cohx_probe_read(1024, 1024, 5, ctypes.byref(rd)) or lib.cohx_probe_mfma(2048, 256, ctypes.byref(mf)):
+        return None
+    return {"hbm_read_GBps": (1 << 30) / (rd.value * 1e-3) / 1e9,
+            "mfma_f16_TFLOPs": 2048 * 4 * 8 * 256 * 16384 / (mf.value * 1e-3) / 1e12,
+            "note": "streaming read of 1 GiB (float4 loads, 1024 workgroups) and back-to-back "
+                    "v_mfma_f32_16x16x32_f16 (2048 workgroups); the roofline fractions use the published peaks"}
+
+
 def kstream_probe():
     """The scores pass's K-row access pattern without its arithmetic
     (libcohx_probe.so, k_probe_kstream): 128 rows, KV U[64,2048], pages
@@ -938,6 +974,8 @@ def main():
                     help="only time a graph of one-element kernels (the cost of a kernel boundary)")
     ap.add_argument("--valu-probe", action="store_true",
                     help="only time the attention pass's f32-product / f64-chain pattern without memory")
+    ap.add_argument("--mfma-probe", action="store_true",
+                    help="only time back-to-back f16 MFMAs (the reachable matrix-core rate)")
     ap.add_argument("--kstream-probe", action="store_true",
                     help="only time the scores pass's K access pattern without arithmetic")
     ap.add_argument("--read-probe", action="store_true",
@@ -967,6 +1005,9 @@ def main():
         return
     if args.kstream_probe:
         kstream_probe()
+        return
+    if args.mfma_probe:
+        mfma_probe()
         return
     if args.summarize_counters:
         summarize_counters(*args.summarize_counters, lanes=args.lanes)
@@ -1044,6 +1085,10 @@ def main():
         "ms_per_step": sec["ms_per_step"],
         "step_frac": sec["step_bytes"] / (sec["ms_per_step"] / 1e3) / HBM_PEAK,
         "roofline": roofline(sec["stats"], args.secondary_lanes)}
+    peaks = measured_peaks()
+    line["measured_peaks"] = peaks
+    if peaks:
+        line["roofline"]["frac_of_measured_read"] = line["roofline"]["achieved"] / peaks["hbm_read_GBps"]
     if not args.no_c4:
         del model
         line["c4"] = run_c4(args.seed, 128, args.warmup)
@@ -1054,6 +1099,9 @@ def main():
         del c4c
     if not args.no_c3:
         line["c3"] = run_c3(args.seed, 8, 2)
+        if peaks:
+            line["c3"]["roofline"]["frac_of_measured_mfma"] = (line["c3"]["roofline"]["achieved"] /
+                                                               peaks["mfma_f16_TFLOPs"])
         c3c = line["c3"].pop("_cpu")
         if not args.no_cpu_baseline:
             log(f"[bench] c3 cpu baseline: oracle, {threads} threads")

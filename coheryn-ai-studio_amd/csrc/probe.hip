@@ -140,7 +140,56 @@ __global__ __launch_bounds__(256) void k_probe_kstream_walk(const float *__restr
   }
 }
 
+typedef _Float16 probe_half8 __attribute__((ext_vector_type(8)));
+typedef float probe_float4 __attribute__((ext_vector_type(4)));
+
+// Matrix-core rate: each wave runs kAcc independent v_mfma_f32_16x16x32_f16
+// accumulation chains for `iters` steps on register operands, then writes one
+// float per lane (so nothing is dead).
+template <int kAcc>
+__global__ __launch_bounds__(256) void k_probe_mfma(int iters, float *__restrict__ out) {
+  probe_half8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    a[i] = (_Float16)(0.001f * (threadIdx.x % 7 + i));
+    b[i] = (_Float16)(0.002f * (threadIdx.x % 5 + i));
+  }
+  probe_float4 acc[kAcc];
+#pragma unroll
+  for (int k = 0; k < kAcc; k++) acc[k] = probe_float4{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < iters; it++) {
+#pragma unroll
+    for (int k = 0; k < kAcc; k++) acc[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[k], 0, 0, 0);
+  }
+  float t = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kAcc; k++) t += acc[k][0] + acc[k][1] + acc[k][2] + acc[k][3];
+  out[(size_t)blockIdx.x * 256 + threadIdx.x] = t;
+}
+
 }  // namespace
+
+// Matrix-core rate: `blocks` workgroups of 4 waves, each wave 8 chains of
+// `iters` 16x16x32 f16 MFMAs (16,384 flops each); returns 0 and the kernel's
+// ms (one untimed launch first).
+extern "C" int cohx_probe_mfma(int blocks, int iters, float *ms) {
+  if (!ms || blocks <= 0 || blocks > 65536 || iters <= 0 || iters > 1 << 20) return 2;
+  float *out = nullptr;
+  if (hipMalloc(&out, (size_t)blocks * 256 * sizeof(float)) != hipSuccess) return 1;
+  hipEvent_t a, b;
+  (void)hipEventCreate(&a);
+  (void)hipEventCreate(&b);
+  hipLaunchKernelGGL(k_probe_mfma<8>, dim3(blocks), dim3(256), 0, 0, iters, out);
+  (void)hipEventRecord(a, 0);
+  hipLaunchKernelGGL(k_probe_mfma<8>, dim3(blocks), dim3(256), 0, 0, iters, out);
+  (void)hipEventRecord(b, 0);
+  (void)hipEventSynchronize(b);
+  (void)hipEventElapsedTime(ms, a, b);
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  (void)hipFree(out);
+  return hipGetLastError() != hipSuccess;
+}
 
 // K-stream probe (see k_probe_kstream), over 24 layer pools in turn: mode 0
 // one workgroup per item, mode 1
