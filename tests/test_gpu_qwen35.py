@@ -163,6 +163,33 @@ def test_tiny_large_packed_step_bit_exact():
     _large_packed_tiny(False)
 
 
+def test_tiny_large_packed_step_without_library_stays_exact(monkeypatch):
+    print("case: tiny Qwen3.5, 141 packed rows with the regime asked for but the library GEMMs off "
+          "(COHX_GEMM_LIB=0): the exact matvecs, bit for bit", flush=True)
+    monkeypatch.setenv("COHX_GEMM_LIB", "0")
+    cfg, t = synth35.in_memory(tiny(), seed=12)
+    p = Pair(cfg, t, max_lanes=4, max_rows=160, max_context=160)
+    p.gpu.close()
+    old = os.environ.get("COHX_PREFILL_MFMA")
+    os.environ["COHX_PREFILL_MFMA"] = "1"
+    try:
+        p.gpu = cohx.Qwen35(cfg, t, max_lanes=4, max_rows=160, max_context=160)
+    finally:
+        if old is None:
+            del os.environ["COHX_PREFILL_MFMA"]
+        else:
+            os.environ["COHX_PREFILL_MFMA"] = old
+    a, b, c = p.alloc(), p.alloc(), p.alloc()
+    rng = np.random.default_rng(13)
+    pa = [int(v) for v in rng.integers(0, cfg["vocabulary"], 100)]
+    pb = [int(v) for v in rng.integers(0, cfg["vocabulary"], 40)]
+    (tc,) = p.step([(c, [5, 6])])
+    ta, tb, tc = p.step([(a, pa), (b, pb), (c, [tc])])
+    p.step([(a, [ta]), (b, [tb]), (c, [tc])])
+    for s_ in (a, b, c):
+        p.check_state(s_)
+
+
 def test_tiny_large_packed_step_prefill_regime_within_tolerance():
     print("case: tiny Qwen3.5, 141 packed rows through the packed-prefill regime (library "
           "BF16 GEMMs on hi/lo activations)", flush=True)
