@@ -204,8 +204,9 @@ __global__ __launch_bounds__(256) void k_q35_mv(const uint16_t *__restrict__ w, 
 // waves.  The tile's weights and the rows' activations pass through LDS in
 // chunks of kChunk inputs, double buffered: each thread holds its share of
 // the next chunk in registers while the current chunk is summed, so a whole
-// chunk of work covers the memory latency.  The k order of each chain is the
-// reference's.
+// chunk of work covers the memory latency.  The weights are widened to f32
+// once, when stored to LDS, rather than by each of the 16 lanes that use
+// them.  The k order of each chain is the reference's.
 template <int kEpi, int kChunk, int kWaves>
 __global__ __launch_bounds__(kWaves * 64) void k_q35_mvd(
     const uint16_t *__restrict__ w, int valid_rows, int K, const float *__restrict__ x, int ldx,
@@ -216,7 +217,7 @@ __global__ __launch_bounds__(kWaves * 64) void k_q35_mvd(
   constexpr int kW4 = kChunk / 8 * 16;        // uint4 words of a weight chunk
   constexpr int kX4 = kRows * kChunk / 4;     // float4 words of an activation chunk
   static_assert(kW4 % kT == 0 && kX4 % kT == 0, "chunk must split evenly over the threads");
-  __shared__ __align__(16) uint4 ws[2][kW4];
+  __shared__ __align__(16) float4 ws[2][2 * kW4];  // f32 weights [k8][half][output]
   __shared__ __align__(16) float xs[2][kRows * kXld];
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int o16 = lane % 16, tile = blockIdx.x, r0 = blockIdx.y * kRows;
@@ -245,7 +246,12 @@ __global__ __launch_bounds__(kWaves * 64) void k_q35_mvd(
   };
   auto stash = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < kW4 / kT; i++) ws[buf][tid + kT * i] = wr[i];
+    for (int i = 0; i < kW4 / kT; i++) {
+      const int idx = tid + kT * i, k8 = idx / 16, oo = idx % 16;
+      const uint4 v = wr[i];
+      ws[buf][(2 * k8) * 16 + oo] = make_float4(bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y));
+      ws[buf][(2 * k8 + 1) * 16 + oo] = make_float4(bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w));
+    }
 #pragma unroll
     for (int i = 0; i < kX4 / kT; i++) {
       const int idx = tid + kT * i, row = idx / (kChunk / 4), c = (idx % (kChunk / 4)) * 4;
@@ -261,20 +267,20 @@ __global__ __launch_bounds__(kWaves * 64) void k_q35_mvd(
     const bool more = k0 + kChunk < K;
     if (more) fetch(k0 + kChunk);
     const int n8 = min(kChunk, K - k0) / 8;
-    const uint4 *wl = ws[buf] + o16;
+    const float4 *wl = ws[buf] + o16;
     const float *xl = xs[buf] + br * kXld;
     for (int k8 = 0; k8 < n8; k8++) {
-      const uint4 v = wl[k8 * 16];
+      const float4 a = wl[(2 * k8) * 16], b = wl[(2 * k8 + 1) * 16];
       const float4 p = *reinterpret_cast<const float4 *>(xl + k8 * 8);
       const float4 q = *reinterpret_cast<const float4 *>(xl + k8 * 8 + 4);
-      acc += (double)(bf_lo(v.x) * p.x);
-      acc += (double)(bf_hi(v.x) * p.y);
-      acc += (double)(bf_lo(v.y) * p.z);
-      acc += (double)(bf_hi(v.y) * p.w);
-      acc += (double)(bf_lo(v.z) * q.x);
-      acc += (double)(bf_hi(v.z) * q.y);
-      acc += (double)(bf_lo(v.w) * q.z);
-      acc += (double)(bf_hi(v.w) * q.w);
+      acc += (double)(a.x * p.x);
+      acc += (double)(a.y * p.y);
+      acc += (double)(a.z * p.z);
+      acc += (double)(a.w * p.w);
+      acc += (double)(b.x * q.x);
+      acc += (double)(b.y * q.y);
+      acc += (double)(b.z * q.z);
+      acc += (double)(b.w * q.w);
     }
     if (more) stash(buf ^ 1);
     __syncthreads();
