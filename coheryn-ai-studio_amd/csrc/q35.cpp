@@ -655,9 +655,13 @@ int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out, const c
         return lrc;
     }
     q35_norm(s, (int)R, q->x, H, nullptr, Ly.post_norm, H, eps, 1, q->nrm, H, q->row_err, nullptr);
-    if ((lrc = linear(kQ35Store, Ly.gu, Ly.gu_rm, q->gu_rows, q->gu_rows, H, q->nrm, H, q->gu_out, q->gu_rows)))
-      return lrc;
-    q35_swiglu(s, (int)R, q->gu_out, q->gu_rows, q->F, q->gu_up, q->hb, q->F);
+    if (regime || !q35_matvec_swiglu(s, Ly.gu, q->gu_up, q->F, H, q->nrm, H, (int)R, q->hb, q->F,
+                                     q->row_err)) {
+      if ((lrc = linear(kQ35Store, Ly.gu, Ly.gu_rm, q->gu_rows, q->gu_rows, H, q->nrm, H, q->gu_out,
+                        q->gu_rows)))
+        return lrc;
+      q35_swiglu(s, (int)R, q->gu_out, q->gu_rows, q->F, q->gu_up, q->hb, q->F);
+    }
     if ((lrc = linear(kQ35Residual, Ly.down, Ly.down_rm, q->h_rows, H, q->F, q->hb, q->F, q->x, H)))
       return lrc;
   }

@@ -39,7 +39,7 @@ inline size_t q35_tiled_index(size_t row, size_t k, size_t K) {
   return (((row / 16) * (K / 8) + k / 8) * 16 + row % 16) * 8 + k % 8;
 }
 
-enum Q35Epi { kQ35Store = 0, kQ35Residual = 1, kQ35Argmax = 2 };
+enum Q35Epi { kQ35Store = 0, kQ35Residual = 1, kQ35Argmax = 2, kQ35Swiglu = 3 };
 
 void q35_embed(hipStream_t s, int rows, const uint16_t *embed, const uint32_t *tokens, int H,
                float *x);
@@ -60,6 +60,13 @@ void q35_split_bf16(hipStream_t s, int rows, int K, const float *x, int ldx, uin
 // row_err[r] |= the matvecs' non-finite bit for rows of out[rows][N] (stride
 // ldo, N % 4 == 0) holding a non-finite value.
 void q35_check_finite(hipStream_t s, int rows, int N, const float *out, int ldo, uint32_t *row_err);
+// Gate+up and SwiGLU in one launch for few rows: h[r][f] = silu(gate) * up
+// with the bits of q35_matvec (gate rows [0, F), up rows [up_off, up_off + F))
+// followed by q35_swiglu.  Returns false (nothing launched) where q35_matvec
+// would not take its one-chain-per-lane form (more than 64 rows, or few
+// enough tiles for the producer/consumer form).
+bool q35_matvec_swiglu(hipStream_t s, const uint16_t *w, int up_off, int F, int K, const float *x,
+                       int ldx, int R, float *h, int ldh, uint32_t *row_err);
 void q35_swiglu(hipStream_t s, int rows, const float *gu, int ldgu, int F, int up_off, float *h,
                 int ldh);
 void q35_conv(hipStream_t s, int lanes, Q35Lanes L, const float *mix, int ldm, const float *w,

@@ -207,34 +207,44 @@ __global__ __launch_bounds__(256) void k_q35_mv(const uint16_t *__restrict__ w, 
 // chunk of work covers the memory latency.  The weights are widened to f32
 // once, when stored to LDS, rather than by each of the 16 lanes that use
 // them.  The k order of each chain is the reference's.
+// kEpi == kQ35Swiglu: eight waves over the same 16 rows, waves 0-3 on gate
+// tile blockIdx.x and waves 4-7 on up tile blockIdx.x + up_off / 16 (up_off
+// passed in valid_rows, F in ldo's place as the output count); the up waves
+// hand their sums to the gate waves through LDS, which write
+// h = (g / (1 + exp(-g))) * u (the SwiGLU pass's expression) to out [R][F].
 template <int kEpi, int kChunk, int kWaves>
 __global__ __launch_bounds__(kWaves * 64) void k_q35_mvd(
     const uint16_t *__restrict__ w, int valid_rows, int K, const float *__restrict__ x, int ldx,
     int R, float *out, int ldo, unsigned long long *__restrict__ part, uint32_t *row_err,
     const uint32_t *__restrict__ err_row) {
-  constexpr int kT = kWaves * 64, kRows = 4 * kWaves;
+  constexpr bool kGlu = kEpi == kQ35Swiglu;
+  constexpr int kTiles = kGlu ? 2 : 1;          // weight tiles per workgroup
+  constexpr int kT = kWaves * 64, kRows = 4 * kWaves / kTiles;
   constexpr int kXld = kChunk + 4;            // padded LDS row (floats)
-  constexpr int kW4 = kChunk / 8 * 16;        // uint4 words of a weight chunk
+  constexpr int kW4 = kChunk / 8 * 16;        // uint4 words of one tile's weight chunk
   constexpr int kX4 = kRows * kChunk / 4;     // float4 words of an activation chunk
-  static_assert(kW4 % kT == 0 && kX4 % kT == 0, "chunk must split evenly over the threads");
-  __shared__ __align__(16) float4 ws[2][2 * kW4];  // f32 weights [k8][half][output]
+  static_assert((kTiles * kW4) % kT == 0 && kX4 % kT == 0, "chunk must split evenly over the threads");
+  __shared__ __align__(16) float4 ws[2][kTiles * 2 * kW4];  // f32 weights [tile][k8][half][output]
   __shared__ __align__(16) float xs[2][kRows * kXld];
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int sel = wave / (kWaves / kTiles), wv = wave % (kWaves / kTiles);
   const int o16 = lane % 16, tile = blockIdx.x, r0 = blockIdx.y * kRows;
-  const int br = wave * 4 + lane / 16, r = r0 + br;
+  const int br = wv * 4 + lane / 16, r = r0 + br;
   const int o = tile * 16 + o16;
   const bool live = r < R;
   const int nk8 = K / 8;
   const uint4 *wt = reinterpret_cast<const uint4 *>(w) + (size_t)tile * nk8 * 16;
-  uint4 wr[kW4 / kT];
+  const uint4 *wt_up = reinterpret_cast<const uint4 *>(w) + (size_t)(tile + (kGlu ? valid_rows / 16 : 0)) * nk8 * 16;
+  uint4 wr[kTiles * kW4 / kT];
   float4 xr[kX4 / kT];
   auto fetch = [&](int k0) {
     const int kc = min(kChunk, K - k0);
     const int n4 = kc / 8 * 16;  // weight words in this chunk
 #pragma unroll
-    for (int i = 0; i < kW4 / kT; i++) {
-      const int idx = tid + kT * i;
-      wr[i] = idx < n4 ? wt[(size_t)k0 / 8 * 16 + idx] : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < kTiles * kW4 / kT; i++) {
+      const int idx = (tid + kT * i) % kW4;
+      const uint4 *src = (tid + kT * i) < kW4 ? wt : wt_up;
+      wr[i] = idx < n4 ? src[(size_t)k0 / 8 * 16 + idx] : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < kX4 / kT; i++) {
@@ -246,11 +256,12 @@ __global__ __launch_bounds__(kWaves * 64) void k_q35_mvd(
   };
   auto stash = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < kW4 / kT; i++) {
-      const int idx = tid + kT * i, k8 = idx / 16, oo = idx % 16;
+    for (int i = 0; i < kTiles * kW4 / kT; i++) {
+      const int idx = tid + kT * i, t2 = idx / kW4, k8 = idx % kW4 / 16, oo = idx % 16;
       const uint4 v = wr[i];
-      ws[buf][(2 * k8) * 16 + oo] = make_float4(bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y));
-      ws[buf][(2 * k8 + 1) * 16 + oo] = make_float4(bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w));
+      float4 *dst = ws[buf] + t2 * 2 * kW4;
+      dst[(2 * k8) * 16 + oo] = make_float4(bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y));
+      dst[(2 * k8 + 1) * 16 + oo] = make_float4(bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w));
     }
 #pragma unroll
     for (int i = 0; i < kX4 / kT; i++) {
@@ -267,7 +278,7 @@ __global__ __launch_bounds__(kWaves * 64) void k_q35_mvd(
     const bool more = k0 + kChunk < K;
     if (more) fetch(k0 + kChunk);
     const int n8 = min(kChunk, K - k0) / 8;
-    const float4 *wl = ws[buf] + o16;
+    const float4 *wl = ws[buf] + sel * 2 * kW4 + o16;
     const float *xl = xs[buf] + br * kXld;
     for (int k8 = 0; k8 < n8; k8++) {
       const float4 a = wl[(2 * k8) * 16], b = wl[(2 * k8 + 1) * 16];
@@ -287,6 +298,18 @@ __global__ __launch_bounds__(kWaves * 64) void k_q35_mvd(
     buf ^= 1;
   }
   const float v = (float)acc;
+  if constexpr (kGlu) {
+    __shared__ float s_up[kRows][16];
+    const bool ok = live && o < ldo;  // ldo: the output count F
+    if (sel == 1) s_up[br][o16] = v;
+    __syncthreads();
+    if (sel == 0 && ok) {
+      const float u = s_up[br][o16];
+      out[(size_t)r * ldo + o] = (v / (1.0f + exp_f32(-v))) * u;
+    }
+    if (ok && !finitef(v)) atomicOr(&row_err[r], kErrNonFinite);
+    return;
+  }
   const bool ok = live && o < valid_rows;
   if (kEpi == kQ35Argmax) {
     unsigned long long key = ok ? argmax_key(v, o) : 0ull;
@@ -1188,6 +1211,17 @@ void q35_split_bf16(hipStream_t s, int rows, int K, const float *x, int ldx, uin
 
 void q35_check_finite(hipStream_t s, int rows, int N, const float *out, int ldo, uint32_t *row_err) {
   hipLaunchKernelGGL(k_q35_finite, dim3(rows), dim3(256), 0, s, out, ldo, N, row_err);
+}
+
+bool q35_matvec_swiglu(hipStream_t s, const uint16_t *w, int up_off, int F, int K, const float *x,
+                       int ldx, int R, float *h, int ldh, uint32_t *row_err) {
+  const int tiles = 2 * up_off / 16;  // gate and up tiles, as q35_matvec sees the matrix
+  if (R > kMvdMaxRows || up_off % 16 || K % 8 || ldh != F ||
+      (K % 16 == 0 && tiles * ((R + 3) / 4) <= 512))
+    return false;
+  hipLaunchKernelGGL((k_q35_mvd<kQ35Swiglu, 128, 8>), dim3(up_off / 16, (R + 15) / 16), dim3(512), 0,
+                     s, w, up_off, K, x, ldx, R, h, F, nullptr, row_err, nullptr);
+  return true;
 }
 
 void q35_swiglu(hipStream_t s, int rows, const float *gu, int ldgu, int F, int up_off, float *h,
