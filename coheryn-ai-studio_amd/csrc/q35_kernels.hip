@@ -580,7 +580,7 @@ __global__ __launch_bounds__(256) void k_q35_delta(Q35Lanes L, const float *__re
                                                    int VH, int VD, float *state, size_t state_seq,
                                                    float *__restrict__ o_out, int ldo,
                                                    uint32_t *row_err) {
-  __shared__ float s_qq[kKD], s_kk[kKD];
+  __shared__ __align__(16) float s_qq[kKD], s_kk[kKD];
   const int ln = blockIdx.x, h = blockIdx.y, j = threadIdx.x;
   const uint32_t first = L.first[ln], n = L.n[ln];
   const int src = (h / (VH / KH)) * kKD;
@@ -596,27 +596,52 @@ __global__ __launch_bounds__(256) void k_q35_delta(Q35Lanes L, const float *__re
   for (int i = 0; i < kKD; i++)
     col[i] = active ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff, i * VD * 4, 0))
                     : 0.0f;
+  // token t + 1's gates, q/k channel j and v channel j are requested while
+  // token t's chains run (the launcher gives at least kKD threads)
+  float4 gt_n = make_float4(0.f, 0.f, 0.f, 0.f);
+  float q_n = 0.0f, k_n = 0.0f, v_n = 0.0f;
+  auto fetch = [&](uint32_t t) {
+    const float *cr = conv + (size_t)(first + t) * ldc;
+    gt_n = gates[(size_t)(first + t) * VH + h];
+    if (j < kKD) {
+      q_n = cr[src + j];
+      k_n = cr[keys + src + j];
+    }
+    if (active) v_n = cr[2 * keys + h * VD + j];
+  };
+  if (n) fetch(0);
   for (uint32_t t = 0; t < n; t++) {
     const uint32_t row = first + t;
-    const float *cr = conv + (size_t)row * ldc;
-    const float4 gt = gates[(size_t)row * VH + h];
+    const float4 gt = gt_n;
+    const float qc = q_n, kc = k_n, v = v_n;
     __syncthreads();
-    for (int i = j; i < kKD; i += blockDim.x) {
-      s_qq[i] = cr[src + i] * gt.x;
-      s_kk[i] = cr[keys + src + i] * gt.y;
+    if (j < kKD) {
+      s_qq[j] = qc * gt.x;
+      s_kk[j] = kc * gt.y;
     }
+    if (t + 1 < n) fetch(t + 1);
     __syncthreads();
     if (!active) continue;
-    const float decay = gt.z, beta = gt.w, v = cr[2 * keys + h * VD + j];
+    const float decay = gt.z, beta = gt.w;
+    // the keys' LDS values are requested two groups of 4 ahead of their use,
+    // so the chains do not wait on LDS at every group
+    const float4 *kk4 = reinterpret_cast<const float4 *>(s_kk);
+    const float4 *qq4 = reinterpret_cast<const float4 *>(s_qq);
+    constexpr int kG4 = kKD / 4;
     double pred = 0.0;
+    float4 ka = kk4[0], kb = kG4 > 1 ? kk4[1] : ka;
 #pragma unroll
     for (int i0 = 0; i0 < kKD; i0 += 4) {
       asm volatile("" ::: "memory");
+      const float4 kq = ka;
+      ka = kb;
+      if (i0 / 4 + 2 < kG4) kb = kk4[i0 / 4 + 2];
+      const float kv[4] = {kq.x, kq.y, kq.z, kq.w};
       float p[4];
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         col[i0 + e] *= decay;
-        p[e] = col[i0 + e] * s_kk[i0 + e];
+        p[e] = col[i0 + e] * kv[e];
       }
       pin_vgprs(p);
       double wd[4];
@@ -628,14 +653,25 @@ __global__ __launch_bounds__(256) void k_q35_delta(Q35Lanes L, const float *__re
     }
     const float corr = (v - (float)pred) * beta;
     double rd = 0.0;
+    ka = kk4[0];
+    kb = kG4 > 1 ? kk4[1] : ka;
+    float4 qa = qq4[0], qb = kG4 > 1 ? qq4[1] : qa;
 #pragma unroll
     for (int i0 = 0; i0 < kKD; i0 += 4) {
       asm volatile("" ::: "memory");
+      const float4 kq = ka, qv4 = qa;
+      ka = kb;
+      qa = qb;
+      if (i0 / 4 + 2 < kG4) {
+        kb = kk4[i0 / 4 + 2];
+        qb = qq4[i0 / 4 + 2];
+      }
+      const float kv[4] = {kq.x, kq.y, kq.z, kq.w}, qv[4] = {qv4.x, qv4.y, qv4.z, qv4.w};
       float p[4];
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        col[i0 + e] += s_kk[i0 + e] * corr;
-        p[e] = col[i0 + e] * s_qq[i0 + e];
+        col[i0 + e] += kv[e] * corr;
+        p[e] = col[i0 + e] * qv[e];
       }
       pin_vgprs(p);
       double wd[4];
@@ -1272,7 +1308,9 @@ void q35_delta(hipStream_t s, int rows, int lanes, Q35Lanes L, const float *conv
                float *o_raw, float *tgt, int ldt, uint32_t *row_err) {
   hipLaunchKernelGGL(k_q35_gates, dim3(rows, value_heads), dim3(128), 0, s, conv, ldc, keys, mix,
                      ldm, a_off, b_off, a_log, dt, key_heads, value_heads, key_dim, gates, row_err);
-  const dim3 grid(lanes, value_heads), block(((value_dim + kWave - 1) / kWave) * kWave);
+  // at least key_dim threads: thread j stages q/k channel j of each token
+  const dim3 grid(lanes, value_heads),
+      block(((std::max(value_dim, key_dim) + kWave - 1) / kWave) * kWave);
 #define L_(KD)                                                                                 \
   case KD:                                                                                     \
     hipLaunchKernelGGL(k_q35_delta<KD>, grid, block, 0, s, L, conv, ldc, keys, gates, key_heads, \
