@@ -747,7 +747,7 @@ __global__ __launch_bounds__(256) void k_q35_linear(
     const float *__restrict__ a_log, const float *__restrict__ dt,
     const float *__restrict__ norm_w, int KH, int VH, int VD, float eps, float *state,
     size_t state_seq, float *__restrict__ tgt, int ldt, uint32_t *row_err) {
-  __shared__ float qv[kKD], kv[kKD], s_qq[kKD], s_kk[kKD];
+  __shared__ __align__(16) float qv[kKD], kv[kKD], s_qq[kKD], s_kk[kKD];
   __shared__ double qsq[kKD], ksq[kKD], osq[256];
   __shared__ float s_qn, s_kn, s_scale;
   __shared__ float4 s_gate;
@@ -822,15 +822,24 @@ __global__ __launch_bounds__(256) void k_q35_linear(
     float o = 0.0f;
     if (has_v) {
       const float decay = gt.z, beta = gt.w;
+      // LDS values two groups of 4 ahead of their use, as in k_q35_delta
+      const float4 *kk4 = reinterpret_cast<const float4 *>(s_kk);
+      const float4 *qq4 = reinterpret_cast<const float4 *>(s_qq);
+      constexpr int kG4 = kKD / 4;
       double pred = 0.0;
+      float4 ka = kk4[0], kb = kG4 > 1 ? kk4[1] : ka;
 #pragma unroll
       for (int i0 = 0; i0 < kKD; i0 += 4) {
         asm volatile("" ::: "memory");
+        const float4 kq = ka;
+        ka = kb;
+        if (i0 / 4 + 2 < kG4) kb = kk4[i0 / 4 + 2];
+        const float k4[4] = {kq.x, kq.y, kq.z, kq.w};
         float p[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           col[i0 + e] *= decay;
-          p[e] = col[i0 + e] * s_kk[i0 + e];
+          p[e] = col[i0 + e] * k4[e];
         }
         pin_vgprs(p);
         double wd[4];
@@ -842,14 +851,25 @@ __global__ __launch_bounds__(256) void k_q35_linear(
       }
       const float corr = (v - (float)pred) * beta;
       double rd = 0.0;
+      ka = kk4[0];
+      kb = kG4 > 1 ? kk4[1] : ka;
+      float4 qa = qq4[0], qb = kG4 > 1 ? qq4[1] : qa;
 #pragma unroll
       for (int i0 = 0; i0 < kKD; i0 += 4) {
         asm volatile("" ::: "memory");
+        const float4 kq = ka, qq = qa;
+        ka = kb;
+        qa = qb;
+        if (i0 / 4 + 2 < kG4) {
+          kb = kk4[i0 / 4 + 2];
+          qb = qq4[i0 / 4 + 2];
+        }
+        const float k4[4] = {kq.x, kq.y, kq.z, kq.w}, q4[4] = {qq.x, qq.y, qq.z, qq.w};
         float p[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          col[i0 + e] += s_kk[i0 + e] * corr;
-          p[e] = col[i0 + e] * s_qq[i0 + e];
+          col[i0 + e] += k4[e] * corr;
+          p[e] = col[i0 + e] * q4[e];
         }
         pin_vgprs(p);
         double wd[4];
