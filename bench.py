@@ -561,7 +561,7 @@ def summarize_c5_trace(trace_csv, bench_json, mfma_csv=None):
               f"{sum(d) / 1e3:.2f} |")
     print("\nThe 30 largest (kernel, grid) groups by total time, over the three runs.  Grid y of the\n"
           "matvec kernels counts row groups: `k_q35_mvpc` 36864x4 and `k_q35_mvd` 131584x1 / 114688x1\n"
-          "are the 16-row steps of the one-token schedule (o/out/down projections; mix and gate+up),\n"
+          "are the 16-row steps of the one-token schedule (o/out/down projections; mix; gate+up with SwiGLU, `k_q35_mvd<3, ...>`),\n"
           "`k_q35_mvd<2, ...>` is the LM head with its argmax, and `k_q35_mv` with grid y in the hundreds\n"
           "are the 256-token prompt chunks (up to 4096 rows) of the exact run; `Cijk_` kernels are\n"
           "the regime's library GEMMs, `k_q35_split` and `k_q35_finite` their operand split and check.\n\n"
