@@ -1,10 +1,8 @@
 """Builds libcohx.so (HIP kernels + C ABI) for gfx950, in-tree.
 
-Flags that carry the engine's float semantics:
-  -ffp-contract=off                    no a*b+c fusion except explicit fmaf
-  -fno-gpu-flush-denormals-to-zero     IEEE subnormals, as on the CPU
-  -fhip-fp32-correctly-rounded-divide-sqrt   IEEE division / sqrt
-Packed fp32 instructions are disabled (-packed-fp32-ops).
+The flags (the engine's float semantics: no contraction, IEEE subnormals,
+division and square root; packed fp32 instructions off), the sources and the
+link line come from build.manifest, which the Rust crate's build.rs reads too.
 """
 import os
 import subprocess
@@ -14,22 +12,33 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libcohx.so")
-SOURCES = ["csrc/kernels.hip", "csrc/cohx.cpp", "csrc/gen.cpp", "csrc/q35_kernels.hip", "csrc/q35.cpp",
-           "csrc/gguf.cpp", "csrc/blas.cpp"]
+MANIFEST = os.path.join(HERE, "build.manifest")
 HEADERS = ["csrc/device.h", "csrc/kernels.h", "csrc/internal.h", "../include/cohx.h"]
 PROBE_SOURCE = "csrc/probe.hip"
 PROBE_LIB = os.path.join(HERE, "libcohx_probe.so")
 ARCH = os.environ.get("COHX_ARCH", "gfx950")
 
-FLAGS = [
-    "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
-    "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero",
-    "-fhip-fp32-correctly-rounded-divide-sqrt",
-    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # matrix-core results straight into VGPRs (no AGPR copies before the VALU chain)
-    "-mllvm", "-amdgpu-mfma-vgpr-form",
-    "-Wall", "-Wno-unused-function", "-I", os.path.join(ROOT, "include"),
-]
+
+def manifest(path=MANIFEST):
+    """The [flags], [sources] and [link] lists of build.manifest (shared with
+    the Rust crate's build.rs)."""
+    sections, current = {}, None
+    with open(path) as f:
+        for line in f:
+            line = line.split("#", 1)[0].strip()
+            if not line:
+                continue
+            if line.startswith("[") and line.endswith("]"):
+                current = sections.setdefault(line[1:-1], [])
+            elif current is not None:
+                current.append(line)
+    return sections
+
+
+_M = manifest()
+SOURCES = _M["sources"]
+FLAGS = [*_M["flags"], f"--offload-arch={ARCH}", "-I", os.path.join(ROOT, "include")]
+LINK = _M["link"]
 
 
 def _hipcc():
@@ -61,7 +70,7 @@ def build(verbose=False):
     tmp = LIB + ".tmp"
     # -z defs: an undefined symbol (say, a kernel stub the host pass dropped) fails the build
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", tmp, *objs,
-           "-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
+           *LINK]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
