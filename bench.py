@@ -339,7 +339,7 @@ def run_c3(seed, steps, warmup):
                         "rows over KV U[256,4096]; linears on the matrix cores (f32 sums)",
             "value": rows / elapsed, "unit": "packed rows/s", "ms_per_step": ms, "steps": steps,
             "mean_rows_per_step": rows / steps,
-            "roofline": {"bound": "mfma", "kernel": "linears (hipBLASLt GEMMs in steps with prompt rows)",
+            "roofline": {"bound": "mfma", "kernel": "linears (k_gemm, the matrix-core GEMM of steps with prompt rows)",
                          "achieved": tflops, "peak": MFMA_F16_PEAK / 1e12, "unit": "TFLOP/s",
                          "frac": tflops * 1e12 / MFMA_F16_PEAK},
             "attention_chunk": chunk_roofline(stats, steps),
@@ -442,8 +442,6 @@ def kernel_instance(name):
     m = re.search(r"\b(k_\w+)(<[^>]*>)?\(", name)
     if m:
         return m.group(1) + (m.group(2) or "")
-    if name.startswith("Cijk_"):  # hipBLASLt (Tensile) GEMM kernels
-        return "hipblaslt " + name[:48] + "..."
     return name
 
 
@@ -563,8 +561,8 @@ def summarize_c5_trace(trace_csv, bench_json, mfma_csv=None):
           "matvec kernels counts row groups: `k_q35_mvpc` 36864x4 and `k_q35_mvd` 131584x1 / 114688x1\n"
           "are the 16-row steps of the one-token schedule (o/out/down projections; mix; gate+up with SwiGLU, `k_q35_mvd<3, ...>`),\n"
           "`k_q35_mvd<2, ...>` is the LM head with its argmax, and `k_q35_mv` with grid y in the hundreds\n"
-          "are the 256-token prompt chunks (up to 4096 rows) of the exact run; `Cijk_` kernels are\n"
-          "the regime's library GEMMs, `k_q35_split` and `k_q35_finite` their operand split and check.\n\n"
+          "are the 256-token prompt chunks (up to 4096 rows) of the exact run; `k_gemm<1, true, ...>` is\n"
+          "the regime's matrix-core GEMM over hi/lo operands, `k_q35_split` their split.\n\n"
           f"Summary: `python bench.py --summarize-c5-trace <dir>/<name>_kernel_trace.csv <bench stdout> "
           f"[<mfma counter_collection.csv>]`")
     if mfma_csv:
@@ -862,7 +860,7 @@ def run_c5(seed, cpu_steps, threads, with_cpu=True):
     weights), 16 sequences with prompts U[64,1024] of random ids, 64 greedy
     tokens each.  Timed from fresh sequences: with prompts in chunks of
     C5_CHUNK rows per lane per step (steps of 128+ rows in the packed-prefill
-    regime, the default: linears as library BF16 GEMMs with f32 sums, within
+    regime, the default: linears on the matrix-core BF16 GEMM with f32 sums, within
     the stated tolerance), the same schedule with the regime off (exact, bit
     for bit against the oracle), and the engine's one-token-per-step schedule
     (exact).  The two exact runs must generate the same tokens; the regime's
@@ -906,7 +904,7 @@ def run_c5(seed, cpu_steps, threads, with_cpu=True):
     ch, ex, es = res["chunked"], res["chunked_exact"], res["engine_schedule"]
     line = {"workload": f"Qwen3.5-0.8B-shape hybrid (bf16 weights, f32 state), {C5_SEQS} sequences, "
                         f"prompts U[{C5_PROMPT[0]},{C5_PROMPT[1]}], {C5_GEN} greedy tokens each; prompt "
-                        f"steps of 128+ rows in the packed-prefill regime (library BF16 GEMMs, f32 sums)",
+                        f"steps of 128+ rows in the packed-prefill regime (matrix-core BF16 GEMM, f32 sums)",
             "value": C5_SEQS * C5_GEN / ch["elapsed"], "unit": "generated tok/s (whole job)",
             "rows_per_s": ch["rows"] / ch["elapsed"], "elapsed_s": ch["elapsed"],
             "steps": ch["steps"], "prompt_chunk": C5_CHUNK, "prompt_rows": sum(plen),

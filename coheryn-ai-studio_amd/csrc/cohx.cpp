@@ -504,7 +504,6 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   if (const char *g = std::getenv("COHX_GRAPHS")) ctx->use_graphs = std::strcmp(g, "0") != 0;
   // COHX_PREFILL_MFMA=0 keeps tall F16 batches on the exact (f64-sum) kernels
   if (const char *g = std::getenv("COHX_PREFILL_MFMA")) ctx->prefill_mfma = std::strcmp(g, "0") != 0;
-  if (const char *g = std::getenv("COHX_GEMM_LIB")) ctx->use_gemm_lib = std::strcmp(g, "0") != 0;
   auto bail = [&](int rc) {
     cohx_destroy(ctx);
     return rc;
@@ -589,7 +588,6 @@ void cohx_destroy(cohx_ctx *ctx) {
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   drop_graphs(ctx);
-  gemm_lib_destroy(ctx->gemm_lib);
   for (void *p : ctx->allocations) (void)hipFree(p);
   for (void *p : {(void *)ctx->host.h_upload, (void *)ctx->host.h_row_err, (void *)ctx->host.h_argmax,
                   (void *)ctx->host.h_tiles, (void *)ctx->host.h_row_skip, (void *)ctx->host.h_row_map})
@@ -1330,32 +1328,9 @@ extern "C" uint32_t cohx_profile_read(const cohx_ctx *ctx, cohx_kernel_stat *out
 // sizes the attention grids; blocks past a row's length exit at once.
 int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_grid, bool any_logits) {
   const cohx_model_desc &d = ctx->desc;
-  set_prefill_mfma(ctx->prefill_mfma);
-  set_gemm_lib(nullptr, nullptr, 0);
-  {
-    // the regime's F16 linears through the library: steps that carry prompt
-    // rows (never captured into a graph, so a step's arithmetic does not
-    // depend on the graph setting), on the context's own workspace (not the
-    // allocation-free call, which keeps the matrix-core kernel); gate+up's
-    // sums go to the attention score buffer, which is dead by then
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    const bool eager = hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone;
-    if (eager && !p.single_token && &w == &ctx->ws && ctx->use_gemm_lib && ctx->prefill_mfma &&
-        d.weight_dtype == COHX_F16 && p.rows >= 128 && !ctx->gemm_lib_failed) {
-      if (!ctx->gemm_lib) {
-        constexpr size_t kGemmWorkspace = 32u << 20;
-        void *gws = nullptr;
-        if (dalloc(ctx, reinterpret_cast<uint8_t **>(&gws), kGemmWorkspace) == COHX_OK)
-          ctx->gemm_lib = gemm_lib_create(gws, kGemmWorkspace);
-        if (!ctx->gemm_lib) {
-          ctx->gemm_lib_failed = true;
-          (void)hipGetLastError();
-        }
-      }
-      if (ctx->gemm_lib)
-        set_gemm_lib(ctx->gemm_lib, w.scores, (size_t)w.rows * d.kv_heads * w.kv_cap * 8);
-    }
-  }
+  // the packed-prefill regime (F16 linears on the matrix cores) is for
+  // steps that carry prompt rows; decode-only steps stay exact at any width
+  set_prefill_mfma(ctx->prefill_mfma && !p.single_token);
   const int pk = prof_begin(ctx, kCatPack, 0.0, 0.0);
   enqueue_pack(ctx, w, (int)p.included.size());
   prof_end(ctx, pk);
@@ -1479,17 +1454,24 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
       prof_end(ctx, e);
     }
     if (!fused_quant && a_down == kActF16) {
-      // F16 in the packed-prefill regime: library GEMM, then SwiGLU into
-      // the down operand (false: nothing launched)
+      // F16 in the packed-prefill regime: gate+up on the matrix cores with
+      // SwiGLU in the epilogue, writing the down projection's binary16
+      // operand into the f32 SwiGLU rows' space, w.h (act.f16 holds gate+up's
+      // own operand, which other workgroups are still reading); false:
+      // nothing launched
+      uint16_t *down16 = reinterpret_cast<uint16_t *>(w.h);
       e = prof_begin(ctx, kCatMvGateUp, matrix_pass_bytes(ly.gu, R, 0, false) + (double)R * F * 2,
                      2.0 * R * 2 * F * H);
       fused_quant = launch_matvec_swiglu_f16(s, ly.gu.view, act, R,
                                              MatvecOut{nullptr, 0, nullptr, nullptr, w.row_err, nullptr},
-                                             w.act_f16);
+                                             down16);
       prof_end(ctx, e);
       if (fused_quant) {
+        ActView down_f16 = act;
+        down_f16.f16 = down16;
         e = prof_begin(ctx, kCatMvDown, matrix_pass_bytes(ly.down, R, H, true), 2.0 * R * H * F);
-        launch_matvec(s, kEpiResidual, ly.down.view, act, R, MatvecOut{w.x, H, nullptr, nullptr, w.row_err, nullptr});
+        launch_matvec(s, kEpiResidual, ly.down.view, down_f16, R,
+                      MatvecOut{w.x, H, nullptr, nullptr, w.row_err, nullptr});
         prof_end(ctx, e);
         continue;
       }
@@ -1516,7 +1498,8 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
   const DeviceMatrix &head = d.tied ? ctx->embd : ctx->output;
   // a step in the packed-prefill regime (its linears on the matrix cores)
   // takes the F16 head there too; otherwise the head stays exact
-  set_head_mfma(p.n_tiles > 0 || (ctx->prefill_mfma && head.view.dtype == kFmtF16 && R >= 128));
+  set_head_mfma(p.n_tiles > 0 ||
+                (ctx->prefill_mfma && !p.single_token && head.view.dtype == kFmtF16 && R >= 128));
   e = prof_begin(ctx, kCatMvHead,
                  matrix_pass_bytes(head, NL, 0, false) + (any_logits ? (double)NL * d.vocabulary * 4 : 0.0) + NL * 8.0,
                  2.0 * NL * d.vocabulary * H);
@@ -1527,7 +1510,6 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
                                w.lane_last, w.argmax}))
     launch_argmax_reduce(s, NL, w.argmax_part, head.view.mtiles, w.argmax);
   set_head_mfma(false);
-  set_gemm_lib(nullptr, nullptr, 0);
   prof_end(ctx, e);
   HIP_TRY(hipGetLastError());
   return COHX_OK;
@@ -1691,16 +1673,20 @@ extern "C" int cohx_step_noalloc(cohx_ctx *ctx, const cohx_batch *batch, cohx_st
     return fail(ctx, COHX_INVALID_REQUEST,
                 "batch width must be in 1..=" + std::to_string(ctx->desc.max_lanes));
   if (!ctx->scratch) return fail(ctx, COHX_DEVICE, "the scratch array was not resolved");
-  // upper bounds of what the step packs: lanes that fail validation only shrink it
+  // upper bounds of what the step packs, over the lanes that can pass
+  // prepare_batch's checks (a live sequence, the start at its length, the
+  // rows within its capacity): a lane that will be refused on its own must
+  // not make the whole call fail for want of scratch
   uint64_t rows = 0;
   uint32_t kv = 1;
   bool logits = false;
   for (uint32_t i = 0; i < batch->n_lanes; i++) {
     const cohx_lane &ln = batch->lanes[i];
+    if (!valid_seq(ctx, ln.seq) || ln.n_tokens == 0) continue;
+    const Sequence &sq = ctx->seqs[ln.seq];
+    const uint64_t start = ln.start_position == COHX_AT_END ? sq.length : ln.start_position;
+    if (start != sq.length || start + ln.n_tokens > sq.capacity) continue;
     rows += ln.n_tokens;
-    const bool live = valid_seq(ctx, ln.seq);
-    const uint64_t start = ln.start_position == COHX_AT_END ? (live ? ctx->seqs[ln.seq].length : 0)
-                                                            : ln.start_position;
     kv = (uint32_t)std::max<uint64_t>(kv, std::min<uint64_t>(start + ln.n_tokens, ctx->desc.max_context));
     logits |= ln.want_logits == 1u && out->lanes[i].logits;
   }

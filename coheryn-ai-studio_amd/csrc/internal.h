@@ -159,11 +159,6 @@ struct cohx_ctx {
   std::map<cohx::StepKey, hipGraphExec_t> graphs;
   cohx::Q35Model *q35 = nullptr;  // set for Qwen3.5 contexts (cohx_create_qwen35)
   hipEvent_t done = nullptr;      // completion event of a hooked step (created on first use)
-  // library GEMMs for the regime's F16 linears (created by the first eager
-  // regime step; COHX_GEMM_LIB=0 keeps them on the matrix-core kernel)
-  bool use_gemm_lib = true;
-  bool gemm_lib_failed = false;
-  cohx::GemmLib *gemm_lib = nullptr;
 };
 
 namespace cohx {

@@ -89,29 +89,14 @@ void launch_norm_act(hipStream_t s, int rows, const float *x, const uint32_t *in
 void launch_quant_act(hipStream_t s, int rows, const float *src, int K, int act_dtype, int nbp,
                       ActView act, uint32_t *row_err);
 // Packed F16 batches of 128+ rows on the matrix cores (f32 sums, within tolerance
-// of the reference's f64 sums) or always on the exact kernels.
+// of the reference's f64 sums) or always on the exact kernels.  The step
+// driver turns it on for steps that carry prompt rows only.
 void set_prefill_mfma(bool on);
 // The F16 LM head of the next launches on the matrix cores too (f32 sums; a
 // step in the packed-prefill regime, at 16 or more logit rows).
 void set_head_mfma(bool on);
 // Timing events for the next launches (see the launch helper); both null ends it.
 void set_launch_events(hipEvent_t start, hipEvent_t stop);
-
-// Library GEMMs (hipBLASLt, blas.cpp) for the packed-prefill regime's
-// linears: Y[M][N] (+)= X[M][K] . W[N][K]^T (W and X row-major), binary16
-// or bfloat16 operands, f32 sums.
-struct GemmLib;
-GemmLib *gemm_lib_create(void *workspace, size_t workspace_bytes);
-void gemm_lib_destroy(GemmLib *lib);
-// false: nothing launched (no algorithm for the shape)
-bool gemm_lib_f16(GemmLib *lib, hipStream_t s, const uint16_t *w, int N, int K, const uint16_t *x, int M,
-                  float *out, int ldo, bool accumulate);
-bool gemm_lib_bf16(GemmLib *lib, hipStream_t s, const uint16_t *w, int N, int K, const uint16_t *x, int M,
-                   float *out, int ldo, bool accumulate);
-// The next launches' F16 linears in the regime go through `lib` (nullptr:
-// the matrix-core kernel); gate+up writes its [rows][2F] f32 sums to
-// `scratch` (at least scratch_floats) before the SwiGLU pass.
-void set_gemm_lib(GemmLib *lib, float *scratch, size_t scratch_floats);
 
 // Returns true when a kEpiArgmax launch wrote o.argmax_final (no reduce needed).
 bool launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActView &act,
@@ -125,12 +110,12 @@ bool launch_matvec(hipStream_t s, Epilogue epi, const MatrixView &w, const ActVi
 // to even.
 bool launch_matvec_swiglu_q8(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
                              const MatvecOut &o, const ActView &qout, int qout_nbp);
-// F16 gate+up of a step in the packed-prefill regime through the library GEMM
-// (set_gemm_lib), its SwiGLU pass writing the down projection's binary16
-// operand rows out_f16[rows_b][F] directly: the bits of launch_matvec
-// (kEpiSwiglu) then launch_quant_act(kActF16) over the same sums.  Returns
-// false (nothing launched) when no library GEMM is set or the shape is not
-// covered (F % 8, scratch room).
+// F16 gate+up of a step in the packed-prefill regime on the matrix-core GEMM
+// (gemm.h) with SwiGLU in its epilogue, writing the down projection's
+// binary16 operand rows out_f16[rows_b][F] directly (the rounding and
+// non-finite checks of launch_quant_act(kActF16)).  Returns false (nothing
+// launched) outside the regime (set_prefill_mfma off, under 128 rows, not
+// F16) or when K is not a multiple of 64.
 bool launch_matvec_swiglu_f16(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
                               const MatvecOut &o, uint16_t *out_f16);
 void launch_argmax_reduce(hipStream_t s, int rows, const unsigned long long *part, int units,

@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include "device.h"
+#include "gemm.h"
 #include "kernels.h"
 
 namespace cohx {
@@ -29,9 +30,6 @@ namespace {
 thread_local hipEvent_t t_ev_start = nullptr, t_ev_stop = nullptr;
 thread_local bool g_prefill_mfma = true;  // set per step from the context
 thread_local bool g_head_mfma = false;    // this step's F16 head on the matrix cores
-thread_local GemmLib *g_lib = nullptr;     // library GEMMs for the regime's F16 linears
-thread_local float *g_lib_scratch = nullptr;
-thread_local size_t g_lib_scratch_floats = 0;
 
 template <typename F, typename... Args>
 void launch_k(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args... args) {
@@ -46,23 +44,6 @@ void launch_k(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args
 
 void set_prefill_mfma(bool on) { g_prefill_mfma = on; }
 void set_head_mfma(bool on) { g_head_mfma = on; }
-// Library GEMMs take no timing events of their own: while they are set, the
-// interval's start and stop are plain markers around the library call.
-static void lib_mark_begin(hipStream_t s) {
-  if (t_ev_start) {
-    (void)hipEventRecord(t_ev_start, s);
-    t_ev_start = nullptr;
-  }
-}
-static void lib_mark_end(hipStream_t s) {
-  if (t_ev_stop) (void)hipEventRecord(t_ev_stop, s);
-}
-
-void set_gemm_lib(GemmLib *lib, float *scratch, size_t scratch_floats) {
-  g_lib = lib;
-  g_lib_scratch = scratch;
-  g_lib_scratch_floats = scratch_floats;
-}
 
 void set_launch_events(hipEvent_t start, hipEvent_t stop) {
   t_ev_start = start;
@@ -1743,210 +1724,6 @@ __global__ __launch_bounds__(256) void k_head_f16(MatrixView w, ActView act, int
 }
 
 // ---------------------------------------------------------------------------
-// Packed-prefill F16 linear on the matrix cores: out[r][f] = sum_k x[r][k] *
-// w[f][k] over binary16 operands (the activations already rounded to
-// binary16, as the reference rounds them, cpu.rs:37-48), f32 accumulation in
-// v_mfma_f32_16x16x32_f16 order.  The reference sums these exact products in
-// f64 (cpu.rs:31-35); this regime differs from it by f32 rounding of the
-// partial sums and is held to a tolerance, while decode batches keep the
-// exact kernels.  A workgroup (4 waves) owns 128 features x 32*kNB rows; wave
-// (wf, wr) computes features wf*64.. and rows wr*16*kNB.. as 4 x kNB MFMA
-// tiles.  K is staged through a ring of kStages LDS stages of 32 K-steps,
-// filled by direct-to-LDS loads with later steps in flight during the
-// MFMAs.  For the SwiGLU epilogue the
-// workgroup's feature tile is 64 gate rows and the 64 matching up rows; the
-// up waves hand their sums to the gate waves through LDS.
-// ---------------------------------------------------------------------------
-// 16 bytes per lane straight from global memory into LDS: lane l's bytes
-// land at l * 16 past `lds` (the same for the whole wave).  Completion counts
-// in vmcnt.
-__device__ __forceinline__ void lds_load16(const void *global, void *lds) {
-  __builtin_amdgcn_global_load_lds(global, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
-}
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float float4v __attribute__((ext_vector_type(4)));
-constexpr int kGemmBM = 128, kGemmBK = 32;
-// LDS ring depth of the 128-row and the 64-row workgroups
-constexpr int kGemmStages4 = 2, kGemmStages2 = 4;
-
-template <int kEpi, int kNB, int kStages>
-__global__ __launch_bounds__(256) void k_gemm_f16(MatrixView w, const uint16_t *__restrict__ x,
-                                                  int rows_b, MatvecOut o) {
-  // kNB MFMA row tiles per wave: a workgroup covers 32 * kNB rows (128 or 64;
-  // 64 doubles the workgroups of the narrow linears, whose 128-row grid
-  // leaves CUs idle).  K steps of 32 go through a ring of kStages LDS stages
-  // filled by direct-to-LDS loads issued kStages - 1 steps ahead.  A stage
-  // holds 128 weight rows and the workgroup's 32 * kNB activation rows, 64
-  // bytes each, as 16-byte segments: segment s of row R sits at slot
-  // 4 R + (s ^ ((R >> 2) & 3)), so a wave's operand read (16 rows x 4
-  // segments) touches every bank once.  The SwiGLU exchange reuses the LDS
-  // after the K loop.
-  constexpr int kBR = 32 * kNB;
-  static_assert(kStages >= 2 && kStages <= 4, "LDS ring of 2 to 4 K steps");
-  constexpr int kWSlots = kGemmBM * 4, kXSlots = kBR * 4, kSlots = kWSlots + kXSlots;
-  constexpr int kPerStage = kSlots / 256;  // direct-to-LDS loads per wave per stage
-  extern __shared__ __align__(16) uint4 g_smem[];
-  uint16_t *s_mem = reinterpret_cast<uint16_t *>(g_smem);
-  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  const int wf = wave / 2, wr = wave % 2;
-  const int K = w.K, nk = K / kGemmBK;
-  const int out_rows = kEpi == kEpiSwiglu ? w.rows / 2 : w.rows;
-  const int f0 = blockIdx.x * (kEpi == kEpiSwiglu ? kGemmBM / 2 : kGemmBM);
-  const int r0 = blockIdx.y * kBR;
-  // this lane's source row and segment for each of its kPerStage loads
-  const uint16_t *src[kPerStage];
-#pragma unroll
-  for (int i = 0; i < kPerStage; i++) {
-    const int slot = (wave * kPerStage + i) * kWave + lane;
-    if (slot < kWSlots) {
-      const int row = slot >> 2, seg = (slot & 3) ^ ((row >> 2) & 3);
-      int f;
-      if (kEpi == kEpiSwiglu)
-        f = row < 64 ? f0 + row : out_rows + f0 + (row - 64);
-      else
-        f = f0 + row;
-      src[i] = w.f16 + (size_t)min(f, w.rows - 1) * K + seg * 8;
-    } else {
-      const int row = (slot - kWSlots) >> 2, seg = (slot & 3) ^ ((row >> 2) & 3);
-      src[i] = x + (size_t)min(r0 + row, rows_b - 1) * K + seg * 8;
-    }
-  }
-  auto issue = [&](int ks) {  // K step ks (clamped to the last) into stage ks % kStages
-    const int kc = min(ks, nk - 1);
-    uint4 *stage = g_smem + (ks % kStages) * kSlots;
-#pragma unroll
-    for (int i = 0; i < kPerStage; i++)
-      lds_load16(src[i] + (size_t)kc * kGemmBK, stage + (wave * kPerStage + i) * kWave);
-  };
-  float4v acc[4][kNB];
-#pragma unroll
-  for (int a = 0; a < 4; a++)
-#pragma unroll
-    for (int b = 0; b < kNB; b++) acc[a][b] = float4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int st = 0; st < kStages - 1; st++) issue(st);
-  const int seg = lane / 16, lr = lane % 16;
-  for (int ks = 0; ks < nk; ks++) {
-    // this wave's loads of step ks are done once at most kStages - 2 later
-    // steps are in flight; the barrier makes every wave's visible and frees
-    // the stage read in step ks - 1 for step ks + kStages - 1
-    constexpr int kInFlight = (kStages - 2) * kPerStage;  // loads of later steps still allowed
-    static_assert(kInFlight < 16, "vmcnt immediate");
-    __builtin_amdgcn_s_waitcnt(0x0F70 | kInFlight);  // vmcnt(kInFlight)
-    __builtin_amdgcn_s_barrier();
-    issue(ks + kStages - 1);
-    const uint4 *stage = g_smem + (ks % kStages) * kSlots;
-    half8 af[4], bf[kNB];
-#pragma unroll
-    for (int a = 0; a < 4; a++) {
-      const int R = wf * 64 + a * 16 + lr;
-      af[a] = *reinterpret_cast<const half8 *>(stage + R * 4 + (seg ^ ((R >> 2) & 3)));
-    }
-#pragma unroll
-    for (int b = 0; b < kNB; b++) {
-      const int R = wr * 16 * kNB + b * 16 + lr;
-      bf[b] = *reinterpret_cast<const half8 *>(stage + kWSlots + R * 4 + (seg ^ ((R >> 2) & 3)));
-    }
-#pragma unroll
-    for (int a = 0; a < 4; a++)
-#pragma unroll
-      for (int b = 0; b < kNB; b++)
-        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bf[b], acc[a][b], 0, 0, 0);
-  }
-  // every load (the clamped ones past the end included) lands before the
-  // LDS is reused
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  __syncthreads();
-  // ---- epilogue: lane holds features (tile row) 4*(lane/16)+i of rows (tile col) lane%16
-  if constexpr (kEpi == kEpiArgmax) {
-    // per (batch row, 16-feature tile) partial keys, as the exact head
-    // kernels write them for k_argmax_reduce; logits on request
-#pragma unroll
-    for (int b = 0; b < kNB; b++) {
-      const int r = r0 + wr * 16 * kNB + b * 16 + lr;
-      const bool rvalid = r < rows_b;
-      bool bad = false;
-#pragma unroll
-      for (int a = 0; a < 4; a++) {
-        const int ft = f0 + wf * 64 + a * 16, fb = ft + 4 * (lane / 16);
-        unsigned long long key = 0ull;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float v = acc[a][b][i];
-          if (rvalid && fb + i < w.rows) {
-            bad |= !finitef(v);
-            if (o.logits) o.logits[(size_t)r * w.rows + fb + i] = v;
-            const unsigned long long k = argmax_key(v, fb + i);
-            key = k > key ? k : key;
-          }
-        }
-        unsigned long long x2 = __shfl_xor(key, 16, kWave);
-        key = x2 > key ? x2 : key;
-        x2 = __shfl_xor(key, 32, kWave);
-        key = x2 > key ? x2 : key;
-        if (lane < 16 && rvalid && ft < w.rows) o.argmax[(size_t)r * w.mtiles + ft / 16] = key;
-      }
-      if (bad) atomicOr(&o.row_err[o.err_rows ? (int)o.err_rows[r] : r], kErrNonFinite);
-    }
-    return;
-  }
-  if (kEpi == kEpiSwiglu) {
-    float *s_up = reinterpret_cast<float *>(s_mem);  // 2 x 4 kNB x 4 x 64 floats
-    if (wf == 1) {
-#pragma unroll
-      for (int a = 0; a < 4; a++)
-#pragma unroll
-        for (int b = 0; b < kNB; b++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) s_up[((wr * 4 * kNB + a * kNB + b) * 4 + i) * 64 + lane] = acc[a][b][i];
-    }
-    __syncthreads();
-    if (wf == 1) return;
-  }
-#pragma unroll
-  for (int b = 0; b < kNB; b++) {
-    const int r = r0 + wr * 16 * kNB + b * 16 + lr;
-    if (r >= rows_b) continue;
-    const int er = o.err_rows ? (int)o.err_rows[r] : r;
-    bool bad = false;
-#pragma unroll
-    for (int a = 0; a < 4; a++) {
-      const int fb = f0 + wf * 64 + a * 16 + 4 * (lane / 16);
-      float v[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        v[i] = acc[a][b][i];
-        if (kEpi == kEpiSwiglu) {
-          const float *s_up = reinterpret_cast<const float *>(s_mem);
-          const float g = v[i], u = s_up[((wr * 4 * kNB + a * kNB + b) * 4 + i) * 64 + lane];
-          bad |= !finitef(g) || !finitef(u);
-          v[i] = (g / (1.0f + exp_f32(-g))) * u;
-        } else {
-          bad |= !finitef(v[i]);
-        }
-      }
-      if (fb + 3 < out_rows && (o.ld % 4) == 0) {
-        float4 *p = reinterpret_cast<float4 *>(o.out + (size_t)r * o.ld + fb);
-        if (kEpi == kEpiResidual) {
-          const float4 q = *p;
-          *p = make_float4(q.x + v[0], q.y + v[1], q.z + v[2], q.w + v[3]);
-        } else {
-          *p = make_float4(v[0], v[1], v[2], v[3]);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          if (fb + i >= out_rows) continue;
-          float *p = o.out + (size_t)r * o.ld + fb + i;
-          *p = kEpi == kEpiResidual ? *p + v[i] : v[i];
-        }
-      }
-    }
-    if (bad) atomicOr(&o.row_err[er], kErrNonFinite);
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Bias add, NeoX RoPE from the host-built table (cos, sin of the engine's
 // iterative angle, cpu.rs:59-73), K/V append into the paged pool
 // (Kv::append, inference.rs:1019-1043; batch.rs:164-184).
@@ -2412,6 +2189,13 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
 // (cpu.rs:133-210); rows handled here are flagged in row_skip so the exact
 // passes leave them.  Tiles arrive sorted by KV length, longest first.
 // ---------------------------------------------------------------------------
+// 16 bytes per lane straight from global memory into LDS: lane l's bytes
+// land at l * 16 past `lds` (the same for the whole wave).  Completion counts
+// in vmcnt.
+__device__ __forceinline__ void lds_load16(const void *global, void *lds) {
+  __builtin_amdgcn_global_load_lds(global, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+}
+typedef float float4v __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -2876,124 +2660,85 @@ static bool mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
   return false;
 }
 
-// Packed batches at least this tall take the matrix-core F16 linear.
+// Packed batches at least this tall take the matrix-core F16 linears.
 constexpr int kPrefillRows = 128;
 
-// SwiGLU over a library GEMM's gate+up sums gu[row][0 .. 2F) (gate, then up):
-// h = (g / (1 + exp(-g))) * u into out[row][i], the same arithmetic and
-// non-finite check as k_gemm_f16's SwiGLU epilogue.  Thread = 4 outputs.
-__global__ __launch_bounds__(256) void k_swiglu_rows(const float *__restrict__ gu, int rows, int F,
-                                                     float *__restrict__ out, int ld, uint32_t *row_err,
-                                                     const uint32_t *err_rows) {
-  const int r = blockIdx.y, i = (blockIdx.x * 256 + threadIdx.x) * 4;
-  if (r >= rows || i >= F) return;
-  const float *g = gu + (size_t)r * 2 * F + i;
-  bool bad = false;
-  float v[4];
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    if (i + k < F) {
-      const float a = g[k], u = g[F + k];
-      bad |= !finitef(a) || !finitef(u);
-      v[k] = (a / (1.0f + exp_f32(-a))) * u;
+// The packed-prefill regime's F16 GEMM (gemm.h) for one projection; false
+// (nothing launched) when K is not a multiple of 64.  Tiles measured on the
+// C3 shapes (2,616 packed rows): 128 x 128 with four K steps in flight for
+// the plain and residual projections (qkv 16.9, o 16.3, down 54.9 us), 256 x
+// 128 on eight waves for gate+up with the SwiGLU epilogue (95 us, which also
+// replaces a separate SwiGLU-to-binary16 pass), 128 x 64 for the head's few
+// logit rows.
+static bool gemm_f16(hipStream_t s, Epilogue epi, const MatrixView &w, const uint16_t *x, int rows_b,
+                     const MatvecOut &o, uint16_t *out16) {
+  using namespace gemm;
+  if (w.K % 64) return false;
+  const bool four = w.K % 128 == 0;  // four K steps of 32 in flight divide K
+  Args g{};
+  g.w = w.f16;
+  g.x = x;
+  g.N = w.rows;
+  g.K = w.K;
+  g.M = rows_b;
+  g.ldx = w.K;
+  g.row_err = o.row_err;
+  g.err_rows = o.err_rows;
+  if (epi == kEpiSwiglu) {
+    g.out16 = out16;
+    const dim3 grid(tile_order(g, w.rows / 2, 128, 128));
+    launch_k(k_gemm<kF16, false, 4, 2, 4, 4, 2, kSwigluF16>, grid, dim3(512),
+             lds_bytes<4, 2, 4, 4, false, kSwigluF16>(), s, g);
+  } else if (epi == kEpiArgmax) {
+    g.keys = o.argmax;
+    g.ktiles = w.mtiles;
+    g.logits = o.logits;
+    const dim3 grid(tile_order(g, w.rows, 128, 64));
+    constexpr int lds = lds_bytes<2, 2, 4, 2, false, kArgmax>();
+    if (four)
+      launch_k(k_gemm<kF16, false, 2, 2, 4, 2, 4, kArgmax>, grid, dim3(256), lds, s, g);
+    else
+      launch_k(k_gemm<kF16, false, 2, 2, 4, 2, 2, kArgmax>, grid, dim3(256), lds, s, g);
+  } else {
+    g.out = o.out;
+    g.ldo = o.ld;
+    const dim3 grid(tile_order(g, w.rows, 128, 128));
+    constexpr int lds = lds_bytes<2, 2, 4, 4, false, kStore>();
+    if (epi == kEpiResidual) {
+      if (four)
+        launch_k(k_gemm<kF16, false, 2, 2, 4, 4, 4, kAccumulate>, grid, dim3(256), lds, s, g);
+      else
+        launch_k(k_gemm<kF16, false, 2, 2, 4, 4, 2, kAccumulate>, grid, dim3(256), lds, s, g);
+    } else {
+      if (four)
+        launch_k(k_gemm<kF16, false, 2, 2, 4, 4, 4, kStore>, grid, dim3(256), lds, s, g);
+      else
+        launch_k(k_gemm<kF16, false, 2, 2, 4, 4, 2, kStore>, grid, dim3(256), lds, s, g);
     }
   }
-#pragma unroll
-  for (int k = 0; k < 4; k++)
-    if (i + k < F) out[(size_t)r * ld + i + k] = v[k];
-  if (bad) atomicOr(&row_err[err_rows ? (int)err_rows[r] : r], kErrNonFinite);
-}
-
-// The same over 8 outputs per thread, rounding h to binary16 into the down
-// projection's operand (k_quant_act's rounding and check): F % 8 == 0.
-__global__ __launch_bounds__(256) void k_swiglu_f16_rows(const float *__restrict__ gu, int rows, int F,
-                                                         uint16_t *__restrict__ out, uint32_t *row_err,
-                                                         const uint32_t *err_rows) {
-  const int r = blockIdx.y, i = (blockIdx.x * 256 + threadIdx.x) * 8;
-  if (r >= rows || i >= F) return;
-  const float4 *g4 = reinterpret_cast<const float4 *>(gu + (size_t)r * 2 * F + i);
-  const float4 *u4 = reinterpret_cast<const float4 *>(gu + (size_t)r * 2 * F + F + i);
-  const float4 ga = g4[0], gb = g4[1], ua = u4[0], ub = u4[1];
-  const float g[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
-  const float u[8] = {ua.x, ua.y, ua.z, ua.w, ub.x, ub.y, ub.z, ub.w};
-  bool bad = false;
-  uint32_t packed[4];
-#pragma unroll
-  for (int k = 0; k < 8; k += 2) {
-    uint16_t hv[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const float a = g[k + j], b = u[k + j];
-      bad |= !finitef(a) || !finitef(b);
-      hv[j] = f2h((a / (1.0f + exp_f32(-a))) * b);
-      bad |= !finitef(h2f(hv[j]));
-    }
-    packed[k / 2] = (uint32_t)hv[0] | ((uint32_t)hv[1] << 16);
-  }
-  *reinterpret_cast<uint4 *>(out + (size_t)r * F + i) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-  if (bad) atomicOr(&row_err[err_rows ? (int)err_rows[r] : r], kErrNonFinite);
+  return true;
 }
 
 bool launch_matvec_swiglu_f16(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
                               const MatvecOut &o, uint16_t *out_f16) {
-  const int F = w.rows / 2;
-  if (!g_lib || !g_prefill_mfma || rows_b < kPrefillRows || w.dtype != kFmtF16 || F % 8 ||
-      (size_t)rows_b * w.rows > g_lib_scratch_floats)
-    return false;
-  lib_mark_begin(s);
-  if (!gemm_lib_f16(g_lib, s, w.f16, w.rows, w.K, (const uint16_t *)act.f16, rows_b, g_lib_scratch, w.rows, false))
-    return false;
-  launch_k(k_swiglu_f16_rows, dim3((F + 2047) / 2048, rows_b), dim3(256), 0, s, (const float *)g_lib_scratch,
-           rows_b, F, out_f16, o.row_err, o.err_rows);
-  return true;
+  if (!g_prefill_mfma || rows_b < kPrefillRows || w.dtype != kFmtF16) return false;
+  return gemm_f16(s, kEpiSwiglu, w, act.f16, rows_b, o, out_f16);
 }
 
 template <int kEpi>
 static void mv_f16(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
                    const MatvecOut &o) {
   const int out_rows = kEpi == kEpiSwiglu ? w.rows / 2 : w.rows;
-  // tall packed batches: matrix cores (f32 sums); the head always stays exact
-  // the head of a step in the packed-prefill regime: the same matrix-core
-  // GEMM, 64 rows per workgroup, partial keys per 16-row tile
-  if (kEpi == kEpiArgmax && g_head_mfma && rows_b >= 16 && w.K % kGemmBK == 0) {
-    launch_k(k_gemm_f16<kEpi, 2, kGemmStages2>, dim3((w.rows + kGemmBM - 1) / kGemmBM, (rows_b + 63) / 64),
-             dim3(256), kGemmStages2 * (128 + 64) * 64, s, w, (const uint16_t *)act.f16, rows_b, o);
+  // the head of a step in the packed-prefill regime (16+ logit rows): the
+  // regime's GEMM with partial keys per 16-row tile
+  if (kEpi == kEpiArgmax && g_head_mfma && rows_b >= 16 &&
+      gemm_f16(s, kEpiArgmax, w, act.f16, rows_b, o, nullptr))
     return;
-  }
-  if (kEpi != kEpiArgmax && g_prefill_mfma && g_lib && rows_b >= kPrefillRows) {
-    // library GEMM; non-finite outputs of the plain and residual forms are
-    // flagged by the row's next consumer (norm, attention) as the same error
-    if (kEpi == kEpiStore || kEpi == kEpiResidual) {
-      lib_mark_begin(s);
-      if (gemm_lib_f16(g_lib, s, w.f16, w.rows, w.K, (const uint16_t *)act.f16, rows_b, o.out, o.ld,
-                       kEpi == kEpiResidual)) {
-        lib_mark_end(s);
-        return;
-      }
-    } else if (kEpi == kEpiSwiglu && (size_t)rows_b * w.rows <= g_lib_scratch_floats) {
-      lib_mark_begin(s);
-      if (gemm_lib_f16(g_lib, s, w.f16, w.rows, w.K, (const uint16_t *)act.f16, rows_b, g_lib_scratch, w.rows,
-                       false)) {
-        launch_k(k_swiglu_rows, dim3((out_rows + 1023) / 1024, rows_b), dim3(256), 0, s,
-                 (const float *)g_lib_scratch, rows_b, out_rows, o.out, o.ld, o.row_err, o.err_rows);
-        return;
-      }
-    }
-  }
-  if (kEpi != kEpiArgmax && g_prefill_mfma && rows_b >= kPrefillRows && w.K % kGemmBK == 0 &&
-      (kEpi != kEpiSwiglu || out_rows % (kGemmBM / 2) == 0)) {
-    const int ftile = kEpi == kEpiSwiglu ? kGemmBM / 2 : kGemmBM;
-    const int fblocks = (out_rows + ftile - 1) / ftile;
-    // 128-row workgroups unless that leaves CUs idle; then 64-row ones
-    // LDS: kStages stages of (128 weight rows + the workgroup's rows) x 64 bytes
-    if (fblocks * ((rows_b + 127) / 128) >= 512)
-      launch_k(k_gemm_f16<kEpi, 4, kGemmStages4>, dim3(fblocks, (rows_b + 127) / 128), dim3(256),
-               kGemmStages4 * (128 + 128) * 64, s, w, (const uint16_t *)act.f16, rows_b, o);
-    else
-      launch_k(k_gemm_f16<kEpi, 2, kGemmStages2>, dim3(fblocks, (rows_b + 63) / 64), dim3(256),
-               kGemmStages2 * (128 + 64) * 64, s, w, (const uint16_t *)act.f16, rows_b, o);
+  // tall packed batches of a prefill step: matrix cores (f32 sums); gate+up
+  // with SwiGLU goes through launch_matvec_swiglu_f16
+  if ((kEpi == kEpiStore || kEpi == kEpiResidual) && g_prefill_mfma && rows_b >= kPrefillRows &&
+      gemm_f16(s, (Epilogue)kEpi, w, act.f16, rows_b, o, nullptr))
     return;
-  }
   if (rows_b >= 16 && w.K % 8 == 0) {  // lane = batch row, sequential f64 chains
     launch_k(k_mv_f16s<kEpi>, dim3((out_rows + 15) / 16, (rows_b + kWave - 1) / kWave), dim3(256), 0,
              s, w, act, rows_b, o);

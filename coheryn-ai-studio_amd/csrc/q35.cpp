@@ -25,7 +25,7 @@ namespace {
 
 int pad16(int n) { return (n + 15) / 16 * 16; }
 
-// Packed batches at least this tall take the library GEMMs (regime on).
+// Packed batches at least this tall take the matrix-core GEMM (regime on).
 constexpr uint32_t kQ35PrefillRows = 128;
 
 #define Q35_TRY(expr)                                                                  \
@@ -60,9 +60,6 @@ struct Q35Layer {
   uint16_t *out = nullptr;   // out_proj / o_proj
   uint16_t *gu = nullptr;    // [gate | up]
   uint16_t *down = nullptr;
-  // row-major copies [rows][K] of the four (padded rows zero) for the
-  // packed-prefill regime's library GEMMs; null when the regime is off
-  uint16_t *mix_rm = nullptr, *out_rm = nullptr, *gu_rm = nullptr, *down_rm = nullptr;
   float *q_norm = nullptr, *k_norm = nullptr;                      // full
   float *conv = nullptr, *a_log = nullptr, *dt = nullptr, *norm = nullptr;  // linear
 };
@@ -93,8 +90,8 @@ struct Q35Model {
   unsigned long long *h_argmax = nullptr;
   bool split_linear = false;  // COHX_Q35_SPLIT_LINEAR=1: the four-kernel mixer (tests)
   // packed-prefill regime: steps of kQ35PrefillRows+ rows run their linears
-  // as library GEMMs (f32 sums, within tolerance); a_hi/a_lo [rows][kmax]
-  // hold the activations' bfloat16 parts
+  // on the matrix-core GEMM (f32 sums, within tolerance); a_hi/a_lo
+  // [rows][kmax] hold the activations' bfloat16 parts
   bool mfma = false;
   int kmax = 0;
   uint16_t *a_hi = nullptr, *a_lo = nullptr;
@@ -108,15 +105,13 @@ struct Q35Model {
 namespace {
 
 // Upload one BF16 matrix [rows][K] into rows [off, off + rows) of a tiled
-// buffer (the part padded to 16 rows with zeros) and, when given, of a
-// row-major copy (its padding rows stay zero).
-int put_matrix(cohx_ctx *ctx, uint16_t *dst, uint16_t *dst_rm, int off, int rows, int K, const uint16_t *src) {
+// buffer (the part padded to 16 rows with zeros).
+int put_matrix(cohx_ctx *ctx, uint16_t *dst, int off, int rows, int K, const uint16_t *src) {
   const int rp = pad16(rows);
   std::vector<uint16_t> tiled((size_t)rp * K, 0);
   for (int r = 0; r < rows; r++)
     for (int k = 0; k < K; k++) tiled[q35_tiled_index(r, k, K)] = src[(size_t)r * K + k];
   Q35_TRY(hipMemcpy(dst + (size_t)off * K, tiled.data(), tiled.size() * 2, hipMemcpyHostToDevice));
-  if (dst_rm) Q35_TRY(hipMemcpy(dst_rm + (size_t)off * K, src, (size_t)rows * K * 2, hipMemcpyHostToDevice));
   return COHX_OK;
 }
 
@@ -177,9 +172,8 @@ int cohx_create_qwen35(const cohx_qwen35_desc *dd, int device, cohx_ctx **out) {
   ctx->device = device;
   ctx->use_graphs = false;
   // COHX_PREFILL_MFMA=0 keeps tall packed steps on the exact (f64-sum)
-  // matvecs; the regime needs the library GEMMs (COHX_GEMM_LIB=0: off)
+  // matvecs
   if (const char *g = std::getenv("COHX_PREFILL_MFMA")) ctx->prefill_mfma = std::strcmp(g, "0") != 0;
-  if (const char *g = std::getenv("COHX_GEMM_LIB")) ctx->use_gemm_lib = std::strcmp(g, "0") != 0;
   cohx_model_desc &m = ctx->desc;
   m.layers = d.layers;
   m.hidden = d.hidden;
@@ -233,7 +227,7 @@ int cohx_create_qwen35(const cohx_qwen35_desc *dd, int device, cohx_ctx **out) {
   q->max_rows = (int)d.max_rows;
   q->max_lanes = (int)d.max_lanes;
   if (const char *e = std::getenv("COHX_Q35_SPLIT_LINEAR")) q->split_linear = std::atoi(e) != 0;
-  q->mfma = ctx->prefill_mfma && ctx->use_gemm_lib && d.max_rows >= kQ35PrefillRows;
+  q->mfma = ctx->prefill_mfma && d.max_rows >= kQ35PrefillRows;
   q->kmax = std::max(std::max(q->H, q->F), std::max(q->qw, q->vals));
   int rc = 0;
   const hipError_t e0 = hipSetDevice(device);
@@ -253,10 +247,6 @@ int cohx_create_qwen35(const cohx_qwen35_desc *dd, int device, cohx_ctx **out) {
     if (!rc) rc = q35_alloc(ctx, &L.post_norm, H);
     if (!rc) rc = q35_alloc(ctx, &L.gu, (size_t)q->gu_rows * H);
     if (!rc) rc = q35_alloc(ctx, &L.down, (size_t)q->h_rows * q->F);
-    if (!rc && q->mfma) rc = q35_alloc(ctx, &L.gu_rm, (size_t)q->gu_rows * H);
-    if (!rc && q->mfma) rc = q35_alloc(ctx, &L.down_rm, (size_t)q->h_rows * q->F);
-    if (!rc && q->mfma) rc = q35_alloc(ctx, &L.mix_rm, (size_t)(L.full ? q->full_rows : q->lin_rows) * H);
-    if (!rc && q->mfma) rc = q35_alloc(ctx, &L.out_rm, (size_t)q->h_rows * (L.full ? q->qw : q->vals));
     if (rc) break;
     if (L.full) {
       rc = q35_alloc(ctx, &L.mix, (size_t)q->full_rows * H);
@@ -368,7 +358,7 @@ int q35_upload(cohx_ctx *ctx, const char *name, uint32_t dtype, uint64_t ne0, ui
   const std::string n(name);
   if (q->uploaded.count(n)) return fail(ctx, COHX_INVALID_GGUF, "tensor uploaded twice: " + n);
   const int H = q->H;
-  auto matrix = [&](uint16_t *dst, uint16_t *dst_rm, int off, int rows, int K) -> int {
+  auto matrix = [&](uint16_t *dst, int off, int rows, int K) -> int {
     if (dtype != COHX_BF16)
       return fail(ctx, COHX_UNSUPPORTED, "Qwen3.5 matrices must be BF16 on the GPU: " + n);
     if (ne0 != (uint64_t)K || ne1 != (uint64_t)rows || bytes != (size_t)rows * K * 2)
@@ -376,7 +366,7 @@ int q35_upload(cohx_ctx *ctx, const char *name, uint32_t dtype, uint64_t ne0, ui
     if (!finite_bf16(static_cast<const uint16_t *>(data), (size_t)rows * K))
       return fail(ctx, COHX_INVALID_GGUF, "non-finite weight in " + n);
     q->matrix_bytes += (uint64_t)rows * K * 2;
-    return put_matrix(ctx, dst, dst_rm, off, rows, K, static_cast<const uint16_t *>(data));
+    return put_matrix(ctx, dst, off, rows, K, static_cast<const uint16_t *>(data));
   };
   auto vector = [&](float *dst, size_t len) -> int {
     if (ne0 * std::max<uint64_t>(ne1, 1) != len)
@@ -391,12 +381,12 @@ int q35_upload(cohx_ctx *ctx, const char *name, uint32_t dtype, uint64_t ne0, ui
     if (!finite_bf16(static_cast<const uint16_t *>(data), (size_t)q->V * H))
       return fail(ctx, COHX_INVALID_GGUF, "non-finite weight in " + n);
     Q35_TRY(hipMemcpy(q->embed, data, bytes, hipMemcpyHostToDevice));  // row gather
-    rc = q->d.tied ? matrix(q->head, nullptr, 0, q->V, H) : COHX_OK;             // tied head tiles
+    rc = q->d.tied ? matrix(q->head, 0, q->V, H) : COHX_OK;             // tied head tiles
   } else if (n == "model.language_model.norm.weight") {
     rc = vector(q->final_norm, H);
   } else if (n == "lm_head.weight") {
     if (q->d.tied) return fail(ctx, COHX_UNSUPPORTED, "lm_head.weight with tied embeddings");
-    rc = matrix(q->head, nullptr, 0, q->V, H);
+    rc = matrix(q->head, 0, q->V, H);
   } else {
     const std::string pre = "model.language_model.layers.";
     if (n.compare(0, pre.size(), pre) != 0)
@@ -409,20 +399,20 @@ int q35_upload(cohx_ctx *ctx, const char *name, uint32_t dtype, uint64_t ne0, ui
     Q35Layer &L = q->layers[l];
     if (t == "input_layernorm.weight") rc = vector(L.input_norm, H);
     else if (t == "post_attention_layernorm.weight") rc = vector(L.post_norm, H);
-    else if (t == "mlp.gate_proj.weight") rc = matrix(L.gu, L.gu_rm, 0, q->F, H);
-    else if (t == "mlp.up_proj.weight") rc = matrix(L.gu, L.gu_rm, q->gu_up, q->F, H);
-    else if (t == "mlp.down_proj.weight") rc = matrix(L.down, L.down_rm, 0, H, q->F);
-    else if (L.full && t == "self_attn.q_proj.weight") rc = matrix(L.mix, L.mix_rm, 0, 2 * q->qw, H);
-    else if (L.full && t == "self_attn.k_proj.weight") rc = matrix(L.mix, L.mix_rm, q->full_k, q->kvw, H);
-    else if (L.full && t == "self_attn.v_proj.weight") rc = matrix(L.mix, L.mix_rm, q->full_v, q->kvw, H);
-    else if (L.full && t == "self_attn.o_proj.weight") rc = matrix(L.out, L.out_rm, 0, H, q->qw);
+    else if (t == "mlp.gate_proj.weight") rc = matrix(L.gu, 0, q->F, H);
+    else if (t == "mlp.up_proj.weight") rc = matrix(L.gu, q->gu_up, q->F, H);
+    else if (t == "mlp.down_proj.weight") rc = matrix(L.down, 0, H, q->F);
+    else if (L.full && t == "self_attn.q_proj.weight") rc = matrix(L.mix, 0, 2 * q->qw, H);
+    else if (L.full && t == "self_attn.k_proj.weight") rc = matrix(L.mix, q->full_k, q->kvw, H);
+    else if (L.full && t == "self_attn.v_proj.weight") rc = matrix(L.mix, q->full_v, q->kvw, H);
+    else if (L.full && t == "self_attn.o_proj.weight") rc = matrix(L.out, 0, H, q->qw);
     else if (L.full && t == "self_attn.q_norm.weight") rc = vector(L.q_norm, q->D);
     else if (L.full && t == "self_attn.k_norm.weight") rc = vector(L.k_norm, q->D);
-    else if (!L.full && t == "linear_attn.in_proj_qkv.weight") rc = matrix(L.mix, L.mix_rm, 0, q->C, H);
-    else if (!L.full && t == "linear_attn.in_proj_z.weight") rc = matrix(L.mix, L.mix_rm, q->lin_z, q->vals, H);
-    else if (!L.full && t == "linear_attn.in_proj_a.weight") rc = matrix(L.mix, L.mix_rm, q->lin_a, q->VH, H);
-    else if (!L.full && t == "linear_attn.in_proj_b.weight") rc = matrix(L.mix, L.mix_rm, q->lin_b, q->VH, H);
-    else if (!L.full && t == "linear_attn.out_proj.weight") rc = matrix(L.out, L.out_rm, 0, H, q->vals);
+    else if (!L.full && t == "linear_attn.in_proj_qkv.weight") rc = matrix(L.mix, 0, q->C, H);
+    else if (!L.full && t == "linear_attn.in_proj_z.weight") rc = matrix(L.mix, q->lin_z, q->vals, H);
+    else if (!L.full && t == "linear_attn.in_proj_a.weight") rc = matrix(L.mix, q->lin_a, q->VH, H);
+    else if (!L.full && t == "linear_attn.in_proj_b.weight") rc = matrix(L.mix, q->lin_b, q->VH, H);
+    else if (!L.full && t == "linear_attn.out_proj.weight") rc = matrix(L.out, 0, H, q->vals);
     else if (!L.full && t == "linear_attn.conv1d.weight") rc = vector(L.conv, (size_t)q->C * q->K);
     else if (!L.full && t == "linear_attn.A_log") rc = vector(L.a_log, q->VH);
     else if (!L.full && t == "linear_attn.dt_bias") rc = vector(L.dt, q->VH);
@@ -582,33 +572,20 @@ int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out, const c
   const int H = q->H;
   const float eps = q->d.epsilon;
   // packed-prefill regime: a step of kQ35PrefillRows+ rows runs its linears
-  // as library GEMMs on the row-major copies (the recurrences, attention,
-  // norms and the head stay exact)
-  bool regime = q->mfma && R >= kQ35PrefillRows && !ctx->gemm_lib_failed;
-  if (regime && !ctx->gemm_lib) {
-    constexpr size_t kGemmWorkspace = 32u << 20;
-    uint8_t *gws = nullptr;
-    if (q35_alloc(ctx, &gws, kGemmWorkspace) == COHX_OK) ctx->gemm_lib = gemm_lib_create(gws, kGemmWorkspace);
-    if (!ctx->gemm_lib) {
-      ctx->gemm_lib_failed = true;
-      (void)hipGetLastError();
-      regime = false;
-    }
-  }
+  // on the matrix-core GEMM over the tiled matrices (the recurrences,
+  // attention, norms and the head stay exact)
+  const bool regime = q->mfma && R >= kQ35PrefillRows;
   // One linear layer, out (=, +=) x . W^T: in the regime the f32 rows enter
-  // as their bfloat16 hi and lo parts (two GEMMs with f32 sums, the residual
-  // taken in by the first), then the matvecs' non-finite row check; else (or
-  // when the library has no algorithm for the shape) the exact matvec.
-  auto linear = [&](int epi, const uint16_t *w, const uint16_t *w_rm, int rows_w, int valid, int K,
-                    const float *x, int ldx, float *o, int ldo) -> int {
-    if (regime && w_rm) {
+  // as their bfloat16 hi and lo parts, both multiplied into the same f32
+  // sums (the residual taken in by the accumulate epilogue, non-finite
+  // outputs flagged per row); else (or for K not a multiple of 64) the exact
+  // matvec.
+  auto linear = [&](int epi, const uint16_t *w, int rows_w, int valid, int K, const float *x, int ldx, float *o,
+                    int ldo) -> int {
+    if (regime && K % 64 == 0) {
       q35_split_bf16(s, (int)R, K, x, ldx, q->a_hi, q->a_lo);
-      if (gemm_lib_bf16(ctx->gemm_lib, s, w_rm, valid, K, q->a_hi, (int)R, o, ldo, epi == kQ35Residual)) {
-        if (!gemm_lib_bf16(ctx->gemm_lib, s, w_rm, valid, K, q->a_lo, (int)R, o, ldo, true))
-          return fail(ctx, COHX_DEVICE, "library GEMM failed after its first half");
-        q35_check_finite(s, (int)R, valid, o, ldo, q->row_err);
-        return COHX_OK;
-      }
+      q35_gemm_split(s, epi == kQ35Residual, w, valid, K, q->a_hi, q->a_lo, (int)R, o, ldo, q->row_err);
+      return COHX_OK;
     }
     q35_matvec(s, epi, w, rows_w, valid, K, x, ldx, (int)R, o, ldo, nullptr, q->row_err, nullptr);
     return COHX_OK;
@@ -618,7 +595,7 @@ int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out, const c
   for (const Q35Layer &Ly : q->layers) {
     q35_norm(s, (int)R, q->x, H, nullptr, Ly.input_norm, H, eps, 1, q->nrm, H, q->row_err, nullptr);
     if (!Ly.full) {
-      if ((lrc = linear(kQ35Store, Ly.mix, Ly.mix_rm, q->lin_rows, q->lin_rows, H, q->nrm, H, q->mix_out,
+      if ((lrc = linear(kQ35Store, Ly.mix, q->lin_rows, q->lin_rows, H, q->nrm, H, q->mix_out,
                         q->ld_mix)))
         return lrc;
       // one launch for the mixer when every lane is a decode row or a short
@@ -639,10 +616,10 @@ int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out, const c
                   q->delta_state + (size_t)Ly.slot * q->VH * q->KD * q->VD, q->delta_seq,
                   q->gates, q->att, q->tgt, q->ld_att, q->row_err);
       }
-      if ((lrc = linear(kQ35Residual, Ly.out, Ly.out_rm, q->h_rows, H, q->vals, q->tgt, q->ld_att, q->x, H)))
+      if ((lrc = linear(kQ35Residual, Ly.out, q->h_rows, H, q->vals, q->tgt, q->ld_att, q->x, H)))
         return lrc;
     } else {
-      if ((lrc = linear(kQ35Store, Ly.mix, Ly.mix_rm, q->full_rows, q->full_rows, H, q->nrm, H, q->mix_out,
+      if ((lrc = linear(kQ35Store, Ly.mix, q->full_rows, q->full_rows, H, q->nrm, H, q->mix_out,
                         q->ld_mix)))
         return lrc;
       q35_qk(s, (int)R, Rw, q->mix_out, q->ld_mix, q->full_k, q->full_v, Ly.q_norm, Ly.k_norm,
@@ -651,18 +628,18 @@ int q35_step(cohx_ctx *ctx, const cohx_batch *batch, cohx_step_out *out, const c
       q35_attention(s, (int)R, Rw, q->q, q->z, q->qw, q->kc + Ly.slot * q->kv_layer,
                     q->vc + Ly.slot * q->kv_layer, q->kv_seq, q->NH, q->NKV, q->D,
                     (int)d.max_context, q->scores, q->att, q->ld_att);
-      if ((lrc = linear(kQ35Residual, Ly.out, Ly.out_rm, q->h_rows, H, q->qw, q->att, q->ld_att, q->x, H)))
+      if ((lrc = linear(kQ35Residual, Ly.out, q->h_rows, H, q->qw, q->att, q->ld_att, q->x, H)))
         return lrc;
     }
     q35_norm(s, (int)R, q->x, H, nullptr, Ly.post_norm, H, eps, 1, q->nrm, H, q->row_err, nullptr);
     if (regime || !q35_matvec_swiglu(s, Ly.gu, q->gu_up, q->F, H, q->nrm, H, (int)R, q->hb, q->F,
                                      q->row_err)) {
-      if ((lrc = linear(kQ35Store, Ly.gu, Ly.gu_rm, q->gu_rows, q->gu_rows, H, q->nrm, H, q->gu_out,
+      if ((lrc = linear(kQ35Store, Ly.gu, q->gu_rows, q->gu_rows, H, q->nrm, H, q->gu_out,
                         q->gu_rows)))
         return lrc;
       q35_swiglu(s, (int)R, q->gu_out, q->gu_rows, q->F, q->gu_up, q->hb, q->F);
     }
-    if ((lrc = linear(kQ35Residual, Ly.down, Ly.down_rm, q->h_rows, H, q->F, q->hb, q->F, q->x, H)))
+    if ((lrc = linear(kQ35Residual, Ly.down, q->h_rows, H, q->F, q->hb, q->F, q->x, H)))
       return lrc;
   }
   // final norm and head over the last row of each lane that needs them

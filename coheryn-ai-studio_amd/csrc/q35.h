@@ -55,11 +55,15 @@ void q35_matvec(hipStream_t s, int epi, const uint16_t *w, int rows_w, int valid
 int q35_matvec_blocks(int rows_w);
 // Packed-prefill regime: rows x[rows][K] (stride ldx; K and ldx multiples of
 // 4) as bfloat16 pairs hi = bf16(x), lo = bf16(x - hi) into hi/lo[rows][K],
-// the operands of the library GEMMs that replace q35_matvec there.
+// the operands of q35_gemm_split.
 void q35_split_bf16(hipStream_t s, int rows, int K, const float *x, int ldx, uint16_t *hi, uint16_t *lo);
-// row_err[r] |= the matvecs' non-finite bit for rows of out[rows][N] (stride
-// ldo, N % 4 == 0) holding a non-finite value.
-void q35_check_finite(hipStream_t s, int rows, int N, const float *out, int ldo, uint32_t *row_err);
+// Packed-prefill regime linear on the matrix cores (gemm.h): out[r][n] (=, or
+// += with accumulate) sum_k (hi[r][k] + lo[r][k]) * w[n][k] for n < N, with w
+// the tiled matrix the exact matvecs read (q35_tiled_index, K % 64 == 0),
+// f32 sums; row_err[r] |= the matvecs' non-finite bit for rows with a
+// non-finite output.
+void q35_gemm_split(hipStream_t s, bool accumulate, const uint16_t *w, int N, int K, const uint16_t *hi,
+                    const uint16_t *lo, int rows, float *out, int ldo, uint32_t *row_err);
 // Gate+up and SwiGLU in one launch for few rows: h[r][f] = silu(gate) * up
 // with the bits of q35_matvec (gate rows [0, F), up rows [up_off, up_off + F))
 // followed by q35_swiglu.  Returns false (nothing launched) where q35_matvec

@@ -13,6 +13,7 @@
 #include <algorithm>
 
 #include "device.h"
+#include "gemm.h"
 #include "log1pf.h"
 #include "q35.h"
 
@@ -1154,8 +1155,8 @@ __global__ __launch_bounds__(576) void k_q35_attn(Q35Rows Rw, const float *__res
 }
 
 // ---------------------------------------------------------------------------
-// Packed-prefill regime (steps of 128+ rows): the linears run as library
-// GEMMs over a row-major BF16 copy of each matrix.  An f32 activation x enters
+// Packed-prefill regime (steps of 128+ rows): the linears run on the
+// matrix-core GEMM (gemm.h) over the tiled BF16 matrices.  An f32 activation x enters
 // as hi = bf16(x) and lo = bf16(x - hi) (round to nearest even), so hi + lo
 // is x to a relative 2^-17 or better, every product of two bfloat16 values is
 // exact in f32, and the f32 sums of hi . w + lo . w are what differ from the
@@ -1179,19 +1180,6 @@ __global__ __launch_bounds__(256) void k_q35_split(const float *__restrict__ x, 
       make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16);
   *reinterpret_cast<uint2 *>(lo + (size_t)r * K + k) =
       make_uint2(l[0] | (uint32_t)l[1] << 16, l[2] | (uint32_t)l[3] << 16);
-}
-
-// The matvecs' non-finite output check for the library GEMM's rows: block =
-// one row of out[.][N] (N % 4 == 0).
-__global__ __launch_bounds__(256) void k_q35_finite(const float *__restrict__ out, int ldo, int N,
-                                                    uint32_t *row_err) {
-  const int r = blockIdx.x;
-  bool bad = false;
-  for (int k = threadIdx.x * 4; k < N; k += 1024) {
-    const float4 v = *reinterpret_cast<const float4 *>(out + (size_t)r * ldo + k);
-    bad |= !finitef(v.x) || !finitef(v.y) || !finitef(v.z) || !finitef(v.w);
-  }
-  if (__syncthreads_or(bad) && threadIdx.x == 0) atomicOr(&row_err[r], kErrNonFinite);
 }
 
 }  // namespace
@@ -1265,8 +1253,33 @@ void q35_split_bf16(hipStream_t s, int rows, int K, const float *x, int ldx, uin
   hipLaunchKernelGGL(k_q35_split, dim3((K / 4 + 255) / 256, rows), dim3(256), 0, s, x, ldx, K, hi, lo);
 }
 
-void q35_check_finite(hipStream_t s, int rows, int N, const float *out, int ldo, uint32_t *row_err) {
-  hipLaunchKernelGGL(k_q35_finite, dim3(rows), dim3(256), 0, s, out, ldo, N, row_err);
+// Tiles measured on the Qwen3.5 prompt-chunk shapes (2,616 rows, hi and lo
+// products counted): 128 x 128 with two K steps in flight for the input-side
+// projections (mix 8,224 x 1024: 138 us; gate+up 7,168 x 1024: 108 us), four
+// for the residual ones (out K 2048: 41 us; down K 3584: 67 us).
+void q35_gemm_split(hipStream_t s, bool accumulate, const uint16_t *w, int N, int K, const uint16_t *hi,
+                    const uint16_t *lo, int rows, float *out, int ldo, uint32_t *row_err) {
+  using namespace gemm;
+  Args g{};
+  g.w = w;
+  g.w_tiled = 1;
+  g.x = hi;
+  g.xlo = lo;
+  g.N = N;
+  g.K = K;
+  g.M = rows;
+  g.ldx = K;
+  g.out = out;
+  g.ldo = ldo;
+  g.row_err = row_err;
+  const dim3 grid(tile_order(g, N, 128, 128));
+  constexpr int lds = lds_bytes<2, 2, 4, 4, true, kStore>();
+  if (accumulate && K % 128 == 0)
+    hipLaunchKernelGGL((k_gemm<kBF16, true, 2, 2, 4, 4, 4, kAccumulate>), grid, dim3(256), lds, s, g);
+  else if (accumulate)
+    hipLaunchKernelGGL((k_gemm<kBF16, true, 2, 2, 4, 4, 2, kAccumulate>), grid, dim3(256), lds, s, g);
+  else
+    hipLaunchKernelGGL((k_gemm<kBF16, true, 2, 2, 4, 4, 2, kStore>), grid, dim3(256), lds, s, g);
 }
 
 bool q35_matvec_swiglu(hipStream_t s, const uint16_t *w, int up_off, int F, int K, const float *x,

@@ -73,7 +73,15 @@ fn main() {
         println!("cargo:rerun-if-changed={}", path.display());
         objects.push(obj);
     }
-    for header in ["csrc/device.h", "csrc/kernels.h", "csrc/internal.h", "csrc/q35.h", "csrc/expf.h", "csrc/log1pf.h"] {
+    for header in [
+        "csrc/device.h",
+        "csrc/gemm.h",
+        "csrc/kernels.h",
+        "csrc/internal.h",
+        "csrc/q35.h",
+        "csrc/expf.h",
+        "csrc/log1pf.h",
+    ] {
         println!("cargo:rerun-if-changed={}", src_dir.join(header).display());
     }
     println!("cargo:rerun-if-changed={}", src_dir.join("build.manifest").display());

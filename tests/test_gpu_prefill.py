@@ -4,7 +4,8 @@ the matrix cores with f32 sums instead of the reference's f64 sums
 logits (max-abs 1e-2), not bit for bit.  Greedy ids must agree wherever the
 reference's top-2 margin exceeds the measured difference.  The same steps
 with the matrix-core path switched off (COHX_PREFILL_MFMA=0) stay bit-exact
-against the oracle."""
+against the oracle, and so does a decode-only step of the regime's width
+(the regime is for steps that carry prompt rows)."""
 import os
 
 import numpy as np
@@ -180,3 +181,39 @@ def test_regime_head_on_matrix_cores_matches_oracle():
         if res["mfma"][i]["argmax"] != res["exact"][i]["argmax"]:
             order = np.sort(w)
             assert order[-1] - order[-2] <= 2 * float(np.abs(res["mfma"][i]["logits"] - w).max()), i
+
+
+def test_wide_f16_decode_step_stays_exact():
+    """A decode-only F16 step of 130 rows, as wide as the regime's steps,
+    keeps the exact kernels (one f64 chain per dot, the exact head): every
+    lane's logits and greedy id equal the oracle's bit for bit, with the
+    regime switched on."""
+    print("case: F16 decode-only step of 130 lanes with the regime on: exact", flush=True)
+    cfg = synth.config(layers=2, hidden=128, intermediate=256, heads=4, kv_heads=2,
+                       vocabulary=300, context=512)
+    c, t = synth.in_memory(cfg, "f16", seed=37)
+    n = 130
+    m = make(c, t, True, max_lanes=n, max_rows=n, max_seqs=n, max_context=256)
+    o = orc.Model(c, t, threads=8)
+    rng = np.random.default_rng(17)
+    toks = [int(v) for v in rng.integers(0, c["vocabulary"], n)]
+    seqs, sess = [], []
+    for i in range(n):
+        s = m.seq_alloc()
+        m.seq_fill_synthetic(s, 10 + i, 19, i)
+        seqs.append(s)
+        so = o.session(256)
+        so.fill_synthetic(10 + i, 19, i)
+        sess.append(so)
+    res = m.step([dict(seq=s, tokens=[tk], logits=True) for s, tk in zip(seqs, toks)])
+    for u in range(0, n, 16):  # the oracle's units of at most 16 lanes
+        o.forward_batch(sess[u:u + 16], toks[u:u + 16])
+    differ = 0
+    for i, (r, so) in enumerate(zip(res, sess)):
+        assert r["status"] == 0, i
+        want = so.logits()
+        differ += int(np.count_nonzero(r["logits"].view(np.uint32) != want.view(np.uint32)))
+        assert r["argmax"] == orc.Sampler().sample(want)[1], i
+    print(f"case: {differ} differing logits of {n * c['vocabulary']}", flush=True)
+    assert differ == 0
+    m.close()

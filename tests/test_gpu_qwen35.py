@@ -32,7 +32,8 @@ REGIME_STATE_TOL = 1e-3
 
 def make_q35(cfg, t, regime, **kw):
     """A GPU context; regime False keeps every step on the exact matvecs
-    (COHX_PREFILL_MFMA=0), True lets steps of 128+ rows take the library GEMMs."""
+    (COHX_PREFILL_MFMA=0), True lets steps of 128+ rows take the matrix-core
+    GEMM."""
     old = os.environ.get("COHX_PREFILL_MFMA")
     os.environ["COHX_PREFILL_MFMA"] = "1" if regime else "0"
     try:
@@ -163,36 +164,9 @@ def test_tiny_large_packed_step_bit_exact():
     _large_packed_tiny(False)
 
 
-def test_tiny_large_packed_step_without_library_stays_exact(monkeypatch):
-    print("case: tiny Qwen3.5, 141 packed rows with the regime asked for but the library GEMMs off "
-          "(COHX_GEMM_LIB=0): the exact matvecs, bit for bit", flush=True)
-    monkeypatch.setenv("COHX_GEMM_LIB", "0")
-    cfg, t = synth35.in_memory(tiny(), seed=12)
-    p = Pair(cfg, t, max_lanes=4, max_rows=160, max_context=160)
-    p.gpu.close()
-    old = os.environ.get("COHX_PREFILL_MFMA")
-    os.environ["COHX_PREFILL_MFMA"] = "1"
-    try:
-        p.gpu = cohx.Qwen35(cfg, t, max_lanes=4, max_rows=160, max_context=160)
-    finally:
-        if old is None:
-            del os.environ["COHX_PREFILL_MFMA"]
-        else:
-            os.environ["COHX_PREFILL_MFMA"] = old
-    a, b, c = p.alloc(), p.alloc(), p.alloc()
-    rng = np.random.default_rng(13)
-    pa = [int(v) for v in rng.integers(0, cfg["vocabulary"], 100)]
-    pb = [int(v) for v in rng.integers(0, cfg["vocabulary"], 40)]
-    (tc,) = p.step([(c, [5, 6])])
-    ta, tb, tc = p.step([(a, pa), (b, pb), (c, [tc])])
-    p.step([(a, [ta]), (b, [tb]), (c, [tc])])
-    for s_ in (a, b, c):
-        p.check_state(s_)
-
-
 def test_tiny_large_packed_step_prefill_regime_within_tolerance():
-    print("case: tiny Qwen3.5, 141 packed rows through the packed-prefill regime (library "
-          "BF16 GEMMs on hi/lo activations)", flush=True)
+    print("case: tiny Qwen3.5, 141 packed rows through the packed-prefill regime (matrix-core "
+          "BF16 GEMM on hi/lo activations over the tiled matrices)", flush=True)
     p = _large_packed_tiny(True)
     print(f"case: worst logit max-abs {p.worst_logit:.3g}, worst state {p.worst_state:.3g}", flush=True)
 
