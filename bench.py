@@ -523,7 +523,7 @@ def summarize_trace(trace_csv, bench_json):
 C5_TRACE_CMD = ("rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o <name> -- "
                 "python3 bench.py --c5-only --no-cpu-baseline")
 C5_PMC_CMD = ("rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_MOPS_BF16 "
-              "GRBM_GUI_ACTIVE --kernel-include-regex \"Cijk\" --output-format csv -d <dir> -o <name> -- "
+              "GRBM_GUI_ACTIVE --kernel-include-regex \"k_gemm\" --output-format csv -d <dir> -o <name> -- "
               "python3 bench.py --c5-only --no-cpu-baseline")
 
 
@@ -640,7 +640,7 @@ def summarize_leg(leg, trace_csv, bench_json, fetch_csv=None, write_csv=None, mf
         cw = counter_means(copy_write_csv)["__amd_rocclr_copyBuffer"][0] * 1024
         ff, fw = float(1 << 30) / cf, float(1 << 30) / cw
         fetch, write = counter_means(fetch_csv), counter_means(write_csv)
-        print(f"\nHBM traffic: `{LEG_PMC_CMD.format(counters='FETCH_SIZE', regex='k_|Cijk', leg=leg)}`, then "
+        print(f"\nHBM traffic: `{LEG_PMC_CMD.format(counters='FETCH_SIZE', regex='k_', leg=leg)}`, then "
               f"`WRITE_SIZE`; scaled by the same counters over a 1 GiB copy (`{COPY_CMD.format(counter='FETCH_SIZE')}`: "
               f"factors {ff:.4f} fetch, {fw:.4f} write).\n")
         print("| kernel | dispatches | FETCH KiB | WRITE KiB | HBM bytes per launch |")
@@ -649,7 +649,7 @@ def summarize_leg(leg, trace_csv, bench_json, fetch_csv=None, write_csv=None, mf
             wk = write.get(k, (0.0, 0))[0]
             print(f"| {k} | {n} | {fk:.0f} | {wk:.0f} | {(fk * ff + wk * fw) * 1024 / 1e6:.2f} MB |")
     if mfma_csv:
-        print_mfma_table(mfma_csv, LEG_PMC_CMD.format(counters=MFMA_COUNTERS, regex='k_gemm_f16|k_attn_chunk|Cijk',
+        print_mfma_table(mfma_csv, LEG_PMC_CMD.format(counters=MFMA_COUNTERS, regex='k_gemm|k_attn_chunk',
                                                       leg=leg))
     print(f"\nSummary: `python3 bench.py --summarize-leg {leg} <trace.csv> <bench stdout> [<fetch.csv> "
           f"<write.csv> <mfma.csv or -> <copy_fetch.csv> <copy_write.csv>]`")
