@@ -430,11 +430,13 @@ __device__ __forceinline__ void argmax_commit(float best, int best_row, bool val
 // lanes, one 16-bit load per lane per 64 values.  Slot s = v * 64 + lane:
 // s < kNM * 32 is weight tile s / 32, block 2p + (s % 32) / 16, row s % 16;
 // the next 32 are the batch tile's, block 2p + (s % 32) / 16, batch row s % 16.
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+
 template <int kNM>
 struct Q8Regs {
   static constexpr int kSV = (kNM + 2) / 2;  // scale values per lane
-  uint4 a[kNM];
-  uint4 b;
+  u32x4v a[kNM];
+  u32x4v b;
   uint16_t sc[kSV];
 };
 
@@ -450,13 +452,13 @@ __device__ __forceinline__ void q8_load(Q8Regs<kNM> &r, const MatrixView &w, con
 #pragma unroll
   for (int m = 0; m < kNM; m++) {
     if constexpr (kFmt == 8) {
-      r.a[m] = *reinterpret_cast<const uint4 *>(w.qs + q8_byte(unit * kNM + m, nbp, pair * 2, lane, 0));
+      r.a[m] = *reinterpret_cast<const u32x4v *>(w.qs + q8_byte(unit * kNM + m, nbp, pair * 2, lane, 0));
     } else {
       const uint2 v = *reinterpret_cast<const uint2 *>(w.qs + q4_byte(unit * kNM + m, nbp, pair * 2, lane, 0));
-      r.a[m] = make_uint4(v.x, v.y, 0u, 0u);
+      r.a[m] = u32x4v{v.x, v.y, 0u, 0u};
     }
   }
-  r.b = *reinterpret_cast<const uint4 *>(act.qs + q8_byte(nt, nbp, pair * 2, lane, 0));
+  r.b = *reinterpret_cast<const u32x4v *>(act.qs + q8_byte(nt, nbp, pair * 2, lane, 0));
 #pragma unroll
   for (int v = 0; v < Q8Regs<kNM>::kSV; v++) {
     const int sl = v * 64 + lane;
@@ -467,6 +469,12 @@ __device__ __forceinline__ void q8_load(Q8Regs<kNM> &r, const MatrixView &w, con
   }
 }
 
+__device__ __forceinline__ long lo64(u32x4v v) {
+  return (long)(((unsigned long)v[1] << 32) | v[0]);
+}
+__device__ __forceinline__ long hi64(u32x4v v) {
+  return (long)(((unsigned long)v[3] << 32) | v[2]);
+}
 __device__ __forceinline__ long lo64(uint4 v) {
   return (long)(((unsigned long)v.y << 32) | v.x);
 }
@@ -511,10 +519,14 @@ __global__ __launch_bounds__(64 * kW) void k_mv_q8s(MatrixView w, ActView act, i
 #pragma unroll
     for (int u = 0; u < kD; u++) {
       const int c = c0 + u;
+      // chunks past the last prefetch a clamped (valid, unused) pair rather
+      // than branch, and the prefetch is issued on every path, also for a
+      // chunk past the end: a path without it would make the compiler wait
+      // for every load in flight where the paths meet (the loop head),
+      // including the prefetch of the next chunk
+      q8_load<kNM, kFmt>(ring[(u + kD - 1) % kD], w, act, unit, nt, min((c + kD - 1) * kW + wave, npairs - 1),
+                         lane);
       if (c < nchunks) {
-        // chunks past the last prefetch a clamped (valid, unused) pair rather than branch
-        q8_load<kNM, kFmt>(ring[(u + kD - 1) % kD], w, act, unit, nt,
-                           min((c + kD - 1) * kW + wave, npairs - 1), lane);
         const Q8Regs<kNM> &cur = ring[u];
         if (c * kW + wave < npairs) {
 #pragma unroll
@@ -527,7 +539,7 @@ __global__ __launch_bounds__(64 * kW) void k_mv_q8s(MatrixView w, ActView act, i
               if constexpr (kFmt == 8)
                 aop = h ? hi64(cur.a[m]) : lo64(cur.a[m]);
               else
-                aop = q4_operand(h ? cur.a[m].y : cur.a[m].x);
+                aop = q4_operand(h ? cur.a[m][1] : cur.a[m][0]);
               const v4i s4 = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, zero, 0, 0, 0);
 #pragma unroll
               for (int i = 0; i < 4; i++)
