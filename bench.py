@@ -271,15 +271,20 @@ def c4_cpu_baseline(c, steps, threads):
 
 C3_CHUNKS, C3_DECODE, C3_CONTEXT = 8, 56, 4608
 MFMA_F16_PEAK = 2.5e15
+MFMA_I8_PEAK = 5.0e15  # dense int8 (OP/s)
 
 
-def run_c3(seed, steps, warmup):
+def run_c3(seed, steps, warmup, dtype="f16"):
     """F16 weights; every step packs 8 prompt chunks of
     U[128,512] tokens (each sequence continuing its prompt) with 56 greedy
     decode rows over KV U[256,4096].  Linears of packed batches run on the
     matrix cores (f32 sums; tolerance-checked by the tests).  Reports packed
-    rows/s and the linears' achieved TFLOP/s against the dense fp16 peak."""
-    path = model_file(seed, "f16")
+    rows/s and the linears' achieved TFLOP/s against the dense fp16 peak.
+    dtype "q8_0": the same schedule on Q8_0 weights, which take the exact
+    path (int8 MFMA block sums and the reference's f32 chain per block,
+    exact attention): the quantized prefill rate, and the linears' int8 MFMA
+    work against the int8 peak."""
+    path = model_file(seed, dtype)
     meta, tensors = gguf.read(path)
     cfg = gguf.qwen2_config(meta)
     n = C3_CHUNKS + C3_DECODE
@@ -333,8 +338,21 @@ def run_c3(seed, steps, warmup):
     lin_ms = sum(x["total_ms"] for x in lin)
     ms = elapsed * 1e3 / steps
     tflops = lin_flops / (lin_ms / 1e3) / 1e12 if lin_ms else 0.0
-    log(f"[bench] c3: {rows / elapsed:.0f} packed rows/s, {ms:.2f} ms/step, linears "
+    log(f"[bench] c3 {dtype}: {rows / elapsed:.0f} packed rows/s, {ms:.2f} ms/step, linears "
         f"{tflops:.0f} TFLOP/s, replay same tokens: {same}")
+    if dtype != "f16":
+        return {"workload": f"Qwen2.5-0.5B-shape {dtype.upper()}, C3's schedule (8 prompt chunks U[128,512] + "
+                            "56 decode rows over KV U[256,4096]) on the exact path: int8 MFMA block sums, "
+                            "the reference's f32 chain per block, exact attention",
+                "value": rows / elapsed, "unit": "packed rows/s", "ms_per_step": ms, "steps": steps,
+                "mean_rows_per_step": rows / steps,
+                "roofline": {"bound": "mfma", "kernel": "linears (exact int8 MFMA + f32 block chain)",
+                             "achieved": tflops, "peak": MFMA_I8_PEAK / 1e12, "unit": "TOP/s",
+                             "frac": tflops * 1e12 / MFMA_I8_PEAK,
+                             "note": "int8 operations of the block sums; the chain's 3 VALU per "
+                                     "(output, row, block) bound these kernels, not the matrix cores"},
+                "kernels": {x["name"]: {"ms_per_step": x["total_ms"] / steps} for x in stats if x["launches"]},
+                "replay_same_tokens": same}
     return {"workload": "Qwen2.5-0.5B-shape F16, each step 8 prompt chunks U[128,512] + 56 decode "
                         "rows over KV U[256,4096]; linears on the matrix cores (f32 sums)",
             "value": rows / elapsed, "unit": "packed rows/s", "ms_per_step": ms, "steps": steps,
@@ -964,7 +982,7 @@ def main():
     ap.add_argument("--no-c5", action="store_true", help="skip the Qwen3.5 hybrid workload")
     ap.add_argument("--c5-only", action="store_true",
                     help="run only the Qwen3.5 hybrid workload and print its JSON")
-    ap.add_argument("--only", choices=["c3", "c4", "c5"],
+    ap.add_argument("--only", choices=["c3", "c3q8", "c4", "c5"],
                     help="run only this workload and print its JSON (profiling runs)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 1 GiB device-to-device 4 times (counter calibration)")
@@ -1040,6 +1058,9 @@ def main():
         r.pop("_cpu")
         print(json.dumps(r), flush=True)
         return
+    if args.only == "c3q8":
+        print(json.dumps(run_c3(args.seed, 8, 2, "q8_0")), flush=True)
+        return
     path = model_file(args.seed)
     meta, tensors = gguf.read(path)
     cfg = gguf.qwen2_config(meta)
@@ -1105,6 +1126,7 @@ def main():
             log(f"[bench] c3 cpu baseline: oracle, {threads} threads")
             line["c3"]["cpu_baseline"] = c3_cpu_baseline(c3c, threads)
         del c3c
+        line["c3_q8_0"] = run_c3(args.seed, 8, 2, "q8_0")
     if not args.no_c5:
         line["c5"] = run_c5(args.seed, args.cpu_steps // 2, threads, with_cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
