@@ -725,6 +725,12 @@ int cohx_finalize(cohx_ctx *ctx) {
     total += ly.qkv.gguf_bytes + ly.o.gguf_bytes + ly.gu.gguf_bytes + ly.down.gguf_bytes;
   // the embedding is read as a matrix only as the tied head
   ctx->matrix_bytes = d.tied ? total : total - ctx->embd.gguf_bytes;
+  // the packed-prefill regime's quantized GEMM covers Q8/Q4 tiles with whole
+  // block pairs per ring stage (K a multiple of 128)
+  ctx->quant_gemm = true;
+  for (auto &ly : ctx->layers)
+    for (const DeviceMatrix *m : {&ly.qkv, &ly.o, &ly.gu, &ly.down})
+      ctx->quant_gemm &= (m->view.dtype == kFmtQ8 || m->view.dtype == kFmtQ4) && m->view.K % 128 == 0;
   ctx->finalized = true;
   return COHX_OK;
 }
@@ -969,6 +975,7 @@ struct Prepared {
   uint64_t kv_chunk_lanes = 0;// KV rows of the lanes the tiles belong to
   uint32_t max_kv_exact = 0;  // longest attended length among the exact passes' rows
   bool single_token = true;   // every lane carries one token (a pure decode step)
+  bool quant_gemm = false;    // Q8/Q4 linears of this step on the quantized GEMM (binary16 operands)
 };
 
 // Host validation (batch.rs:119-131) and upload of the device batch into w.
@@ -1027,10 +1034,13 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
   int rc = sync_page_table(ctx);
   if (rc) return rc;
   const size_t n = p.included.size();
-  // prefill regime: F16 linears on the matrix cores, and lanes of 16+ tokens
-  // take the matrix-core chunk attention (both held to a tolerance)
+  // packed-prefill regime (a step of 128+ rows carrying prompt rows, F16 or
+  // Q8_0/Q5_0/Q4_0 weights): linears on the matrix cores, and lanes of 16+
+  // tokens take the matrix-core chunk attention (both held to a tolerance)
   const int G = (int)(d.heads / d.kv_heads);
-  const bool regime = ctx->prefill_mfma && d.weight_dtype == COHX_F16 && p.rows >= 128 &&
+  const bool wide = ctx->prefill_mfma && p.rows >= 128;
+  p.quant_gemm = wide && ctx->quant_gemm && !p.single_token;
+  const bool regime = wide && (d.weight_dtype == COHX_F16 || ctx->quant_gemm) &&
                       attention_chunk_supported((int)d.head_dim, G);
   p.n_tiles = 0;
   p.n_exact = p.rows;
@@ -1375,12 +1385,29 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
     Layer &ly = ctx->layers[l];
     float *kp = ctx->kpool + (size_t)l * ctx->layer_stride;
     float *vp = ctx->vpool + (size_t)l * ctx->layer_stride;
-    const int a_qkv = act_of(ly.qkv), a_o = act_of(ly.o), a_gu = act_of(ly.gu), a_down = act_of(ly.down);
+    // the quantized GEMM of the packed-prefill regime takes the reference's
+    // Q8_0 operand values as binary16 rows
+    const bool qg = p.quant_gemm;
+    const int a_qkv = qg ? kActQ8H : act_of(ly.qkv), a_o = qg ? kActQ8H : act_of(ly.o),
+              a_gu = qg ? kActQ8H : act_of(ly.gu), a_down = qg ? kActQ8H : act_of(ly.down);
     e = prof_begin(ctx, kCatNorm, b_norm, 0);
     launch_norm_act(s, R, w.x, nullptr, ly.attn_norm, H, d.norm_epsilon, a_qkv, act_blocks(a_qkv, H), act,
                     w.row_err);
     prof_end(ctx, e);
-    if (ly.qkv.view.dtype != kFmtQ8 && ly.qkv.view.dtype != kFmtQ4) {
+    if (qg) {
+      // quantized GEMM into f32 rows (query/key features back in source
+      // order), then the bias, RoPE and K/V append pass
+      e = prof_begin(ctx, kCatMvQkv, matrix_pass_bytes(ly.qkv, R, H + 2 * KVD, false),
+                     2.0 * R * (H + 2 * KVD) * H);
+      if (!launch_gemm_q(s, kEpiStore, ly.qkv.view, act.f16, R,
+                        MatvecOut{w.qkv, H + 2 * KVD, nullptr, nullptr, w.row_err, nullptr}, nullptr, D, H + KVD))
+        return fail(ctx, COHX_UNSUPPORTED, "matrix outside the quantized GEMM's shapes");
+      prof_end(ctx, e);
+      e = prof_begin(ctx, kCatQkvPost, b_post, 0);
+      launch_qkv_post(s, R, sd, w.qkv, ly.bqkv, ctx->rope, w.row_pos, w.row_slot, w.q_rot, kp, vp,
+                      w.row_err);
+      prof_end(ctx, e);
+    } else if (ly.qkv.view.dtype != kFmtQ8 && ly.qkv.view.dtype != kFmtQ4) {
       e = prof_begin(ctx, kCatMvQkv, matrix_pass_bytes(ly.qkv, R, H + 2 * KVD, false),
                      2.0 * R * (H + 2 * KVD) * H);
       launch_matvec(s, kEpiStore, ly.qkv.view, act, R,
@@ -1432,8 +1459,14 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
       prof_end(ctx, e);
     }
     e = prof_begin(ctx, kCatMvO, matrix_pass_bytes(ly.o, R, H, true), 2.0 * R * H * H);
-    launch_matvec(s, kEpiResidual, ly.o.view, act, R,
-                  MatvecOut{w.x, H, nullptr, nullptr, w.row_err, nullptr});
+    if (qg) {
+      if (!launch_gemm_q(s, kEpiResidual, ly.o.view, act.f16, R,
+                        MatvecOut{w.x, H, nullptr, nullptr, w.row_err, nullptr}, nullptr, 0, 0))
+        return fail(ctx, COHX_UNSUPPORTED, "matrix outside the quantized GEMM's shapes");
+    } else {
+      launch_matvec(s, kEpiResidual, ly.o.view, act, R,
+                    MatvecOut{w.x, H, nullptr, nullptr, w.row_err, nullptr});
+    }
     prof_end(ctx, e);
     e = prof_begin(ctx, kCatNorm, b_norm, 0);
     launch_norm_act(s, R, w.x, nullptr, ly.ffn_norm, H, d.norm_epsilon, a_gu, act_blocks(a_gu, H), act,
@@ -1443,6 +1476,25 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
     // the SwiGLU quantizer runs in gate+up's epilogue into the down operand
     // buffer; otherwise its own pass
     const ActView down_act{w.down_qs, w.down_ds, nullptr, nullptr, nullptr, nullptr};
+    if (qg) {
+      // quantized GEMMs: gate+up with SwiGLU and its Q8_0 rounding in the
+      // epilogue writes the down projection's binary16 rows into w.h
+      // (act.f16 holds gate+up's own operand, still being read), then down
+      // accumulates into x
+      uint16_t *down16 = reinterpret_cast<uint16_t *>(w.h);
+      e = prof_begin(ctx, kCatMvGateUp, matrix_pass_bytes(ly.gu, R, 0, false) + (double)R * F * 2,
+                     2.0 * R * 2 * F * H);
+      if (!launch_gemm_q(s, kEpiSwiglu, ly.gu.view, act.f16, R,
+                        MatvecOut{nullptr, 0, nullptr, nullptr, w.row_err, nullptr}, down16, 0, 0))
+        return fail(ctx, COHX_UNSUPPORTED, "matrix outside the quantized GEMM's shapes");
+      prof_end(ctx, e);
+      e = prof_begin(ctx, kCatMvDown, matrix_pass_bytes(ly.down, R, H, true), 2.0 * R * H * F);
+      if (!launch_gemm_q(s, kEpiResidual, ly.down.view, down16, R,
+                        MatvecOut{w.x, H, nullptr, nullptr, w.row_err, nullptr}, nullptr, 0, 0))
+        return fail(ctx, COHX_UNSUPPORTED, "matrix outside the quantized GEMM's shapes");
+      prof_end(ctx, e);
+      continue;
+    }
     bool fused_quant = false;
     if (w.down_qs && a_down == kActQ8) {
       e = prof_begin(ctx, kCatMvGateUp,

@@ -63,6 +63,22 @@ __device__ __forceinline__ int8_t sat_i8(float v) {
   return (int8_t)v;
 }
 
+// Q8_0 activation rounding (QuantizedInput::prepare, quant.rs:193-213) of a
+// block whose largest magnitude is m: d = m/127, inv = 1/d (0 when d == 0),
+// stored scale f16(d), value q = round-half-away(x*inv) as i8.
+struct Q8Scale {
+  float inv;
+  uint16_t hd;  // the stored binary16 scale
+};
+__device__ __forceinline__ Q8Scale q8_scale_of(float m) {
+  const float d = m / 127.0f;
+  return Q8Scale{d == 0.0f ? 0.0f : 1.0f / d, f2h(d)};
+}
+__device__ __forceinline__ int8_t q8_round(float v, float inv) { return sat_i8(roundf(v * inv)); }
+// The value the reference's dot product multiplies for q, q * f16(d), as
+// binary16 (q * d is exact in f32; one rounding).
+__device__ __forceinline__ uint16_t q8_value_h(int8_t q, float dh) { return f2h((float)q * dh); }
+
 // Wave-level reductions (butterfly: every lane ends with the result; the
 // combination order is fixed, so results are deterministic).
 __device__ __forceinline__ double wave_sum_f64(double v) {

@@ -43,7 +43,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 32;  // K per ring stage: one MFMA step
 
-enum Epi { kStore = 0, kAccumulate = 1, kSwigluF16 = 2, kArgmax = 3 };
+// kSwigluQ8: SwiGLU rounded as the reference's Q8_0 operand of the down
+// projection (q * f16(d) per 32-feature block, as binary16; quant.rs:193-213)
+enum Epi { kStore = 0, kAccumulate = 1, kSwigluF16 = 2, kArgmax = 3, kSwigluQ8 = 4 };
 enum Type { kF16 = 0, kBF16 = 1 };
 
 struct Args {
@@ -64,7 +66,25 @@ struct Args {
   // tile order (see tile_of): tiles along features (nf) and token rows (nr),
   // tiles per XCD, and whether feature blocks are the major index
   int nf, nr, per_xcd, feature_major;
+  // k_gemm_q: W as the exact matvecs' 16-row tiles of Q8_0 (int8 values) or
+  // Q4_0 (nibbles) blocks and their binary16 scales [tile][nbp][16]
+  // (device.h q8_byte / q4_byte / q8_scale); SwiGLU matrices hold gate tile
+  // i at tile 2i and up tile i at tile 2i + 1
+  const void *qs;
+  const uint16_t *ds;
+  int nbp;
+  // kStore: features [0, rope_rows) are query and key heads of rope_d
+  // features uploaded in rope order (cohx.cpp rope_row); each is stored at
+  // its source column
+  int rope_d, rope_rows;
 };
+
+// Source column of feature f of a rope-ordered head block: even features are
+// a head's first half in order, odd ones its second half.
+__device__ __forceinline__ int rope_col(int f, int d) {
+  const int i = f % d;
+  return f - i + ((i & 1) ? (i >> 1) + d / 2 : (i >> 1));
+}
 
 // Workgroup -> output tile.  The dispatcher hands workgroup ids to the 8 XCDs
 // round robin (id % 8), and each XCD has its own L2.  Tiles are numbered in
@@ -103,12 +123,14 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
 // returns the 1-D grid size.  The major index is the one whose blocks are the
 // more expensive to re-read: an XCD's range then spans few major blocks and
 // all minor ones, and the smaller of the two slice sums wins.
-inline int tile_order(Args &g, int out_features, int bm, int bn) {
+// w_bytes: bytes per weight value in HBM (2 for binary16 and bfloat16,
+// 34/32 for Q8_0 blocks, 18/32 for Q4_0).
+inline int tile_order(Args &g, int out_features, int bm, int bn, double w_bytes = 2.0) {
   g.nf = (out_features + bm - 1) / bm;
   g.nr = (g.M + bn - 1) / bn;
   const int tiles = g.nf * g.nr;
   g.per_xcd = (tiles + 7) / 8;
-  const double wb = (double)bm * g.K, xb = (double)bn * g.K * (g.xlo ? 2 : 1);
+  const double wb = (double)bm * g.K * w_bytes, xb = 2.0 * bn * g.K * (g.xlo ? 2 : 1);
   const double f_major = (double)g.per_xcd / g.nr * wb + (double)g.nr * xb;  // few W blocks, all X
   const double r_major = (double)g.per_xcd / g.nf * xb + (double)g.nf * wb;  // few X blocks, all W
   g.feature_major = f_major <= r_major;
@@ -122,6 +144,177 @@ constexpr int lds_bytes() {
   constexpr int ring = 2 * (16 * kWM * kTM + (kLo ? 2 : 1) * 16 * kWN * kTN) * 64;
   constexpr int park = kEpi == kSwigluF16 ? (kWM / 2) * kWN * kTM * kTN * 4 * 64 * 4 : 0;
   return ring > park ? ring : park;
+}
+
+// Output tile of a workgroup: the accumulators of its waves at features
+// f0 + ..., token rows r0 + ... (SwiGLU: f0 counts gate features).  The LDS
+// is free (all waves are past the main loop's last barrier).
+template <int kWM, int kWN, int kTM, int kTN, int kEpi>
+__device__ __forceinline__ void epilogue(const Args &g, f32x4 (&acc)[kTM][kTN], int f0, int r0,
+                                         uint4 *smem) {
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int wm = wave / kWN, wn = wave % kWN, lr = lane % 16;
+  const int F = g.N / 2;
+  if constexpr (kEpi == kArgmax) {
+#pragma unroll
+    for (int b = 0; b < kTN; b++) {
+      const int r = r0 + (wn * kTN + b) * 16 + lr;
+      const bool rvalid = r < g.M;
+      bool bad = false;
+#pragma unroll
+      for (int a = 0; a < kTM; a++) {
+        const int ft = f0 + (wm * kTM + a) * 16, fb = ft + 4 * (lane / 16);
+        unsigned long long key = 0ull;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float v = acc[a][b][i];
+          if (rvalid && fb + i < g.N) {
+            bad |= !finitef(v);
+            if (g.logits) g.logits[(size_t)r * g.N + fb + i] = v;
+            const unsigned long long k = argmax_key(v, fb + i);
+            key = k > key ? k : key;
+          }
+        }
+        unsigned long long o = __shfl_xor(key, 16, kWave);
+        key = o > key ? o : key;
+        o = __shfl_xor(key, 32, kWave);
+        key = o > key ? o : key;
+        if (lane < 16 && rvalid && ft < g.N) g.keys[(size_t)r * g.ktiles + ft / 16] = key;
+      }
+      if (bad) atomicOr(&g.row_err[g.err_rows ? (int)g.err_rows[r] : r], kErrNonFinite);
+    }
+    return;
+  } else if constexpr (kEpi == kSwigluF16 || kEpi == kSwigluQ8) {
+    // up waves (wm >= kWM/2) park their sums; the gate wave at wm - kWM/2
+    // holds the matching gate sums in the same registers
+    float *park = reinterpret_cast<float *>(smem);
+    constexpr int kPair = kTM * kTN * 4;  // floats per lane per wave
+    const int pair = (wm % (kWM / 2)) * kWN + wn;
+    if (wm >= kWM / 2) {
+#pragma unroll
+      for (int a = 0; a < kTM; a++)
+#pragma unroll
+        for (int b = 0; b < kTN; b++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) park[((pair * kPair) + (a * kTN + b) * 4 + i) * kWave + lane] = acc[a][b][i];
+    }
+    __syncthreads();
+    if (wm >= kWM / 2) return;
+    if constexpr (kEpi == kSwigluQ8) {
+      // a 32-feature block is tiles a, a + 1 (a even, 32-aligned) of one
+      // token column: 8 values in each of the lanes l, l + 16, l + 32, l + 48
+      static_assert(kTM % 2 == 0, "whole Q8_0 blocks per wave");
+#pragma unroll
+      for (int b = 0; b < kTN; b++) {
+        const int r = r0 + (wn * kTN + b) * 16 + lr;
+        const bool rvalid = r < g.M;
+        bool bad = false;
+#pragma unroll
+        for (int a = 0; a < kTM; a += 2) {
+          const int fb = f0 + (wm * kTM + a) * 16 + 4 * (lane / 16);
+          const bool live = rvalid && fb < F;  // F % 32 == 0: whole blocks in or out
+          float h[8];
+          float m = 0.0f;
+#pragma unroll
+          for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              const float gv = acc[a + t][b][i];
+              const float uv = park[((pair * kPair) + ((a + t) * kTN + b) * 4 + i) * kWave + lane];
+              h[4 * t + i] = (gv / (1.0f + exp_f32(-gv))) * uv;
+              bad |= live && !finitef(h[4 * t + i]);
+              m = fmaxf(m, live ? fabsf(h[4 * t + i]) : 0.0f);
+            }
+          m = fmaxf(m, __shfl_xor(m, 16, kWave));
+          m = fmaxf(m, __shfl_xor(m, 32, kWave));
+          const Q8Scale sc = q8_scale_of(m);
+          const float dh = h2f(sc.hd);
+          if (!live) continue;
+          bad |= !finitef(dh) || !finitef(sc.inv);
+#pragma unroll
+          for (int t = 0; t < 2; t++) {
+            uint16_t q[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              q[i] = q8_value_h(q8_round(h[4 * t + i], sc.inv), dh);
+              bad |= !finitef(h2f(q[i]));
+            }
+            *reinterpret_cast<uint2 *>(g.out16 + (size_t)r * F + fb + 16 * t) =
+                make_uint2(q[0] | (uint32_t)q[1] << 16, q[2] | (uint32_t)q[3] << 16);
+          }
+        }
+        if (bad) atomicOr(&g.row_err[g.err_rows ? (int)g.err_rows[r] : r], kErrNonFinite);
+      }
+      return;
+    }
+#pragma unroll
+    for (int b = 0; b < kTN; b++) {
+      const int r = r0 + (wn * kTN + b) * 16 + lr;
+      if (r >= g.M) continue;
+      bool bad = false;
+#pragma unroll
+      for (int a = 0; a < kTM; a++) {
+        const int fb = f0 + (wm * kTM + a) * 16 + 4 * (lane / 16);
+        uint16_t h[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float gv = acc[a][b][i];
+          const float uv = park[((pair * kPair) + (a * kTN + b) * 4 + i) * kWave + lane];
+          bad |= !finitef(gv) || !finitef(uv);
+          h[i] = f2h((gv / (1.0f + exp_f32(-gv))) * uv);
+          bad |= !finitef(h2f(h[i]));
+        }
+        if (fb + 3 < F && F % 4 == 0) {
+          *reinterpret_cast<uint2 *>(g.out16 + (size_t)r * F + fb) =
+              make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            if (fb + i < F) g.out16[(size_t)r * F + fb + i] = h[i];
+        }
+      }
+      if (bad) atomicOr(&g.row_err[g.err_rows ? (int)g.err_rows[r] : r], kErrNonFinite);
+    }
+  } else {
+#pragma unroll
+    for (int b = 0; b < kTN; b++) {
+      const int r = r0 + (wn * kTN + b) * 16 + lr;
+      if (r >= g.M) continue;
+      bool bad = false;
+#pragma unroll
+      for (int a = 0; a < kTM; a++) {
+        const int fb = f0 + (wm * kTM + a) * 16 + 4 * (lane / 16);
+        if (kEpi == kStore && fb < g.rope_rows) {  // query/key features back in source order
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float v = acc[a][b][i];
+            bad |= !finitef(v);
+            g.out[(size_t)r * g.ldo + rope_col(fb + i, g.rope_d)] = v;
+          }
+          continue;
+        }
+        float *p = g.out + (size_t)r * g.ldo + fb;
+        if (fb + 3 < g.N && g.ldo % 4 == 0) {
+          float4 v = make_float4(acc[a][b][0], acc[a][b][1], acc[a][b][2], acc[a][b][3]);
+          if (kEpi == kAccumulate) {
+            const float4 q = *reinterpret_cast<const float4 *>(p);
+            v = make_float4(q.x + v.x, q.y + v.y, q.z + v.z, q.w + v.w);
+          }
+          bad |= !finitef(v.x) || !finitef(v.y) || !finitef(v.z) || !finitef(v.w);
+          *reinterpret_cast<float4 *>(p) = v;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            if (fb + i >= g.N) continue;
+            const float v = kEpi == kAccumulate ? p[i] + acc[a][b][i] : acc[a][b][i];
+            bad |= !finitef(v);
+            p[i] = v;
+          }
+        }
+      }
+      if (bad) atomicOr(&g.row_err[g.err_rows ? (int)g.err_rows[r] : r], kErrNonFinite);
+    }
+  }
 }
 
 template <int kType, bool kLo, int kWM, int kWN, int kTM, int kTN, int kR, int kEpi>
@@ -235,111 +428,201 @@ __global__ __launch_bounds__(64 * kWM * kWN) void k_gemm(Args g) {
   }
   // the last step's readers are done before the LDS is reused by the epilogue
   __syncthreads();
+  epilogue<kWM, kWN, kTM, kTN, kEpi>(g, acc, f0, r0, smem);
+}
 
-  if constexpr (kEpi == kArgmax) {
+// ---------------------------------------------------------------------------
+// Quantized weights (the packed-prefill regime over Q8_0 / Q5_0 / Q4_0
+// models).  W stays in the exact matvecs' 16-row tiles: per (tile, block
+// pair) lane l of a 64-lane slot row holds row l % 16, inputs 8 (l / 16) ..
+// + 8 of both blocks (Q8: 16 bytes, Q4: 8), which is the MFMA's own operand
+// order.  Each ring stage covers one block pair (K advances 64): every thread
+// loads its (row, input group) slot and the row's two block scales, and on
+// the way into LDS turns each value into binary16 times its block's scale,
+// rounded once (int8 and nibble values are exact in binary16, and the
+// product of an 8-bit value and an 11-bit scale is exact in f32 before the
+// rounding).  The reference multiplies Q8_0 activations with the int8
+// weights per block and applies both scales in an f32 chain
+// (quant.rs:245-292).  The operand rows here hold the same Q8_0 activation
+// values, q * f16(d) as binary16 (their producers round each row block as
+// the reference does; the SwiGLU epilogue kSwigluQ8 too), so the regime keeps
+// the reference's activation rounding; its tolerance covers the binary16
+// rounding of q * d on both sides and the f32 sums in MFMA order.
+//
+// LDS per stage: BM weight rows and BN token rows of 64 binary16 inputs
+// (eight 16-byte segments each); segment s of row R sits at slot
+// 8R + (s ^ ((R >> 1) & 7)), so a wave's 16 rows of one segment spread over
+// all banks.
+// ---------------------------------------------------------------------------
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+template <int kQ>
+struct QSlot;
+template <>
+struct QSlot<8> {
+  typedef u32x4 type;
+  static constexpr int kBytes = 16, kPair = 1024;  // per lane / per tile, one block pair
+};
+template <>
+struct QSlot<4> {
+  typedef u32x2 type;
+  static constexpr int kBytes = 8, kPair = 512;
+};
+
+// Eight signed values (bytes of lo then hi, in order) times their block
+// scale as binary16.
+__device__ __forceinline__ f16x8 scale8(uint32_t lo, uint32_t hi, _Float16 d) {
+  f16x8 v;
 #pragma unroll
-    for (int b = 0; b < kTN; b++) {
-      const int r = r0 + (wn * kTN + b) * 16 + lr;
-      const bool rvalid = r < g.M;
-      bool bad = false;
+  for (int j = 0; j < 4; j++) {
+    v[j] = (_Float16)(short)(signed char)(lo >> (8 * j));
+    v[4 + j] = (_Float16)(short)(signed char)(hi >> (8 * j));
+  }
+  return v * d;
+}
+
+__device__ __forceinline__ int qswz(int R) { return (R >> 1) & 7; }
+
+template <int kWM, int kWN, int kTM, int kTN, int kEpi>
+constexpr int lds_bytes_q() {
+  constexpr int ring = 2 * (16 * kWM * kTM + 16 * kWN * kTN) * 128;
+  constexpr int park = kEpi == kSwigluF16 || kEpi == kSwigluQ8 ? (kWM / 2) * kWN * kTM * kTN * 4 * 64 * 4 : 0;
+  return ring > park ? ring : park;
+}
+
+template <int kQ, int kWM, int kWN, int kTM, int kTN, int kR, int kEpi>
+__global__ __launch_bounds__(64 * kWM * kWN) void k_gemm_q(Args g) {
+  constexpr int kThreads = 64 * kWM * kWN;
+  constexpr int kBM = 16 * kWM * kTM, kBN = 16 * kWN * kTN;
+  constexpr int kWLoads = kBM * 4, kXLoads = kBN * 8;  // per stage
+  static_assert(kWLoads % kThreads == 0 && kXLoads % kThreads == 0, "whole loads per thread");
+  constexpr int kPW = kWLoads / kThreads, kPX = kXLoads / kThreads;
+  constexpr int kStage = (kBM + kBN) * 8;  // 16-byte LDS slots per stage
+  static_assert(kR == 2 || kR == 4, "two or four block pairs in flight (K / 64 a multiple of kR)");
+  constexpr bool kGlu = kEpi == kSwigluF16 || kEpi == kSwigluQ8;
+  static_assert(!kGlu || kWM % 2 == 0, "gate and up waves in pairs");
+  using QT = typename QSlot<kQ>::type;
+  extern __shared__ __align__(16) uint4 smem[];
+  f16x8 *lds = reinterpret_cast<f16x8 *>(smem);
+  u32x4 *ldsx = reinterpret_cast<u32x4 *>(smem);
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int wm = wave / kWN, wn = wave % kWN;
+  const int nk = g.K / 64;
+  const int2 tile = tile_of(g);
+  if (tile.x < 0) return;
+  const int f0 = tile.x * (kGlu ? kBM / 2 : kBM);
+  const int r0 = tile.y * kBN;
+  // weight slots: a 64-slot row of the load index is one 16-row tile of the
+  // workgroup (tl), lane = the tile's own lane order; tiles past the end
+  // clamp to the last (their results are never stored)
+  const char *qsrc[kPW];
+  const uint16_t *dsrc[kPW];
+  int wdst[kPW];  // LDS row of the slot
+  const int last = kGlu ? (g.N / 2 - 1) / 16 : (g.N - 1) / 16;
+#pragma unroll
+  for (int i = 0; i < kPW; i++) {
+    const int tl = wave * kPW + i;
+    int dt;
+    if (kGlu) {
+      const bool up = tl >= kBM / 32;
+      dt = 2 * min(f0 / 16 + tl - (up ? kBM / 32 : 0), last) + (up ? 1 : 0);
+    } else {
+      dt = min(f0 / 16 + tl, last);
+    }
+    qsrc[i] = static_cast<const char *>(g.qs) + (size_t)dt * (g.nbp / 2) * QSlot<kQ>::kPair +
+              lane * QSlot<kQ>::kBytes;
+    dsrc[i] = g.ds + (size_t)dt * g.nbp * 16 + lane % 16;
+    wdst[i] = tl * 16 + lane % 16;
+  }
+  const uint16_t *xsrc[kPX];
+  int xdst[kPX];
+#pragma unroll
+  for (int i = 0; i < kPX; i++) {
+    const int slot = (wave * kPX + i) * kWave + lane, row = slot >> 3, sg = slot & 7;
+    xsrc[i] = g.x + (size_t)min(r0 + row, g.M - 1) * g.ldx + sg * 8;
+    xdst[i] = kBM * 8 + row * 8 + (sg ^ qswz(row));
+  }
+  QT qreg[kR][kPW];
+  uint32_t dreg[kR][kPW];
+  u32x4 xreg[kR][kPX];
+  auto load = [&](int j, int kc) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kPW; i++) {
+      qreg[j][i] = *reinterpret_cast<const QT *>(qsrc[i] + (size_t)kc * QSlot<kQ>::kPair);
+      dreg[j][i] = (uint32_t)dsrc[i][kc * 32] | (uint32_t)dsrc[i][kc * 32 + 16] << 16;
+    }
+#pragma unroll
+    for (int i = 0; i < kPX; i++) xreg[j][i] = *reinterpret_cast<const u32x4 *>(xsrc[i] + (size_t)kc * 64);
+  };
+  // ring registers j -> LDS stage st (dequantizing the weights)
+  auto store = [&](int j, int st) __attribute__((always_inline)) {
+    const int base = st * kStage;
+#pragma unroll
+    for (int i = 0; i < kPW; i++) {
+      const int R = wdst[i], sw = qswz(R), kg = lane / 16;
+      uint32_t b0lo, b0hi, b1lo, b1hi;
+      if constexpr (kQ == 8) {
+        b0lo = qreg[j][i][0], b0hi = qreg[j][i][1], b1lo = qreg[j][i][2], b1hi = qreg[j][i][3];
+      } else {
+        const long a = q4_operand(qreg[j][i][0]), b = q4_operand(qreg[j][i][1]);
+        b0lo = (uint32_t)a, b0hi = (uint32_t)((unsigned long)a >> 32);
+        b1lo = (uint32_t)b, b1hi = (uint32_t)((unsigned long)b >> 32);
+      }
+      const _Float16 d0 = __builtin_bit_cast(_Float16, (uint16_t)(dreg[j][i] & 0xffffu));
+      const _Float16 d1 = __builtin_bit_cast(_Float16, (uint16_t)(dreg[j][i] >> 16));
+      lds[base + R * 8 + (kg ^ sw)] = scale8(b0lo, b0hi, d0);
+      lds[base + R * 8 + ((4 + kg) ^ sw)] = scale8(b1lo, b1hi, d1);
+    }
+#pragma unroll
+    for (int i = 0; i < kPX; i++) ldsx[base + xdst[i]] = xreg[j][i];
+  };
+#pragma unroll
+  for (int j = 0; j < kR; j++) load(j, min(j, nk - 1));
+  store(0, 0);
+  f32x4 acc[kTM][kTN];
+#pragma unroll
+  for (int a = 0; a < kTM; a++)
+#pragma unroll
+    for (int b = 0; b < kTN; b++) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int seg = lane / 16, lr = lane % 16;
+  auto step = [&](auto J, int k0) __attribute__((always_inline)) {
+    constexpr int j = decltype(J)::value;
+    const int ks = k0 + j;
+    __syncthreads();
+    const f16x8 *stage = lds + (j % 2) * kStage;
+    f16x8 af[2][kTM], bf[2][kTN];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
 #pragma unroll
       for (int a = 0; a < kTM; a++) {
-        const int ft = f0 + (wm * kTM + a) * 16, fb = ft + 4 * (lane / 16);
-        unsigned long long key = 0ull;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float v = acc[a][b][i];
-          if (rvalid && fb + i < g.N) {
-            bad |= !finitef(v);
-            if (g.logits) g.logits[(size_t)r * g.N + fb + i] = v;
-            const unsigned long long k = argmax_key(v, fb + i);
-            key = k > key ? k : key;
-          }
-        }
-        unsigned long long o = __shfl_xor(key, 16, kWave);
-        key = o > key ? o : key;
-        o = __shfl_xor(key, 32, kWave);
-        key = o > key ? o : key;
-        if (lane < 16 && rvalid && ft < g.N) g.keys[(size_t)r * g.ktiles + ft / 16] = key;
+        const int R = (wm * kTM + a) * 16 + lr;
+        af[h][a] = stage[R * 8 + ((4 * h + seg) ^ qswz(R))];
       }
-      if (bad) atomicOr(&g.row_err[g.err_rows ? (int)g.err_rows[r] : r], kErrNonFinite);
+#pragma unroll
+      for (int b = 0; b < kTN; b++) {
+        const int R = (wn * kTN + b) * 16 + lr;
+        bf[h][b] = stage[kBM * 8 + R * 8 + ((4 * h + seg) ^ qswz(R))];
+      }
     }
-    return;
-  } else if constexpr (kEpi == kSwigluF16) {
-    // up waves (wm >= kWM/2) park their sums; the gate wave at wm - kWM/2
-    // holds the matching gate sums in the same registers
-    float *park = reinterpret_cast<float *>(smem);
-    constexpr int kPair = kTM * kTN * 4;  // floats per lane per wave
-    const int pair = (wm % (kWM / 2)) * kWN + wn;
-    if (wm >= kWM / 2) {
+    store((j + 1) % kR, (j + 1) % 2);
+    load(j, min(ks + kR, nk - 1));
+#pragma unroll
+    for (int h = 0; h < 2; h++)
 #pragma unroll
       for (int a = 0; a < kTM; a++)
 #pragma unroll
-        for (int b = 0; b < kTN; b++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) park[((pair * kPair) + (a * kTN + b) * 4 + i) * kWave + lane] = acc[a][b][i];
-    }
-    __syncthreads();
-    if (wm >= kWM / 2) return;
-#pragma unroll
-    for (int b = 0; b < kTN; b++) {
-      const int r = r0 + (wn * kTN + b) * 16 + lr;
-      if (r >= g.M) continue;
-      bool bad = false;
-#pragma unroll
-      for (int a = 0; a < kTM; a++) {
-        const int fb = f0 + (wm * kTM + a) * 16 + 4 * (lane / 16);
-        uint16_t h[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float gv = acc[a][b][i];
-          const float uv = park[((pair * kPair) + (a * kTN + b) * 4 + i) * kWave + lane];
-          bad |= !finitef(gv) || !finitef(uv);
-          h[i] = f2h((gv / (1.0f + exp_f32(-gv))) * uv);
-          bad |= !finitef(h2f(h[i]));
-        }
-        if (fb + 3 < F && F % 4 == 0) {
-          *reinterpret_cast<uint2 *>(g.out16 + (size_t)r * F + fb) =
-              make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; i++)
-            if (fb + i < F) g.out16[(size_t)r * F + fb + i] = h[i];
-        }
-      }
-      if (bad) atomicOr(&g.row_err[g.err_rows ? (int)g.err_rows[r] : r], kErrNonFinite);
-    }
-  } else {
-#pragma unroll
-    for (int b = 0; b < kTN; b++) {
-      const int r = r0 + (wn * kTN + b) * 16 + lr;
-      if (r >= g.M) continue;
-      bool bad = false;
-#pragma unroll
-      for (int a = 0; a < kTM; a++) {
-        const int fb = f0 + (wm * kTM + a) * 16 + 4 * (lane / 16);
-        float *p = g.out + (size_t)r * g.ldo + fb;
-        if (fb + 3 < g.N && g.ldo % 4 == 0) {
-          float4 v = make_float4(acc[a][b][0], acc[a][b][1], acc[a][b][2], acc[a][b][3]);
-          if (kEpi == kAccumulate) {
-            const float4 q = *reinterpret_cast<const float4 *>(p);
-            v = make_float4(q.x + v.x, q.y + v.y, q.z + v.z, q.w + v.w);
-          }
-          bad |= !finitef(v.x) || !finitef(v.y) || !finitef(v.z) || !finitef(v.w);
-          *reinterpret_cast<float4 *>(p) = v;
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            if (fb + i >= g.N) continue;
-            const float v = kEpi == kAccumulate ? p[i] + acc[a][b][i] : acc[a][b][i];
-            bad |= !finitef(v);
-            p[i] = v;
-          }
-        }
-      }
-      if (bad) atomicOr(&g.row_err[g.err_rows ? (int)g.err_rows[r] : r], kErrNonFinite);
+        for (int b = 0; b < kTN; b++) acc[a][b] = mfma(af[h][a], bf[h][b], acc[a][b]);
+  };
+  for (int k0 = 0; k0 < nk; k0 += kR) {
+    step(std::integral_constant<int, 0>{}, k0);
+    step(std::integral_constant<int, 1>{}, k0);
+    if constexpr (kR == 4) {
+      step(std::integral_constant<int, 2>{}, k0);
+      step(std::integral_constant<int, 3>{}, k0);
     }
   }
+  __syncthreads();
+  epilogue<kWM, kWN, kTM, kTN, kEpi>(g, acc, f0, r0, smem);
 }
 
 }  // namespace gemm

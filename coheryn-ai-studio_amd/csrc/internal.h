@@ -155,7 +155,9 @@ struct cohx_ctx {
   cohx::Profiler prof;
   std::vector<void *> allocations;
   bool use_graphs = true;    // replay each step's launches as one captured graph
-  bool prefill_mfma = true;  // F16 batches of 128+ rows on the matrix cores
+  bool prefill_mfma = true;  // packed-prefill regime (F16, Q8_0/Q5_0/Q4_0) on the matrix cores
+  // every layer linear is a Q8/Q4 tile matrix the quantized GEMM takes (set at finalize)
+  bool quant_gemm = false;
   std::map<cohx::StepKey, hipGraphExec_t> graphs;
   cohx::Q35Model *q35 = nullptr;  // set for Qwen3.5 contexts (cohx_create_qwen35)
   hipEvent_t done = nullptr;      // completion event of a hooked step (created on first use)

@@ -13,6 +13,10 @@ namespace cohx {
 constexpr int kFmtF16 = 1, kFmtQ8 = 8, kFmtQ4 = 2, kFmtKQ = 12;
 // Activation operand kinds: binary16-rounded rows, Q8_0 blocks, Q8_K blocks.
 constexpr int kActF16 = 1, kActQ8 = 8, kActQ8K = 15;
+// Q8_0 blocks written out as binary16 rows [rows][K] of the values the
+// reference's dot multiplies (q * f16(d), one rounding): the operand of the
+// packed-prefill regime's quantized GEMM.  Rows of nbp * 32 == K values.
+constexpr int kActQ8H = 9;
 // Producer-only kind: f32 rows into ActView::f32, quantized by a following
 // launch_quant_act(kActQ8K).
 constexpr int kActF32 = 32;
@@ -118,6 +122,16 @@ bool launch_matvec_swiglu_q8(hipStream_t s, const MatrixView &w, const ActView &
 // F16) or when K is not a multiple of 64.
 bool launch_matvec_swiglu_f16(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
                               const MatvecOut &o, uint16_t *out_f16);
+// Q8_0/Q4_0 linears of a step in the packed-prefill regime on the matrix
+// cores (gemm.h k_gemm_q): binary16 operand rows x[rows_b][K], the weights
+// dequantized to binary16 on their way into LDS, f32 sums.  kEpiStore into
+// o.out (features [0, rope_rows) of a rope-ordered qkv matrix, heads of
+// rope_d, back to their source columns; rope_d 0: none), kEpiResidual
+// accumulates into o.out, kEpiSwiglu writes the down projection's binary16
+// rows out16[rows_b][F] (gate/up tiles interleaved).  Returns false (nothing
+// launched) for other formats or epilogues, or K not a multiple of 128.
+bool launch_gemm_q(hipStream_t s, Epilogue epi, const MatrixView &w, const uint16_t *x, int rows_b,
+                   const MatvecOut &o, uint16_t *out16, int rope_d, int rope_rows);
 void launch_argmax_reduce(hipStream_t s, int rows, const unsigned long long *part, int units,
                           unsigned long long *out);
 // Q8_0/Q4_0 qkv projection with launch_qkv_post's work in its epilogue (bias,

@@ -147,8 +147,9 @@ __global__ __launch_bounds__(256) void k_embed(MatrixView e, const uint32_t *__r
 // groups of a block sit in lanes kStride apart (kStride 1: four consecutive
 // aligned lanes; 16: lanes l, l+16, l+32, l+48), combine their maxima with
 // two shuffles, and each writes its 8 quantized values as one 8-byte store
-// into the B-operand tile layout.
-template <int kStride = 1>
+// into the B-operand tile layout.  kRows (kActQ8H): the 8 values q * f16(d)
+// as binary16 into act.f16 row `row` (stride nbp * 32) instead.
+template <int kStride = 1, bool kRows = false>
 __device__ __forceinline__ bool quant_group_q8(const float (&v)[8], bool active, int row, int kg,
                                                int nbp, ActView act) {
   float m = 0.0f;
@@ -160,21 +161,32 @@ __device__ __forceinline__ bool quant_group_q8(const float (&v)[8], bool active,
   }
   m = fmaxf(m, __shfl_xor(m, kStride, kWave));
   m = fmaxf(m, __shfl_xor(m, 2 * kStride, kWave));
-  const float d = m / 127.0f;
-  const float inv = d == 0.0f ? 0.0f : 1.0f / d;
-  const uint16_t hd = f2h(d);
+  const Q8Scale sc = q8_scale_of(m);
   if (active) {
-    bad |= !finitef(h2f(hd)) || !finitef(inv);
-    uint32_t lo = 0, hi = 0;
+    bad |= !finitef(h2f(sc.hd)) || !finitef(sc.inv);
+    if constexpr (kRows) {
+      const float dh = h2f(sc.hd);
+      uint32_t p[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      lo |= (uint32_t)(uint8_t)sat_i8(roundf(v[i] * inv)) << (8 * i);
-      hi |= (uint32_t)(uint8_t)sat_i8(roundf(v[i + 4] * inv)) << (8 * i);
+      for (int i = 0; i < 4; i++) {
+        const uint16_t a = q8_value_h(q8_round(v[2 * i], sc.inv), dh);
+        const uint16_t b = q8_value_h(q8_round(v[2 * i + 1], sc.inv), dh);
+        bad |= !finitef(h2f(a)) || !finitef(h2f(b));
+        p[i] = a | (uint32_t)b << 16;
+      }
+      *reinterpret_cast<uint4 *>(act.f16 + (size_t)row * nbp * 32 + kg * 8) = make_uint4(p[0], p[1], p[2], p[3]);
+    } else {
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        lo |= (uint32_t)(uint8_t)q8_round(v[i], sc.inv) << (8 * i);
+        hi |= (uint32_t)(uint8_t)q8_round(v[i + 4], sc.inv) << (8 * i);
+      }
+      const int b = kg / 4, g = kg % 4;
+      *reinterpret_cast<uint2 *>(act.qs + q8_byte(row / 16, nbp, b, g * 16 + row % 16, 0)) =
+          make_uint2(lo, hi);
+      if (g == 0) act.ds[q8_scale(row / 16, nbp, b, row % 16)] = sc.hd;
     }
-    const int b = kg / 4, g = kg % 4;
-    *reinterpret_cast<uint2 *>(act.qs + q8_byte(row / 16, nbp, b, g * 16 + row % 16, 0)) =
-        make_uint2(lo, hi);
-    if (g == 0) act.ds[q8_scale(row / 16, nbp, b, row % 16)] = hd;
   }
   return bad;
 }
@@ -292,14 +304,14 @@ __global__ __launch_bounds__(256) void k_norm_act(const float *__restrict__ x,
   for (int k = threadIdx.x + kPer * 256; k < H; k += 256) y[k] = xr[k] * scale * w[k];
   __syncthreads();
   bool bad = false;
-  if (kAct == 8) {
+  if (kAct == 8 || kAct == kActQ8H) {
     for (int base = 0; base < nbp * 4; base += 256) {
       const int kg = base + threadIdx.x;
       const bool active = kg < nbp * 4;
       float v[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) v[i] = (active && kg * 8 + i < H) ? y[kg * 8 + i] : 0.0f;
-      bad |= quant_group_q8(v, active, ob, kg, nbp, act);
+      bad |= quant_group_q8<1, kAct == kActQ8H>(v, active, ob, kg, nbp, act);
     }
   } else if (kAct == kActQ8K) {
     // one wave per 256-element block (H % 256 == 0; nbp = H / 256)
@@ -327,6 +339,7 @@ __global__ __launch_bounds__(256) void k_norm_act(const float *__restrict__ x,
 // once, sums its squares in element order, and after the workgroup's f64 tree
 // normalizes and quantizes its group in registers: no LDS staging of the row
 // and one barrier pair fewer than k_norm_act.
+template <bool kRows>
 __global__ __launch_bounds__(256) void k_norm_q8(const float *__restrict__ x,
                                                  const uint32_t *__restrict__ in_rows,
                                                  const float *__restrict__ w, int H, float eps, int nbp,
@@ -353,7 +366,7 @@ __global__ __launch_bounds__(256) void k_norm_q8(const float *__restrict__ x,
   float v[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) v[i] = inrow ? xv[i] * scale * wv[i] : 0.0f;
-  if (quant_group_q8(v, active, ob, kg, nbp, act)) atomicOr(&row_err[ib], kErrNonFinite);
+  if (quant_group_q8<1, kRows>(v, active, ob, kg, nbp, act)) atomicOr(&row_err[ib], kErrNonFinite);
 }
 
 // Operand preparation of an f32 row (SwiGLU output before ffn_down).
@@ -2499,7 +2512,7 @@ __global__ __launch_bounds__(128) void k_attn_combine(StepDims d,
     o = O / L;
   }
   bool bad = active && !finitef(o);
-  if (kAct == 8) {
+  if (kAct == 8 || kAct == kActQ8H) {
     if (active) o_s[j] = o;
     __syncthreads();
     // D/8 groups of this head: group kg of the row is h*D/8 + j
@@ -2507,7 +2520,8 @@ __global__ __launch_bounds__(128) void k_attn_combine(StepDims d,
     float v[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) v[i] = j < ng ? o_s[j * 8 + i] : 0.0f;
-    if (j < ((ng + 3) & ~3)) bad |= quant_group_q8(v, j < ng, r, h * ng + j, nbp, act);
+    if (j < ((ng + 3) & ~3))
+      bad |= quant_group_q8<1, kAct == kActQ8H>(v, j < ng, r, h * ng + j, nbp, act);
   } else if (kAct == kActF32) {  // f32 rows for a following Q8_K quantizer
     if (active) act.f32[(size_t)r * d.H + h * d.D + j] = o;
   } else if (active) {
@@ -2593,7 +2607,12 @@ void launch_norm_act(hipStream_t s, int rows, const float *x, const uint32_t *in
                      uint32_t *row_err) {
   const size_t lds = (size_t)H * sizeof(float);
   if (act_dtype == 8 && nbp * 4 <= 256 && H % 8 == 0)  // one 8-element group per thread
-    launch_k(k_norm_q8, dim3(rows), dim3(256), 0, s, x, in_rows, weight, H, eps, nbp, act, row_err);
+    launch_k(k_norm_q8<false>, dim3(rows), dim3(256), 0, s, x, in_rows, weight, H, eps, nbp, act, row_err);
+  else if (act_dtype == kActQ8H && nbp * 4 <= 256 && H % 8 == 0)
+    launch_k(k_norm_q8<true>, dim3(rows), dim3(256), 0, s, x, in_rows, weight, H, eps, nbp, act, row_err);
+  else if (act_dtype == kActQ8H)
+    launch_k(k_norm_act<kActQ8H>, dim3(rows), dim3(256), lds, s, x, in_rows, weight, H, eps,
+                       nbp, act, row_err);
   else if (act_dtype == kActQ8K)  // nbp = H / 256 blocks
     launch_k(k_norm_act<kActQ8K>, dim3(rows), dim3(256), lds, s, x, in_rows, weight, H, eps,
                        nbp, act, row_err);
@@ -2727,6 +2746,54 @@ static bool gemm_f16(hipStream_t s, Epilogue epi, const MatrixView &w, const uin
       else
         launch_k(k_gemm<kF16, false, 2, 2, 4, 4, 2, kStore>, grid, dim3(256), lds, s, g);
     }
+  }
+  return true;
+}
+
+bool launch_gemm_q(hipStream_t s, Epilogue epi, const MatrixView &w, const uint16_t *x, int rows_b,
+                   const MatvecOut &o, uint16_t *out16, int rope_d, int rope_rows) {
+  using namespace gemm;
+  if ((w.dtype != kFmtQ8 && w.dtype != kFmtQ4) || w.K % 128 || w.nbp * 32 != w.K) return false;
+  if (epi != kEpiStore && epi != kEpiResidual && epi != kEpiSwiglu) return false;
+  Args g{};
+  g.qs = w.qs;
+  g.ds = w.ds;
+  g.nbp = w.nbp;
+  g.x = x;
+  g.N = w.rows;
+  g.K = w.K;
+  g.M = rows_b;
+  g.ldx = w.K;
+  g.row_err = o.row_err;
+  g.err_rows = o.err_rows;
+  const bool q8 = w.dtype == kFmtQ8;
+  const double wb = q8 ? 34.0 / 32 : 18.0 / 32;
+  if (epi == kEpiSwiglu) {
+    g.out16 = out16;
+    const dim3 grid(tile_order(g, w.rows / 2, 64, 128, wb));
+    constexpr int lds = lds_bytes_q<2, 2, 4, 4, kSwigluQ8>();
+    if (q8)
+      launch_k(k_gemm_q<8, 2, 2, 4, 4, 2, kSwigluQ8>, grid, dim3(256), lds, s, g);
+    else
+      launch_k(k_gemm_q<4, 2, 2, 4, 4, 2, kSwigluQ8>, grid, dim3(256), lds, s, g);
+    return true;
+  }
+  g.out = o.out;
+  g.ldo = o.ld;
+  g.rope_d = rope_d;
+  g.rope_rows = rope_d ? rope_rows : 0;
+  const dim3 grid(tile_order(g, w.rows, 128, 128, wb));
+  constexpr int lds = lds_bytes_q<2, 2, 4, 4, kStore>();
+  if (epi == kEpiResidual) {
+    if (q8)
+      launch_k(k_gemm_q<8, 2, 2, 4, 4, 2, kAccumulate>, grid, dim3(256), lds, s, g);
+    else
+      launch_k(k_gemm_q<4, 2, 2, 4, 4, 2, kAccumulate>, grid, dim3(256), lds, s, g);
+  } else {
+    if (q8)
+      launch_k(k_gemm_q<8, 2, 2, 4, 4, 2, kStore>, grid, dim3(256), lds, s, g);
+    else
+      launch_k(k_gemm_q<4, 2, 2, 4, 4, 2, kStore>, grid, dim3(256), lds, s, g);
   }
   return true;
 }
@@ -2985,6 +3052,9 @@ void launch_attn_combine(hipStream_t s, int rows, const StepDims &d, const uint3
   const int threads = ((d.D + kWave - 1) / kWave) * kWave;
   if (act_dtype == kActQ8)
     launch_k(k_attn_combine<kActQ8>, dim3(rows, d.NH), dim3(threads), 0, s, d, row_pos,
+                       partial, nbp, act, row_err);
+  else if (act_dtype == kActQ8H)
+    launch_k(k_attn_combine<kActQ8H>, dim3(rows, d.NH), dim3(threads), 0, s, d, row_pos,
                        partial, nbp, act, row_err);
   else if (act_dtype == kActF32)
     launch_k(k_attn_combine<kActF32>, dim3(rows, d.NH), dim3(threads), 0, s, d, row_pos,

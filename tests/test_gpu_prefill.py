@@ -1,7 +1,14 @@
 """Packed-prefill regime (F16 weights, 128+ packed rows): the linears run on
 the matrix cores with f32 sums instead of the reference's f64 sums
 (cpu.rs:31-35), so this regime is checked to the north_star tolerance for F16
-logits (max-abs 1e-2), not bit for bit.  Greedy ids must agree wherever the
+logits (max-abs 1e-2), not bit for bit.  Q8_0/Q5_0/Q4_0 weights take the
+regime's quantized GEMM (weights dequantized to binary16 in LDS, binary16
+activations, f32 sums) where the reference multiplies Q8_0-quantized
+activations with the int8 blocks (quant.rs:245-292): checked to the
+quantized tolerance (max-abs 3e-2) on 2-layer models, and at the full
+24-layer shape against the reference's own response to a binary16-sized
+perturbation (its Q8_0 activation rounding makes that path ill-conditioned
+there; see test_mixed_prefill_and_decode_full_shape).  Greedy ids must agree wherever the
 reference's top-2 margin exceeds the measured difference.  The same steps
 with the matrix-core path switched off (COHX_PREFILL_MFMA=0) stay bit-exact
 against the oracle, and so does a decode-only step of the regime's width
@@ -12,12 +19,14 @@ import numpy as np
 import pytest
 
 import cohx
+import gguf
 import orc
 import synth
 
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-2
+TOL_Q = 3e-2  # quantized weights
 
 
 def make(cfg, t, mfma, **kw):
@@ -32,12 +41,12 @@ def make(cfg, t, mfma, **kw):
             os.environ["COHX_PREFILL_MFMA"] = old
 
 
-def close(got, want, what):
+def close(got, want, what, tol=TOL):
     diff = float(np.abs(got.astype(np.float64) - want).max())
     order = np.sort(want)
     margin = float(order[-1] - order[-2])
     print(f"{what}: max-abs {diff:.3g}, top1-top2 margin {margin:.3g}", flush=True)
-    assert diff <= TOL, what
+    assert diff <= tol, what
     if margin > 2 * diff:
         assert int(np.argmax(got)) == int(np.argmax(want)), what
     return diff
@@ -73,32 +82,118 @@ def test_prefill_chunk_matches_oracle_within_tolerance():
     close(r1["logits"], s.logits(), "decode after matrix-core chunk")
 
 
-def test_mixed_prefill_and_decode_full_shape():
+@pytest.mark.parametrize("dtype", ["q8_0", "q5_0", "q4_0"])
+def test_quantized_prefill_matches_oracle_within_tolerance(dtype):
+    """A quantized model's prefill chunk of 150 rows after 40 prompt tokens,
+    beside a decode lane (head_dim 64: the chunk attention on the matrix
+    cores too), against the oracle: logits and appended K/V rows within the
+    quantized tolerance, greedy ids equal where the oracle's margin allows;
+    the same step with the regime off is bit-exact."""
+    print(f"case: {dtype} prefill chunk of 150 rows + a decode lane, quantized GEMM vs oracle", flush=True)
+    cfg = synth.config(layers=2, hidden=256, intermediate=512, heads=4, kv_heads=2,
+                       vocabulary=500, context=512)
+    c, t = synth.in_memory(cfg, dtype, seed=34)
+    kw = dict(max_lanes=4, max_rows=256, max_seqs=4, max_context=512)
+    o = orc.Model(c, t, threads=8)
+    rng = np.random.default_rng(8)
+    head = [int(v) for v in rng.integers(0, c["vocabulary"], 40)]
+    chunk = [int(v) for v in rng.integers(0, c["vocabulary"], 150)]
+    sa, sb = o.session(512), o.session(512)
+    for tok in head:
+        o.forward_batch([sa], [tok])
+    sb.fill_synthetic(300, 9, 1)
+    for tok in chunk:
+        o.forward_batch([sa], [tok])
+    o.forward_batch([sb], [77])
+    want = [sa.logits(), sb.logits()]
+    for mfma in (True, False):
+        m = make(c, t, mfma, **kw)
+        a, b = m.seq_alloc(), m.seq_alloc()
+        assert m.step([dict(seq=a, tokens=head)])[0]["status"] == 0
+        m.seq_fill_synthetic(b, 300, 9, 1)
+        res = m.step([dict(seq=a, tokens=chunk, logits=True), dict(seq=b, tokens=[77], logits=True)])
+        assert res[0]["status"] == 0 and res[1]["status"] == 0
+        if not mfma:
+            for r, w in zip(res, want):
+                assert np.array_equal(r["logits"], w)  # exact kernels: bit for bit
+            m.close()
+            continue
+        close(res[0]["logits"], want[0], f"{dtype} chunk lane", TOL_Q)
+        close(res[1]["logits"], want[1], f"{dtype} decode lane", TOL_Q)
+        for layer in range(c["layers"]):
+            for v in (False, True):
+                kv = float(np.abs(m.seq_read_kv(a, layer, v) - sa.kv(layer, v)).max())
+                print(f"layer {layer} {'V' if v else 'K'} rows: max-abs {kv:.3g}", flush=True)
+                assert kv <= TOL_Q, (layer, v, kv)
+        m.close()
+
+
+def scaled(t, name, factor):
+    """The model with tensor `name` (f32) multiplied by `factor` (in f32)."""
+    x = t[name]
+    f = (x.data.view(np.float32) * np.float32(factor)).astype(np.float32)
+    out = dict(t)
+    out[name] = gguf.Tensor(x.name, x.shape, x.dtype, f.view(np.uint8))
+    return out
+
+
+def mixed_step(m, chunks, kv):
+    lanes = []
+    for ch in chunks:
+        lanes.append(dict(seq=m.seq_alloc(), tokens=ch, logits=True))
+    for i, n in enumerate(kv):
+        s = m.seq_alloc()
+        m.seq_fill_synthetic(s, n, 8, i)
+        lanes.append(dict(seq=s, tokens=[int(10 + i)], logits=True))
+    res = m.step(lanes)
+    assert all(r["status"] == 0 for r in res)
+    return [r["logits"].astype(np.float64) for r in res]
+
+
+@pytest.mark.parametrize("dtype", ["f16", "q8_0"])
+def test_mixed_prefill_and_decode_full_shape(dtype):
     """Config 3's form at the full shape, shortened: two prefill chunks plus
     decode rows over seeded KV in one packed step; the matrix-core context
     against the exact context (itself pinned to the oracle by the other GPU
-    tests)."""
-    print("case: full-shape F16 mixed packed step, matrix cores vs exact", flush=True)
-    c, t = synth.in_memory(synth.config(), "f16", seed=32)
+    tests).
+
+    F16: every lane within 1e-2.  Q8_0: at 24 layers the reference's
+    quantized path is ill-conditioned.  Its Q8_0 activation rounding turns a
+    last-bit difference into a whole quantization step (which then feeds
+    every later layer), so a 1-ulp change of one norm weight vector already
+    moves its own logits by about 0.07 max-abs, past the 3e-2 quantized
+    tolerance (which the 2-layer tests meet).  The regime rounds operands to
+    binary16, so its yardstick is the reference's own response to one
+    binary16 step: the exact context with blk.0.attn_norm.weight scaled by
+    1 + 2^-11, measured here on the same lanes (about 0.08 max-abs on the
+    prefill lanes and 0.2 on the decode lanes over synthetic KV).  Each
+    lane's max-abs and rms distance from the exact context must stay within
+    twice that lane's yardstick."""
+    print(f"case: full-shape {dtype} mixed packed step, matrix cores vs exact", flush=True)
+    c, t = synth.in_memory(synth.config(), dtype, seed=32)
     kw = dict(max_lanes=8, max_rows=512, max_seqs=8, max_context=1024)
-    mm, me = make(c, t, True, **kw), make(c, t, False, **kw)
     rng = np.random.default_rng(6)
     chunks = [[int(v) for v in rng.integers(0, c["vocabulary"], n)] for n in (200, 131)]
     kv = [300, 900, 64, 512]
-    lanes_m, lanes_e = [], []
-    for m, lanes in ((mm, lanes_m), (me, lanes_e)):
-        for ch in chunks:
-            lanes.append(dict(seq=m.seq_alloc(), tokens=ch, logits=True))
-        for i, n in enumerate(kv):
-            s = m.seq_alloc()
-            m.seq_fill_synthetic(s, n, 8, i)
-            lanes.append(dict(seq=s, tokens=[int(10 + i)], logits=True))
-    rm, re = mm.step(lanes_m), me.step(lanes_e)
-    worst = 0.0
-    for i, (a, b) in enumerate(zip(rm, re)):
-        assert a["status"] == 0 and b["status"] == 0
-        worst = max(worst, close(a["logits"], b["logits"], f"lane {i}"))
-    print(f"worst lane max-abs {worst:.3g}", flush=True)
+    got = mixed_step(make(c, t, True, **kw), chunks, kv)
+    want = mixed_step(make(c, t, False, **kw), chunks, kv)
+    if dtype == "f16":
+        worst = max(close(a, b, f"lane {i}") for i, (a, b) in enumerate(zip(got, want)))
+        print(f"worst lane max-abs {worst:.3g}", flush=True)
+        return
+    moved = mixed_step(make(c, scaled(t, "blk.0.attn_norm.weight", 1 + 2**-11), False, **kw), chunks, kv)
+    rms = lambda d: float(np.sqrt(np.mean(d * d)))
+    for i, (a, b, y) in enumerate(zip(got, want, moved)):
+        d_reg, d_y = a - b, y - b
+        print(f"lane {i}: regime vs exact max-abs {np.abs(d_reg).max():.3g} rms {rms(d_reg):.3g}; "
+              f"exact under a 2^-11 norm change max-abs {np.abs(d_y).max():.3g} rms {rms(d_y):.3g}",
+              flush=True)
+        assert np.abs(d_y).max() > 0, i  # the yardstick is not degenerate
+        assert np.abs(d_reg).max() <= 2 * np.abs(d_y).max(), i
+        assert rms(d_reg) <= 2 * rms(d_y), i
+        order = np.sort(b)
+        if order[-1] - order[-2] > 2 * float(np.abs(d_reg).max()):
+            assert int(np.argmax(a)) == int(np.argmax(b)), i
 
 
 def test_chunk_attention_matches_oracle_within_tolerance():

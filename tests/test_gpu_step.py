@@ -8,6 +8,8 @@ sequential ones unless a partial sum rounds — the test reports any such
 difference with its size rather than hiding it (tolerance: max-abs <= 1e-2 for
 F16, <= 3e-2 for quantized, the bound stated for this path).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -22,13 +24,25 @@ TINY = synth.config(layers=2, hidden=128, intermediate=256, heads=4, kv_heads=2,
 TOL = {"f16": 1e-2, "q8_0": 3e-2, "q4_0": 3e-2}
 
 
-def build(dtype, seed, cfg=TINY, **kw):
+def build(dtype, seed, cfg=TINY, exact=False, **kw):
+    """exact: the context keeps the exact kernels at every row count (the
+    packed-prefill regime, held to a tolerance by test_gpu_prefill.py, off)."""
     c, t = synth.in_memory(cfg, dtype, seed=seed)
     kw.setdefault("max_lanes", 8)
     kw.setdefault("max_rows", 64)
     kw.setdefault("max_seqs", 8)
     kw.setdefault("max_context", 256)
-    return c, t, cohx.Model(c, t, **kw), orc.Model(c, t, threads=8)
+    old = os.environ.get("COHX_PREFILL_MFMA")
+    if exact:
+        os.environ["COHX_PREFILL_MFMA"] = "0"
+    try:
+        m = cohx.Model(c, t, **kw)
+    finally:
+        if old is None:
+            os.environ.pop("COHX_PREFILL_MFMA", None)
+        else:
+            os.environ["COHX_PREFILL_MFMA"] = old
+    return c, t, m, orc.Model(c, t, threads=8)
 
 
 def compare_logits(got, want, dtype, what):
@@ -309,12 +323,14 @@ WIDE_H = synth.config(layers=2, hidden=1152, intermediate=256, heads=18, kv_head
 @pytest.mark.parametrize("dtype", ["q8_0", "q4_0"])
 def test_tall_ragged_steps_match_oracle(dtype, shape):
     """Packed steps of 197 rows (13 batch tiles: more than one row of the
-    8-tile gate+up workgroups, the second one partial), then a decode step,
-    bit for bit against the oracle: logits of every lane, greedy ids, the K/V
-    rows of every layer."""
+    8-tile gate+up workgroups, the second one partial) on the exact kernels
+    (the packed-prefill regime off), then a decode step, bit for bit against
+    the oracle: logits of every lane, greedy ids, the K/V rows of every
+    layer."""
     cfg = {"tiny": TINY, "odd_f": ODD_F, "wide_h": WIDE_H}[shape]
     print(f"case: tall ragged steps {dtype} {shape}", flush=True)
-    c, t, m, o = build(dtype, 12, cfg=cfg, max_lanes=4, max_rows=200, max_seqs=4, max_context=256)
+    c, t, m, o = build(dtype, 12, cfg=cfg, exact=True, max_lanes=4, max_rows=200, max_seqs=4,
+                       max_context=256)
     rng = np.random.default_rng(13)
     V = c["vocabulary"]
     seqs = [m.seq_alloc() for _ in range(3)]
