@@ -79,6 +79,15 @@ struct Args {
   int rope_d, rope_rows;
 };
 
+// SwiGLU's gate activation g / (1 + e^-g) in the regime's epilogues, on the
+// hardware exp2 and reciprocal (about 1 ulp each, ~1e-6 relative in all:
+// far inside the regime's binary16 operand rounding; the exact kernels keep
+// the reference's expf and IEEE division).  Large negative g gives -0, +inf
+// gives +inf, -inf and NaN give NaN, as the exact formula does.
+__device__ __forceinline__ float silu_fast(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.44269504f));
+}
+
 // Source column of feature f of a rope-ordered head block: even features are
 // a head's first half in order, odd ones its second half.
 __device__ __forceinline__ int rope_col(int f, int d) {
@@ -184,7 +193,68 @@ __device__ __forceinline__ void epilogue(const Args &g, f32x4 (&acc)[kTM][kTN], 
       if (bad) atomicOr(&g.row_err[g.err_rows ? (int)g.err_rows[r] : r], kErrNonFinite);
     }
     return;
-  } else if constexpr (kEpi == kSwigluF16 || kEpi == kSwigluQ8) {
+  } else if constexpr (kEpi == kSwigluQ8) {
+    // Every wave parks its sums in LDS as [token][feature] rows, gate
+    // features [0, BM/2) and up features apart; then each thread takes whole
+    // 32-feature blocks of one token: SwiGLU, the block's Q8_0 rounding and
+    // one contiguous 64-byte store.  Rows hold BM/2 features as float4
+    // quads, quad c of token t at slot 16 t' + (c ^ (t % 16)) within each
+    // 16-quad group (conflict-free for 16 consecutive tokens on both sides).
+    constexpr int kHalf = 16 * kWM * kTM / 2, kBN = 16 * kWN * kTN, kQuads = kHalf / 4;
+    static_assert(kHalf % 64 == 0, "whole 16-quad groups per row");
+    float4 *park = reinterpret_cast<float4 *>(smem);
+    auto slot = [](int t, int c) { return (t * kQuads + (c & ~15)) + ((c & 15) ^ (t & 15)); };
+#pragma unroll
+    for (int a = 0; a < kTM; a++) {
+      const int R = (wm * kTM + a) * 16 + 4 * (lane / 16);  // feature row within the tile
+      const bool up = R >= kHalf;
+      const int c = (R - (up ? kHalf : 0)) / 4;
+#pragma unroll
+      for (int b = 0; b < kTN; b++) {
+        const int t = (wn * kTN + b) * 16 + lr;
+        park[(up ? kBN * kQuads : 0) + slot(t, c)] =
+            make_float4(acc[a][b][0], acc[a][b][1], acc[a][b][2], acc[a][b][3]);
+      }
+    }
+    __syncthreads();
+    constexpr int kTasks = kBN * (kHalf / 32), kThreads = 64 * kWM * kWN;
+    for (int task = tid; task < kTasks; task += kThreads) {
+      const int t = task % kBN, blk = task / kBN;
+      const int r = r0 + t, fb = f0 + 32 * blk;
+      if (r >= g.M || fb >= F) continue;  // F % 32 == 0: whole blocks in or out
+      float h[32];
+      float m = 0.0f;
+      bool bad = false;
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const float4 gv = park[slot(t, 8 * blk + q)];
+        const float4 uv = park[kBN * kQuads + slot(t, 8 * blk + q)];
+        const float gq[4] = {gv.x, gv.y, gv.z, gv.w}, uq[4] = {uv.x, uv.y, uv.z, uv.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float v = silu_fast(gq[i]) * uq[i];
+          h[4 * q + i] = v;
+          bad |= !finitef(v);
+          m = fmaxf(m, fabsf(v));
+        }
+      }
+      const Q8Scale sc = q8_scale_of(m);
+      const float dh = h2f(sc.hd);
+      bad |= !finitef(dh) || !finitef(sc.inv);
+      uint32_t w[16];
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const uint16_t lo = q8_value_h(q8_round(h[2 * i], sc.inv), dh);
+        const uint16_t hi = q8_value_h(q8_round(h[2 * i + 1], sc.inv), dh);
+        bad |= !finitef(h2f(lo)) || !finitef(h2f(hi));
+        w[i] = lo | (uint32_t)hi << 16;
+      }
+      uint4 *dst = reinterpret_cast<uint4 *>(g.out16 + (size_t)r * F + fb);
+#pragma unroll
+      for (int i = 0; i < 4; i++) dst[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+      if (bad) atomicOr(&g.row_err[g.err_rows ? (int)g.err_rows[r] : r], kErrNonFinite);
+    }
+  } else if constexpr (kEpi == kSwigluF16) {
     // up waves (wm >= kWM/2) park their sums; the gate wave at wm - kWM/2
     // holds the matching gate sums in the same registers
     float *park = reinterpret_cast<float *>(smem);
@@ -200,53 +270,6 @@ __device__ __forceinline__ void epilogue(const Args &g, f32x4 (&acc)[kTM][kTN], 
     }
     __syncthreads();
     if (wm >= kWM / 2) return;
-    if constexpr (kEpi == kSwigluQ8) {
-      // a 32-feature block is tiles a, a + 1 (a even, 32-aligned) of one
-      // token column: 8 values in each of the lanes l, l + 16, l + 32, l + 48
-      static_assert(kTM % 2 == 0, "whole Q8_0 blocks per wave");
-#pragma unroll
-      for (int b = 0; b < kTN; b++) {
-        const int r = r0 + (wn * kTN + b) * 16 + lr;
-        const bool rvalid = r < g.M;
-        bool bad = false;
-#pragma unroll
-        for (int a = 0; a < kTM; a += 2) {
-          const int fb = f0 + (wm * kTM + a) * 16 + 4 * (lane / 16);
-          const bool live = rvalid && fb < F;  // F % 32 == 0: whole blocks in or out
-          float h[8];
-          float m = 0.0f;
-#pragma unroll
-          for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-              const float gv = acc[a + t][b][i];
-              const float uv = park[((pair * kPair) + ((a + t) * kTN + b) * 4 + i) * kWave + lane];
-              h[4 * t + i] = (gv / (1.0f + exp_f32(-gv))) * uv;
-              bad |= live && !finitef(h[4 * t + i]);
-              m = fmaxf(m, live ? fabsf(h[4 * t + i]) : 0.0f);
-            }
-          m = fmaxf(m, __shfl_xor(m, 16, kWave));
-          m = fmaxf(m, __shfl_xor(m, 32, kWave));
-          const Q8Scale sc = q8_scale_of(m);
-          const float dh = h2f(sc.hd);
-          if (!live) continue;
-          bad |= !finitef(dh) || !finitef(sc.inv);
-#pragma unroll
-          for (int t = 0; t < 2; t++) {
-            uint16_t q[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-              q[i] = q8_value_h(q8_round(h[4 * t + i], sc.inv), dh);
-              bad |= !finitef(h2f(q[i]));
-            }
-            *reinterpret_cast<uint2 *>(g.out16 + (size_t)r * F + fb + 16 * t) =
-                make_uint2(q[0] | (uint32_t)q[1] << 16, q[2] | (uint32_t)q[3] << 16);
-          }
-        }
-        if (bad) atomicOr(&g.row_err[g.err_rows ? (int)g.err_rows[r] : r], kErrNonFinite);
-      }
-      return;
-    }
 #pragma unroll
     for (int b = 0; b < kTN; b++) {
       const int r = r0 + (wn * kTN + b) * 16 + lr;
@@ -261,7 +284,7 @@ __device__ __forceinline__ void epilogue(const Args &g, f32x4 (&acc)[kTM][kTN], 
           const float gv = acc[a][b][i];
           const float uv = park[((pair * kPair) + (a * kTN + b) * 4 + i) * kWave + lane];
           bad |= !finitef(gv) || !finitef(uv);
-          h[i] = f2h((gv / (1.0f + exp_f32(-gv))) * uv);
+          h[i] = f2h(silu_fast(gv) * uv);
           bad |= !finitef(h2f(h[i]));
         }
         if (fb + 3 < F && F % 4 == 0) {
@@ -486,7 +509,7 @@ __device__ __forceinline__ int qswz(int R) { return (R >> 1) & 7; }
 template <int kWM, int kWN, int kTM, int kTN, int kEpi>
 constexpr int lds_bytes_q() {
   constexpr int ring = 2 * (16 * kWM * kTM + 16 * kWN * kTN) * 128;
-  constexpr int park = kEpi == kSwigluF16 || kEpi == kSwigluQ8 ? (kWM / 2) * kWN * kTM * kTN * 4 * 64 * 4 : 0;
+  constexpr int park = kEpi == kSwigluQ8 ? 16 * kWM * kTM * 16 * kWN * kTN * 4 : 0;
   return ring > park ? ring : park;
 }
 
@@ -498,7 +521,7 @@ __global__ __launch_bounds__(64 * kWM * kWN) void k_gemm_q(Args g) {
   static_assert(kWLoads % kThreads == 0 && kXLoads % kThreads == 0, "whole loads per thread");
   constexpr int kPW = kWLoads / kThreads, kPX = kXLoads / kThreads;
   constexpr int kStage = (kBM + kBN) * 8;  // 16-byte LDS slots per stage
-  static_assert(kR == 2 || kR == 4, "two or four block pairs in flight (K / 64 a multiple of kR)");
+  static_assert(kR == 2 || kR == 4, "two or four block pairs in flight");
   constexpr bool kGlu = kEpi == kSwigluF16 || kEpi == kSwigluQ8;
   static_assert(!kGlu || kWM % 2 == 0, "gate and up waves in pairs");
   using QT = typename QSlot<kQ>::type;
@@ -585,9 +608,12 @@ __global__ __launch_bounds__(64 * kWM * kWN) void k_gemm_q(Args g) {
 #pragma unroll
     for (int b = 0; b < kTN; b++) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int seg = lane / 16, lr = lane % 16;
+  // the last round of kR steps may run past the end (K / 64 need not be a
+  // multiple of kR): those steps do nothing (ks is the same in every thread)
   auto step = [&](auto J, int k0) __attribute__((always_inline)) {
     constexpr int j = decltype(J)::value;
     const int ks = k0 + j;
+    if (ks >= nk) return;
     __syncthreads();
     const f16x8 *stage = lds + (j % 2) * kStage;
     f16x8 af[2][kTM], bf[2][kTN];
