@@ -687,67 +687,6 @@ def copy_probe():
           flush=True)
 
 
-def launch_floor(n=200, reps=20):
-    """The GPU's cost per kernel boundary: a HIP graph of n one-element
-    kernels (torch's add_, plumbing) replayed back to back, timed with
-    events on the stream that replays it, next to the same kernel timed one
-    launch at a time with dispatch events."""
-    import torch
-    x = torch.zeros(1, device="cuda")
-    s = torch.cuda.Stream()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(s):
-        for _ in range(3):
-            x.add_(1.0)
-    torch.cuda.synchronize()
-    with torch.cuda.graph(g, stream=s):
-        for _ in range(n):
-            x.add_(1.0)
-    with torch.cuda.stream(s):
-        g.replay()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(reps):
-            g.replay()
-        b.record()
-    torch.cuda.synchronize()
-    graph_us = a.elapsed_time(b) * 1e3 / (n * reps)
-    single = []
-    with torch.cuda.stream(s):
-        for _ in range(n):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            x.add_(1.0)
-            b.record()
-            b.synchronize()
-            single.append(a.elapsed_time(b) * 1e3)
-    print(json.dumps({"graph_us_per_kernel": graph_us, "kernels_per_graph": n,
-                      "event_bracketed_us_per_kernel": sum(single) / len(single)}), flush=True)
-
-
-def valu_probe():
-    """The exact attention pass's instruction pattern without memory traffic
-    (libcohx_probe.so, csrc/probe.hip): per thread, C independent f64 chains
-    fed by f32 products and widenings, E elements per group, timed at 1280,
-    2560 and 5120 workgroups of 256 threads (about 1.25, 2.5 and 5 waves per
-    SIMD on 1024 SIMDs).  Reports ns per wave triple per SIMD."""
-    import ctypes
-    lib = ctypes.CDLL(os.path.join(ROOT, "coheryn-ai-studio_amd", "libcohx_probe.so"))
-    lib.cohx_probe_triples.argtypes = [ctypes.c_int] * 4 + [ctypes.POINTER(ctypes.c_float)]
-    steps, out = 64, []
-    for blocks in (1280, 2560, 5120):
-        for c, e in ((7, 4), (4, 4), (3, 2), (14, 2), (7, 8)):
-            ms = ctypes.c_float()
-            rc = lib.cohx_probe_triples(c, e, blocks, steps, ctypes.byref(ms))
-            if rc:
-                raise RuntimeError(f"probe failed ({rc})")
-            wave_triples_per_simd = blocks * 256 * steps * e * c / 64 / 1024
-            out.append({"chains": c, "elements": e, "workgroups": blocks, "us": ms.value * 1e3,
-                        "ns_per_wave_triple_per_simd": ms.value * 1e6 / wave_triples_per_simd})
-    print(json.dumps({"valu_probe": out}), flush=True)
-
-
 def read_probe():
     """The HBM read rate this device reaches with a plain streaming kernel
     (libcohx_probe.so): 1 GiB and 4 GiB buffers (past the 256 MB last-level
@@ -801,30 +740,6 @@ def measured_peaks():
             "mfma_f16_TFLOPs": 2048 * 4 * 8 * 256 * 16384 / (mf.value * 1e-3) / 1e12,
             "note": "streaming read of 1 GiB (float4 loads, 1024 workgroups) and back-to-back "
                     "v_mfma_f32_16x16x32_f16 (2048 workgroups); the roofline fractions use the published peaks"}
-
-
-def kstream_probe():
-    """The scores pass's K-row access pattern without its arithmetic
-    (libcohx_probe.so, k_probe_kstream): 128 rows, KV U[64,2048], pages
-    scattered over an owned pool, 24 layer pools read in turn (past the 256 MB
-    last-level cache, as in a step).  Mode 0 launches one workgroup per (row,
-    head, 256-token chunk) as the pass does, mode 1 loads every chunk twice
-    (the pass's two head parts), mode 3 loads it twice within one 512-thread
-    workgroup, mode 2 walks the items with a fixed number of persistent
-    workgroups."""
-    import ctypes
-    lib = ctypes.CDLL(os.path.join(ROOT, "coheryn-ai-studio_amd", "libcohx_probe.so"))
-    lib.cohx_probe_kstream.argtypes = [ctypes.c_int] * 3 + [ctypes.POINTER(ctypes.c_float),
-                                                            ctypes.POINTER(ctypes.c_double)]
-    out = []
-    for mode, blocks in ((0, 1), (1, 1), (3, 1), (2, 512), (2, 1024)):
-        ms, nbytes = ctypes.c_float(), ctypes.c_double()
-        rc = lib.cohx_probe_kstream(mode, blocks, 48, ctypes.byref(ms), ctypes.byref(nbytes))
-        if rc:
-            raise RuntimeError(f"probe failed ({rc})")
-        out.append({"mode": mode, "workgroups": blocks if mode == 2 else None, "us": ms.value * 1e3,
-                    "k_bytes": nbytes.value, "TBps": nbytes.value / (ms.value * 1e-3) / 1e12})
-    print(json.dumps({"kstream_probe": out}), flush=True)
 
 
 C5_SEQS, C5_PROMPT, C5_GEN, C5_CHUNK = 16, (64, 1024), 64, 256
@@ -985,14 +900,8 @@ def main():
                     help="run only this workload and print its JSON (profiling runs)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 1 GiB device-to-device 4 times (counter calibration)")
-    ap.add_argument("--launch-floor", action="store_true",
-                    help="only time a graph of one-element kernels (the cost of a kernel boundary)")
-    ap.add_argument("--valu-probe", action="store_true",
-                    help="only time the attention pass's f32-product / f64-chain pattern without memory")
     ap.add_argument("--mfma-probe", action="store_true",
                     help="only time back-to-back f16 MFMAs (the reachable matrix-core rate)")
-    ap.add_argument("--kstream-probe", action="store_true",
-                    help="only time the scores pass's K access pattern without arithmetic")
     ap.add_argument("--read-probe", action="store_true",
                     help="only time a plain streaming read of 1 and 4 GiB (the reachable HBM read rate)")
     ap.add_argument("--summarize-counters", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
@@ -1009,17 +918,8 @@ def main():
     if args.copy_probe:
         copy_probe()
         return
-    if args.launch_floor:
-        launch_floor()
-        return
-    if args.valu_probe:
-        valu_probe()
-        return
     if args.read_probe:
         read_probe()
-        return
-    if args.kstream_probe:
-        kstream_probe()
         return
     if args.mfma_probe:
         mfma_probe()

@@ -437,6 +437,7 @@ size_t layout_workspace(const cohx_model_desc &d, int nbp_h, int nbp_f, uint32_t
   }
   c.take(w.scores, R * NKV * kv_cap * 8);
   c.take(w.chunk_max, R * NH * nsc);
+  c.take(w.row_max, R * NH);
   c.take(w.den_part, R * NH * nsc);
   c.take(w.tiles, w.max_tiles);
   c.take(w.row_skip, R);
@@ -1441,11 +1442,11 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
                          ctx->page_table, w.scores, w.chunk_max, w.row_err);
       prof_end(ctx, e);
       e = prof_begin(ctx, kCatAttnSoftmax, b_softmax, 0);
-      launch_attn_exp(s, RX, kv_grid, sd, w.row_pos, w.scores, w.chunk_max, w.den_part);
+      launch_attn_exp(s, RX, kv_grid, sd, w.row_pos, w.scores, w.chunk_max, w.den_part, w.row_max);
       prof_end(ctx, e);
       e = prof_begin(ctx, kCatAttnPv, b_pv, f_attn);
       launch_attn_pv(s, RX, kv_grid, sd, vp, w.row_pos, w.row_seq, ctx->page_table, w.scores,
-                     w.den_part, w.partial);
+                     w.den_part, w.row_max, w.partial);
       prof_end(ctx, e);
     }
     // Q8_K operands: the combine writes f32 rows, then their blocks

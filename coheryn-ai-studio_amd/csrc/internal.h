@@ -56,8 +56,9 @@ struct Workspace {
   float *act_kd = nullptr;
   int16_t *act_ksum = nullptr;
   float *act_f32 = nullptr;
-  float *scores = nullptr;  // [rows][kv_heads][kv_cap][8]: scores, then weights
+  float *scores = nullptr;  // [rows][kv_heads][kv_cap][8]: scores (head slot within the group)
   float *chunk_max = nullptr, *logits = nullptr;
+  float *row_max = nullptr;  // [rows][heads] softmax maximum of each exact-pass row
   double *partial = nullptr;   // [rows][heads][max_chunks][head_dim] (chunk rows: f32 segment records)
   double *den_part = nullptr;  // [rows][heads][256-token chunks] softmax denominator partials
   // prefill chunks on the matrix cores: (16-row tile, key segment) work

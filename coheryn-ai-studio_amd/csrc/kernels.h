@@ -159,14 +159,18 @@ void launch_attn_scores(hipStream_t s, int rows, int max_kv, const StepDims &d, 
                         const float *kpool, const uint32_t *row_pos, const uint32_t *row_seq,
                         const int32_t *page_table, float *scores, float *chunk_max,
                         uint32_t *row_err);
-// Scores [row][kv_head][t][8] replaced in place by e = exp(s - max); the f64
-// sums of e per 256-token chunk into den_part[row][head][chunk].
+// The f64 sums of e = exp(s - max) per 256-token chunk into
+// den_part[row][head][chunk], and each row's maximum into row_max[row][head]
+// (scores [row][kv_head][t][8] are only read).
 void launch_attn_exp(hipStream_t s, int rows, int max_kv, const StepDims &d,
-                     const uint32_t *row_pos, float *scores, const float *chunk_max,
-                     double *den_part);
+                     const uint32_t *row_pos, const float *scores, const float *chunk_max,
+                     double *den_part, float *row_max);
+// Values: e again from the scores and row_max, p = e / den, the f64 partial
+// sums of p v per 128-token chunk into partial.
 void launch_attn_pv(hipStream_t s, int rows, int max_kv, const StepDims &d, const float *vpool,
                     const uint32_t *row_pos, const uint32_t *row_seq, const int32_t *page_table,
-                    const float *escores, const double *den_part, double *partial);
+                    const float *scores, const double *den_part, const float *row_max,
+                    double *partial);
 // Matrix-core attention for prefill chunks (tolerance regime): tiles[i] =
 // {first packed row, rows (<= 16) | key segment << 8, sequence, position of
 // the first row}; a workgroup attends to keys [seg * kChunkSegKeys, + kChunkSegKeys)

@@ -2002,15 +2002,17 @@ __global__ __launch_bounds__(256) void k_attn_scores(StepDims d, const float *__
 
 // Pass 2 (exponentials), one block per (row, KV head, 256-token chunk); a
 // thread owns one head slot (tid % 8) of tokens tid/8 + 32k, k < 8, so the
-// scores are read and written as consecutive floats.  M = max over the
-// row's chunk maxima; e = f32(exp(s - M)) replaces s in place; the chunk's
-// f64 sum of e per head (token order within a thread, then a fixed tree)
-// goes to den_part[row][head][chunk].
+// scores are read as consecutive floats.  M = max over the row's chunk
+// maxima (chunk 0's block stores it in row_max[row][head]); the chunk's f64
+// sum of e = f32(exp(s - M)) per head (token order within a thread, then a
+// fixed tree) goes to den_part[row][head][chunk].  The exponentials are not
+// stored: the value pass forms the same e from s and M.
 template <int kG>
 __global__ __launch_bounds__(256) void k_attn_exp(StepDims d, const uint32_t *__restrict__ row_pos,
-                                                  float *__restrict__ scores,
+                                                  const float *__restrict__ scores,
                                                   const float *__restrict__ chunk_max,
-                                                  double *__restrict__ den_part) {
+                                                  double *__restrict__ den_part,
+                                                  float *__restrict__ row_max) {
   constexpr int kT = 256, kW = kT / kWave, kK = kT / 32;
   __shared__ float redf[kW][8];
   __shared__ double redd[kW][8];
@@ -2024,7 +2026,7 @@ __global__ __launch_bounds__(256) void k_attn_exp(StepDims d, const uint32_t *__
   const int slot = threadIdx.x % 8, tok = threadIdx.x / 8;
   const int nch = (kv + kT - 1) / kT, nsc = (d.kv_cap + kT - 1) / kT;
   const bool live = slot < kG;
-  float *base = scores + (((size_t)r * d.NKV + g) * d.kv_cap + t0) * 8 + threadIdx.x;
+  const float *base = scores + (((size_t)r * d.NKV + g) * d.kv_cap + t0) * 8 + threadIdx.x;
   float sv[kK];
 #pragma unroll
   for (int k = 0; k < kK; k++) {
@@ -2042,15 +2044,12 @@ __global__ __launch_bounds__(256) void k_attn_exp(StepDims d, const uint32_t *__
   if (lane < 8) redf[w][lane] = m;
   __syncthreads();
   m = fmaxf(fmaxf(redf[0][slot], redf[1][slot]), fmaxf(redf[2][slot], redf[3][slot]));
+  if (c == 0 && threadIdx.x < kG) row_max[(size_t)r * d.NH + g * kG + threadIdx.x] = m;
   double den = 0.0;
 #pragma unroll
   for (int k = 0; k < kK; k++) {
     const int t = t0 + tok + 32 * k;
-    if (t < kv && live) {
-      const float e = exp_f32_tab(sv[k] - m, s_tab);
-      base[k * kT] = e;
-      den += (double)e;
-    }
+    if (t < kv && live) den += (double)exp_f32_tab(sv[k] - m, s_tab);
   }
   den += __shfl_xor(den, 8, kWave);
   den += __shfl_xor(den, 16, kWave);
@@ -2065,8 +2064,10 @@ __global__ __launch_bounds__(256) void k_attn_exp(StepDims d, const uint32_t *__
 }
 
 // Pass 3 (values).  Prologue: den = the row's chunk partials summed in a
-// fixed order (lane-strided, then butterfly), inv = f32(1/den), and the
-// block's 128 tokens of weights p = e * inv (cpu.rs:196-201) staged in LDS.
+// fixed order (lane-strided, then butterfly), inv = f32(1/den), e =
+// f32(exp(s - M)) again from the scores and the row maximum (the exponent
+// pass's bits), and the block's 128 tokens of weights p = e * inv
+// (cpu.rs:196-201) staged in LDS.
 // Then wave w takes pages 2w and 2w+1 of the block's 128 tokens (16 tokens
 // each), lane = element j: acc[h] += f64(p_t[h] * v_t[j]) in token order; the
 // 4 waves' sums are combined in a fixed order into the chunk's f64 partial.
@@ -2078,8 +2079,9 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
                                                  const uint32_t *__restrict__ row_pos,
                                                  const uint32_t *__restrict__ row_seq,
                                                  const int32_t *__restrict__ pt,
-                                                 const float *__restrict__ escores,
+                                                 const float *__restrict__ scores,
                                                  const double *__restrict__ den_part,
+                                                 const float *__restrict__ row_max,
                                                  double *__restrict__ partial) {
   constexpr int kE = (kD + kWave - 1) / kWave;  // elements per lane (lanes >= kD idle when kD < 64)
   static_assert(kChunk * 2 == 256, "one float4 of weights per thread");
@@ -2094,6 +2096,8 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
   __shared__ double red[3][kG][kD];
   __shared__ float s_inv[8];
   __shared__ float4 s_p[kChunk * 2];
+  __shared__ uint64_t s_tab[32];  // expf's table, read per lane below
+  if (threadIdx.x < 32) s_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int nch = (kv + 255) / 256, nsc = (d.kv_cap + 255) / 256;
@@ -2105,11 +2109,17 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
     const int hh = wave + 4 * i;
     if (hh < kG && lane < nch) dsum[i] = den_part[((size_t)r * d.NH + g * kG + hh) * nsc + lane];
   }
-  // (2) this thread's 4 exponentials
+  // (2) this thread's 4 scores and their heads' row maxima
   const int et = t0 + threadIdx.x / 2, ehalf = threadIdx.x % 2;
   float4 e = make_float4(0.f, 0.f, 0.f, 0.f);
   if (et < kv)
-    e = reinterpret_cast<const float4 *>(escores + (((size_t)r * d.NKV + g) * d.kv_cap + et) * 8)[ehalf];
+    e = reinterpret_cast<const float4 *>(scores + (((size_t)r * d.NKV + g) * d.kv_cap + et) * 8)[ehalf];
+  float mx[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int hh = ehalf * 4 + i;
+    mx[i] = hh < kG ? row_max[(size_t)r * d.NH + g * kG + hh] : 0.0f;
+  }
   // (3) the wave's two pages of V, zero past the sequence's end.  Addresses
   // are clamped into the last valid page so the loads need no branch.
   const int32_t *ptr = pt + (size_t)row_seq[r] * d.max_pages;
@@ -2141,11 +2151,13 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
   }
   __syncthreads();
   {
+    // tokens past the end keep p = 0 (their products must be +-0)
     const int b = ehalf * 4;
-    e.x = b + 0 < kG ? e.x * s_inv[b + 0] : 0.0f;
-    e.y = b + 1 < kG ? e.y * s_inv[b + 1] : 0.0f;
-    e.z = b + 2 < kG ? e.z * s_inv[b + 2] : 0.0f;
-    e.w = b + 3 < kG ? e.w * s_inv[b + 3] : 0.0f;
+    const bool live = et < kv;
+    e.x = live && b + 0 < kG ? exp_f32_tab(e.x - mx[0], s_tab) * s_inv[b + 0] : 0.0f;
+    e.y = live && b + 1 < kG ? exp_f32_tab(e.y - mx[1], s_tab) * s_inv[b + 1] : 0.0f;
+    e.z = live && b + 2 < kG ? exp_f32_tab(e.z - mx[2], s_tab) * s_inv[b + 2] : 0.0f;
+    e.w = live && b + 3 < kG ? exp_f32_tab(e.w - mx[3], s_tab) * s_inv[b + 3] : 0.0f;
     s_p[threadIdx.x] = e;
   }
   __syncthreads();
@@ -2997,14 +3009,14 @@ void launch_attn_scores(hipStream_t s, int rows, int max_kv, const StepDims &d, 
 }
 
 void launch_attn_exp(hipStream_t s, int rows, int max_kv, const StepDims &d,
-                     const uint32_t *row_pos, float *scores, const float *chunk_max,
-                     double *den_part) {
+                     const uint32_t *row_pos, const float *scores, const float *chunk_max,
+                     double *den_part, float *row_max) {
   const dim3 grid(rows, d.NKV, (max_kv + 255) / 256);
   switch (d.G) {
 #define L(GG)                                                                               \
   case GG:                                                                                  \
     launch_k(k_attn_exp<GG>, grid, dim3(256), 0, s, d, row_pos, scores, chunk_max, \
-                       den_part);                                                           \
+                       den_part, row_max);                                                  \
     break;
     L(1) L(2) L(4) L(6) L(7) L(8)
 #undef L
@@ -3014,12 +3026,13 @@ void launch_attn_exp(hipStream_t s, int rows, int max_kv, const StepDims &d,
 
 void launch_attn_pv(hipStream_t s, int rows, int max_kv, const StepDims &d, const float *vpool,
                     const uint32_t *row_pos, const uint32_t *row_seq, const int32_t *page_table,
-                    const float *escores, const double *den_part, double *partial) {
+                    const float *scores, const double *den_part, const float *row_max,
+                    double *partial) {
   const dim3 grid(rows, d.NKV, (max_kv + kChunk - 1) / kChunk);
   bool ok = true;
 #define L(DD, GG)                                                                          \
   launch_k((k_attn_pv<DD, GG>), grid, dim3(256), 0, s, d, vpool, row_pos, row_seq, \
-                     page_table, escores, den_part, partial)
+                     page_table, scores, den_part, row_max, partial)
   COHX_DG_DISPATCH(d.D, d.G, L);
 #undef L
   (void)ok;
