@@ -2210,10 +2210,13 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
 // Prefill chunks on the matrix cores (tolerance regime, used only with the
 // matrix-core linears).  A workgroup takes up to 16 consecutive rows of one
 // lane and one KV head; wave w is query head g*kG + w.  Key tiles of 64
-// tokens are staged in LDS as bf16 hi/lo pairs (x = hi + lo + O(2^-17 x)),
-// and every product runs as three v_mfma_f32_16x16x32_bf16 (lo*hi + hi*lo +
-// hi*hi, f32 sums), which keeps scores and outputs within ~2^-16 relative of
-// f32 arithmetic at the bf16 rate and f32 exponent range.
+// tokens are staged in LDS as binary16: K as a hi/lo pair (k = hi + lo to
+// about 2^-22 relative), V rounded once; Q and P enter rounded to binary16
+// (2^-12 relative, the rounding the regime's linears already give their
+// operands).  S = (K_lo + K_hi) Q^T takes two v_mfma_f32_16x16x32_f16, O =
+// V P one, all with f32 sums.  (A bfloat16 hi/lo split of every operand,
+// three MFMAs per product, ran 2.46 against 1.83 ms/step at C3; with V split
+// too, 2.22.)
 //   S^T = K Q^T: lane (grp, c) ends up holding S[row c][key 16n + 4grp + i]
 //     for n, i in 0..3, so one lane owns one query row: the row max and sum
 //     need two cross-lane steps, and P never leaves registers.
@@ -2233,9 +2236,6 @@ __device__ __forceinline__ void lds_load16(const void *global, void *lds) {
   __builtin_amdgcn_global_load_lds(global, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
 }
 typedef float float4v __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // Segment record of a chunk row: in the row's own partial-sum space (the
 // exact passes skip chunk rows), kChunkSegFloats floats per key segment.
@@ -2244,13 +2244,17 @@ __device__ __forceinline__ float *chunk_seg_at(double *partial, const StepDims &
          seg * kChunkSegFloats;
 }
 
+typedef _Float16 f16x8c __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4c __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2c __attribute__((ext_vector_type(2)));
+
 namespace chunk {
-constexpr int kD = 64, kKT = 64, kS = 72;  // head dim, keys per tile, LDS row stride (bf16)
+constexpr int kD = 64, kKT = 64, kS = 72;  // head dim, keys per tile, LDS row stride (16-bit elements)
 constexpr int kItems = kKT / 2 * kD / 4;   // staging items: (token pair, 4 dims)
 
-__device__ __forceinline__ void split(float x, __bf16 &hi, __bf16 &lo) {
-  hi = (__bf16)x;
-  lo = (__bf16)(x - (float)hi);
+__device__ __forceinline__ void split(float x, _Float16 &hi, _Float16 &lo) {
+  hi = (_Float16)x;
+  lo = (_Float16)(x - (float)hi);
 }
 
 // Position of key k (0..63 within a tile) in the V^T rows: the k-slot order
@@ -2271,10 +2275,16 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
   using namespace chunk;
   constexpr int kThreads = 64 * kG, kPer = (kItems + kThreads - 1) / kThreads;
   constexpr int kRawSlots = kKT * kD / 4;  // 16-byte slots of one raw f32 tile: [token][dim quad]
-  __shared__ __align__(16) __bf16 s_kh[kKT * kS];
-  __shared__ __align__(16) __bf16 s_kl[kKT * kS];
-  __shared__ __align__(16) __bf16 s_vh[kD * kS];
-  __shared__ __align__(16) __bf16 s_vl[kD * kS];
+  using E = _Float16;
+  using E8 = f16x8c;
+  using E4 = f16x4c;
+  using E2 = f16x2c;
+  auto mfma = [](E8 a, E8 b, float4v c) __attribute__((always_inline)) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  };
+  __shared__ __align__(16) E s_kh[kKT * kS];
+  __shared__ __align__(16) E s_kl[kKT * kS];
+  __shared__ __align__(16) E s_v[kD * kS];  // V^T
   __shared__ __align__(16) float4 s_rk[kRawSlots];  // the next tile's raw K and V, straight from memory
   __shared__ __align__(16) float4 s_rv[kRawSlots];
   __shared__ int32_t s_pages[kChunkSegKeys / kPage];
@@ -2290,8 +2300,8 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
     const int np = (t_end - t_begin + kPage - 1) / kPage;
     for (int i = threadIdx.x; i < np; i += kThreads) s_pages[i] = ptr[t_begin / kPage + i];
   }
-  // B operand of S^T: Q[row c][dims 32ks + 8grp .. +7] in log2 units, split
-  bf16x8 qh[2], ql[2];
+  // B operand of S^T: Q[row c][dims 32ks + 8grp .. +7] in log2 units
+  E8 qh[2];
   {
     const float qs = d.scale * 1.4426950408889634f;
     const float *qrow = q_rot + (size_t)(tile.x + min(c, nr - 1)) * d.H + h * kD;
@@ -2301,12 +2311,7 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
       const float4 b = *reinterpret_cast<const float4 *>(qrow + 32 * ks + 8 * grp + 4);
       const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        __bf16 hi, lo;
-        split(v[j] * qs, hi, lo);
-        qh[ks][j] = hi;
-        ql[ks][j] = lo;
-      }
+      for (int j = 0; j < 8; j++) qh[ks][j] = (E)(v[j] * qs);
     }
   }
   float4v o[4];
@@ -2325,7 +2330,7 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
     }
   };
   // split: item i = (token pair i / 16, dims 4 * (i % 16)) from the raw tile
-  // into bf16 hi/lo K rows and V^T rows (zeros past the segment)
+  // into binary16 hi/lo K rows and binary16 V^T rows (zeros past the segment)
   auto stash = [&](int t0) {
 #pragma unroll
     for (int u = 0; u < kPer; u++) {
@@ -2342,32 +2347,26 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
 #pragma unroll
       for (int e = 0; e < 2; e++) {
         const float kx[4] = {rk[e].x, rk[e].y, rk[e].z, rk[e].w};
-        bf16x4 hi, lo;
+        E4 hi, lo;
 #pragma unroll
         for (int x = 0; x < 4; x++) {
-          __bf16 a, b;
+          E a, b;
           split(kx[x], a, b);
           hi[x] = a;
           lo[x] = b;
         }
-        *reinterpret_cast<bf16x4 *>(s_kh + (k + e) * kS + d4) = hi;
-        *reinterpret_cast<bf16x4 *>(s_kl + (k + e) * kS + d4) = lo;
+        *reinterpret_cast<E4 *>(s_kh + (k + e) * kS + d4) = hi;
+        *reinterpret_cast<E4 *>(s_kl + (k + e) * kS + d4) = lo;
       }
       // keys k and k+1 sit side by side in the V^T order (vperm keeps pairs)
       const float v0[4] = {rv[0].x, rv[0].y, rv[0].z, rv[0].w};
       const float v1[4] = {rv[1].x, rv[1].y, rv[1].z, rv[1].w};
 #pragma unroll
       for (int x = 0; x < 4; x++) {
-        bf16x2 hi, lo;
-        __bf16 a, b;
-        split(v0[x], a, b);
-        hi[0] = a;
-        lo[0] = b;
-        split(v1[x], a, b);
-        hi[1] = a;
-        lo[1] = b;
-        *reinterpret_cast<bf16x2 *>(s_vh + (d4 + x) * kS + vp) = hi;
-        *reinterpret_cast<bf16x2 *>(s_vl + (d4 + x) * kS + vp) = lo;
+        E2 v2;
+        v2[0] = (E)v0[x];
+        v2[1] = (E)v1[x];
+        *reinterpret_cast<E2 *>(s_v + (d4 + x) * kS + vp) = v2;
       }
     }
   };
@@ -2387,11 +2386,10 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
 #pragma unroll
       for (int ks = 0; ks < 2; ks++) {
         const int at = (16 * n + c) * kS + 32 * ks + 8 * grp;
-        const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(s_kh + at);
-        const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(s_kl + at);
-        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[ks], s[n], 0, 0, 0);
-        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[ks], s[n], 0, 0, 0);
-        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[ks], s[n], 0, 0, 0);
+        const E8 kh = *reinterpret_cast<const E8 *>(s_kh + at);
+        const E8 kl = *reinterpret_cast<const E8 *>(s_kl + at);
+        s[n] = mfma(kl, qh[ks], s[n]);
+        s[n] = mfma(kh, qh[ks], s[n]);
       }
     }
     if (t0 + kKT - 1 > pos0 || t0 + kKT > t_end) {  // causal mask key <= row; keys past the segment
@@ -2415,8 +2413,9 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
     const float mref = mx == -__builtin_inff() ? 0.0f : mx;
     const float alpha = __builtin_amdgcn_exp2f(m - mref);  // 0 on the first live tile
     m = mx;
-    // B operand of O^T: P[row c][k-slot j of step ks], split into hi/lo
-    bf16x8 ph[2], pl[2];
+    // B operand of O^T: P[row c][k-slot j of step ks] (the f32 sum keeps
+    // the unrounded p)
+    E8 ph[2];
     float sum = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < 2; ks++)
@@ -2424,10 +2423,7 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
       for (int j = 0; j < 8; j++) {
         const float p = __builtin_amdgcn_exp2f(s[2 * ks + j / 4][j % 4] - mref);
         sum += p;
-        __bf16 hi, lo;
-        split(p, hi, lo);
-        ph[ks][j] = hi;
-        pl[ks][j] = lo;
+        ph[ks][j] = (E)p;
       }
     l = l * alpha + sum;  // this lane's share of the row sum
 #pragma unroll
@@ -2438,11 +2434,7 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
 #pragma unroll
       for (int ks = 0; ks < 2; ks++) {
         const int at = (16 * n + c) * kS + 32 * ks + 8 * grp;
-        const bf16x8 vh = *reinterpret_cast<const bf16x8 *>(s_vh + at);
-        const bf16x8 vl = *reinterpret_cast<const bf16x8 *>(s_vl + at);
-        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph[ks], o[n], 0, 0, 0);
-        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl[ks], o[n], 0, 0, 0);
-        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[ks], o[n], 0, 0, 0);
+        o[n] = mfma(*reinterpret_cast<const E8 *>(s_v + at), ph[ks], o[n]);
       }
   }
   l += __shfl_xor(l, 16, kWave);
