@@ -356,3 +356,40 @@ def test_tall_ragged_steps_match_oracle(dtype, shape):
             for values in (False, True):
                 assert np.array_equal(m.seq_read_kv(seqs[i], layer, values), sess[i].kv(layer, values))
     assert mismatched == 0
+
+
+LONG = synth.config(layers=2, hidden=128, intermediate=256, heads=4, kv_heads=2, vocabulary=300,
+                    context=8192)
+
+
+@pytest.mark.parametrize("dtype", ["q8_0", "f16"])
+def test_long_rows_match_oracle(dtype):
+    """Decode steps whose rows attend to up to 4700 positions (19 score
+    chunks of 256 keys, 37 value chunks of 128) beside rows of 2 to 30
+    positions, bit for bit against the oracle: logits of every lane, greedy
+    ids, the K/V rows appended."""
+    print(f"case: long rows {dtype}", flush=True)
+    c, t, m, o = build(dtype, 14, cfg=LONG, max_lanes=4, max_rows=8, max_seqs=4, max_context=4800)
+    rng = np.random.default_rng(15)
+    mismatched = 0
+    for k, lens in enumerate(((4599, 30, 1000), (4699, 2, 4200))):
+        seqs = [m.seq_alloc() for _ in lens]
+        sess = [o.session(4800) for _ in lens]
+        for i, n in enumerate(lens):
+            m.seq_fill_synthetic(seqs[i], n, 8, i)
+            sess[i].fill_synthetic(n, 8, i)
+        for step in range(2):
+            toks = [int(v) for v in rng.integers(0, c["vocabulary"], len(lens))]
+            res = m.step([dict(seq=s, tokens=[x], logits=True) for s, x in zip(seqs, toks)])
+            assert not o.forward_batch(sess, toks).any()
+            for i, r in enumerate(res):
+                assert r["status"] == 0
+                want = sess[i].logits()
+                mismatched += compare_logits(r["logits"], want, dtype, f"case {k} step {step} lane {i}")
+                assert r["argmax"] == orc.Sampler().sample(want)[1]
+        for i, n in enumerate(lens):
+            for values in (False, True):
+                got = m.seq_read_kv_rows(seqs[i], 1, n, 2, values)
+                assert np.array_equal(got, sess[i].kv(1, values)[n:n + 2]), (k, i, values)
+            m.seq_free(seqs[i])
+    assert mismatched == 0
