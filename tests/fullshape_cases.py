@@ -54,12 +54,15 @@ def kv_rows_digest(rows_by_layer):
 def c2(lanes):
     """BASELINE configs[1] (32 lanes) and its 128-lane headline form: Q8_0
     weights, decode-only lanes over seeded KV of U[64, 2048] tokens, one
-    greedy token per lane per step, two steps."""
+    greedy token per lane per step: 16 steps at 32 lanes, 8 at 128 (each
+    step's greedy ids feed the next, so a lane's whole continuation is
+    checked)."""
     rng = np.random.default_rng(1000 + lanes)
     kv = [int(v) for v in rng.integers(64, 2049, lanes)]
     tokens = [int(v) for v in rng.integers(0, V_QWEN2, lanes)]
     return {"model_seed": SEED_Q8, "dtype": "q8_0", "fill_seed": 7000 + lanes, "kv": kv,
-            "tokens": tokens, "steps": 2, "context": 2048 + 8, "kv_check_layers": [0, 11, 23]}
+            "tokens": tokens, "steps": 16 if lanes <= 32 else 8, "context": 2048 + 24,
+            "kv_check_layers": [0, 11, 23]}
 
 
 def q4km(lanes=32):
@@ -81,13 +84,13 @@ def c4():
     """Q4_0 weights, 128 decode lanes in 8 groups of 16
     forked from one 256-token prefix per group (the prefix rows are filled
     once with the group's stream; each lane's private suffix with its own),
-    contexts up to 4096, two greedy steps."""
+    contexts up to 4096, eight greedy steps."""
     rng = np.random.default_rng(4004)
     lanes = C4_GROUPS * C4_GROUP
     suffix = [int(v) for v in rng.integers(0, C4_CONTEXT - C4_PREFIX - 8 + 1, lanes)]
     tokens = [int(v) for v in rng.integers(0, V_QWEN2, lanes)]
     return {"model_seed": SEED_Q4, "dtype": "q4_0", "fill_seed": 8004, "groups": C4_GROUPS,
-            "group": C4_GROUP, "prefix": C4_PREFIX, "suffix": suffix, "tokens": tokens, "steps": 2,
+            "group": C4_GROUP, "prefix": C4_PREFIX, "suffix": suffix, "tokens": tokens, "steps": 8,
             "context": C4_CONTEXT, "kv_check_layers": [0, 23]}
 
 
@@ -120,12 +123,11 @@ def c3():
 def c5():
     """the Qwen3.5-0.8B hybrid shape (bf16 weights), 16
     sequences with prompts of U[64, 1024] random ids, through the prompt's end
-    and 4 greedy tokens (the configuration's 64 are a throughput figure; the
-    parity check stops after 4)."""
+    and the configuration's 64 greedy tokens."""
     rng = np.random.default_rng(1005)
     plen = [int(v) for v in rng.integers(64, 1025, 16)]
     prompts = [[int(v) for v in rng.integers(0, 248320, n)] for n in plen]
-    return {"model_seed": SEED_Q35, "prompts": prompts, "generate": 4, "context": 1024 + 16}
+    return {"model_seed": SEED_Q35, "prompts": prompts, "generate": 64, "context": 1024 + 72}
 
 
 def spec_digest(spec):

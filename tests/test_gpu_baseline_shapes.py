@@ -289,9 +289,13 @@ def test_c3_f16_mixed_prefill_step_matches_oracle():
 
 def test_c5_qwen35_prefill_regime_greedy_ids_and_top_logits():
     """configs[4] with the packed-prefill regime on (the default): the prompt
-    steps' linears run as library BF16 GEMMs.  Greedy ids must equal the
-    oracle's; every sampled lane's top-1 and top-2 logits (the fixture keeps
-    those values) within 1e-2 of the oracle's."""
+    steps' linears run on the bfloat16 matrix-core GEMM (hi/lo operands, f32
+    sums).  Every sampled lane's top-1 and top-2 logits (the fixture keeps
+    those values) within 1e-2 of the oracle's, and greedy ids equal to the
+    oracle's over the whole 64-token continuation, except where the oracle's
+    own top-1/top-2 gap is within twice that deviation: a lane that takes the
+    other id there continues on its own tokens, and its check ends at that
+    sample."""
     import synth35
     spec = fc.c5()
     fx = fixture("c5", spec)
@@ -310,11 +314,12 @@ def test_c5_qwen35_prefill_regime_greedy_ids_and_top_logits():
     seqs = [m.seq_alloc() for _ in prompts]
     cursor = [0] * len(prompts)
     got = [[] for _ in prompts]
-    worst, gap = 0.0, float("inf")
-    while any(len(g) < spec["generate"] + 1 for g in got):
+    done = [False] * len(prompts)  # a lane's check ended (sampled all, or a near-tie took the other id)
+    worst, gap, compared, diverged = 0.0, float("inf"), 0, []
+    while not all(done):
         lanes, idx = [], []
         for i, p in enumerate(prompts):
-            if len(got[i]) >= spec["generate"] + 1:
+            if done[i]:
                 continue
             if cursor[i] < len(p):
                 toks = p[cursor[i]:cursor[i] + 256]
@@ -328,23 +333,32 @@ def test_c5_qwen35_prefill_regime_greedy_ids_and_top_logits():
         for (i, n, sampled), r in zip(idx, res):
             assert r["status"] == 0
             cursor[i] += n
-            if sampled:
-                k = len(got[i])
-                want = fx["samples"][i][k]
-                sm = fc.summary(r["logits"])
-                worst = max(worst, abs(sm["top1"] - want["top1"]), abs(sm["top2"] - want["top2"]))
-                gap = min(gap, want["top1"] - want["top2"])
-                got[i].append(int(r["argmax"]))
-    print(f"case c5 regime: worst top-1/top-2 logit deviation {worst:.3g}, "
-          f"smallest oracle top-1/top-2 gap {gap:.3g}", flush=True)
-    assert got == [[x["argmax"] for x in s] for s in fx["samples"]]
+            if not sampled:
+                continue
+            k = len(got[i])
+            want = fx["samples"][i][k]
+            sm = fc.summary(r["logits"])
+            dev = max(abs(sm["top1"] - want["top1"]), abs(sm["top2"] - want["top2"]))
+            worst = max(worst, dev)
+            gap = min(gap, want["top1"] - want["top2"])
+            compared += 1
+            got[i].append(int(r["argmax"]))
+            if got[i][-1] != want["argmax"]:
+                assert want["top1"] - want["top2"] <= 2 * max(dev, 1e-7), (i, k, want, sm)
+                diverged.append((i, k))
+                done[i] = True
+            elif len(got[i]) == spec["generate"] + 1:
+                done[i] = True
+    print(f"case c5 regime: {compared} samples compared, worst top-1/top-2 logit deviation "
+          f"{worst:.3g}, smallest oracle top-1/top-2 gap {gap:.3g}, near-tie divergences "
+          f"{diverged}", flush=True)
     assert worst <= 1e-2
     m.close()
 
 
 def test_c5_qwen35_sixteen_prompts_match_oracle():
     """Qwen3.5-0.8B shape, 16 prompts of U[64, 1024] ids in chunks
-    of 256 rows (rows before a prompt's end skip the head), then 4 greedy
+    of 256 rows (rows before a prompt's end skip the head), then 64 greedy
     tokens: every sampled lane's logits, the ids, and the last linear layer's
     conv ring and delta memory and the last full layer's K/V tail, bit for bit
     (the packed-prefill regime off: every step on the exact matvecs)."""
