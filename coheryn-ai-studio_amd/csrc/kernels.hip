@@ -2700,11 +2700,12 @@ constexpr int kPrefillRows = 128;
 
 // The packed-prefill regime's F16 GEMM (gemm.h) for one projection; false
 // (nothing launched) when K is not a multiple of 64.  Tiles measured on the
-// C3 shapes (2,616 packed rows): 128 x 128 with four K steps in flight for
-// the plain and residual projections (qkv 16.9, o 16.3, down 54.9 us), 256 x
-// 128 on eight waves for gate+up with the SwiGLU epilogue (95 us, which also
-// replaces a separate SwiGLU-to-binary16 pass), 128 x 64 for the head's few
-// logit rows.
+// C3 shapes (2,616 packed rows): 128 x 128 on eight waves of 64 features x 32
+// rows with four K steps in flight for the plain and residual projections
+// (qkv 15.8, o 15.8, down 49.0 us; on four waves of 64 x 64: 16.5, 18.4,
+// 55.6), 256 x 128 on eight waves for gate+up with the SwiGLU epilogue (67
+// us, which also replaces a separate SwiGLU-to-binary16 pass), 128 x 64 for
+// the head's few logit rows.
 static bool gemm_f16(hipStream_t s, Epilogue epi, const MatrixView &w, const uint16_t *x, int rows_b,
                      const MatvecOut &o, uint16_t *out16) {
   using namespace gemm;
@@ -2738,17 +2739,17 @@ static bool gemm_f16(hipStream_t s, Epilogue epi, const MatrixView &w, const uin
     g.out = o.out;
     g.ldo = o.ld;
     const dim3 grid(tile_order(g, w.rows, 128, 128));
-    constexpr int lds = lds_bytes<2, 2, 4, 4, false, kStore>();
+    constexpr int lds = lds_bytes<2, 4, 4, 2, false, kStore>();
     if (epi == kEpiResidual) {
       if (four)
-        launch_k(k_gemm<kF16, false, 2, 2, 4, 4, 4, kAccumulate>, grid, dim3(256), lds, s, g);
+        launch_k(k_gemm<kF16, false, 2, 4, 4, 2, 4, kAccumulate>, grid, dim3(512), lds, s, g);
       else
-        launch_k(k_gemm<kF16, false, 2, 2, 4, 4, 2, kAccumulate>, grid, dim3(256), lds, s, g);
+        launch_k(k_gemm<kF16, false, 2, 4, 4, 2, 2, kAccumulate>, grid, dim3(512), lds, s, g);
     } else {
       if (four)
-        launch_k(k_gemm<kF16, false, 2, 2, 4, 4, 4, kStore>, grid, dim3(256), lds, s, g);
+        launch_k(k_gemm<kF16, false, 2, 4, 4, 2, 4, kStore>, grid, dim3(512), lds, s, g);
       else
-        launch_k(k_gemm<kF16, false, 2, 2, 4, 4, 2, kStore>, grid, dim3(256), lds, s, g);
+        launch_k(k_gemm<kF16, false, 2, 4, 4, 2, 2, kStore>, grid, dim3(512), lds, s, g);
     }
   }
   return true;
@@ -2772,14 +2773,17 @@ bool launch_gemm_q(hipStream_t s, Epilogue epi, const MatrixView &w, const uint1
   g.err_rows = o.err_rows;
   const bool q8 = w.dtype == kFmtQ8;
   const double wb = q8 ? 34.0 / 32 : 18.0 / 32;
+  // 128 x 128 tiles on eight waves of 64 features x 32 rows, two block pairs
+  // in flight: on the C3 shapes (Q8_0) qkv 15.3, o 15.7, down 51.2, gate+up
+  // 76.6 us against 17.0, 18.5, 64.8, 83.5 on four waves of 64 x 64
   if (epi == kEpiSwiglu) {
     g.out16 = out16;
     const dim3 grid(tile_order(g, w.rows / 2, 64, 128, wb));
-    constexpr int lds = lds_bytes_q<2, 2, 4, 4, kSwigluQ8>();
+    constexpr int lds = lds_bytes_q<2, 4, 4, 2, kSwigluQ8>();
     if (q8)
-      launch_k(k_gemm_q<8, 2, 2, 4, 4, 2, kSwigluQ8>, grid, dim3(256), lds, s, g);
+      launch_k(k_gemm_q<8, 2, 4, 4, 2, 2, kSwigluQ8>, grid, dim3(512), lds, s, g);
     else
-      launch_k(k_gemm_q<4, 2, 2, 4, 4, 2, kSwigluQ8>, grid, dim3(256), lds, s, g);
+      launch_k(k_gemm_q<4, 2, 4, 4, 2, 2, kSwigluQ8>, grid, dim3(512), lds, s, g);
     return true;
   }
   g.out = o.out;
@@ -2787,17 +2791,17 @@ bool launch_gemm_q(hipStream_t s, Epilogue epi, const MatrixView &w, const uint1
   g.rope_d = rope_d;
   g.rope_rows = rope_d ? rope_rows : 0;
   const dim3 grid(tile_order(g, w.rows, 128, 128, wb));
-  constexpr int lds = lds_bytes_q<2, 2, 4, 4, kStore>();
+  constexpr int lds = lds_bytes_q<2, 4, 4, 2, kStore>();
   if (epi == kEpiResidual) {
     if (q8)
-      launch_k(k_gemm_q<8, 2, 2, 4, 4, 2, kAccumulate>, grid, dim3(256), lds, s, g);
+      launch_k(k_gemm_q<8, 2, 4, 4, 2, 2, kAccumulate>, grid, dim3(512), lds, s, g);
     else
-      launch_k(k_gemm_q<4, 2, 2, 4, 4, 2, kAccumulate>, grid, dim3(256), lds, s, g);
+      launch_k(k_gemm_q<4, 2, 4, 4, 2, 2, kAccumulate>, grid, dim3(512), lds, s, g);
   } else {
     if (q8)
-      launch_k(k_gemm_q<8, 2, 2, 4, 4, 2, kStore>, grid, dim3(256), lds, s, g);
+      launch_k(k_gemm_q<8, 2, 4, 4, 2, 2, kStore>, grid, dim3(512), lds, s, g);
     else
-      launch_k(k_gemm_q<4, 2, 2, 4, 4, 2, kStore>, grid, dim3(256), lds, s, g);
+      launch_k(k_gemm_q<4, 2, 4, 4, 2, 2, kStore>, grid, dim3(512), lds, s, g);
   }
   return true;
 }
