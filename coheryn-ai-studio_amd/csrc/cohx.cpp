@@ -404,8 +404,12 @@ size_t layout_workspace(const cohx_model_desc &d, int nbp_h, int nbp_f, uint32_t
   w.lanes = NL;
   w.kv_cap = kv_cap;
   w.max_chunks = (uint32_t)chunks;
-  // prefill-chunk attention work items: 16-row tiles x key segments
+  // prefill-chunk attention work items: 16-row tiles x key segments; key
+  // tile images of the chunk lanes (16+ rows each, so at most R / 16 of them)
   w.max_tiles = ((R + 15) / 16 + NL) * ((kv_cap + kChunkSegKeys - 1) / kChunkSegKeys);
+  w.max_images = D == 64 ? (uint32_t)(std::min<size_t>(NL, R / 16) *
+                                      ((kv_cap + kChunkTileKeys - 1) / kChunkTileKeys) * NKV)
+                         : 0;
   w.logits_room = logits;
   Carver c{base};
   c.take(w.lane_info, (size_t)NL * 4);
@@ -440,6 +444,8 @@ size_t layout_workspace(const cohx_model_desc &d, int nbp_h, int nbp_f, uint32_t
   c.take(w.row_max, R * NH);
   c.take(w.den_part, R * NH * nsc);
   c.take(w.tiles, w.max_tiles);
+  c.take(w.stage, w.max_images);
+  c.take(w.img, (size_t)w.max_images * kChunkImgUnits);
   c.take(w.row_skip, R);
   c.take(w.row_map, R);
   c.take(w.partial, R * NH * chunks * D);
@@ -574,6 +580,7 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   Staging &h = ctx->host;
   const uint32_t NL = d->max_lanes;
   if (!rc) rc = halloc(ctx, &h.h_tiles, (size_t)ctx->ws.max_tiles);
+  if (!rc) rc = halloc(ctx, &h.h_stage, (size_t)std::max(ctx->ws.max_images, 1u));
   if (!rc) rc = halloc(ctx, &h.h_row_skip, (size_t)R);
   if (!rc) rc = halloc(ctx, &h.h_row_map, (size_t)R);
   if (!rc) rc = halloc(ctx, &h.h_upload, (size_t)NL * 4 + R);
@@ -591,7 +598,7 @@ void cohx_destroy(cohx_ctx *ctx) {
   drop_graphs(ctx);
   for (void *p : ctx->allocations) (void)hipFree(p);
   for (void *p : {(void *)ctx->host.h_upload, (void *)ctx->host.h_row_err, (void *)ctx->host.h_argmax,
-                  (void *)ctx->host.h_tiles, (void *)ctx->host.h_row_skip, (void *)ctx->host.h_row_map})
+                  (void *)ctx->host.h_tiles, (void *)ctx->host.h_stage, (void *)ctx->host.h_row_skip, (void *)ctx->host.h_row_map})
     if (p) (void)hipHostFree(p);
   q35_free(ctx);
   if (ctx->done) (void)hipEventDestroy(ctx->done);
@@ -971,6 +978,7 @@ struct Prepared {
   uint32_t max_kv = 0;
   uint64_t kv_rows_read = 0;
   int n_tiles = 0;            // prefill-chunk attention tiles on the matrix cores
+  uint32_t n_images = 0;      // key tile images of the chunk lanes (per layer)
   uint32_t n_exact = 0;       // rows left to the exact attention passes
   uint64_t kv_rows_chunk = 0; // attended positions of the tiles' rows
   uint64_t kv_chunk_lanes = 0;// KV rows of the lanes the tiles belong to
@@ -1044,6 +1052,7 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
   const bool regime = wide && (d.weight_dtype == COHX_F16 || ctx->quant_gemm) &&
                       attention_chunk_supported((int)d.head_dim, G);
   p.n_tiles = 0;
+  p.n_images = 0;
   p.n_exact = p.rows;
   p.max_kv_exact = p.max_kv;
   if (regime) {
@@ -1056,10 +1065,18 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
         continue;
       }
       p.kv_chunk_lanes += start + nt;
+      // the lane's key tile images: tile-major, KV head minor
+      const uint32_t lane_end = start + nt, img0 = p.n_images,
+                     n_img = (lane_end + kChunkTileKeys - 1) / kChunkTileKeys * d.kv_heads;
+      if (img0 + n_img > w.max_images) return fail(ctx, COHX_RESOURCE, "chunk tile images exceed the workspace");
+      for (uint32_t i = 0; i < n_img; i++)
+        hs.h_stage[img0 + i] = int4{(int)seq, (int)lane_end, (int)(i / d.kv_heads * kChunkTileKeys),
+                                    (int)(i % d.kv_heads)};
+      p.n_images += n_img;
       for (uint32_t t = 0; t < nt; t += 16) {
         const uint32_t rows_t = std::min(16u, nt - t), kv_end = start + t + rows_t;
         for (uint32_t sg = 0; sg * kChunkSegKeys < kv_end; sg++)
-          hs.h_tiles[p.n_tiles++] = int4{(int)(row0 + t), (int)(rows_t | (sg << 8)), (int)seq, (int)(start + t)};
+          hs.h_tiles[p.n_tiles++] = int4{(int)(row0 + t), (int)(rows_t | (sg << 8)), (int)img0, (int)(start + t)};
         for (uint32_t j = t; j < std::min(nt, t + 16); j++) {
           hs.h_row_skip[row0 + j] = 1;
           p.kv_rows_chunk += (uint64_t)start + j + 1;
@@ -1080,6 +1097,8 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
       for (uint32_t r = 0; r < p.rows; r++)
         if (!hs.h_row_skip[r]) hs.h_row_map[p.n_exact++] = r;
       HIP_TRY(hipMemcpyAsync(w.tiles, hs.h_tiles, p.n_tiles * sizeof(int4), hipMemcpyHostToDevice,
+                             ctx->stream));
+      HIP_TRY(hipMemcpyAsync(w.stage, hs.h_stage, p.n_images * sizeof(int4), hipMemcpyHostToDevice,
                              ctx->stream));
       HIP_TRY(hipMemcpyAsync(w.row_skip, hs.h_row_skip, p.rows * sizeof(uint32_t),
                              hipMemcpyHostToDevice, ctx->stream));
@@ -1258,7 +1277,7 @@ namespace {
 const char *kCatNames[kCatCount] = {
     "pack", "embed", "rmsnorm_act", "matvec_qkv", "qkv_rope_append", "attn_scores",
     "attn_softmax_stats", "attn_pv", "attn_combine_act", "matvec_o_residual", "matvec_gate_up_swiglu",
-    "swiglu_act", "matvec_down_residual", "matvec_head_argmax", "attn_chunk_mfma"};
+    "swiglu_act", "matvec_down_residual", "matvec_head_argmax", "attn_chunk_mfma", "attn_chunk_stage"};
 
 int prof_begin(cohx_ctx *ctx, int cat, double bytes, double flops) {
   Profiler &p = ctx->prof;
@@ -1374,8 +1393,10 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
   const double b_softmax = 0.0;
   const double b_pv = kv_rows * KVD * 4;
   const double f_attn = kv_rows * NH * D * 2;
-  // chunk tiles: each lane's K and V once, Q in and O out; QK^T and PV flops
-  const double b_chunk = (double)p.kv_chunk_lanes * KVD * 4 * 2 + (R - RX) * (double)H * 4 * 2;
+  // chunk tiles: each lane's K and V once (read by the staging pass, whose
+  // binary16 images are intermediates), Q in and O out; QK^T and PV flops
+  const double b_stage = (double)p.kv_chunk_lanes * KVD * 4 * 2;
+  const double b_chunk = (R - RX) * (double)H * 4 * 2;
   const double f_chunk = kv_chunk * NH * D * 4;
   const double b_combine = (double)R * H * 4 + R * act_row;
   const double b_post = (double)R * (H + 2 * KVD) * 4 * 2 + (H + 2 * KVD) * 4;
@@ -1432,8 +1453,11 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
       prof_end(ctx, e);
     }
     if (p.n_tiles) {
+      e = prof_begin(ctx, kCatAttnStage, b_stage, 0);
+      launch_attn_stage(s, (int)p.n_images, sd, w.stage, kp, vp, ctx->page_table, w.img);
+      prof_end(ctx, e);
       e = prof_begin(ctx, kCatAttnChunk, b_chunk, f_chunk);
-      launch_attn_chunk(s, p.n_tiles, sd, w.tiles, w.q_rot, kp, vp, ctx->page_table, w.partial);
+      launch_attn_chunk(s, p.n_tiles, sd, w.tiles, w.q_rot, w.img, w.partial);
       prof_end(ctx, e);
     }
     if (RX) {

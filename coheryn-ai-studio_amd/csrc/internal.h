@@ -67,10 +67,14 @@ struct Workspace {
   int4 *tiles = nullptr;
   uint32_t *row_skip = nullptr;
   uint32_t *row_map = nullptr;
+  // the chunk lanes' key tiles as binary16 LDS images (rewritten every layer)
+  // and the work items that make them
+  int4 *stage = nullptr;
+  uint4 *img = nullptr;
   unsigned long long *argmax = nullptr;  // final keys per lane, zeroed by the packer
   unsigned long long *argmax_part = nullptr;  // [lanes][head m-tiles]
   // capacities the buffers were laid out for
-  uint32_t rows = 0, lanes = 0, kv_cap = 0, max_chunks = 0, max_tiles = 0;
+  uint32_t rows = 0, lanes = 0, kv_cap = 0, max_chunks = 0, max_tiles = 0, max_images = 0;
   bool logits_room = false;
 };
 
@@ -79,6 +83,7 @@ struct Staging {
   uint32_t *h_upload = nullptr;  // lane_info then tokens
   uint32_t *h_row_err = nullptr;
   int4 *h_tiles = nullptr;        // tiles, row flags and the row list of the prefill regime
+  int4 *h_stage = nullptr;        // the regime's tile image items
   uint32_t *h_row_skip = nullptr;
   uint32_t *h_row_map = nullptr;
   unsigned long long *h_argmax = nullptr;
@@ -93,7 +98,7 @@ size_t layout_workspace(const cohx_model_desc &d, int nbp_h, int nbp_f, uint32_t
 enum ProfCat {
   kCatPack, kCatEmbed, kCatNorm, kCatMvQkv, kCatQkvPost, kCatAttnScores, kCatAttnSoftmax,
   kCatAttnPv, kCatAttnCombine, kCatMvO, kCatMvGateUp, kCatQuant, kCatMvDown, kCatMvHead,
-  kCatAttnChunk, kCatCount
+  kCatAttnChunk, kCatAttnStage, kCatCount
 };
 
 struct Profiler {

@@ -172,17 +172,24 @@ void launch_attn_pv(hipStream_t s, int rows, int max_kv, const StepDims &d, cons
                     const float *scores, const double *den_part, const float *row_max,
                     double *partial);
 // Matrix-core attention for prefill chunks (tolerance regime): tiles[i] =
-// {first packed row, rows (<= 16) | key segment << 8, sequence, position of
-// the first row}; a workgroup attends to keys [seg * kChunkSegKeys, + kChunkSegKeys)
-// and writes the segment's row max, row sum and unnormalized output as f32
-// (chunk_seg_at) into the rows' partial-sum space, which the combine pass
-// merges in segment order.
+// {first packed row, rows (<= 16) | key segment << 8, index of the lane's
+// first tile image, position of the first row}; a workgroup attends to keys
+// [seg * kChunkSegKeys, + kChunkSegKeys) and writes the segment's row max,
+// row sum and unnormalized output as f32 (chunk_seg_at) into the rows'
+// partial-sum space, which the combine pass merges in segment order.
 constexpr int kChunkSegKeys = 1024;
 constexpr int kChunkSegFloats = 2 + 64;  // m, l, o[64] (head_dim 64)
+// The chunk kernel's key tiles (64 keys of one lane and KV head, head_dim
+// 64) as binary16 LDS images of kChunkImgUnits 16-byte units, written by
+// launch_attn_stage once per layer: items[i] = {sequence, end of the lane's
+// keys, first key of the tile, KV head} makes image i; a lane's images run
+// tile-major from its first (image = first + tile * kv_heads + head).
+constexpr int kChunkTileKeys = 64, kChunkImgUnits = 3 * 64 * 8;
 bool attention_chunk_supported(int D, int G);
-void launch_attn_chunk(hipStream_t s, int n_tiles, const StepDims &d, const int4 *tiles,
-                       const float *q_rot, const float *kpool, const float *vpool,
-                       const int32_t *page_table, double *partial);
+void launch_attn_stage(hipStream_t s, int n_images, const StepDims &d, const int4 *items, const float *kpool,
+                       const float *vpool, const int32_t *page_table, uint4 *img);
+void launch_attn_chunk(hipStream_t s, int n_tiles, const StepDims &d, const int4 *tiles, const float *q_rot,
+                       const uint4 *img, double *partial);
 void launch_attn_combine(hipStream_t s, int rows, const StepDims &d, const uint32_t *row_pos,
                          const double *partial, int act_dtype, int nbp, ActView act,
                          uint32_t *row_err);

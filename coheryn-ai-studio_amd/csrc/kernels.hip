@@ -2210,19 +2210,23 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
 // Prefill chunks on the matrix cores (tolerance regime, used only with the
 // matrix-core linears).  A workgroup takes up to 16 consecutive rows of one
 // lane and one KV head; wave w is query head g*kG + w.  Key tiles of 64
-// tokens are staged in LDS as binary16: K as a hi/lo pair (k = hi + lo to
-// about 2^-22 relative), V rounded once; Q and P enter rounded to binary16
-// (2^-12 relative, the rounding the regime's linears already give their
-// operands).  S = (K_lo + K_hi) Q^T takes two v_mfma_f32_16x16x32_f16, O =
-// V P one, all with f32 sums.  (A bfloat16 hi/lo split of every operand,
-// three MFMAs per product, ran 2.46 against 1.83 ms/step at C3; with V split
-// too, 2.22.)
+// tokens enter in binary16: K as a hi/lo pair (k = hi + lo to about 2^-22
+// relative), V rounded once; Q and P are rounded to binary16 (2^-12
+// relative, the rounding the regime's linears already give their operands).
+// S = (K_lo + K_hi) Q^T takes two v_mfma_f32_16x16x32_f16, O = V P one, all
+// with f32 sums.  (A bfloat16 hi/lo split of every operand, three MFMAs per
+// product, ran 2.46 against 1.83 ms/step at C3; with V split too, 2.22.)
 //   S^T = K Q^T: lane (grp, c) ends up holding S[row c][key 16n + 4grp + i]
 //     for n, i in 0..3, so one lane owns one query row: the row max and sum
 //     need two cross-lane steps, and P never leaves registers.
 //   O^T = V^T P^T: the lane's 16 probabilities are exactly its B operand when
 //     the k-slots of each 32-key step are ordered 16*(j/4) + 4grp + j%4;
 //     V^T is staged in that key order, so each A operand is one 16-byte read.
+// Key tiles are converted once per layer and step (k_attn_stage) into the
+// exact LDS image the chunk kernel multiplies from, which it copies with
+// direct-to-LDS loads, one tile ahead; every row tile of a lane shares them.
+// (Converting each tile from f32 in every workgroup cost about 0.45 of the
+// kernel's 1.77 ms/step at C3.)
 // Scores are taken in log2 units (Q pre-scaled by scale*log2(e)) and
 // exponentiated with v_exp_f32; rows are normalized once at the end.  The
 // reference computes the same attention with f64 dot products and sums
@@ -2245,61 +2249,107 @@ __device__ __forceinline__ float *chunk_seg_at(double *partial, const StepDims &
 }
 
 typedef _Float16 f16x8c __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4c __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x2c __attribute__((ext_vector_type(2)));
 
 namespace chunk {
-constexpr int kD = 64, kKT = 64, kS = 72;  // head dim, keys per tile, LDS row stride (16-bit elements)
-constexpr int kItems = kKT / 2 * kD / 4;   // staging items: (token pair, 4 dims)
+constexpr int kD = 64, kKT = 64;  // head dim, keys per tile
+// A tile image: three blocks of 64 rows x 8 units of 16 bytes (K hi rows,
+// K lo rows, V^T rows), unit u of row R stored at R * 8 + (u ^ swz(R)) so
+// the 16 rows one MFMA operand read touches spread over all banks.
+constexpr int kRowUnits = 8, kBlock = kKT * kRowUnits;
+static_assert(kChunkImgUnits == 3 * kBlock, "K hi, K lo and V^T blocks");
+__device__ __forceinline__ int swz(int R) { return (R >> 1) & 7; }
+__device__ __forceinline__ int unit_at(int R, int u) { return R * kRowUnits + (u ^ swz(R)); }
 
 __device__ __forceinline__ void split(float x, _Float16 &hi, _Float16 &lo) {
   hi = (_Float16)x;
   lo = (_Float16)(x - (float)hi);
 }
 
-// Position of key k (0..63 within a tile) in the V^T rows: the k-slot order
-// of the P operand (see above).
-__device__ __forceinline__ int vperm(int k) {
-  const int ks = k / 32, r = k % 32, h = r / 16, grp = (r % 16) / 4, j = r % 4;
-  return ks * 32 + grp * 8 + h * 4 + j;
+// Key of k-slot s (0..63 within a tile) in the V^T rows: the k-slot order
+// of the P operand (see above): slot 32ks + 8grp + 4h + j holds key
+// 32ks + 16h + 4grp + j.
+__device__ __forceinline__ int vkey(int s) {
+  const int ks = s / 32, r = s % 32, grp = r / 8, h = (r % 8) / 4, j = r % 4;
+  return ks * 32 + h * 16 + grp * 4 + j;
 }
 }  // namespace chunk
+
+// One tile image per workgroup: item = {sequence, end of the lane's keys,
+// first key of the tile, KV head}; keys at or past the end are zero.
+// Thread t converts K row t / 4, dims 16 (t % 4) .. + 15, and then V^T row
+// (dim) t / 4, k-slots 16 (t % 4) .. + 15 from the tile's V staged in LDS.
+__global__ __launch_bounds__(256) void k_attn_stage(StepDims d, const int4 *__restrict__ items,
+                                                    const float *__restrict__ kpool,
+                                                    const float *__restrict__ vpool,
+                                                    const int32_t *__restrict__ pt, uint4 *__restrict__ img) {
+  using namespace chunk;
+  __shared__ float s_vr[kKT][kD + 1];  // the tile's V rows, f32
+  const int4 it = items[blockIdx.x];
+  const int tid = threadIdx.x, k = tid >> 2, q = tid & 3, t = it.z + k, g = it.w;
+  float kx[16], vx[16];
+  if (t < it.y) {
+    const int32_t phys = pt[(size_t)it.x * d.max_pages + t / kPage];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float4 a = *reinterpret_cast<const float4 *>(
+          kpool + k_at(phys, (uint32_t)(t / kPage), g, d.NKV, t % kPage, 16 * q + 4 * j, kD));
+      const float4 b = *reinterpret_cast<const float4 *>(vpool + v_at(phys, g, d.NKV, t % kPage, 16 * q + 4 * j, kD));
+      kx[4 * j] = a.x, kx[4 * j + 1] = a.y, kx[4 * j + 2] = a.z, kx[4 * j + 3] = a.w;
+      vx[4 * j] = b.x, vx[4 * j + 1] = b.y, vx[4 * j + 2] = b.z, vx[4 * j + 3] = b.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; j++) kx[j] = vx[j] = 0.0f;
+  }
+  uint4 *out = img + (size_t)blockIdx.x * kChunkImgUnits;
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    f16x8c hi, lo;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      _Float16 a, b;
+      split(kx[8 * h + e], a, b);
+      hi[e] = a;
+      lo[e] = b;
+    }
+    const int at = unit_at(k, 2 * q + h);
+    out[at] = __builtin_bit_cast(uint4, hi);
+    out[kBlock + at] = __builtin_bit_cast(uint4, lo);
+  }
+#pragma unroll
+  for (int j = 0; j < 16; j++) s_vr[k][16 * q + j] = vx[j];
+  __syncthreads();
+  const int dim = k;
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int u = 2 * q + h;
+    f16x8c v;
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = (_Float16)s_vr[vkey(8 * u + e)][dim];
+    out[2 * kBlock + unit_at(dim, u)] = __builtin_bit_cast(uint4, v);
+  }
+}
 
 template <int kG>
 __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *__restrict__ tiles,
                                                         const float *__restrict__ q_rot,
-                                                        const float *__restrict__ kpool,
-                                                        const float *__restrict__ vpool,
-                                                        const int32_t *__restrict__ pt,
+                                                        const uint4 *__restrict__ img,
                                                         double *__restrict__ partial) {
   using namespace chunk;
-  constexpr int kThreads = 64 * kG, kPer = (kItems + kThreads - 1) / kThreads;
-  constexpr int kRawSlots = kKT * kD / 4;  // 16-byte slots of one raw f32 tile: [token][dim quad]
+  constexpr int kThreads = 64 * kG;
   using E = _Float16;
   using E8 = f16x8c;
-  using E4 = f16x4c;
-  using E2 = f16x2c;
   auto mfma = [](E8 a, E8 b, float4v c) __attribute__((always_inline)) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   };
-  __shared__ __align__(16) E s_kh[kKT * kS];
-  __shared__ __align__(16) E s_kl[kKT * kS];
-  __shared__ __align__(16) E s_v[kD * kS];  // V^T
-  __shared__ __align__(16) float4 s_rk[kRawSlots];  // the next tile's raw K and V, straight from memory
-  __shared__ __align__(16) float4 s_rv[kRawSlots];
-  __shared__ int32_t s_pages[kChunkSegKeys / kPage];
-  const int4 tile = tiles[blockIdx.x / d.NKV];  // first row, rows | segment << 8, sequence, position of first row
+  __shared__ __align__(16) uint4 s_img[2][kChunkImgUnits];  // two tile images, one in flight
+  // first row, rows | segment << 8, the lane's first tile image, position of first row
+  const int4 tile = tiles[blockIdx.x / d.NKV];
   const int g = blockIdx.x % d.NKV, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int h = g * kG + wave, grp = lane / 16, c = lane % 16;
   const int nr = tile.y & 0xff, seg = tile.y >> 8, pos0 = tile.w, kv_end = pos0 + nr;
   const int t_begin = seg * kChunkSegKeys, t_end = min(t_begin + kChunkSegKeys, kv_end);
   const int prow = pos0 + min(c, nr - 1);  // rows past the tile repeat its last row
-  {
-    // the segment's page-table entries (pages past the segment's keys unused)
-    const int32_t *ptr = pt + (size_t)tile.z * d.max_pages;
-    const int np = (t_end - t_begin + kPage - 1) / kPage;
-    for (int i = threadIdx.x; i < np; i += kThreads) s_pages[i] = ptr[t_begin / kPage + i];
-  }
   // B operand of S^T: Q[row c][dims 32ks + 8grp .. +7] in log2 units
   E8 qh[2];
   {
@@ -2318,78 +2368,30 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
 #pragma unroll
   for (int n = 0; n < 4; n++) o[n] = float4v{0.f, 0.f, 0.f, 0.f};
   float m = -__builtin_inff(), l = 0.0f;
-  // raw staging: slot sl = token * 16 + dim quad of the tile; wave w issues
-  // slots 64u + lane for u = w, w + kG, ...: 16 bytes per lane straight into
-  // LDS (tokens past the segment read its last token; the split zeroes them)
-  auto fetch = [&](int t0) {
-    for (int u = wave; u < kRawSlots / kWave; u += kG) {
-      const int sl = u * kWave + lane, t = min(t0 + sl / 16, t_end - 1), qd = sl % 16;
-      const int32_t phys = s_pages[(t - t_begin) / kPage];
-      lds_load16(kpool + k_at(phys, t / kPage, g, d.NKV, t % kPage, 4 * qd, kD), s_rk + u * kWave);
-      lds_load16(vpool + v_at(phys, g, d.NKV, t % kPage, 4 * qd, kD), s_rv + u * kWave);
-    }
+  // image of key tile t0 / 64 into stage st: wave w copies 16-byte units
+  // 64u + lane for u = w, w + kG, ...
+  auto fetch = [&](int t0, int st) {
+    const uint4 *src = img + ((size_t)tile.z + (size_t)(t0 / kKT) * d.NKV + g) * kChunkImgUnits;
+    for (int u = wave; u < kChunkImgUnits / kWave; u += kG)
+      lds_load16(src + u * kWave + lane, &s_img[st][u * kWave]);
   };
-  // split: item i = (token pair i / 16, dims 4 * (i % 16)) from the raw tile
-  // into binary16 hi/lo K rows and binary16 V^T rows (zeros past the segment)
-  auto stash = [&](int t0) {
-#pragma unroll
-    for (int u = 0; u < kPer; u++) {
-      const int i = threadIdx.x + u * kThreads;
-      if (i >= kItems) continue;
-      const int k = 2 * (i / 16), d4 = 4 * (i % 16), vp = vperm(k);
-      float4 rk[2], rv[2];
-#pragma unroll
-      for (int e = 0; e < 2; e++) {
-        const bool live = t0 + k + e < t_end;
-        rk[e] = live ? s_rk[(k + e) * 16 + i % 16] : make_float4(0.f, 0.f, 0.f, 0.f);
-        rv[e] = live ? s_rv[(k + e) * 16 + i % 16] : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-#pragma unroll
-      for (int e = 0; e < 2; e++) {
-        const float kx[4] = {rk[e].x, rk[e].y, rk[e].z, rk[e].w};
-        E4 hi, lo;
-#pragma unroll
-        for (int x = 0; x < 4; x++) {
-          E a, b;
-          split(kx[x], a, b);
-          hi[x] = a;
-          lo[x] = b;
-        }
-        *reinterpret_cast<E4 *>(s_kh + (k + e) * kS + d4) = hi;
-        *reinterpret_cast<E4 *>(s_kl + (k + e) * kS + d4) = lo;
-      }
-      // keys k and k+1 sit side by side in the V^T order (vperm keeps pairs)
-      const float v0[4] = {rv[0].x, rv[0].y, rv[0].z, rv[0].w};
-      const float v1[4] = {rv[1].x, rv[1].y, rv[1].z, rv[1].w};
-#pragma unroll
-      for (int x = 0; x < 4; x++) {
-        E2 v2;
-        v2[0] = (E)v0[x];
-        v2[1] = (E)v1[x];
-        *reinterpret_cast<E2 *>(s_v + (d4 + x) * kS + vp) = v2;
-      }
-    }
-  };
-  __syncthreads();  // page entries
-  fetch(t_begin);
-  for (int t0 = t_begin; t0 < t_end; t0 += kKT) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's raw slots have landed
-    __syncthreads();                     // every wave's slots; every wave is done with the previous tile
-    stash(t0);
-    __syncthreads();
-    if (t0 + kKT < t_end) fetch(t0 + kKT);  // the next raw tile lands while this one is multiplied
-  // S^T tile: s[n][i] = S[row c][key t0 + 16n + 4grp + i]
+  fetch(t_begin, 0);
+  for (int t0 = t_begin, st = 0; t0 < t_end; t0 += kKT, st ^= 1) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's units of the tile have landed
+    __syncthreads();                     // every wave's units; every wave is done with the other stage
+    if (t0 + kKT < t_end) fetch(t0 + kKT, st ^ 1);  // the next image lands while this one is multiplied
+    const E8 *kh = reinterpret_cast<const E8 *>(s_img[st]);
+    const E8 *kl = kh + kBlock, *vt = kh + 2 * kBlock;
+    // S^T tile: s[n][i] = S[row c][key t0 + 16n + 4grp + i]
     float4v s[4];
 #pragma unroll
     for (int n = 0; n < 4; n++) {
       s[n] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 2; ks++) {
-        const int at = (16 * n + c) * kS + 32 * ks + 8 * grp;
-        const E8 kh = *reinterpret_cast<const E8 *>(s_kh + at);
-        const E8 kl = *reinterpret_cast<const E8 *>(s_kl + at);
-        s[n] = mfma(kl, qh[ks], s[n]);
-        s[n] = mfma(kh, qh[ks], s[n]);
+        const int at = unit_at(16 * n + c, 4 * ks + grp);
+        s[n] = mfma(kl[at], qh[ks], s[n]);
+        s[n] = mfma(kh[at], qh[ks], s[n]);
       }
     }
     if (t0 + kKT - 1 > pos0 || t0 + kKT > t_end) {  // causal mask key <= row; keys past the segment
@@ -2432,10 +2434,7 @@ __global__ __launch_bounds__(64 * kG) void k_attn_chunk(StepDims d, const int4 *
 #pragma unroll
     for (int n = 0; n < 4; n++)
 #pragma unroll
-      for (int ks = 0; ks < 2; ks++) {
-        const int at = (16 * n + c) * kS + 32 * ks + 8 * grp;
-        o[n] = mfma(*reinterpret_cast<const E8 *>(s_v + at), ph[ks], o[n]);
-      }
+      for (int ks = 0; ks < 2; ks++) o[n] = mfma(vt[unit_at(16 * n + c, 4 * ks + grp)], ph[ks], o[n]);
   }
   l += __shfl_xor(l, 16, kWave);
   l += __shfl_xor(l, 32, kWave);
@@ -3038,16 +3037,20 @@ bool attention_chunk_supported(int D, int G) {
   return D == 64 && (G == 1 || G == 2 || G == 4 || G == 6 || G == 7 || G == 8);
 }
 
-void launch_attn_chunk(hipStream_t s, int n_tiles, const StepDims &d, const int4 *tiles,
-                       const float *q_rot, const float *kpool, const float *vpool,
-                       const int32_t *page_table, double *partial) {
+void launch_attn_stage(hipStream_t s, int n_images, const StepDims &d, const int4 *items, const float *kpool,
+                       const float *vpool, const int32_t *page_table, uint4 *img) {
+  if (n_images <= 0) return;
+  launch_k(k_attn_stage, dim3(n_images), dim3(256), 0, s, d, items, kpool, vpool, page_table, img);
+}
+
+void launch_attn_chunk(hipStream_t s, int n_tiles, const StepDims &d, const int4 *tiles, const float *q_rot,
+                       const uint4 *img, double *partial) {
   if (n_tiles <= 0) return;
   const dim3 grid(n_tiles * d.NKV);  // tile-major: the longest tiles of every KV head first
   switch (d.G) {
-#define L(GG)                                                                                 \
-  case GG:                                                                                    \
-    launch_k(k_attn_chunk<GG>, grid, dim3(64 * GG), 0, s, d, tiles, q_rot, kpool, vpool,      \
-             page_table, partial);                                                            \
+#define L(GG)                                                                        \
+  case GG:                                                                           \
+    launch_k(k_attn_chunk<GG>, grid, dim3(64 * GG), 0, s, d, tiles, q_rot, img, partial); \
     break;
     L(1) L(2) L(4) L(6) L(7) L(8)
 #undef L
