@@ -1253,10 +1253,11 @@ void q35_split_bf16(hipStream_t s, int rows, int K, const float *x, int ldx, uin
   hipLaunchKernelGGL(k_q35_split, dim3((K / 4 + 255) / 256, rows), dim3(256), 0, s, x, ldx, K, hi, lo);
 }
 
-// Tiles measured on the Qwen3.5 prompt-chunk shapes (2,616 rows, hi and lo
-// products counted): 128 x 128 with two K steps in flight for the input-side
-// projections (mix 8,224 x 1024: 138 us; gate+up 7,168 x 1024: 108 us), four
-// for the residual ones (out K 2048: 41 us; down K 3584: 67 us).
+// Tiles measured on the Qwen3.5 prompt-chunk shapes (4,096 rows, hi and lo
+// products counted): 128 x 128 on eight waves of 64 features x 32 rows with
+// two K steps in flight (mix 8,224 x 1024: 170 us; gate+up 7,168 x 1024:
+// 130 us; out K 2048: 41 us; down K 3584: 63 us; on four waves of 64 x 64:
+// 181, 128, 48, 72).
 void q35_gemm_split(hipStream_t s, bool accumulate, const uint16_t *w, int N, int K, const uint16_t *hi,
                     const uint16_t *lo, int rows, float *out, int ldo, uint32_t *row_err) {
   using namespace gemm;
@@ -1273,13 +1274,11 @@ void q35_gemm_split(hipStream_t s, bool accumulate, const uint16_t *w, int N, in
   g.ldo = ldo;
   g.row_err = row_err;
   const dim3 grid(tile_order(g, N, 128, 128));
-  constexpr int lds = lds_bytes<2, 2, 4, 4, true, kStore>();
-  if (accumulate && K % 128 == 0)
-    hipLaunchKernelGGL((k_gemm<kBF16, true, 2, 2, 4, 4, 4, kAccumulate>), grid, dim3(256), lds, s, g);
-  else if (accumulate)
-    hipLaunchKernelGGL((k_gemm<kBF16, true, 2, 2, 4, 4, 2, kAccumulate>), grid, dim3(256), lds, s, g);
+  constexpr int lds = lds_bytes<2, 4, 4, 2, true, kStore>();
+  if (accumulate)
+    hipLaunchKernelGGL((k_gemm<kBF16, true, 2, 4, 4, 2, 2, kAccumulate>), grid, dim3(512), lds, s, g);
   else
-    hipLaunchKernelGGL((k_gemm<kBF16, true, 2, 2, 4, 4, 2, kStore>), grid, dim3(256), lds, s, g);
+    hipLaunchKernelGGL((k_gemm<kBF16, true, 2, 4, 4, 2, 2, kStore>), grid, dim3(512), lds, s, g);
 }
 
 bool q35_matvec_swiglu(hipStream_t s, const uint16_t *w, int up_off, int F, int K, const float *x,
