@@ -367,14 +367,19 @@ def run_c3(seed, steps, warmup, dtype="f16"):
 
 def chunk_roofline(stats, steps):
     """The prefill chunks' attention on the matrix cores: QK^T and PV flops of
-    the chunk rows (4 * heads * head_dim per attended position) over its time."""
+    the chunk rows (4 * heads * head_dim per attended position) over its time,
+    and the per-layer pass that converts the key tiles into its binary16
+    operands."""
     x = next((x for x in stats if x["name"] == "attn_chunk_mfma" and x["launches"]), None)
     if not x:
         return None
+    st = next((y for y in stats if y["name"] == "attn_chunk_stage" and y["launches"]), None)
     tf = x["flops"] / (x["total_ms"] / 1e3) / 1e12
     return {"bound": "mfma", "kernel": "k_attn_chunk", "achieved": tf, "peak": MFMA_F16_PEAK / 1e12,
             "unit": "TFLOP/s", "frac": tf * 1e12 / MFMA_F16_PEAK, "ms_per_step": x["total_ms"] / steps,
-            "note": "three bf16 products per f32 product (hi/lo split); the peak is one product's"}
+            "staging_ms_per_step": st["total_ms"] / steps if st else None,
+            "note": "S = (K_hi + K_lo) Q^T takes two binary16 products per f32 product, O = V P one; "
+                    "the peak is one product's"}
 
 
 C3_CPU_TOKENS = 24
@@ -619,8 +624,8 @@ def print_mfma_table(mfma_csv, cmd):
         tf = mops * 512 / (a["_ns"] * 1e-9) / 1e12 if a["_ns"] else 0.0
         print(f"| {k} | {len(a['_d'])} | {busy:.3f} | {a.get('SQ_INSTS_VALU_MFMA_MOPS_F16', 0.0):.3g} | "
               f"{a.get('SQ_INSTS_VALU_MFMA_MOPS_BF16', 0.0):.3g} | {tf:.0f} |")
-    print("\nThe counted rate covers every MFMA issued (the chunk attention's three bf16 products per "
-          "f32 product, the Qwen3.5 regime's hi and lo GEMMs); the bench's TFLOP/s count the "
+    print("\nThe counted rate covers every MFMA issued (the chunk attention's two binary16 products for "
+          "each score, the Qwen3.5 regime's hi and lo GEMMs); the bench's TFLOP/s count the "
           "algorithmic flops once.")
 
 
