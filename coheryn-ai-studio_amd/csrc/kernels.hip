@@ -64,11 +64,17 @@ __global__ __launch_bounds__(1024) void k_pack(int n, const uint32_t *__restrict
                                                uint32_t *row_err, unsigned long long *keys,
                                                int n_keys) {
   __shared__ uint32_t scan[1024];
+  __shared__ uint32_t s_start[1024], s_seq[1024], s_toff[1024];
   const int i = threadIdx.x;
   // the step's final argmax keys start at zero (the head raises them)
   for (int k = i; k < n_keys; k += 1024) keys[k] = 0ull;
   const uint32_t nt = i < n ? info[i * 4] : 0u;
   scan[i] = nt;
+  if (i < n) {
+    s_start[i] = info[i * 4 + 1];
+    s_seq[i] = info[i * 4 + 2];
+    s_toff[i] = info[i * 4 + 3];
+  }
   __syncthreads();
   for (int off = 1; off < 1024; off <<= 1) {
     uint32_t v = i >= off ? scan[i - off] : 0u;
@@ -78,20 +84,27 @@ __global__ __launch_bounds__(1024) void k_pack(int n, const uint32_t *__restrict
   }
   if (i == 0) cu[0] = 0;
   if (i < n) {
-    const uint32_t end = scan[i], base = end - nt;
-    const uint32_t start = info[i * 4 + 1], seq = info[i * 4 + 2], toff = info[i * 4 + 3];
-    cu[i + 1] = end;
-    for (uint32_t j = 0; j < nt; j++) {
-      const uint32_t r = base + j, pos = start + j, pidx = pos / kPage;
-      const int32_t phys = pidx < (uint32_t)max_pages ? pt[(size_t)seq * max_pages + pidx] : -1;
-      row_pos[r] = pos;
-      row_lane[r] = (uint32_t)i;
-      row_token[r] = tokens[toff + j];
-      row_seq[r] = seq;
-      row_slot[r] = phys < 0 ? -1 : phys * kPage + (int32_t)(pos % kPage);
-      row_err[r] = phys < 0 ? kErrPage : 0u;
+    cu[i + 1] = scan[i];
+    lane_last[i] = scan[i] - 1;
+  }
+  // rows r = i, i + 1024, ...: the lane is the first whose inclusive end
+  // exceeds r (lanes with no rows never match)
+  const uint32_t rows = n > 0 ? scan[n - 1] : 0u;
+  for (uint32_t r = i; r < rows; r += 1024) {
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (scan[mid] > r) hi = mid; else lo = mid + 1;
     }
-    lane_last[i] = end - 1;
+    const uint32_t base = lo > 0 ? scan[lo - 1] : 0u, j = r - base;
+    const uint32_t pos = s_start[lo] + j, seq = s_seq[lo], pidx = pos / kPage;
+    const int32_t phys = pidx < (uint32_t)max_pages ? pt[(size_t)seq * max_pages + pidx] : -1;
+    row_pos[r] = pos;
+    row_lane[r] = (uint32_t)lo;
+    row_token[r] = tokens[s_toff[lo] + j];
+    row_seq[r] = seq;
+    row_slot[r] = phys < 0 ? -1 : phys * kPage + (int32_t)(pos % kPage);
+    row_err[r] = phys < 0 ? kErrPage : 0u;
   }
 }
 
