@@ -586,6 +586,8 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   if (!rc) rc = halloc(ctx, &h.h_upload, (size_t)NL * 4 + R);
   if (!rc) rc = halloc(ctx, &h.h_row_err, R);
   if (!rc) rc = halloc(ctx, &h.h_argmax, NL);
+  if (!rc) rc = halloc(ctx, &ctx->h_pt_stage, ctx->h_page_table.size());
+  if (!rc && hipEventCreateWithFlags(&ctx->pt_done, hipEventDisableTiming) != hipSuccess) rc = COHX_DEVICE;
   if (rc) return bail(rc);
   *out = ctx;
   return COHX_OK;
@@ -598,10 +600,12 @@ void cohx_destroy(cohx_ctx *ctx) {
   drop_graphs(ctx);
   for (void *p : ctx->allocations) (void)hipFree(p);
   for (void *p : {(void *)ctx->host.h_upload, (void *)ctx->host.h_row_err, (void *)ctx->host.h_argmax,
-                  (void *)ctx->host.h_tiles, (void *)ctx->host.h_stage, (void *)ctx->host.h_row_skip, (void *)ctx->host.h_row_map})
+                  (void *)ctx->host.h_tiles, (void *)ctx->host.h_stage, (void *)ctx->host.h_row_skip, (void *)ctx->host.h_row_map,
+                  (void *)ctx->h_pt_stage})
     if (p) (void)hipHostFree(p);
   q35_free(ctx);
   if (ctx->done) (void)hipEventDestroy(ctx->done);
+  if (ctx->pt_done) (void)hipEventDestroy(ctx->pt_done);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -794,17 +798,26 @@ static int ensure_pages(cohx_ctx *ctx, uint32_t seq, uint32_t from, uint32_t row
   return COHX_OK;
 }
 
+// Uploads the page-table rows changed since the last upload: the range from
+// the first to the last changed sequence (rows between them are unchanged,
+// so equal on both sides) goes through pinned staging in one copy, and the
+// mirror may change again as soon as this returns.
 static int sync_page_table(cohx_ctx *ctx) {
-  for (uint32_t s = 0; s < ctx->pt_dirty.size(); s++) {
-    if (!ctx->pt_dirty[s]) continue;
-    HIP_TRY(hipMemcpyAsync(ctx->page_table + (size_t)s * ctx->max_pages,
-                           ctx->h_page_table.data() + (size_t)s * ctx->max_pages,
-                           (size_t)ctx->max_pages * sizeof(int32_t), hipMemcpyHostToDevice,
-                           ctx->stream));
-    ctx->pt_dirty[s] = 0;
-  }
-  // pageable source: make the copies complete before the host mirror changes
-  HIP_TRY(hipStreamSynchronize(ctx->stream));
+  size_t lo = ctx->pt_dirty.size(), hi = 0;
+  for (size_t s = 0; s < ctx->pt_dirty.size(); s++)
+    if (ctx->pt_dirty[s]) {
+      lo = std::min(lo, s);
+      hi = s;
+    }
+  if (lo > hi) return COHX_OK;
+  if (ctx->pt_pending) HIP_TRY(hipEventSynchronize(ctx->pt_done));  // the staging rows are free again
+  const size_t first = lo * ctx->max_pages, count = (hi - lo + 1) * ctx->max_pages;
+  std::memcpy(ctx->h_pt_stage + first, ctx->h_page_table.data() + first, count * sizeof(int32_t));
+  HIP_TRY(hipMemcpyAsync(ctx->page_table + first, ctx->h_pt_stage + first, count * sizeof(int32_t),
+                         hipMemcpyHostToDevice, ctx->stream));
+  HIP_TRY(hipEventRecord(ctx->pt_done, ctx->stream));
+  ctx->pt_pending = true;
+  std::fill(ctx->pt_dirty.begin() + lo, ctx->pt_dirty.begin() + hi + 1, (uint8_t)0);
   return COHX_OK;
 }
 

@@ -147,6 +147,12 @@ struct cohx_ctx {
   int32_t *page_table = nullptr;
   std::vector<int32_t> h_page_table;
   std::vector<uint8_t> pt_dirty;
+  // pinned copy of the mirror's changed rows for one upload per step, and
+  // the event after that upload (the staging rows are reused only once it
+  // has completed)
+  int32_t *h_pt_stage = nullptr;
+  hipEvent_t pt_done = nullptr;
+  bool pt_pending = false;
   std::vector<int32_t> free_pages;
   std::vector<int32_t> page_refs;
   std::vector<cohx::Sequence> seqs;
