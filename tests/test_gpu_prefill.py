@@ -236,6 +236,40 @@ def test_chunk_attention_matches_oracle_within_tolerance():
     close(res[0]["logits"], sa.logits(), "chunk-only step")
 
 
+def test_chunk_attention_over_several_key_segments():
+    """Chunk rows whose keys span two and three 1024-key segments (segment
+    records merged by the combine pass) and end inside a 64-key tile of the
+    staged key images: a 160-row chunk after 1500 cached tokens and a
+    24-row chunk after 2100, next to a decode lane; logits of every lane and
+    the appended K/V rows against the oracle."""
+    print("case: D=64 chunk attention across key segments", flush=True)
+    cfg = synth.config(layers=2, hidden=256, intermediate=512, heads=4, kv_heads=2,
+                       vocabulary=500, context=4096)
+    c, t = synth.in_memory(cfg, "f16", seed=35)
+    m = make(c, t, True, max_lanes=4, max_rows=256, max_seqs=4, max_context=2400)
+    o = orc.Model(c, t, threads=8)
+    rng = np.random.default_rng(9)
+    fill = (1500, 2100, 700)
+    seqs = [m.seq_alloc() for _ in fill]
+    sess = [o.session(2400) for _ in fill]
+    for i, n in enumerate(fill):
+        m.seq_fill_synthetic(seqs[i], n, 21, i)
+        sess[i].fill_synthetic(n, 21, i)
+    toks = [[int(v) for v in rng.integers(0, c["vocabulary"], n)] for n in (160, 24, 1)]
+    res = m.step([dict(seq=s, tokens=tk, logits=True) for s, tk in zip(seqs, toks)])
+    for i, tk in enumerate(toks):
+        for tok in tk:
+            assert o.forward_batch([sess[i]], [tok])[0] == 0
+    for i, what in enumerate(("two segments", "three segments", "decode lane")):
+        assert res[i]["status"] == 0
+        close(res[i]["logits"], sess[i].logits(), what)
+    for i, n in enumerate(fill):
+        for layer in range(c["layers"]):
+            for values in (False, True):
+                got = m.seq_read_kv_rows(seqs[i], layer, n, len(toks[i]), values)
+                assert float(np.abs(got - sess[i].kv(layer, values)[n:]).max()) < 1e-3, (i, layer, values)
+
+
 def test_regime_head_on_matrix_cores_matches_oracle():
     """A packed-prefill step with 18 logit rows: the F16 head runs on the
     matrix cores too (f32 sums), every lane within tolerance of the oracle,
