@@ -2671,10 +2671,14 @@ static bool mv_q8(hipStream_t s, const MatrixView &w, const ActView &act, int ro
     // LM head: persistent workgroups streaming weight tiles through LDS, two
     // per CU (4 waves per SIMD); always 8 waves, since the tile copy needs
     // them all (waves past the last batch tile only copy)
-    const int nthreads = 512;
-    const int blocks = units < 512 ? units : 512;
     const size_t tile = (size_t)(w.nbp / 2) * (kFmt == 8 ? 1024 : 512) + (size_t)w.nbp * 32;
     const size_t lds = 2 * tile + (size_t)n_tiles * w.nbp * 32;
+    // up to 4 batch tiles: workgroups of 4 waves, four per CU (a Q8_0 tile
+    // of K <= 896 is at most 952 copy items, four per thread), so that more
+    // weight tiles are in flight per CU
+    const int nthreads = n_tiles <= 4 && w.nbp <= 28 ? 256 : 512;
+    const int max_blocks = nthreads == 256 ? 1024 : 512;
+    const int blocks = units < max_blocks ? units : max_blocks;
     if (w.nbp <= 28)  // K <= 896: 14 register pairs of B operand
       launch_k((k_mv_q8h<kFmt, 14>), dim3(blocks), dim3(nthreads), lds, s, w, act, rows_b, n_tiles, o);
     else
