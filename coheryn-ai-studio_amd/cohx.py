@@ -425,31 +425,46 @@ class Model:
         self._check(entry(self.h, ctypes.byref(batch), ctypes.byref(so)))
         res = [dict(status=outs[i].status, argmax=outs[i].argmax, logits=bufs[i])
                for i in range(len(lanes))]
-        self.last_step = dict(width=so.width, rows=so.rows, matrix_bytes=so.matrix_bytes,
-                              kv_bytes=so.kv_bytes, elapsed_ns=so.elapsed_ns)
+        self._last_out = so
         return res
 
     def step_decode(self, seqs, tokens):
         """One decode token per lane, vectorized: seqs and tokens are equal-length
-        uint32 arrays.  Returns (status, argmax) int32/uint32 arrays."""
+        uint32 arrays.  Returns (status, argmax) int32/uint32 arrays.  The lane,
+        token and output buffers of the last sequence list are kept and reused
+        while the list stays the same (a decode loop's per-step Python work is
+        then one token copy and the call)."""
         seqs = np.ascontiguousarray(seqs, np.uint32)
-        tokens = np.ascontiguousarray(tokens, np.uint32)
         n = seqs.size
-        if tokens.size != n:
+        if np.size(tokens) != n:
             raise ValueError("one token per sequence")
-        lanes = np.zeros(n, LANE_DTYPE)
-        lanes["seq"] = seqs
-        lanes["n_tokens"] = 1
-        lanes["tokens"] = tokens.ctypes.data + 4 * np.arange(n, dtype=np.uint64)
-        lanes["start_position"] = AT_END
-        outs = np.zeros(n, LANE_OUT_DTYPE)
-        batch = Batch(n, lanes.ctypes.data_as(ctypes.POINTER(Lane)))
-        so = StepOut()
-        so.lanes = outs.ctypes.data_as(ctypes.POINTER(LaneOut))
-        self._check(lib().cohx_step(self.h, ctypes.byref(batch), ctypes.byref(so)))
-        self.last_step = dict(width=so.width, rows=so.rows, matrix_bytes=so.matrix_bytes,
-                              kv_bytes=so.kv_bytes, elapsed_ns=so.elapsed_ns)
+        key = seqs.tobytes()
+        cache = getattr(self, "_decode_bufs", None)
+        if cache is None or cache[0] != key:
+            tok = np.zeros(n, np.uint32)
+            lanes = np.zeros(n, LANE_DTYPE)
+            lanes["seq"] = seqs
+            lanes["n_tokens"] = 1
+            lanes["tokens"] = tok.ctypes.data + 4 * np.arange(n, dtype=np.uint64)
+            lanes["start_position"] = AT_END
+            outs = np.zeros(n, LANE_OUT_DTYPE)
+            batch = Batch(n, lanes.ctypes.data_as(ctypes.POINTER(Lane)))
+            so = StepOut()
+            so.lanes = outs.ctypes.data_as(ctypes.POINTER(LaneOut))
+            cache = self._decode_bufs = (key, tok, lanes, outs, batch, so, ctypes.byref(batch),
+                                         ctypes.byref(so))
+        _, tok, _, outs, _, so, batch_ref, so_ref = cache
+        np.copyto(tok, tokens, casting="unsafe")
+        self._check(lib().cohx_step(self.h, batch_ref, so_ref))
+        self._last_out = so  # read by last_step when asked for
         return outs["status"].copy(), outs["argmax"].copy()
+
+    @property
+    def last_step(self):
+        """The last step's width, rows, matrix and KV bytes and host time."""
+        so = self._last_out
+        return dict(width=so.width, rows=so.rows, matrix_bytes=so.matrix_bytes, kv_bytes=so.kv_bytes,
+                    elapsed_ns=so.elapsed_ns)
 
     @property
     def matrix_bytes(self):
