@@ -2270,6 +2270,7 @@ constexpr int kD = 64, kKT = 64;  // head dim, keys per tile
 // the 16 rows one MFMA operand read touches spread over all banks.
 constexpr int kRowUnits = 8, kBlock = kKT * kRowUnits;
 static_assert(kChunkImgUnits == 3 * kBlock, "K hi, K lo and V^T blocks");
+static_assert(kChunkTileKeys == kKT && kChunkSegKeys % kKT == 0, "segments of whole key tiles");
 __device__ __forceinline__ int swz(int R) { return (R >> 1) & 7; }
 __device__ __forceinline__ int unit_at(int R, int u) { return R * kRowUnits + (u ^ swz(R)); }
 
