@@ -22,8 +22,12 @@
 // about 10 TB/s of L2-to-LDS traffic its loads alone took longer than this
 // whole kernel, and they slowed the LDS reads beside them.)  Within a step a
 // row's 64 bytes are four 16-byte segments; segment s of row R sits at slot
-// 4R + (s ^ ((R >> 2) & 3)), so the 16 rows x 4 segments a wave reads for one
-// operand spread over all banks.
+// 4R + (s ^ ((R >> 1) & 3)).  The LDS serves a 16-byte access eight lanes at
+// a time, free of bank conflicts when the eight addresses differ modulo 128
+// bytes; a fragment read gives those eight lanes rows R..R+7 of one segment,
+// and this swizzle puts them on eight distinct 16-byte positions.  (With
+// (R >> 2) & 3 rows R and R + 2 met, and about a third of all LDS cycles
+// were bank conflicts.)
 //
 // Epilogues: store or accumulate f32 rows (ldo), SwiGLU of a [gate | up]
 // matrix into the down projection's binary16 operand (gate waves and their up
@@ -373,7 +377,7 @@ __global__ __launch_bounds__(64 * kWM * kWN) void k_gemm(Args g) {
   for (int i = 0; i < kPer; i++) {
     const int slot = (wave * kPer + i) * kWave + lane;
     if (slot < kWSlots) {
-      const int row = slot >> 2, seg = (slot & 3) ^ ((row >> 2) & 3);
+      const int row = slot >> 2, seg = (slot & 3) ^ ((row >> 1) & 3);
       int f = f0 + row;
       if (kEpi == kSwigluF16) f = row < kBM / 2 ? f0 + row : F + f0 + row - kBM / 2;
       f = min(f, g.N - 1);
@@ -383,7 +387,7 @@ __global__ __launch_bounds__(64 * kWM * kWN) void k_gemm(Args g) {
     } else {
       const int xs = slot - kWSlots;
       const bool lo = kLo && xs >= kXSlots;
-      const int row = (xs - (lo ? kXSlots : 0)) >> 2, seg = (slot & 3) ^ ((row >> 2) & 3);
+      const int row = (xs - (lo ? kXSlots : 0)) >> 2, seg = (slot & 3) ^ ((row >> 1) & 3);
       src[i] = (lo ? g.xlo : g.x) + (size_t)min(r0 + row, g.M - 1) * g.ldx + seg * 8;
       step_of[i] = kBK;
     }
@@ -417,14 +421,14 @@ __global__ __launch_bounds__(64 * kWM * kWN) void k_gemm(Args g) {
 #pragma unroll
     for (int a = 0; a < kTM; a++) {
       const int R = (wm * kTM + a) * 16 + lr;
-      af[a] = *reinterpret_cast<const frag *>(stage + R * 4 + (seg ^ ((R >> 2) & 3)));
+      af[a] = *reinterpret_cast<const frag *>(stage + R * 4 + (seg ^ ((R >> 1) & 3)));
     }
 #pragma unroll
     for (int b = 0; b < kTN; b++) {
       const int R = (wn * kTN + b) * 16 + lr;
-      bf[b] = *reinterpret_cast<const frag *>(stage + kWSlots + R * 4 + (seg ^ ((R >> 2) & 3)));
+      bf[b] = *reinterpret_cast<const frag *>(stage + kWSlots + R * 4 + (seg ^ ((R >> 1) & 3)));
       if constexpr (kLo)
-        lf[b] = *reinterpret_cast<const frag *>(stage + kWSlots + kXSlots + R * 4 + (seg ^ ((R >> 2) & 3)));
+        lf[b] = *reinterpret_cast<const frag *>(stage + kWSlots + kXSlots + R * 4 + (seg ^ ((R >> 1) & 3)));
     }
     // step ks + 1 into the other half, then step ks + kR into its registers
     constexpr int jn = (j + 1) % kR;
@@ -474,8 +478,11 @@ __global__ __launch_bounds__(64 * kWM * kWN) void k_gemm(Args g) {
 //
 // LDS per stage: BM weight rows and BN token rows of 64 binary16 inputs
 // (eight 16-byte segments each); segment s of row R sits at slot
-// 8R + (s ^ ((R >> 1) & 7)), so a wave's 16 rows of one segment spread over
-// all banks.
+// 8R + (s ^ (R & 7)), so the eight rows that one pass of a 16-byte LDS
+// access serves (R..R+7 of one segment, in the fragment reads and the weight
+// stores alike) sit at eight distinct positions modulo 128 bytes, free of
+// bank conflicts.  ((R >> 1) & 7 paired rows R and R + 1: a sixth of the
+// LDS cycles were conflicts.)
 // ---------------------------------------------------------------------------
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
@@ -504,7 +511,7 @@ __device__ __forceinline__ f16x8 scale8(uint32_t lo, uint32_t hi, _Float16 d) {
   return v * d;
 }
 
-__device__ __forceinline__ int qswz(int R) { return (R >> 1) & 7; }
+__device__ __forceinline__ int qswz(int R) { return R & 7; }
 
 template <int kWM, int kWN, int kTM, int kTN, int kEpi>
 constexpr int lds_bytes_q() {

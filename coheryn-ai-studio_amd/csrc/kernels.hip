@@ -2266,12 +2266,14 @@ typedef _Float16 f16x8c __attribute__((ext_vector_type(8)));
 namespace chunk {
 constexpr int kD = 64, kKT = 64;  // head dim, keys per tile
 // A tile image: three blocks of 64 rows x 8 units of 16 bytes (K hi rows,
-// K lo rows, V^T rows), unit u of row R stored at R * 8 + (u ^ swz(R)) so
-// the 16 rows one MFMA operand read touches spread over all banks.
+// K lo rows, V^T rows), unit u of row R stored at R * 8 + (u ^ swz(R)).  An
+// MFMA operand read gives each eight lanes that one pass of a 16-byte LDS
+// access serves the rows R..R+7 of one unit; swz(R) = R & 7 puts them at
+// eight distinct positions modulo 128 bytes, which is free of bank conflicts.
 constexpr int kRowUnits = 8, kBlock = kKT * kRowUnits;
 static_assert(kChunkImgUnits == 3 * kBlock, "K hi, K lo and V^T blocks");
 static_assert(kChunkTileKeys == kKT && kChunkSegKeys % kKT == 0, "segments of whole key tiles");
-__device__ __forceinline__ int swz(int R) { return (R >> 1) & 7; }
+__device__ __forceinline__ int swz(int R) { return R & 7; }
 __device__ __forceinline__ int unit_at(int R, int u) { return R * kRowUnits + (u ^ swz(R)); }
 
 __device__ __forceinline__ void split(float x, _Float16 &hi, _Float16 &lo) {
