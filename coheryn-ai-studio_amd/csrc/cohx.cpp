@@ -389,6 +389,10 @@ size_t row_bytes(uint32_t dtype, uint64_t width) {
 }  // namespace
 
 namespace cohx {
+size_t upload_words(uint32_t rows, uint32_t lanes, uint32_t kv_cap) {
+  return (size_t)lanes * 4 + rows + 1 + (size_t)rows * ((kv_cap + 255) / 256);
+}
+
 size_t layout_workspace(const cohx_model_desc &d, int nbp_h, int nbp_f, uint32_t R, uint32_t NL,
                         uint32_t kv_cap, bool logits, uint8_t *base, Workspace *out) {
   const size_t H = d.hidden, F = d.intermediate, V = d.vocabulary, NH = d.heads, NKV = d.kv_heads,
@@ -412,8 +416,11 @@ size_t layout_workspace(const cohx_model_desc &d, int nbp_h, int nbp_f, uint32_t
                          : 0;
   w.logits_room = logits;
   Carver c{base};
-  c.take(w.lane_info, (size_t)NL * 4);
-  c.take(w.tokens, R);
+  c.take(w.lane_info, upload_words(R, NL, kv_cap));
+  if (base) {
+    w.tokens = w.lane_info + (size_t)NL * 4;
+    w.att_items = w.tokens + R;
+  }
   c.take(w.cu, NL + 1);
   c.take(w.row_pos, R);
   c.take(w.row_slot, R);
@@ -583,7 +590,8 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
   if (!rc) rc = halloc(ctx, &h.h_stage, (size_t)std::max(ctx->ws.max_images, 1u));
   if (!rc) rc = halloc(ctx, &h.h_row_skip, (size_t)R);
   if (!rc) rc = halloc(ctx, &h.h_row_map, (size_t)R);
-  if (!rc) rc = halloc(ctx, &h.h_upload, (size_t)NL * 4 + R);
+  if (!rc) rc = halloc(ctx, &h.h_kv, (size_t)R);
+  if (!rc) rc = halloc(ctx, &h.h_upload, upload_words(R, NL, d->max_context));
   if (!rc) rc = halloc(ctx, &h.h_row_err, R);
   if (!rc) rc = halloc(ctx, &h.h_argmax, NL);
   if (!rc) rc = halloc(ctx, &ctx->h_pt_stage, ctx->h_page_table.size());
@@ -601,7 +609,7 @@ void cohx_destroy(cohx_ctx *ctx) {
   for (void *p : ctx->allocations) (void)hipFree(p);
   for (void *p : {(void *)ctx->host.h_upload, (void *)ctx->host.h_row_err, (void *)ctx->host.h_argmax,
                   (void *)ctx->host.h_tiles, (void *)ctx->host.h_stage, (void *)ctx->host.h_row_skip, (void *)ctx->host.h_row_map,
-                  (void *)ctx->h_pt_stage})
+                  (void *)ctx->host.h_kv, (void *)ctx->h_pt_stage})
     if (p) (void)hipHostFree(p);
   q35_free(ctx);
   if (ctx->done) (void)hipEventDestroy(ctx->done);
@@ -1009,8 +1017,9 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
                 "batch width must be in 1..=" + std::to_string(d.max_lanes));
   if (!ctx->finalized) return fail(ctx, COHX_INVALID_REQUEST, "model tensors not finalized");
   Staging &hs = ctx->host;
+  // the staging mirrors the workspace's upload region (same offsets)
   uint32_t *info = hs.h_upload;
-  uint32_t *toks = info + (size_t)d.max_lanes * 4;
+  uint32_t *toks = info + (size_t)w.lanes * 4;
   // duplicate sequences within one step are a shared failure
   for (uint32_t i = 0; i < batch->n_lanes; i++)
     for (uint32_t j = i + 1; j < batch->n_lanes; j++)
@@ -1120,10 +1129,29 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
                                hipMemcpyHostToDevice, ctx->stream));
     }
   }
-  HIP_TRY(hipMemcpyAsync(w.lane_info, info, n * 4 * sizeof(uint32_t), hipMemcpyHostToDevice,
-                         ctx->stream));
-  HIP_TRY(hipMemcpyAsync(w.tokens, toks, p.rows * sizeof(uint32_t), hipMemcpyHostToDevice,
-                         ctx->stream));
+  // the exact passes' work list: (256-key chunk, row) pairs of the rows they
+  // attend for, chunks descending, rows ascending (x indexes row_map in a
+  // step with prefill chunks, else the packed rows)
+  {
+    uint32_t *items = toks + w.rows, *kvx = hs.h_kv;
+    uint32_t nx = 0;
+    for (size_t k = 0; k < n; k++) {
+      const uint32_t nt = info[k * 4 + 0], start = info[k * 4 + 1], row0 = info[k * 4 + 3];
+      for (uint32_t j = 0; j < nt; j++)
+        if (!p.n_tiles || !hs.h_row_skip[row0 + j]) kvx[nx++] = start + j + 1;
+    }
+    if (nx != p.n_exact) return fail(ctx, COHX_DEVICE, "exact attention rows do not match the row list");
+    uint32_t ni = 0, top = 0;
+    for (uint32_t x = 0; x < nx; x++) top = std::max(top, (kvx[x] + 255) / 256);
+    for (uint32_t c = top; c-- > 0;)
+      for (uint32_t x = 0; x < nx; x++)
+        if (c * 256 < kvx[x]) items[1 + ni++] = c << 16 | x;
+    items[0] = ni;
+    const size_t words = (size_t)w.lanes * 4 + w.rows + 1 + ni;
+    if (words > upload_words(w.rows, w.lanes, w.kv_cap) || nx > 65536)
+      return fail(ctx, COHX_DEVICE, "the attention work list exceeds its room");
+    HIP_TRY(hipMemcpyAsync(w.lane_info, info, words * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
+  }
   return COHX_OK;
 }
 
@@ -1388,7 +1416,7 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
   hipStream_t s = ctx->stream;
   StepDims sd{H, F, (int)d.vocabulary, NH, NKV, D, KVD, NH / NKV, d.norm_epsilon,
               1.0f / sqrtf((float)D), ctx->max_pages, (int)w.kv_cap, (int)w.max_chunks,
-              p.n_tiles ? w.row_skip : nullptr, p.n_tiles ? w.row_map : nullptr};
+              p.n_tiles ? w.row_skip : nullptr, p.n_tiles ? w.row_map : nullptr, w.att_items};
   const int RX = (int)p.n_exact;  // rows of the exact attention passes
   if (p.n_tiles) kv_grid = (int)((p.max_kv_exact + 255) / 256 * 256);
   const ActView act = act_view(w);

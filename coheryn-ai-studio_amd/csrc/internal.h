@@ -40,7 +40,9 @@ struct Sequence {
 // Device scratch of one step, carved from one block of device memory by
 // layout_workspace (the context's own block, sized for its capacities).
 struct Workspace {
-  uint32_t *lane_info = nullptr, *tokens = nullptr;
+  // one upload region: lane_info [lanes][4], tokens [rows], then the exact
+  // attention passes' work list (StepDims::att_items)
+  uint32_t *lane_info = nullptr, *tokens = nullptr, *att_items = nullptr;
   uint32_t *cu = nullptr, *row_pos = nullptr, *row_lane = nullptr, *row_token = nullptr,
            *row_seq = nullptr, *lane_last = nullptr, *row_err = nullptr;
   int32_t *row_slot = nullptr;
@@ -80,12 +82,13 @@ struct Workspace {
 
 // Pinned host staging of a context (uploads of the batch, read-back of results).
 struct Staging {
-  uint32_t *h_upload = nullptr;  // lane_info then tokens
+  uint32_t *h_upload = nullptr;  // the workspace's upload region (lane_info, tokens, work list), same offsets
   uint32_t *h_row_err = nullptr;
   int4 *h_tiles = nullptr;        // tiles, row flags and the row list of the prefill regime
   int4 *h_stage = nullptr;        // the regime's tile image items
   uint32_t *h_row_skip = nullptr;
   uint32_t *h_row_map = nullptr;
+  uint32_t *h_kv = nullptr;       // attended length of each exact-pass row (the work list's source)
   unsigned long long *h_argmax = nullptr;
 };
 
@@ -94,6 +97,8 @@ struct Staging {
 // non-null base, also fills `w` with buffers carved from it (256-byte aligned).
 size_t layout_workspace(const cohx_model_desc &d, int nbp_h, int nbp_f, uint32_t rows, uint32_t lanes,
                         uint32_t kv_cap, bool logits, uint8_t *base, Workspace *w);
+// 32-bit words of a workspace's upload region (lane_info, tokens, work list)
+size_t upload_words(uint32_t rows, uint32_t lanes, uint32_t kv_cap);
 
 enum ProfCat {
   kCatPack, kCatEmbed, kCatNorm, kCatMvQkv, kCatQkvPost, kCatAttnScores, kCatAttnSoftmax,

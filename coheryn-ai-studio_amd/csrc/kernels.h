@@ -62,6 +62,13 @@ struct StepDims {
   // (nullptr: row x)
   const uint32_t *row_skip;
   const uint32_t *row_map;
+  // the exact passes' work list (nullptr: full grids over rows x chunks):
+  // [0] = n, then n entries (chunk << 16) | x, one per live (row x, 256-key
+  // chunk), chunks descending and rows ascending within a chunk.  The
+  // scores, exponent and value passes then take 1-D grids over the list's
+  // bound (rows x chunks of the grid's longest row), and their workgroups
+  // past entry n exit at once
+  const uint32_t *att_items;
 };
 
 enum Epilogue { kEpiStore = 0, kEpiResidual = 1, kEpiSwiglu = 2, kEpiArgmax = 3 };

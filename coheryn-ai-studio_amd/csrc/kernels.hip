@@ -1958,6 +1958,25 @@ __device__ __forceinline__ void attn_item(int &row_x, int &g, int &crev, int &pa
   crev = (int)(q / (X * Y));
 }
 
+// Item of a 1-D pass grid over the work list: the same pairing of head parts
+// (ids 8 apart in each block of 16) over the grid's linear ids.
+template <int kS>
+__device__ __forceinline__ void list_item(int &q, int &part) {
+  const unsigned L = blockIdx.x, total = gridDim.x;
+  q = (int)L;
+  part = 0;
+  if constexpr (kS == 2) {
+    const unsigned full = total & ~15u;
+    if (L < full) {
+      q = (int)((L / 16) * 8 + L % 8);
+      part = (int)((L / 8) % 2);
+    } else {
+      q = (int)(full / 2 + (L - full) / 2);
+      part = (int)((L - full) % 2);
+    }
+  }
+}
+
 template <int kD, int kG, int kS>
 __global__ __launch_bounds__(256) void k_attn_scores(StepDims d, const float *__restrict__ q_rot,
                                                      const float *__restrict__ kpool,
@@ -1969,12 +1988,26 @@ __global__ __launch_bounds__(256) void k_attn_scores(StepDims d, const float *__
   constexpr int kH = (kG + kS - 1) / kS;                               // heads of every part but the last
   constexpr int kHL = kG - (kS - 1) * kH > 0 ? kG - (kS - 1) * kH : 1;  // heads of the last part
   constexpr int kE = kD == 64 ? (kH > 4 ? 4 : 2) : 1;                  // elements per group (VGPR budget)
-  int x, g, crev, part;
-  attn_item<kS>(x, g, crev, part);
+  int x, g, c, part;
+  if (d.att_items) {
+    // list entry i = q / NKV (the grid never exceeds the list's room); KV
+    // head fastest, as below
+    int q;
+    list_item<kS>(q, part);
+    g = q % d.NKV;
+    const int i = q / d.NKV;
+    const uint32_t n = d.att_items[0], e = d.att_items[1 + i];
+    if ((uint32_t)i >= n) return;
+    x = (int)(e & 0xffffu);
+    c = (int)(e >> 16);
+  } else {
+    int crev;
+    attn_item<kS>(x, g, crev, part);
+    // chunks in reverse launch order: the high chunks only the longest rows
+    // have are dispatched first, the dense low chunks fill in behind them
+    c = (int)(gridDim.z / kS) - 1 - crev;
+  }
   const int r = d.row_map ? (int)d.row_map[x] : x;
-  // chunks in reverse launch order: the high chunks only the longest rows
-  // have are dispatched first, the dense low chunks fill in behind them
-  const int c = (int)(gridDim.z / kS) - 1 - crev;
   const int kv = (int)row_pos[r] + 1;
   const int t0 = c * kT;
   if (t0 >= kv) return;
@@ -2031,8 +2064,16 @@ __global__ __launch_bounds__(256) void k_attn_exp(StepDims d, const uint32_t *__
   __shared__ double redd[kW][8];
   __shared__ uint64_t s_tab[32];  // expf's table, read per lane below
   if (threadIdx.x < 32) s_tab[threadIdx.x] = kExp2Tab[threadIdx.x];
-  const int r = d.row_map ? (int)d.row_map[blockIdx.x] : (int)blockIdx.x;
-  const int g = blockIdx.y, c = blockIdx.z;
+  int x = (int)blockIdx.x, g = (int)blockIdx.y, c = (int)blockIdx.z;
+  if (d.att_items) {  // 1-D grid over the work list, KV head fastest
+    g = (int)(blockIdx.x % (unsigned)d.NKV);
+    const int i = (int)(blockIdx.x / (unsigned)d.NKV);
+    const uint32_t n = d.att_items[0], e = d.att_items[1 + i];
+    if ((uint32_t)i >= n) return;
+    x = (int)(e & 0xffffu);
+    c = (int)(e >> 16);
+  }
+  const int r = d.row_map ? (int)d.row_map[x] : x;
   const int kv = (int)row_pos[r] + 1, t0 = c * kT;
   if (t0 >= kv) return;
   const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
@@ -2099,11 +2140,20 @@ __global__ __launch_bounds__(256) void k_attn_pv(StepDims d, const float *__rest
   constexpr int kE = (kD + kWave - 1) / kWave;  // elements per lane (lanes >= kD idle when kD < 64)
   static_assert(kChunk * 2 == 256, "one float4 of weights per thread");
   static_assert(kG <= 8, "a wave sums the denominators of at most two heads");
-  const int r = d.row_map ? (int)d.row_map[blockIdx.x] : (int)blockIdx.x;
-  // high chunks first, as in the scores pass; rows run fastest here (the scores
-  // pass's KV-head-fastest order measured 25.3 -> 25.9 us per launch at 128
-  // decode rows over the default 256 steps)
-  const int g = blockIdx.y, c = (int)gridDim.z - 1 - (int)blockIdx.z;
+  // high chunks first, as in the scores pass; with the full grid rows run
+  // fastest (the scores pass's KV-head-fastest order measured 25.3 -> 25.9 us
+  // per launch at 128 decode rows over the default 256 steps); over the work
+  // list, KV head fastest, then the upper and lower half of each 256-key chunk
+  int x = (int)blockIdx.x, g = (int)blockIdx.y, c = (int)gridDim.z - 1 - (int)blockIdx.z;
+  if (d.att_items) {
+    g = (int)(blockIdx.x % (unsigned)d.NKV);
+    const int j = (int)(blockIdx.x / (unsigned)d.NKV), i = j / 2;
+    const uint32_t n = d.att_items[0], e = d.att_items[1 + i];
+    if ((uint32_t)i >= n) return;
+    x = (int)(e & 0xffffu);
+    c = 2 * (int)(e >> 16) + 1 - j % 2;
+  }
+  const int r = d.row_map ? (int)d.row_map[x] : x;
   const int kv = (int)row_pos[r] + 1, t0 = c * kChunk;
   if (t0 >= kv) return;
   __shared__ double red[3][kG][kD];
@@ -3009,7 +3059,8 @@ void launch_attn_scores(hipStream_t s, int rows, int max_kv, const StepDims &d, 
   // groups of 4+ heads in two workgroups (measured at 128 decode rows, G = 7:
   // 26.7 us against 28.3 us in one)
   const int ks = d.G >= 4 ? 2 : 1;
-  const dim3 grid(rows, d.NKV, (max_kv + 255) / 256 * ks);
+  const dim3 grid = d.att_items ? dim3(rows * d.NKV * ((max_kv + 255) / 256) * ks)
+                                : dim3(rows, d.NKV, (max_kv + 255) / 256 * ks);
   bool ok = true;
 #define L(DD, GG)                                                                                       \
   if (ks == 2)                                                                                          \
@@ -3026,7 +3077,7 @@ void launch_attn_scores(hipStream_t s, int rows, int max_kv, const StepDims &d, 
 void launch_attn_exp(hipStream_t s, int rows, int max_kv, const StepDims &d,
                      const uint32_t *row_pos, const float *scores, const float *chunk_max,
                      double *den_part, float *row_max) {
-  const dim3 grid(rows, d.NKV, (max_kv + 255) / 256);
+  const dim3 grid = d.att_items ? dim3(rows * d.NKV * ((max_kv + 255) / 256)) : dim3(rows, d.NKV, (max_kv + 255) / 256);
   switch (d.G) {
 #define L(GG)                                                                               \
   case GG:                                                                                  \
@@ -3043,7 +3094,8 @@ void launch_attn_pv(hipStream_t s, int rows, int max_kv, const StepDims &d, cons
                     const uint32_t *row_pos, const uint32_t *row_seq, const int32_t *page_table,
                     const float *scores, const double *den_part, const float *row_max,
                     double *partial) {
-  const dim3 grid(rows, d.NKV, (max_kv + kChunk - 1) / kChunk);
+  const dim3 grid = d.att_items ? dim3(rows * d.NKV * ((max_kv + 255) / 256) * 2)
+                                : dim3(rows, d.NKV, (max_kv + kChunk - 1) / kChunk);
   bool ok = true;
 #define L(DD, GG)                                                                          \
   launch_k((k_attn_pv<DD, GG>), grid, dim3(256), 0, s, d, vpool, row_pos, row_seq, \
