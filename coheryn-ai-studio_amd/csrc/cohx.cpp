@@ -1143,13 +1143,14 @@ int prepare_batch(cohx_ctx *ctx, const cohx_batch *batch, cohx_lane_out *outs, P
     if (nx != p.n_exact) return fail(ctx, COHX_DEVICE, "exact attention rows do not match the row list");
     uint32_t ni = 0, top = 0;
     for (uint32_t x = 0; x < nx; x++) top = std::max(top, (kvx[x] + 255) / 256);
+    // room: rows x chunks of the workspace (the kernels' grids never exceed it)
+    if (nx > w.rows || nx > 65536 || top > (w.kv_cap + 255) / 256)
+      return fail(ctx, COHX_DEVICE, "the attention work list exceeds its room");
     for (uint32_t c = top; c-- > 0;)
       for (uint32_t x = 0; x < nx; x++)
         if (c * 256 < kvx[x]) items[1 + ni++] = c << 16 | x;
     items[0] = ni;
     const size_t words = (size_t)w.lanes * 4 + w.rows + 1 + ni;
-    if (words > upload_words(w.rows, w.lanes, w.kv_cap) || nx > 65536)
-      return fail(ctx, COHX_DEVICE, "the attention work list exceeds its room");
     HIP_TRY(hipMemcpyAsync(w.lane_info, info, words * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
   }
   return COHX_OK;
