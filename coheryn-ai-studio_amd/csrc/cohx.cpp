@@ -523,7 +523,10 @@ int cohx_create(const cohx_model_desc *d, int device, cohx_ctx **out) {
     return rc;
   };
   if (hipSetDevice(device) != hipSuccess) return bail(COHX_DEVICE);
-  if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess)
+  if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
+      hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->join_ev, hipEventDisableTiming) != hipSuccess)
     return bail(COHX_DEVICE);
   if (int rc_s = resolve_scratch(ctx)) return bail(rc_s);
   const int H = d->hidden, F = d->intermediate, V = d->vocabulary, NH = d->heads,
@@ -614,6 +617,9 @@ void cohx_destroy(cohx_ctx *ctx) {
   q35_free(ctx);
   if (ctx->done) (void)hipEventDestroy(ctx->done);
   if (ctx->pt_done) (void)hipEventDestroy(ctx->pt_done);
+  if (ctx->fork_ev) (void)hipEventDestroy(ctx->fork_ev);
+  if (ctx->join_ev) (void)hipEventDestroy(ctx->join_ev);
+  if (ctx->side) (void)hipStreamDestroy(ctx->side);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -1494,6 +1500,30 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
                         QkvEpi{ly.bqkv, ctx->rope, w.row_pos, w.row_slot, w.q_rot, kp, vp, H, KVD, D, NKV});
       prof_end(ctx, e);
     }
+    // with prefill chunks the decode rows' exact passes (VALU and f64
+    // chains) run on the side stream beside the chunk attention (matrix
+    // cores); they touch disjoint rows of every buffer they write.  Timed
+    // runs keep one stream, so each launch is measured alone.
+    const bool fork = p.n_tiles && RX && !ctx->prof.on;
+    hipStream_t sx = s;
+    if (fork) {
+      HIP_TRY(hipEventRecord(ctx->fork_ev, s));
+      HIP_TRY(hipStreamWaitEvent(ctx->side, ctx->fork_ev, 0));
+      sx = ctx->side;
+    }
+    if (RX) {
+      e = prof_begin(ctx, kCatAttnScores, b_scores, f_attn);
+      launch_attn_scores(sx, RX, kv_grid, sd, w.q_rot, kp, w.row_pos, w.row_seq,
+                         ctx->page_table, w.scores, w.chunk_max, w.row_err);
+      prof_end(ctx, e);
+      e = prof_begin(ctx, kCatAttnSoftmax, b_softmax, 0);
+      launch_attn_exp(sx, RX, kv_grid, sd, w.row_pos, w.scores, w.chunk_max, w.den_part, w.row_max);
+      prof_end(ctx, e);
+      e = prof_begin(ctx, kCatAttnPv, b_pv, f_attn);
+      launch_attn_pv(sx, RX, kv_grid, sd, vp, w.row_pos, w.row_seq, ctx->page_table, w.scores,
+                     w.den_part, w.row_max, w.partial);
+      prof_end(ctx, e);
+    }
     if (p.n_tiles) {
       e = prof_begin(ctx, kCatAttnStage, b_stage, 0);
       launch_attn_stage(s, (int)p.n_images, sd, w.stage, kp, vp, ctx->page_table, w.img);
@@ -1502,18 +1532,9 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
       launch_attn_chunk(s, p.n_tiles, sd, w.tiles, w.q_rot, w.img, w.partial);
       prof_end(ctx, e);
     }
-    if (RX) {
-      e = prof_begin(ctx, kCatAttnScores, b_scores, f_attn);
-      launch_attn_scores(s, RX, kv_grid, sd, w.q_rot, kp, w.row_pos, w.row_seq,
-                         ctx->page_table, w.scores, w.chunk_max, w.row_err);
-      prof_end(ctx, e);
-      e = prof_begin(ctx, kCatAttnSoftmax, b_softmax, 0);
-      launch_attn_exp(s, RX, kv_grid, sd, w.row_pos, w.scores, w.chunk_max, w.den_part, w.row_max);
-      prof_end(ctx, e);
-      e = prof_begin(ctx, kCatAttnPv, b_pv, f_attn);
-      launch_attn_pv(s, RX, kv_grid, sd, vp, w.row_pos, w.row_seq, ctx->page_table, w.scores,
-                     w.den_part, w.row_max, w.partial);
-      prof_end(ctx, e);
+    if (fork) {
+      HIP_TRY(hipEventRecord(ctx->join_ev, ctx->side));
+      HIP_TRY(hipStreamWaitEvent(s, ctx->join_ev, 0));
     }
     // Q8_K operands: the combine writes f32 rows, then their blocks
     const int a_comb = a_o == kActQ8K ? kActF32 : a_o;

@@ -139,6 +139,11 @@ struct cohx_ctx {
   cohx_model_desc desc{};
   int device = 0;
   hipStream_t stream = nullptr;
+  // steps with prefill chunks: the exact passes over the decode rows run on
+  // `side` (default priority) beside the chunk attention, forked from and
+  // joined back into `stream` by these events
+  hipStream_t side = nullptr;
+  hipEvent_t fork_ev = nullptr, join_ev = nullptr;
   std::string err;
   int nbp_h = 0, nbp_f = 0, nbp_max = 0;
   int max_pages = 0;  // pages per sequence
