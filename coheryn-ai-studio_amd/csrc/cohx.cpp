@@ -1464,7 +1464,21 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
     launch_norm_act(s, R, w.x, nullptr, ly.attn_norm, H, d.norm_epsilon, a_qkv, act_blocks(a_qkv, H), act,
                     w.row_err);
     prof_end(ctx, e);
-    if (qg) {
+    // the regime's GEMMs take the qkv projection with its bias, RoPE and K/V
+    // append in their epilogue
+    const QkvEpi qe{ly.bqkv, ctx->rope, w.row_pos, w.row_slot, w.q_rot, kp, vp, H, KVD, D, NKV};
+    const bool f16_gemm = ly.qkv.view.dtype == kFmtF16 && ctx->prefill_mfma && !p.single_token && R >= 128;
+    const double b_qkv_fused =
+        matrix_pass_bytes(ly.qkv, R, 0, false) + (double)R * (H + 2 * KVD) * 4 + (H + 2 * KVD) * 4;
+    bool fused = false;
+    if (qg || f16_gemm) {
+      e = prof_begin(ctx, kCatMvQkv, b_qkv_fused, 2.0 * R * (H + 2 * KVD) * H);
+      fused = launch_gemm_qkv(s, ly.qkv.view, act.f16, R, w.row_err, qe);
+      prof_end(ctx, e);
+    }
+    if (fused) {
+      // done
+    } else if (qg) {
       // quantized GEMM into f32 rows (query/key features back in source
       // order), then the bias, RoPE and K/V append pass
       e = prof_begin(ctx, kCatMvQkv, matrix_pass_bytes(ly.qkv, R, H + 2 * KVD, false),
@@ -1491,13 +1505,8 @@ int enqueue_device_step(cohx_ctx *ctx, Workspace &w, const Prepared &p, int kv_g
       // Q8_0/Q4_0: bias, RoPE and the K/V append run in the matvec's epilogue
       // (rows uploaded in rope_row order); the bytes are the matrix pass plus
       // the post pass's writes
-      e = prof_begin(ctx, kCatMvQkv,
-                     matrix_pass_bytes(ly.qkv, R, 0, false) + (double)R * (H + 2 * KVD) * 4 +
-                         (H + 2 * KVD) * 4,
-                     2.0 * R * (H + 2 * KVD) * H);
-      launch_matvec_qkv(s, ly.qkv.view, act, R,
-                        MatvecOut{nullptr, 0, nullptr, nullptr, w.row_err, nullptr},
-                        QkvEpi{ly.bqkv, ctx->rope, w.row_pos, w.row_slot, w.q_rot, kp, vp, H, KVD, D, NKV});
+      e = prof_begin(ctx, kCatMvQkv, b_qkv_fused, 2.0 * R * (H + 2 * KVD) * H);
+      launch_matvec_qkv(s, ly.qkv.view, act, R, MatvecOut{nullptr, 0, nullptr, nullptr, w.row_err, nullptr}, qe);
       prof_end(ctx, e);
     }
     // with prefill chunks the decode rows' exact passes (VALU and f64

@@ -49,7 +49,10 @@ constexpr int kBK = 32;  // K per ring stage: one MFMA step
 
 // kSwigluQ8: SwiGLU rounded as the reference's Q8_0 operand of the down
 // projection (q * f16(d) per 32-feature block, as binary16; quant.rs:193-213)
-enum Epi { kStore = 0, kAccumulate = 1, kSwigluF16 = 2, kArgmax = 3, kSwigluQ8 = 4 };
+// kQkvRope: the qkv projection's bias, RoPE and K/V append (the operations
+// of the separate post pass, cohx k_qkv_post) applied to the tile in place of
+// a store
+enum Epi { kStore = 0, kAccumulate = 1, kSwigluF16 = 2, kArgmax = 3, kSwigluQ8 = 4, kQkvRope = 5 };
 enum Type { kF16 = 0, kBF16 = 1 };
 
 struct Args {
@@ -81,6 +84,18 @@ struct Args {
   // features uploaded in rope order (cohx.cpp rope_row); each is stored at
   // its source column
   int rope_d, rope_rows;
+  // kQkvRope: features [0, H) query heads, [H, H + KVD) key heads, then value
+  // heads, of D = 64 features each (rope_rows > 0: the query and key rows in
+  // rope order as above, else in source order, where a wave's 64 features
+  // are one head); bias in source order, rope [position][D/2] (cos, sin),
+  // the rows' positions and KV slots (< 0: no append), the rotated queries
+  // [M][H] and the layer's pools
+  const float *qk_bias;
+  const float2 *qk_rope;
+  const uint32_t *qk_pos;
+  const int32_t *qk_slot;
+  float *qk_q, *qk_kpool, *qk_vpool;
+  int qk_H, qk_KVD, qk_NKV;
 };
 
 // SwiGLU's gate activation g / (1 + e^-g) in the regime's epilogues, on the
@@ -168,7 +183,77 @@ __device__ __forceinline__ void epilogue(const Args &g, f32x4 (&acc)[kTM][kTN], 
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int wm = wave / kWN, wn = wave % kWN, lr = lane % 16;
   const int F = g.N / 2;
-  if constexpr (kEpi == kArgmax) {
+  if constexpr (kEpi == kQkvRope) {
+    constexpr int kD = 64, kHalf = 32;
+    static_assert(kTM == 4, "source order: a wave's four 16-feature tiles are one head");
+#pragma unroll
+    for (int b = 0; b < kTN; b++) {
+      const int r = r0 + (wn * kTN + b) * 16 + lr;
+      if (r >= g.M) continue;
+      const uint32_t pos = g.qk_pos[r];
+      const int32_t slot = g.qk_slot[r];
+      const float2 *rp = g.qk_rope + (size_t)pos * kHalf;
+      const int page = slot / kPage, off = slot % kPage;
+      bool bad = false;
+      // n consecutive (i, i + D/2) pairs of one head, element i of the first
+      // at source index src, rotated as k_qkv_post does it and stored as
+      // vectors (n = 4: one K quad; n = 2: half of one)
+      auto rotate = [&](auto N, int src, int i, const float *x, const float *y) __attribute__((always_inline)) {
+        constexpr int n = decltype(N)::value;
+        float lo[n], hi[n];
+#pragma unroll
+        for (int u = 0; u < n; u++) {
+          const float qa = x[u] + g.qk_bias[src + u], qb = y[u] + g.qk_bias[src + u + kHalf];
+          const float2 cs = rp[i + u];
+          lo[u] = fmaf(qa, cs.x, -(qb * cs.y));
+          hi[u] = fmaf(qa, cs.y, qb * cs.x);
+        }
+        float *dlo, *dhi;
+        if (src < g.qk_H) {
+          dlo = g.qk_q + (size_t)r * g.qk_H + src;
+          dhi = dlo + kHalf;
+        } else if (slot >= 0) {
+          const int kg = (src - g.qk_H) / kD;
+          dlo = g.qk_kpool + k_at(page, pos / kPage, kg, g.qk_NKV, off, i, kD);
+          dhi = g.qk_kpool + k_at(page, pos / kPage, kg, g.qk_NKV, off, i + kHalf, kD);
+        } else {
+          return;
+        }
+        if constexpr (n == 4) {
+          *reinterpret_cast<float4 *>(dlo) = make_float4(lo[0], lo[1], lo[2], lo[3]);
+          *reinterpret_cast<float4 *>(dhi) = make_float4(hi[0], hi[1], hi[2], hi[3]);
+        } else {
+          *reinterpret_cast<float2 *>(dlo) = make_float2(lo[0], lo[1]);
+          *reinterpret_cast<float2 *>(dhi) = make_float2(hi[0], hi[1]);
+        }
+      };
+#pragma unroll
+      for (int a = 0; a < kTM; a++) {
+        const int fb = f0 + (wm * kTM + a) * 16 + 4 * (lane / 16);
+        if (fb >= g.N) continue;
+        const float *v = reinterpret_cast<const float *>(&acc[a][b]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) bad |= !finitef(v[i]);
+        if (fb >= g.qk_H + g.qk_KVD) {  // value features: bias and append
+          if (slot >= 0) {
+            const int e = fb - g.qk_H - g.qk_KVD;
+            *reinterpret_cast<float4 *>(g.qk_vpool + v_at(page, e / kD, g.qk_NKV, off, e % kD, kD)) =
+                make_float4(v[0] + g.qk_bias[fb], v[1] + g.qk_bias[fb + 1], v[2] + g.qk_bias[fb + 2],
+                            v[3] + g.qk_bias[fb + 3]);
+          }
+        } else if (g.rope_rows > 0) {  // rope order: pairs (2i, 2i + 1) adjacent
+          const int i = (fb % kD) / 2;
+          const float x[2] = {v[0], v[2]}, y[2] = {v[1], v[3]};
+          rotate(std::integral_constant<int, 2>{}, fb - fb % kD + i, i, x, y);
+        } else if (a < 2) {  // source order: element i in tile a, i + D/2 in tile a + 2
+          const float *y = reinterpret_cast<const float *>(&acc[a + 2][b]);
+          rotate(std::integral_constant<int, 4>{}, fb, fb % kD, v, y);
+        }
+      }
+      if (bad) atomicOr(&g.row_err[g.err_rows ? (int)g.err_rows[r] : r], kErrNonFinite);
+    }
+    return;
+  } else if constexpr (kEpi == kArgmax) {
 #pragma unroll
     for (int b = 0; b < kTN; b++) {
       const int r = r0 + (wn * kTN + b) * 16 + lr;

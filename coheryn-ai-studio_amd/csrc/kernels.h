@@ -139,12 +139,11 @@ bool launch_matvec_swiglu_f16(hipStream_t s, const MatrixView &w, const ActView 
 // launched) for other formats or epilogues, or K not a multiple of 128.
 bool launch_gemm_q(hipStream_t s, Epilogue epi, const MatrixView &w, const uint16_t *x, int rows_b,
                    const MatvecOut &o, uint16_t *out16, int rope_d, int rope_rows);
+
 void launch_argmax_reduce(hipStream_t s, int rows, const unsigned long long *part, int units,
                           unsigned long long *out);
-// Q8_0/Q4_0 qkv projection with launch_qkv_post's work in its epilogue (bias,
-// NeoX RoPE, K/V append into the paged pool), for weights whose query and key
-// rows were uploaded in rope_row order.  Gives the same bits as the matvec and
-// launch_qkv_post in sequence; out.out is unused.
+// The qkv projection's post work (bias, NeoX RoPE, K/V append into the paged
+// pool), done by launch_qkv_post or inside the projection below.
 struct QkvEpi {
   const float *bias;         // [H + 2 KVD], the source row order
   const float2 *rope;        // [position][D/2] (cos, sin)
@@ -154,8 +153,19 @@ struct QkvEpi {
   float *kpool, *vpool;      // the layer's pools
   int H, KVD, D, NKV;
 };
+// Q8_0/Q4_0 qkv projection with launch_qkv_post's work in its epilogue, for
+// weights whose query and key rows were uploaded in rope_row order.  Gives
+// the same bits as the matvec and launch_qkv_post in sequence; out.out is
+// unused.
 void launch_matvec_qkv(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
                        const MatvecOut &o, const QkvEpi &q);
+// The packed-prefill regime's qkv projection with the same work in the
+// GEMM's epilogue (F16 rows in source order, Q8_0/Q4_0 tiles with the query
+// and key rows in rope order): the same bits as the regime's GEMM and
+// launch_qkv_post in sequence.  False (nothing launched) for shapes it does
+// not take (D != 64, K not a multiple of 128).
+bool launch_gemm_qkv(hipStream_t s, const MatrixView &w, const uint16_t *x, int rows_b, uint32_t *row_err,
+                     const QkvEpi &q);
 void launch_qkv_post(hipStream_t s, int rows, const StepDims &d, const float *qkv,
                      const float *bias, const float2 *rope, const uint32_t *row_pos,
                      const int32_t *row_slot, float *q_rot, float *kpool, float *vpool,

@@ -2875,6 +2875,52 @@ bool launch_gemm_q(hipStream_t s, Epilogue epi, const MatrixView &w, const uint1
   return true;
 }
 
+bool launch_gemm_qkv(hipStream_t s, const MatrixView &w, const uint16_t *x, int rows_b, uint32_t *row_err,
+                     const QkvEpi &q) {
+  using namespace gemm;
+  const bool f16 = w.dtype == kFmtF16, quant = w.dtype == kFmtQ8 || w.dtype == kFmtQ4;
+  if (!f16 && !quant) return false;
+  if (q.D != 64 || q.H % 64 || q.KVD % 64 || w.rows != q.H + 2 * q.KVD || w.K % 128) return false;
+  if (quant && w.nbp * 32 != w.K) return false;
+  Args g{};
+  g.x = x;
+  g.N = w.rows;
+  g.K = w.K;
+  g.M = rows_b;
+  g.ldx = w.K;
+  g.row_err = row_err;
+  g.qk_bias = q.bias;
+  g.qk_rope = q.rope;
+  g.qk_pos = q.row_pos;
+  g.qk_slot = q.row_slot;
+  g.qk_q = q.q_rot;
+  g.qk_kpool = q.kpool;
+  g.qk_vpool = q.vpool;
+  g.qk_H = q.H;
+  g.qk_KVD = q.KVD;
+  g.qk_NKV = q.NKV;
+  if (f16) {  // source row order
+    g.w = w.f16;
+    const dim3 grid(tile_order(g, w.rows, 128, 128));
+    launch_k(k_gemm<kF16, false, 2, 4, 4, 2, 4, kQkvRope>, grid, dim3(512), lds_bytes<2, 4, 4, 2, false, kQkvRope>(),
+             s, g);
+    return true;
+  }
+  // the quantized tiles hold the query and key rows in rope order
+  g.qs = w.qs;
+  g.ds = w.ds;
+  g.nbp = w.nbp;
+  g.rope_d = q.D;
+  g.rope_rows = q.H + q.KVD;
+  const dim3 grid(tile_order(g, w.rows, 128, 128, w.dtype == kFmtQ8 ? 34.0 / 32 : 18.0 / 32));
+  constexpr int lds = lds_bytes_q<2, 4, 4, 2, kQkvRope>();
+  if (w.dtype == kFmtQ8)
+    launch_k(k_gemm_q<8, 2, 4, 4, 2, 2, kQkvRope>, grid, dim3(512), lds, s, g);
+  else
+    launch_k(k_gemm_q<4, 2, 4, 4, 2, 2, kQkvRope>, grid, dim3(512), lds, s, g);
+  return true;
+}
+
 bool launch_matvec_swiglu_f16(hipStream_t s, const MatrixView &w, const ActView &act, int rows_b,
                               const MatvecOut &o, uint16_t *out_f16) {
   if (!g_prefill_mfma || rows_b < kPrefillRows || w.dtype != kFmtF16) return false;
