@@ -31,8 +31,9 @@
 //
 // Epilogues: store or accumulate f32 rows (ldo), SwiGLU of a [gate | up]
 // matrix into the down projection's binary16 operand (gate waves and their up
-// partner waves hold the same positions; the up sums cross through LDS), and
-// the argmax head keys.  Non-finite outputs set the row's error bit.
+// partner waves hold the same positions; the up sums cross through LDS), the
+// argmax head keys, and the qkv projection's bias, rotation and K/V append
+// (kQkvRope).  Non-finite outputs set the row's error bit.
 #pragma once
 #include <type_traits>
 
