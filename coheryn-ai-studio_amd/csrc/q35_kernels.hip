@@ -683,9 +683,10 @@ __global__ __launch_bounds__(256) void k_q35_delta(Q35Lanes L, const float *__re
       for (int e = 0; e < 4; e++) rd += wd[e];
     }
     const float o = (float)rd;
-    bool bad = !finitef(o) || !finitef(v);
-#pragma unroll
-    for (int i = 0; i < kKD; i++) bad |= !finitef(col[i]);
+    // a non-finite cell makes its read product non-finite (inf * 0 is NaN),
+    // and no f64 sum brings an inf or NaN term back to a finite value, so o
+    // is non-finite whenever any updated cell is: o covers the cells' check
+    const bool bad = !finitef(o) || !finitef(v);
     o_out[(size_t)row * ldo + h * VD + j] = o;
     if (bad) atomicOr(&row_err[row], kErrRequest);
   }
@@ -881,9 +882,9 @@ __global__ __launch_bounds__(256) void k_q35_linear(
         for (int e = 0; e < 4; e++) rd += wd[e];
       }
       o = (float)rd;
+      // a non-finite updated cell makes o non-finite (its read product is
+      // inf or NaN, and no f64 sum returns from those), so o covers the cells
       bad |= !finitef(o);
-#pragma unroll
-      for (int i = 0; i < kKD; i++) bad |= !finitef(col[i]);
       osq[j] = (double)(o * o);
     }
     __syncthreads();
