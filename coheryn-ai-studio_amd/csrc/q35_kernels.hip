@@ -87,7 +87,25 @@ __global__ __launch_bounds__(256) void k_q35_norm(const float *__restrict__ x, i
   const int r = blockIdx.x;
   const float *xr = x + (size_t)(src ? src[r] : r) * ldx;
   bool bad = false;
-  for (int i = threadIdx.x; i < n; i += 256) {
+  // the first kHeld elements per thread (n <= 1024) keep x and the weight in
+  // registers across the ordered sum, so the scaling pass issues no loads
+  constexpr int kHeld = 4;
+  float xv[kHeld], wv[kHeld];
+#pragma unroll
+  for (int c = 0; c < kHeld; c++) {
+    const int i = threadIdx.x + c * 256;
+    xv[c] = i < n ? xr[i] : 0.0f;
+    wv[c] = i < n ? w[i] : 0.0f;
+  }
+#pragma unroll
+  for (int c = 0; c < kHeld; c++) {
+    const int i = threadIdx.x + c * 256;
+    if (i < n) {
+      sq[i] = (double)(xv[c] * xv[c]);
+      bad |= !finitef(xv[c]);
+    }
+  }
+  for (int i = threadIdx.x + kHeld * 256; i < n; i += 256) {
     const float v = xr[i];
     sq[i] = (double)(v * v);
     bad |= !finitef(v);
@@ -101,7 +119,16 @@ __global__ __launch_bounds__(256) void k_q35_norm(const float *__restrict__ x, i
   }
   __syncthreads();
   const float scale = s_scale, add = zc ? 1.0f : 0.0f;
-  for (int i = threadIdx.x; i < n; i += 256) {
+#pragma unroll
+  for (int c = 0; c < kHeld; c++) {
+    const int i = threadIdx.x + c * 256;
+    if (i < n) {
+      const float y = (xv[c] * scale) * (wv[c] + add);
+      out[(size_t)r * ldo + i] = y;
+      bad |= !finitef(y);
+    }
+  }
+  for (int i = threadIdx.x + kHeld * 256; i < n; i += 256) {
     const float y = (xr[i] * scale) * (w[i] + add);
     out[(size_t)r * ldo + i] = y;
     bad |= !finitef(y);
