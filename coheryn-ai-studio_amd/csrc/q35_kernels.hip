@@ -1119,18 +1119,21 @@ __global__ __launch_bounds__(576) void k_q35_attn(Q35Rows Rw, const float *__res
     m = fmaxf(m, sc[t]);
     mx[t] = m;
   }
-  seg[tid] = m;
-  __syncthreads();
-  if (tid == 0) {
-    float run = -__builtin_inff();
-    for (int i = 0; i < nt; i++) {
-      const float s = seg[i];
-      seg[i] = run;
-      run = fmaxf(run, s);
-    }
+  // exclusive prefix maxima of the segment maxima (a maximum is exact in any
+  // order): a shuffle scan within each wave, then the earlier waves' totals
+  // (the block is whole waves)
+  const int lane = tid % kWave, wave = tid / kWave;
+  float inc = m;
+#pragma unroll
+  for (int d = 1; d < kWave; d *= 2) {
+    const float u = __shfl_up(inc, d, kWave);
+    if (lane >= d) inc = fmaxf(inc, u);
   }
+  float base = __shfl_up(inc, 1, kWave);
+  if (lane == 0) base = -__builtin_inff();
+  if (lane == kWave - 1) seg[wave] = inc;
   __syncthreads();
-  const float base = seg[tid];
+  for (int i = 0; i < wave; i++) base = fmaxf(base, seg[i]);
   for (int t = lo; t < hi; t++) mx[t] = fmaxf(base, mx[t]);
   __syncthreads();
   for (int t = lo; t < hi; t++) {
