@@ -529,22 +529,41 @@ __global__ __launch_bounds__(256) void k_q35_conv(Q35Lanes L, const float *__res
     tap[i] = i < K ? h[(c0 + i) % K] : 0.0f;
     wv[i] = i < K ? w[(size_t)ch * K + i] : 0.0f;
   }
-  for (uint32_t t = 0; t < n; t++) {
-    const uint32_t row = first + t;
-    const float in = mix[(size_t)row * ldm + ch];
+  // the inputs load a group of kAhead tokens at a time, the next group
+  // requested before the current one is folded in, so a chunk's walk waits
+  // on memory once per group rather than once per token
+  constexpr int kAhead = 8;
+  const float *mc = mix + ch;
+  float cur[kAhead], nxt[kAhead];
 #pragma unroll
-    for (int i = 0; i < kMaxConv - 1; i++)
-      if (i < K - 1) tap[i] = tap[i + 1];
+  for (int j = 0; j < kAhead; j++) cur[j] = (uint32_t)j < n ? mc[(size_t)(first + j) * ldm] : 0.0f;
+  for (uint32_t t0 = 0; t0 < n; t0 += kAhead) {
 #pragma unroll
-    for (int i = 0; i < kMaxConv; i++)
-      if (i == K - 1) tap[i] = in;
-    double sum = -0.0;
+    for (int j = 0; j < kAhead; j++) {
+      const uint32_t tn = t0 + kAhead + j;
+      nxt[j] = tn < n ? mc[(size_t)(first + tn) * ldm] : 0.0f;
+    }
 #pragma unroll
-    for (int i = 0; i < kMaxConv; i++)
-      if (i < K) sum += (double)(tap[i] * wv[i]);
-    const float y = silu_f32((float)sum);
-    out[(size_t)row * ldo + ch] = y;
-    if (!finitef(in) || !finitef(y)) atomicOr(&row_err[row], kErrRequest);
+    for (int j = 0; j < kAhead; j++) {
+      if (t0 + j >= n) break;
+      const uint32_t row = first + t0 + j;
+      const float in = cur[j];
+#pragma unroll
+      for (int i = 0; i < kMaxConv - 1; i++)
+        if (i < K - 1) tap[i] = tap[i + 1];
+#pragma unroll
+      for (int i = 0; i < kMaxConv; i++)
+        if (i == K - 1) tap[i] = in;
+      double sum = -0.0;
+#pragma unroll
+      for (int i = 0; i < kMaxConv; i++)
+        if (i < K) sum += (double)(tap[i] * wv[i]);
+      const float y = silu_f32((float)sum);
+      out[(size_t)row * ldo + ch] = y;
+      if (!finitef(in) || !finitef(y)) atomicOr(&row_err[row], kErrRequest);
+    }
+#pragma unroll
+    for (int j = 0; j < kAhead; j++) cur[j] = nxt[j];
   }
   const int c1 = (int)((start + n) % (uint32_t)K);
 #pragma unroll
